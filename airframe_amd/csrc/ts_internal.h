@@ -1,0 +1,96 @@
+// ts_internal.h -- shared definitions of the gfx950 INT4 KV-cache library (not part of the ABI).
+//
+// HBM layout of one layer (S sequences, H kv heads, P = max_seq rounded up to 64, hd dims):
+//
+//   K packed  [S][H][P][hd/2 bytes]            row p = the reference's per-(pos, head) row:
+//                                              word u holds dims 8u..8u+7, dim 8u+n in bits 4n..
+//   V packed  [S][H][P/32][hd*16 bytes]        32-position blocks, "position-packed": word
+//                                              (g, dl, td) of a block sits at index
+//                                              (g*16 + dl)*(hd/16) + td and holds dim 16*td+dl
+//                                              at 8 positions: nibble n<4 -> position 4g+n,
+//                                              nibble n>=4 -> position 16+4g+(n-4)
+//   K scale   [S][H][P] f32
+//   V scale   [S][H][P] f32
+//
+// Each (sequence, kv head) is one contiguous stream per buffer, so a decode workgroup reads
+// whole 1-2 KB runs.  The V block layout is what the PV matrix-core step consumes directly:
+// every 32-bit word is the 8 positions one lane feeds to one v_mfma_f32_16x16x32_f16.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "../../include/turboshimmy.h"
+
+namespace ts {
+
+constexpr int kPosAlign = 64;  // P is a multiple of this (one decode window)
+
+struct KvLayerView {
+    uint8_t *kp;  // K packed
+    uint8_t *vp;  // V packed
+    float *ks;    // K scales
+    float *vs;    // V scales
+    int S, H, P, hd;
+};
+
+}  // namespace ts
+
+struct ts_kv {
+    ts_kv_desc d;
+    int P;                    // padded positions per (seq, head)
+    uint64_t layer_bytes;
+    uint8_t *base;            // one allocation for all layers
+    int32_t *d_len;           // device mirror of lengths
+    std::vector<int32_t> h_len;
+    int device;
+
+    ts::KvLayerView layer(int l) const {
+        ts::KvLayerView v;
+        uint64_t nrow = (uint64_t)d.n_seq * d.n_head_kv * P;
+        uint8_t *b = base + (uint64_t)l * layer_bytes;
+        v.kp = b;
+        v.vp = b + nrow * (d.head_dim / 2);
+        v.ks = (float *)(b + nrow * d.head_dim);
+        v.vs = v.ks + nrow;
+        v.S = d.n_seq;
+        v.H = d.n_head_kv;
+        v.P = P;
+        v.hd = d.head_dim;
+        return v;
+    }
+};
+
+struct ts_rope {
+    float *d_table;  // [n_pos][rope_dim/2][2]
+    int32_t n_pos;
+    int32_t rope_dim;
+};
+
+namespace ts {
+
+// Kernel launchers (defined in the .hip files).  All return hipError_t of the launch.
+hipError_t launch_quantize_rows(const KvLayerView &L, const float *k, const float *v,
+                                const int32_t *d_start, int32_t fixed_start, int32_t count,
+                                int32_t ld_tok, const float *rope, int32_t rope_pairs,
+                                int32_t max_blocks, hipStream_t st);
+hipError_t launch_export(const KvLayerView &L, int seq, int pos0, int n_pos, uint32_t *kp,
+                         uint32_t *vp, float *ks, float *vs, hipStream_t st);
+hipError_t launch_len_update(int32_t *d_len, int n, int32_t seq, int32_t value, int mode,
+                             hipStream_t st);
+
+struct DecodePlan {
+    int chunk;    // positions per split (multiple of 64)
+    int n_split;  // splits for the longest sequence
+    int cap;      // upper bound of n_split for any context <= the one planned for
+};
+DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx);
+hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
+                         const float *rope, int rope_pairs, float softcap, float *out,
+                         float *ws, const DecodePlan &plan, hipStream_t st);
+hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const float *q,
+                          int n_head, int n_tok, const float *rope, int rope_pairs,
+                          float softcap, float *out, hipStream_t st);
+
+}  // namespace ts

@@ -1,0 +1,322 @@
+// ts_kv.cpp -- host side of the C ABI: cache allocation and bookkeeping, RoPE table, argument
+// checking and kernel dispatch.  Reference call surface: src/backend/bindless/kv_cache.rs
+// (KVCache), pipeline/layer.rs:805-1246 (run_layer_with_cache_int4 / requantize_all_kv_int4),
+// preflight.rs:28-142 (RoPE table).
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+
+#include "ts_internal.h"
+
+namespace {
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+int hip_status(hipError_t e) { return e == hipSuccess ? TS_OK : TS_ERR_HIP; }
+
+bool desc_valid(const ts_kv_desc *d) {
+    return d && d->n_layers > 0 && d->n_seq > 0 && d->n_head_kv > 0 && d->head_dim > 0 &&
+           d->max_seq > 0 && d->head_dim % 8 == 0;
+}
+
+// head_dim values with a built kernel (the reference accepts any multiple of 8).
+bool head_dim_built(int hd) { return hd == 64 || hd == 128; }
+
+int padded_positions(int max_seq) { return (max_seq + ts::kPosAlign - 1) / ts::kPosAlign * ts::kPosAlign; }
+
+uint64_t layer_bytes_of(const ts_kv_desc *d) {
+    return (uint64_t)d->n_seq * d->n_head_kv * padded_positions(d->max_seq) * (d->head_dim + 8);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ts_status_string(int status) {
+    switch (status) {
+        case TS_OK: return "ok";
+        case TS_ERR_INVALID: return "invalid argument";
+        case TS_ERR_OVERFLOW: return "KV cache overflow (context window exceeded)";
+        case TS_ERR_UNSUPPORTED: return "unsupported configuration";
+        case TS_ERR_HIP: return "HIP runtime error";
+        case TS_ERR_NOMEM: return "device allocation failed";
+        case TS_ERR_WORKSPACE: return "workspace too small";
+        default: return "unknown status";
+    }
+}
+
+// ---- RoPE ----------------------------------------------------------------------------------
+
+// theta_i = scale / base^(2i/rope_dim) in f32; entry = (cos, sin)(pos * theta_i) in f32.
+// preflight.rs:84-90 (non-YaRN branch) and :97-105.
+int ts_rope_table_host(float *table, int32_t n_pos, int32_t rope_dim, float base, float scale) {
+    if (!table || n_pos <= 0 || rope_dim <= 0 || (rope_dim & 1) || !(base > 0.0f))
+        return TS_ERR_INVALID;
+    if (!(scale >= 1.0f)) return TS_ERR_UNSUPPORTED;
+    const int pairs = rope_dim / 2;
+    std::vector<float> theta(pairs);
+    for (int i = 0; i < pairs; i++) {
+        volatile float expo = (2.0f * (float)i) / (float)rope_dim;
+        volatile float inv = 1.0f / powf(base, expo);
+        theta[i] = inv * scale;
+    }
+    for (int p = 0; p < n_pos; p++) {
+        float *row = table + (size_t)p * pairs * 2;
+        for (int i = 0; i < pairs; i++) {
+            volatile float angle = (float)p * theta[i];
+            row[2 * i] = cosf(angle);
+            row[2 * i + 1] = sinf(angle);
+        }
+    }
+    return TS_OK;
+}
+
+int ts_rope_create(int32_t n_pos, int32_t rope_dim, float base, float scale, ts_rope **out) {
+    if (!out) return TS_ERR_INVALID;
+    *out = nullptr;
+    std::vector<float> host;
+    try {
+        host.resize((size_t)std::max(n_pos, 1) * std::max(rope_dim, 2));
+    } catch (...) {
+        return TS_ERR_NOMEM;
+    }
+    int rc = ts_rope_table_host(host.data(), n_pos, rope_dim, base, scale);
+    if (rc) return rc;
+    ts_rope *r = new (std::nothrow) ts_rope();
+    if (!r) return TS_ERR_NOMEM;
+    size_t bytes = (size_t)n_pos * rope_dim * sizeof(float);
+    if (hipMalloc(&r->d_table, bytes) != hipSuccess) {
+        delete r;
+        return TS_ERR_NOMEM;
+    }
+    if (hipMemcpy(r->d_table, host.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        hipFree(r->d_table);
+        delete r;
+        return TS_ERR_HIP;
+    }
+    r->n_pos = n_pos;
+    r->rope_dim = rope_dim;
+    *out = r;
+    return TS_OK;
+}
+
+int ts_rope_destroy(ts_rope *rope) {
+    if (!rope) return TS_ERR_INVALID;
+    hipError_t e = hipFree(rope->d_table);
+    delete rope;
+    return hip_status(e);
+}
+
+int ts_rope_info(const ts_rope *rope, const float **d_table, int32_t *n_pos, int32_t *rope_dim) {
+    if (!rope) return TS_ERR_INVALID;
+    if (d_table) *d_table = rope->d_table;
+    if (n_pos) *n_pos = rope->n_pos;
+    if (rope_dim) *rope_dim = rope->rope_dim;
+    return TS_OK;
+}
+
+// ---- cache -----------------------------------------------------------------------------------
+
+int ts_kv_bytes(const ts_kv_desc *desc, uint64_t *bytes) {
+    if (!desc_valid(desc) || !bytes) return TS_ERR_INVALID;
+    *bytes = layer_bytes_of(desc) * (uint64_t)desc->n_layers;
+    return TS_OK;
+}
+
+int ts_kv_create(const ts_kv_desc *desc, ts_kv **out) {
+    if (!out) return TS_ERR_INVALID;
+    *out = nullptr;
+    if (!desc_valid(desc)) return TS_ERR_INVALID;
+    if (!head_dim_built(desc->head_dim)) return TS_ERR_UNSUPPORTED;
+    ts_kv *kv = new (std::nothrow) ts_kv();
+    if (!kv) return TS_ERR_NOMEM;
+    kv->d = *desc;
+    kv->P = padded_positions(desc->max_seq);
+    kv->layer_bytes = layer_bytes_of(desc);
+    kv->h_len.assign(desc->n_seq, 0);
+    if (hipGetDevice(&kv->device) != hipSuccess) {
+        delete kv;
+        return TS_ERR_HIP;
+    }
+    uint64_t total = kv->layer_bytes * (uint64_t)desc->n_layers;
+    if (hipMalloc(&kv->base, total) != hipSuccess) {
+        delete kv;
+        return TS_ERR_NOMEM;
+    }
+    if (hipMalloc(&kv->d_len, sizeof(int32_t) * desc->n_seq) != hipSuccess) {
+        hipFree(kv->base);
+        delete kv;
+        return TS_ERR_NOMEM;
+    }
+    // Zero fill once at creation: unwritten positions then dequantize to finite values.
+    if (hipMemset(kv->base, 0, total) != hipSuccess ||
+        hipMemset(kv->d_len, 0, sizeof(int32_t) * desc->n_seq) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        hipFree(kv->base);
+        hipFree(kv->d_len);
+        delete kv;
+        return TS_ERR_HIP;
+    }
+    *out = kv;
+    return TS_OK;
+}
+
+int ts_kv_destroy(ts_kv *kv) {
+    if (!kv) return TS_ERR_INVALID;
+    hipError_t e1 = hipFree(kv->base);
+    hipError_t e2 = hipFree(kv->d_len);
+    delete kv;
+    return (e1 == hipSuccess && e2 == hipSuccess) ? TS_OK : TS_ERR_HIP;
+}
+
+int ts_kv_desc_get(const ts_kv *kv, ts_kv_desc *desc) {
+    if (!kv || !desc) return TS_ERR_INVALID;
+    *desc = kv->d;
+    return TS_OK;
+}
+
+int ts_kv_seq_len(const ts_kv *kv, int32_t seq, int32_t *len) {
+    if (!kv || !len || seq < 0 || seq >= kv->d.n_seq) return TS_ERR_INVALID;
+    *len = kv->h_len[seq];
+    return TS_OK;
+}
+
+int ts_kv_max_len(const ts_kv *kv, int32_t *max_len) {
+    if (!kv || !max_len) return TS_ERR_INVALID;
+    *max_len = kv->d.max_seq;
+    return TS_OK;
+}
+
+int ts_kv_increment(ts_kv *kv, int32_t n_tok, void *stream) {
+    if (!kv || n_tok < 0) return TS_ERR_INVALID;
+    for (int32_t l : kv->h_len)
+        if ((int64_t)l + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;
+    if (n_tok == 0) return TS_OK;
+    hipError_t e = ts::launch_len_update(kv->d_len, kv->d.n_seq, -1, n_tok, 0, as_stream(stream));
+    if (e != hipSuccess) return TS_ERR_HIP;
+    for (auto &l : kv->h_len) l += n_tok;
+    return TS_OK;
+}
+
+int ts_kv_set_seq_len(ts_kv *kv, int32_t seq, int32_t len, void *stream) {
+    if (!kv || seq < 0 || seq >= kv->d.n_seq || len < 0) return TS_ERR_INVALID;
+    if (len > kv->d.max_seq) return TS_ERR_OVERFLOW;
+    hipError_t e = ts::launch_len_update(kv->d_len, kv->d.n_seq, seq, len, 1, as_stream(stream));
+    if (e != hipSuccess) return TS_ERR_HIP;
+    kv->h_len[seq] = len;
+    return TS_OK;
+}
+
+int ts_kv_reset(ts_kv *kv, void *stream) {
+    if (!kv) return TS_ERR_INVALID;
+    hipError_t e = ts::launch_len_update(kv->d_len, kv->d.n_seq, -1, 0, 1, as_stream(stream));
+    if (e != hipSuccess) return TS_ERR_HIP;
+    std::fill(kv->h_len.begin(), kv->h_len.end(), 0);
+    return TS_OK;
+}
+
+int ts_kv_export(const ts_kv *kv, int32_t layer, int32_t seq, int32_t pos0, int32_t n_pos,
+                 uint32_t *d_k_packed, uint32_t *d_v_packed, float *d_k_scale, float *d_v_scale,
+                 void *stream) {
+    if (!kv || layer < 0 || layer >= kv->d.n_layers || seq < 0 || seq >= kv->d.n_seq ||
+        pos0 < 0 || n_pos < 0 || (int64_t)pos0 + n_pos > kv->d.max_seq || !d_k_packed ||
+        !d_v_packed || !d_k_scale || !d_v_scale)
+        return TS_ERR_INVALID;
+    if (n_pos == 0) return TS_OK;
+    return hip_status(ts::launch_export(kv->layer(layer), seq, pos0, n_pos, d_k_packed,
+                                        d_v_packed, d_k_scale, d_v_scale, as_stream(stream)));
+}
+
+// ---- hot path --------------------------------------------------------------------------------
+
+static int check_rope(const ts_rope *rope, int hd, int64_t max_pos_exclusive) {
+    if (!rope) return TS_ERR_INVALID;
+    if (rope->rope_dim > hd) return TS_ERR_INVALID;
+    if (max_pos_exclusive > rope->n_pos) return TS_ERR_INVALID;
+    return TS_OK;
+}
+
+int ts_append_quant(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v, int32_t n_tok,
+                    const ts_rope *rope, void *stream) {
+    if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_k || !d_v || n_tok < 0)
+        return TS_ERR_INVALID;
+    int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
+    if ((int64_t)max_len + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;
+    int rc = check_rope(rope, kv->d.head_dim, (int64_t)max_len + n_tok);
+    if (rc) return rc;
+    if (n_tok == 0) return TS_OK;
+    // Blocks of 32 positions touched by [len, len+n_tok): at most n_tok/32 + 2.
+    int32_t max_blocks = n_tok / 32 + 2;
+    return hip_status(ts::launch_quantize_rows(kv->layer(layer), d_k, d_v, kv->d_len, 0, n_tok,
+                                               n_tok, rope->d_table, rope->rope_dim / 2,
+                                               max_blocks, as_stream(stream)));
+}
+
+int ts_requant_all(ts_kv *kv, int32_t layer, const float *d_k_cache, const float *d_v_cache,
+                   int32_t seq_len, int32_t ld_pos, const ts_rope *rope, void *stream) {
+    if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_k_cache || !d_v_cache || seq_len < 0 ||
+        ld_pos < seq_len)
+        return TS_ERR_INVALID;
+    if (seq_len > kv->d.max_seq) return TS_ERR_OVERFLOW;
+    if (rope) {
+        int rc = check_rope(rope, kv->d.head_dim, seq_len);
+        if (rc) return rc;
+    }
+    if (seq_len == 0) return TS_OK;
+    int32_t blocks = (seq_len + 31) / 32;
+    return hip_status(ts::launch_quantize_rows(kv->layer(layer), d_k_cache, d_v_cache, nullptr, 0,
+                                               seq_len, ld_pos, rope ? rope->d_table : nullptr,
+                                               rope ? rope->rope_dim / 2 : 0, blocks,
+                                               as_stream(stream)));
+}
+
+static bool heads_ok(const ts_kv *kv, int32_t n_head) {
+    return n_head > 0 && n_head % kv->d.n_head_kv == 0 && n_head / kv->d.n_head_kv <= 8;
+}
+
+int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes) {
+    if (!kv || !bytes || !heads_ok(kv, n_head)) return TS_ERR_INVALID;
+    ts::DecodePlan plan = ts::decode_plan(kv->d.n_seq, kv->d.n_head_kv, kv->d.max_seq);
+    *bytes = (uint64_t)kv->d.n_seq * n_head * plan.cap * (kv->d.head_dim + 2) * sizeof(float);
+    return TS_OK;
+}
+
+int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
+                   const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
+                   uint64_t workspace_bytes, void *stream) {
+    if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_q || !d_out || !heads_ok(kv, n_head) ||
+        !(softcap >= 0.0f))
+        return TS_ERR_INVALID;
+    int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
+    if (max_len + 1 > kv->d.max_seq) return TS_ERR_OVERFLOW;
+    int rc = check_rope(rope, kv->d.head_dim, (int64_t)max_len + 1);
+    if (rc) return rc;
+    uint64_t need = 0;
+    ts_attn_decode_workspace(kv, n_head, &need);
+    ts::DecodePlan plan = ts::decode_plan(kv->d.n_seq, kv->d.n_head_kv, max_len + 1);
+    if (plan.n_split > 1 && (!d_workspace || workspace_bytes < need)) return TS_ERR_WORKSPACE;
+    // plan.n_split <= cap(max_seq), the count the workspace was sized for.
+    return hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
+                                        rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
+                                        plan, as_stream(stream)));
+}
+
+int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
+                    int32_t n_tok, const ts_rope *rope, float softcap, float *d_out,
+                    void *stream) {
+    if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_q || !d_out || !heads_ok(kv, n_head) ||
+        n_tok < 0 || !(softcap >= 0.0f))
+        return TS_ERR_INVALID;
+    int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
+    if ((int64_t)max_len + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;
+    int rc = check_rope(rope, kv->d.head_dim, (int64_t)max_len + n_tok);
+    if (rc) return rc;
+    if (n_tok == 0) return TS_OK;
+    return hip_status(ts::launch_prefill(kv->layer(layer), kv->d_len, d_q, n_head, n_tok,
+                                         rope->d_table, rope->rope_dim / 2, softcap, d_out,
+                                         as_stream(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,215 @@
+"""Host-side mirror of airframe's INT4 KV-cache call surface over the C ABI.
+
+Names follow the reference (src/backend/bindless/kv_cache.rs, pipeline/layer.rs,
+preflight.rs); buffers are torch tensors on the current HIP device, used only as device
+memory and streams.  Errors the reference reports as panics or ``Err`` raise ``TsError``
+with the library's status code (``TS_ERR_OVERFLOW`` for ``increment`` past the window, as
+kv_cache.rs:284-293 returns Err).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import KvDesc, check, load
+
+
+def _stream(stream=None) -> ctypes.c_void_p:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _ptr(t: torch.Tensor, dtype: torch.dtype, what: str) -> ctypes.c_void_p:
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{what} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class RopeTable:
+    """PreflightResources' RoPE table (preflight.rs:71-142): host-computed cos/sin, uploaded."""
+
+    def __init__(self, n_pos: int, rope_dim: int, base: float, scale: float = 1.0):
+        L = load()
+        h = ctypes.c_void_p()
+        check("ts_rope_create", L.ts_rope_create(n_pos, rope_dim, base, scale, ctypes.byref(h)))
+        self._h = h
+        self.n_pos, self.rope_dim, self.base, self.scale = n_pos, rope_dim, base, scale
+
+    @staticmethod
+    def host_table(n_pos: int, rope_dim: int, base: float, scale: float = 1.0):
+        import numpy as np
+        t = np.zeros((n_pos, rope_dim // 2, 2), np.float32)
+        check("ts_rope_table_host",
+              load().ts_rope_table_host(t.ctypes.data_as(ctypes.c_void_p), n_pos, rope_dim, base, scale))
+        return t
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        if self._h:
+            load().ts_rope_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KVCache:
+    """INT4 KV cache for ``n_seq`` independent sequences (kv_cache.rs KVCache with a batch
+    dimension; each sequence behaves like one reference cache)."""
+
+    def __init__(self, n_layers: int, n_head_kv: int, head_dim: int, max_seq_len: int,
+                 n_seq: int = 1):
+        L = load()
+        d = KvDesc(n_layers, n_seq, n_head_kv, head_dim, max_seq_len)
+        h = ctypes.c_void_p()
+        check("ts_kv_create", L.ts_kv_create(ctypes.byref(d), ctypes.byref(h)))
+        self._h = h
+        self.n_layers, self.n_seq, self.n_head_kv = n_layers, n_seq, n_head_kv
+        self.head_dim, self.max_seq_len = head_dim, max_seq_len
+        self._ws = {}
+
+    @classmethod
+    def new_int4(cls, n_layers, n_head_kv, head_dim, max_seq_len, n_seq=1):
+        """KVCache::new_int4 (kv_cache.rs:88-96)."""
+        return cls(n_layers, n_head_kv, head_dim, max_seq_len, n_seq)
+
+    @staticmethod
+    def bytes_for(n_layers, n_head_kv, head_dim, max_seq_len, n_seq=1) -> int:
+        d = KvDesc(n_layers, n_seq, n_head_kv, head_dim, max_seq_len)
+        b = ctypes.c_uint64()
+        check("ts_kv_bytes", load().ts_kv_bytes(ctypes.byref(d), ctypes.byref(b)))
+        return b.value
+
+    @property
+    def handle(self):
+        return self._h
+
+    def is_int4(self) -> bool:
+        return True
+
+    def get_seq_len(self, seq: int = 0) -> int:
+        v = ctypes.c_int32()
+        check("ts_kv_seq_len", load().ts_kv_seq_len(self._h, seq, ctypes.byref(v)))
+        return v.value
+
+    def seq_lens(self):
+        return [self.get_seq_len(s) for s in range(self.n_seq)]
+
+    def max_len(self) -> int:
+        return self.max_seq_len
+
+    def increment(self, n_tok: int = 1, stream=None):
+        check("ts_kv_increment", load().ts_kv_increment(self._h, n_tok, _stream(stream)))
+
+    def set_seq_len(self, new_len: int, seq: int = 0, stream=None):
+        check("ts_kv_set_seq_len", load().ts_kv_set_seq_len(self._h, seq, new_len, _stream(stream)))
+
+    def reset(self, stream=None):
+        check("ts_kv_reset", load().ts_kv_reset(self._h, _stream(stream)))
+
+    # ---- hot path ----------------------------------------------------------------------
+
+    def append_quant(self, layer: int, k: torch.Tensor, v: torch.Tensor, rope: RopeTable,
+                     stream=None):
+        """Quantize-on-append (sh_quantize_kv.wgsl, RoPE fused on K).  k, v:
+        [n_seq, n_tok, n_head_kv, head_dim] f32 on the device."""
+        n_tok = k.shape[1]
+        self._check_kv(k, v, n_tok)
+        check("ts_append_quant",
+              load().ts_append_quant(self._h, layer, _ptr(k, torch.float32, "k"),
+                                     _ptr(v, torch.float32, "v"), n_tok, rope.handle,
+                                     _stream(stream)))
+
+    def requantize_all_kv_int4(self, layer: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                               seq_len: int, rope: RopeTable | None = None, stream=None):
+        """requantize_all_kv_int4 (layer.rs:1161-1246) for one layer from f32 caches
+        [n_seq, ld_pos, n_head_kv, head_dim]."""
+        if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != self.n_seq:
+            raise ValueError("k_cache/v_cache must be [n_seq, ld_pos, n_head_kv, head_dim]")
+        check("ts_requant_all",
+              load().ts_requant_all(self._h, layer, _ptr(k_cache, torch.float32, "k_cache"),
+                                    _ptr(v_cache, torch.float32, "v_cache"), seq_len,
+                                    k_cache.shape[1], rope.handle if rope else None,
+                                    _stream(stream)))
+
+    def workspace(self, n_head: int) -> torch.Tensor:
+        if n_head not in self._ws:
+            b = ctypes.c_uint64()
+            check("ts_attn_decode_workspace",
+                  load().ts_attn_decode_workspace(self._h, n_head, ctypes.byref(b)))
+            self._ws[n_head] = torch.empty(max(b.value, 4), dtype=torch.uint8, device="cuda")
+        return self._ws[n_head]
+
+    def attn_decode(self, layer: int, q: torch.Tensor, rope: RopeTable, out: torch.Tensor = None,
+                    softcap: float = 0.0, workspace: torch.Tensor = None, stream=None):
+        """INT4 decode attention (main_attn_out_int4's role).  q: [n_seq, n_head, head_dim]."""
+        n_head = q.shape[1]
+        if q.dim() != 3 or q.shape[0] != self.n_seq or q.shape[2] != self.head_dim:
+            raise ValueError("q must be [n_seq, n_head, head_dim]")
+        if out is None:
+            out = torch.empty_like(q)
+        ws = workspace if workspace is not None else self.workspace(n_head)
+        check("ts_attn_decode",
+              load().ts_attn_decode(self._h, layer, _ptr(q, torch.float32, "q"), n_head,
+                                    rope.handle, softcap, _ptr(out, torch.float32, "out"),
+                                    ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
+        return out
+
+    def attn_prefill(self, layer: int, q: torch.Tensor, rope: RopeTable, out: torch.Tensor = None,
+                     softcap: float = 0.0, stream=None):
+        """Chunked-prefill causal attention.  q: [n_seq, n_tok, n_head, head_dim]."""
+        if q.dim() != 4 or q.shape[0] != self.n_seq or q.shape[3] != self.head_dim:
+            raise ValueError("q must be [n_seq, n_tok, n_head, head_dim]")
+        if out is None:
+            out = torch.empty_like(q)
+        check("ts_attn_prefill",
+              load().ts_attn_prefill(self._h, layer, _ptr(q, torch.float32, "q"), q.shape[2],
+                                     q.shape[1], rope.handle, softcap,
+                                     _ptr(out, torch.float32, "out"), _stream(stream)))
+        return out
+
+    def export(self, layer: int, seq: int, pos0: int, n_pos: int, stream=None):
+        """Packed K/V and scales of positions [pos0, pos0+n_pos) in the reference layout
+        ([pos][n_head_kv][head_dim/8] u32 as int32 bits, [pos][n_head_kv] f32)."""
+        dev = torch.device("cuda")
+        kp = torch.empty((n_pos, self.n_head_kv, self.head_dim // 8), dtype=torch.int32, device=dev)
+        vp = torch.empty_like(kp)
+        ks = torch.empty((n_pos, self.n_head_kv), dtype=torch.float32, device=dev)
+        vs = torch.empty_like(ks)
+        check("ts_kv_export",
+              load().ts_kv_export(self._h, layer, seq, pos0, n_pos, ctypes.c_void_p(kp.data_ptr()),
+                                  ctypes.c_void_p(vp.data_ptr()), ctypes.c_void_p(ks.data_ptr()),
+                                  ctypes.c_void_p(vs.data_ptr()), _stream(stream)))
+        return kp, vp, ks, vs
+
+    def _check_kv(self, k, v, n_tok):
+        want = (self.n_seq, n_tok, self.n_head_kv, self.head_dim)
+        if tuple(k.shape) != want or tuple(v.shape) != want:
+            raise ValueError(f"k/v must be {want}")
+
+    def close(self):
+        if self._h:
+            load().ts_kv_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# keep the status codes reachable from the package
+TS_ERR_OVERFLOW = _lib.TS_ERR_OVERFLOW

@@ -1,0 +1,160 @@
+/*
+ * turboshimmy.h -- C ABI of airframe_amd's MI355X (gfx950) INT4 KV-cache path.
+ *
+ * Drop-in boundary for airframe's TurboShimmy path (reference repository paths):
+ *   KVCache                  src/backend/bindless/kv_cache.rs
+ *   run_layer_with_cache_int4 (its quantize + INT4-attention part)
+ *                            src/backend/bindless/pipeline/layer.rs:805-1159
+ *   requantize_all_kv_int4   src/backend/bindless/pipeline/layer.rs:1161-1246
+ *   RoPE table               src/backend/bindless/preflight.rs:28-142
+ *
+ * Conventions
+ *   - Every function returns an int status: TS_OK (0) or a negative TS_ERR_* code.  Nothing
+ *     aborts; the reference's panics (bad head_dim, getter misuse, overflow) become codes.
+ *   - Pointers named d_* are device pointers owned by the caller; the cache's own buffers are
+ *     allocated by ts_kv_create and freed by ts_kv_destroy.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Work is
+ *     enqueued on it asynchronously; nothing synchronises the host unless stated.
+ *   - A cache handle is not thread-safe: callers serialise use of one handle, as the
+ *     reference does with its Arc<Mutex<KVCache>> (src/bin/shimmy_server_gpu.rs:839).
+ *   - B = n_seq independent sequences.  The reference path has batch 1
+ *     (pipeline/layer.rs:845-855); every sequence here behaves like its own reference cache.
+ *
+ * Quantisation (bit-exact with the reference CPU quantizer, test_int4_parity.rs:56-75):
+ *   per (position, kv head) head vector x[hd]: scale = max|x|/7 (1 if 0);
+ *   code = clamp(round_half_away(x/scale) + 8, 1, 15); dequant = (code - 8) * scale.
+ *   K is rotated (RoPE at its absolute position, rope.rs:180-197) before quantisation,
+ *   V is not (attention.rs:195-209 stores post-RoPE K).
+ */
+#ifndef TURBOSHIMMY_H
+#define TURBOSHIMMY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TS_OK = 0,
+    TS_ERR_INVALID = -1,     /* bad argument or shape (reference: panic / Err) */
+    TS_ERR_OVERFLOW = -2,    /* context window exceeded (reference: KVCache::increment Err) */
+    TS_ERR_UNSUPPORTED = -3, /* valid for the reference but not built here (e.g. head_dim) */
+    TS_ERR_HIP = -4,         /* a HIP runtime call failed */
+    TS_ERR_NOMEM = -5,       /* device allocation failed */
+    TS_ERR_WORKSPACE = -6    /* caller workspace smaller than ts_attn_decode_workspace */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char *ts_status_string(int status);
+
+/* ---- RoPE table ----------------------------------------------------------------------- */
+
+typedef struct ts_rope ts_rope;
+
+/* Fill a host table[n_pos][rope_dim/2][2] = (cos, sin)(pos * theta_i),
+ * theta_i = scale / base^(2i/rope_dim).  Replaces PreflightResources::compute_rope_table
+ * (preflight.rs:71-111) for scale >= 1 (plain and linear); YaRN (scale < 1) returns
+ * TS_ERR_UNSUPPORTED.  Host only; needs no GPU. */
+int ts_rope_table_host(float *table, int32_t n_pos, int32_t rope_dim, float base, float scale);
+
+/* Build the table on the host and upload it (preflight.rs:114-142, upload_rope_table). */
+int ts_rope_create(int32_t n_pos, int32_t rope_dim, float base, float scale, ts_rope **out);
+int ts_rope_destroy(ts_rope *rope);
+/* Device pointer of the uploaded table and its size (n_pos, rope_dim). */
+int ts_rope_info(const ts_rope *rope, const float **d_table, int32_t *n_pos, int32_t *rope_dim);
+
+/* ---- INT4 KV cache ---------------------------------------------------------------------- */
+
+typedef struct ts_kv_desc {
+    int32_t n_layers;
+    int32_t n_seq;     /* independent sequences (batch) */
+    int32_t n_head_kv;
+    int32_t head_dim;  /* 64 or 128 (reference accepts any multiple of 8: kv_cache.rs:152-156) */
+    int32_t max_seq;   /* per-sequence capacity, positions */
+} ts_kv_desc;
+
+typedef struct ts_kv ts_kv;
+
+/* Device bytes ts_kv_create would allocate for this descriptor (host only; no GPU needed).
+ * Replaces the per-layer sizing of KVCache::new_inner (kv_cache.rs:98-233) minus the f32
+ * staging buffers, which this path never allocates. */
+int ts_kv_bytes(const ts_kv_desc *desc, uint64_t *bytes);
+
+/* KVCache::new_int4 (kv_cache.rs:88-96).  Allocates packed K/V and scales for all layers and
+ * sequences on the current HIP device, zero-filled; all lengths start at 0. */
+int ts_kv_create(const ts_kv_desc *desc, ts_kv **out);
+int ts_kv_destroy(ts_kv *kv);
+int ts_kv_desc_get(const ts_kv *kv, ts_kv_desc *desc);
+
+/* KVCache::get_seq_len / max_len (kv_cache.rs:236-240, :352-355): host-side lengths. */
+int ts_kv_seq_len(const ts_kv *kv, int32_t seq, int32_t *len);
+int ts_kv_max_len(const ts_kv *kv, int32_t *max_len);
+
+/* KVCache::increment (kv_cache.rs:284-293) for every sequence, by n_tok positions (the
+ * reference calls it once per token after all layers).  Returns TS_ERR_OVERFLOW, and changes
+ * nothing, if any sequence would exceed max_seq. */
+int ts_kv_increment(ts_kv *kv, int32_t n_tok, void *stream);
+
+/* KVCache::set_seq_len (kv_cache.rs:265-274) for one sequence (TS_ERR_OVERFLOW instead of
+ * the reference's panic).  Used for ragged batches. */
+int ts_kv_set_seq_len(ts_kv *kv, int32_t seq, int32_t len, void *stream);
+
+/* KVCache::reset (kv_cache.rs:256-259): all lengths to 0; buffers stay allocated. */
+int ts_kv_reset(ts_kv *kv, void *stream);
+
+/* Copy positions [pos0, pos0+n_pos) of one sequence and layer out of the cache into the
+ * reference's layout (kv_cache.rs:26-37): packed [n_pos][n_head_kv][head_dim/8] u32, scales
+ * [n_pos][n_head_kv] f32.  All four outputs are device pointers.  Stands in for the
+ * get_{k,v}_{packed,scale}_buffer getters (kv_cache.rs:312-345). */
+int ts_kv_export(const ts_kv *kv, int32_t layer, int32_t seq, int32_t pos0, int32_t n_pos,
+                 uint32_t *d_k_packed, uint32_t *d_v_packed, float *d_k_scale, float *d_v_scale,
+                 void *stream);
+
+/* ---- hot path ------------------------------------------------------------------------------ */
+
+/* RoPE-fused quantize-on-append.  Replaces quantize_kv (sh_quantize_kv.wgsl:39-90, dispatched
+ * at layer.rs:1092-1099) plus the RoPE step of attention.rs:196-199.
+ * d_k, d_v: [n_seq][n_tok][n_head_kv][head_dim] raw f32.  Token t of sequence s is written
+ * at position len[s] + t; K is rotated there with `rope`.  Lengths do not change (call
+ * ts_kv_increment after all layers, as the reference does). */
+int ts_append_quant(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v, int32_t n_tok,
+                    const ts_rope *rope, void *stream);
+
+/* requantize_all_kv_int4 (layer.rs:1161-1246) for one layer: quantize positions
+ * [0, seq_len) of every sequence from f32 caches d_k_cache, d_v_cache laid out
+ * [n_seq][ld_pos][n_head_kv][head_dim] (ld_pos >= seq_len).  With rope != NULL, K is rotated
+ * at each position first; with NULL it is taken as already rotated (the CPU KvCache stores
+ * post-RoPE K).  Lengths do not change. */
+int ts_requant_all(ts_kv *kv, int32_t layer, const float *d_k_cache, const float *d_v_cache,
+                   int32_t seq_len, int32_t ld_pos, const ts_rope *rope, void *stream);
+
+/* Bytes of scratch ts_attn_decode needs for n_head query heads (worst case over lengths up
+ * to max_seq).  Host only. */
+int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes);
+
+/* INT4 GQA decode attention.  Replaces main_attn_out_int4 (sh_layer_v1_int4.wgsl:1042-1143,
+ * dispatched at layer.rs:1100-1107) with the CPU path's semantics (attention.rs:236-313).
+ * d_q: [n_seq][n_head][head_dim] raw f32 for the token just appended; it is rotated at
+ * position len[s] and attends to positions 0..len[s] (len[s]+1 keys, the state between
+ * ts_append_quant and ts_kv_increment, like CacheParams{current_pos, seq_len+1}).
+ * d_out: [n_seq][n_head][head_dim] f32.  n_head must be a multiple of n_head_kv with
+ * n_head/n_head_kv <= 8.  softcap > 0 applies tanh(s/softcap)*softcap to the scaled scores
+ * (sh_layer_v1_int4.wgsl:1116-1118).  d_workspace: ts_attn_decode_workspace bytes. */
+int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
+                   const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
+                   uint64_t workspace_bytes, void *stream);
+
+/* Chunked-prefill attention over the INT4 cache.  Stands in for the f32 main_attn_out of
+ * batched prefill (sh_layer_v1.wgsl:662-762, inference.rs:1160-1166) with the INT4 cache as
+ * its source.  d_q: [n_seq][n_tok][n_head][head_dim] raw f32 for the n_tok tokens just
+ * appended at len[s]..len[s]+n_tok-1; query t is rotated at len[s]+t and sees keys
+ * 0..len[s]+t (causal).  d_out has the shape of d_q. */
+int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
+                    int32_t n_tok, const ts_rope *rope, float softcap, float *d_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TURBOSHIMMY_H */

@@ -1,0 +1,267 @@
+/*
+ * ts_oracle.c -- CPU restatement of airframe's TurboShimmy INT4 KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP kernels of
+ * airframe_amd are compared against, and the CPU baseline timed beside them.
+ * Nothing in the product library links, loads or calls it.
+ *
+ * Every function restates one piece of the reference (paths relative to the
+ * reference repository root):
+ *
+ *   or_rope_table       src/backend/bindless/preflight.rs:71-111  (compute_rope_table,
+ *                       plain/linear branch; theta as in src/ops/reference/rope.rs:150-152)
+ *   or_rope_rotate      src/ops/reference/rope.rs:180-197          (adjacent-pair rotation)
+ *   or_quantize_row     src/backend/bindless/test_int4_parity.rs:56-75 (cpu_quantize),
+ *                       same arithmetic as sh_quantize_kv.wgsl:56-89
+ *   or_dequantize_row   src/backend/bindless/test_int4_parity.rs:78-87 (cpu_dequantize)
+ *   or_append           src/ops/reference/attention.rs:195-209 (RoPE on K at the absolute
+ *                       position, V raw, store at current_len) + src/runtime/kvcache.rs:111-177,
+ *                       with the store replaced by the INT4 quantizer (layout
+ *                       src/backend/bindless/kv_cache.rs:26-37: packed [pos][n_kv][hd/8] u32,
+ *                       scales [pos][n_kv] f32)
+ *   or_attend_head      src/ops/reference/attention.rs:236-313 (per-head QK^T, scale,
+ *                       causal softmax, PV), src/ops/reference/matmul.rs:91-104 (f32 products
+ *                       accumulated in f64), src/ops/reference/softmax.rs:91-129 (mask to -inf,
+ *                       max, f32 exp, f64 sum, f64 reciprocal cast to f32 then multiply), reading
+ *                       K and V through cpu_dequantize.  The optional tanh softcap follows
+ *                       sh_layer_v1_int4.wgsl:1115-1118 (0 disables it; the CPU path has none).
+ *
+ * Build: gcc -O2 -fno-fast-math -ffp-contract=off (no FMA contraction anywhere), with
+ * OpenMP only for the multi-threaded baseline entry point.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---- RoPE ------------------------------------------------------------------------- */
+
+/* table[pos][pair][0]=cos(pos*theta_pair), [1]=sin(...), theta_i = 1/base^(2i/rope_dim),
+ * times `scale` (the non-YaRN branch of preflight.rs:88-90; rope.rs:154-155 is identical for
+ * scale == 1).  YaRN (scale < 1) is rejected: no configuration of this path uses it. */
+int or_rope_table(float *table, int n_pos, int rope_dim, float base, float scale) {
+    if (rope_dim <= 0 || (rope_dim & 1) || n_pos <= 0 || scale < 1.0f) return -1;
+    int n_pairs = rope_dim / 2;
+    float *theta = (float *)malloc(sizeof(float) * n_pairs);
+    if (!theta) return -1;
+    for (int i = 0; i < n_pairs; i++) {
+        float e = (2.0f * (float)i) / (float)rope_dim;
+        float t = 1.0f / powf(base, e);
+        theta[i] = t * scale;
+    }
+    for (int p = 0; p < n_pos; p++) {
+        for (int i = 0; i < n_pairs; i++) {
+            float angle = (float)p * theta[i];
+            table[((size_t)p * n_pairs + i) * 2 + 0] = cosf(angle);
+            table[((size_t)p * n_pairs + i) * 2 + 1] = sinf(angle);
+        }
+    }
+    free(theta);
+    return 0;
+}
+
+/* In-place rotation of one head vector at one position (rope.rs:186-196). */
+void or_rope_rotate(float *x, int rope_dim, const float *table_row) {
+    for (int i = 0; i < rope_dim / 2; i++) {
+        float c = table_row[2 * i], s = table_row[2 * i + 1];
+        float a = x[2 * i], b = x[2 * i + 1];
+        float xc = a * c, ys = b * s, xs = a * s, yc = b * c;
+        x[2 * i] = xc - ys;
+        x[2 * i + 1] = xs + yc;
+    }
+}
+
+/* ---- INT4 quantizer ------------------------------------------------------------------ */
+
+/* Rust `f32 as i32`: saturating, NaN -> 0. */
+static int32_t rust_f32_to_i32(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483648.0f) return INT32_MAX;
+    if (v <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)v;
+}
+
+/* cpu_quantize: max_abs = fold(0, f32::max) over |x|; scale = max_abs/7 (1 if 0);
+ * q = clamp(round(x/scale) + 8, 1, 15), round = half away from zero; word u holds elements
+ * 8u..8u+7, element n in bits 4n..4n+3. */
+void or_quantize_row(const float *x, int hd, float *scale_out, uint32_t *words) {
+    float max_abs = 0.0f;
+    for (int d = 0; d < hd; d++) max_abs = fmaxf(max_abs, fabsf(x[d]));
+    float scale = (max_abs == 0.0f) ? 1.0f : max_abs / 7.0f;
+    *scale_out = scale;
+    for (int u = 0; u < hd / 8; u++) {
+        uint32_t w = 0;
+        for (int n = 0; n < 8; n++) {
+            float r = roundf(x[u * 8 + n] / scale);
+            int32_t q = rust_f32_to_i32(r);
+            /* i32 + 8 cannot overflow here: |r| <= 8 whenever r is finite (|x| <= max_abs). */
+            q = q + 8;
+            if (q < 1) q = 1;
+            if (q > 15) q = 15;
+            w |= (uint32_t)q << (4 * n);
+        }
+        words[u] = w;
+    }
+}
+
+void or_dequantize_row(const uint32_t *words, int hd, float scale, float *out) {
+    for (int u = 0; u < hd / 8; u++)
+        for (int n = 0; n < 8; n++) {
+            uint32_t nib = (words[u] >> (4 * n)) & 0xFu;
+            out[u * 8 + n] = ((float)nib - 8.0f) * scale;
+        }
+}
+
+/* ---- cache append ---------------------------------------------------------------------- */
+
+/* One sequence's INT4 cache in the reference layout. */
+typedef struct {
+    uint32_t *k_packed; /* [max_seq][n_kv][hd/8] */
+    uint32_t *v_packed;
+    float *k_scale; /* [max_seq][n_kv] */
+    float *v_scale;
+} or_cache;
+
+/* Append n_tok tokens at positions pos0..pos0+n_tok-1.  k, v: [n_tok][n_kv][hd] raw f32.
+ * K is rotated at its absolute position with the table (rope_dim <= hd), V is not. */
+void or_append(or_cache c, int n_kv, int hd, int rope_dim, const float *table,
+               const float *k, const float *v, int pos0, int n_tok) {
+    float *tmp = (float *)malloc(sizeof(float) * hd);
+    int n_pairs = rope_dim / 2;
+    for (int t = 0; t < n_tok; t++) {
+        int pos = pos0 + t;
+        for (int h = 0; h < n_kv; h++) {
+            size_t src = ((size_t)t * n_kv + h) * hd;
+            size_t row = (size_t)pos * n_kv + h;
+            memcpy(tmp, k + src, sizeof(float) * hd);
+            or_rope_rotate(tmp, rope_dim, table + (size_t)pos * n_pairs * 2);
+            or_quantize_row(tmp, hd, &c.k_scale[row], c.k_packed + row * (hd / 8));
+            or_quantize_row(v + src, hd, &c.v_scale[row], c.v_packed + row * (hd / 8));
+        }
+    }
+    free(tmp);
+}
+
+/* ---- attention ---------------------------------------------------------------------------- */
+
+/* One (sequence, query head) over n_q_tok query tokens at absolute positions
+ * q_pos0..q_pos0+n_q_tok-1; keys 0..q_pos0+n_q_tok-1 (causal).  q: [n_q_tok][n_head][hd] raw
+ * (rotated here at the query position), out: [n_q_tok][n_head][hd]. */
+void or_attend_head(or_cache c, int n_head, int n_kv, int hd, int rope_dim, const float *table,
+                    const float *q, int q_pos0, int n_q_tok, int head, float softcap, float *out) {
+    int group = n_head / n_kv;
+    int kvh = head / group;
+    int key_len = q_pos0 + n_q_tok;
+    int n_pairs = rope_dim / 2;
+    float *qr = (float *)malloc(sizeof(float) * hd);
+    float *kd = (float *)malloc(sizeof(float) * (size_t)key_len * hd);
+    float *vd = (float *)malloc(sizeof(float) * (size_t)key_len * hd);
+    float *row = (float *)malloc(sizeof(float) * key_len);
+    for (int j = 0; j < key_len; j++) {
+        size_t r = (size_t)j * n_kv + kvh;
+        or_dequantize_row(c.k_packed + r * (hd / 8), hd, c.k_scale[r], kd + (size_t)j * hd);
+        or_dequantize_row(c.v_packed + r * (hd / 8), hd, c.v_scale[r], vd + (size_t)j * hd);
+    }
+    float base_scale = 1.0f / sqrtf((float)hd);
+    float scl = base_scale * 1.0f; /* per-head attention.scale is 1.0 (attention.rs:267-271) */
+    for (int t = 0; t < n_q_tok; t++) {
+        int qpos = q_pos0 + t;
+        memcpy(qr, q + ((size_t)t * n_head + head) * hd, sizeof(float) * hd);
+        or_rope_rotate(qr, rope_dim, table + (size_t)qpos * n_pairs * 2);
+        for (int j = 0; j < key_len; j++) {
+            double acc = 0.0;
+            for (int d = 0; d < hd; d++) acc += (double)(qr[d] * kd[(size_t)j * hd + d]);
+            float s = (float)acc * scl;
+            if (softcap > 0.0f) s = tanhf(s / softcap) * softcap;
+            row[j] = s;
+        }
+        /* softmax.rs:104-127: query at absolute position qpos sees keys 0..=qpos */
+        for (int j = qpos + 1; j < key_len; j++) row[j] = -INFINITY;
+        float mx = -INFINITY;
+        for (int j = 0; j < key_len; j++) mx = fmaxf(mx, row[j]);
+        double sum = 0.0;
+        for (int j = 0; j < key_len; j++) {
+            row[j] = expf(row[j] - mx);
+            sum += (double)row[j];
+        }
+        if (sum > 0.0) {
+            float inv = (float)(1.0 / sum);
+            for (int j = 0; j < key_len; j++) row[j] *= inv;
+        }
+        float *o = out + ((size_t)t * n_head + head) * hd;
+        for (int d = 0; d < hd; d++) {
+            double acc = 0.0;
+            for (int j = 0; j < key_len; j++) acc += (double)(row[j] * vd[(size_t)j * hd + d]);
+            o[d] = (float)acc;
+        }
+    }
+    free(qr);
+    free(kd);
+    free(vd);
+    free(row);
+}
+
+/* ---- batched entry points (one independent cache per sequence) ---------------------------- */
+
+/* Caches for n_seq sequences laid out back to back: sequence s's k_packed starts at
+ * k_packed + s*max_seq*n_kv*hd/8, its scales at k_scale + s*max_seq*n_kv. */
+static or_cache seq_cache(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int s, int max_seq,
+                          int n_kv, int hd) {
+    or_cache c;
+    size_t wp = (size_t)s * max_seq * n_kv * (hd / 8), sp = (size_t)s * max_seq * n_kv;
+    c.k_packed = kp + wp;
+    c.v_packed = vp + wp;
+    c.k_scale = ks + sp;
+    c.v_scale = vs + sp;
+    return c;
+}
+
+/* Append n_tok tokens to every sequence at its own length lens[s].  k, v: [n_seq][n_tok][n_kv][hd]. */
+void or_append_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq, int max_seq,
+                     int n_kv, int hd, int rope_dim, const float *table, const float *k,
+                     const float *v, const int32_t *lens, int n_tok) {
+    for (int s = 0; s < n_seq; s++) {
+        size_t off = (size_t)s * n_tok * n_kv * hd;
+        or_append(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_kv, hd, rope_dim, table,
+                  k + off, v + off, lens[s], n_tok);
+    }
+}
+
+/* Attention for n_tok query tokens of every sequence, queries at lens[s]..lens[s]+n_tok-1
+ * (the tokens just appended).  q, out: [n_seq][n_tok][n_head][hd].  n_threads <= 1 runs the
+ * faithful single-threaded loop; otherwise OpenMP over (sequence, head). */
+void or_attend_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq, int max_seq,
+                     int n_head, int n_kv, int hd, int rope_dim, const float *table, const float *q,
+                     const int32_t *lens, int n_tok, float softcap, float *out, int n_threads) {
+    long total = (long)n_seq * n_head;
+    if (n_threads <= 1) {
+        for (long i = 0; i < total; i++) {
+            int s = (int)(i / n_head), h = (int)(i % n_head);
+            size_t off = (size_t)s * n_tok * n_head * hd;
+            or_attend_head(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_head, n_kv, hd,
+                           rope_dim, table, q + off, lens[s], n_tok, h, softcap, out + off);
+        }
+        return;
+    }
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads)
+#endif
+    for (long i = 0; i < total; i++) {
+        int s = (int)(i / n_head), h = (int)(i % n_head);
+        size_t off = (size_t)s * n_tok * n_head * hd;
+        or_attend_head(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_head, n_kv, hd, rope_dim,
+                       table, q + off, lens[s], n_tok, h, softcap, out + off);
+    }
+}
+
+/* One (sequence, head) of a batch laid out as in or_attend_batch: used to check a sample of
+ * heads at sizes where running every head would take minutes. */
+void or_attend_one(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int max_seq, int n_head,
+                   int n_kv, int hd, int rope_dim, const float *table, const float *q_seq,
+                   int q_pos0, int n_tok, int seq, int head, float softcap, float *out_seq) {
+    or_attend_head(seq_cache(kp, vp, ks, vs, seq, max_seq, n_kv, hd), n_head, n_kv, hd, rope_dim,
+                   table, q_seq, q_pos0, n_tok, head, softcap, out_seq);
+}

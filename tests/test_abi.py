@@ -1,0 +1,93 @@
+"""CPU-side checks of the C ABI: the library loads, exports exactly what include/turboshimmy.h
+declares, and its host-only entry points (RoPE table, sizing, argument validation) behave.
+No GPU is touched here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import airframe_amd
+from airframe_amd import _lib
+from oracle import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "turboshimmy.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ts_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    L = airframe_amd.load()
+    names = declared_functions()
+    assert len(names) >= 19
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T (ts_[a-z0-9_]+)$", out, flags=re.M))
+    assert exported == set(names)
+
+
+def test_header_compiles_as_c():
+    src = f'#include "{HEADER}"\nint main(void){{ ts_kv_desc d = {{1,1,1,64,1}}; (void)d; return 0; }}\n'
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-x", "c", "-", "-fsyntax-only"],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_status_strings():
+    L = airframe_amd.load()
+    assert L.ts_status_string(0) == b"ok"
+    assert b"overflow" in L.ts_status_string(_lib.TS_ERR_OVERFLOW)
+
+
+@pytest.mark.parametrize("n_pos,rope_dim,base,scale", [
+    (600, 64, 500000.0, 1.0), (300, 128, 1000000.0, 1.0), (50, 128, 10000.0, 4.0), (9000, 128, 500000.0, 1.0)])
+def test_host_rope_table_bit_exact_with_oracle(n_pos, rope_dim, base, scale):
+    from airframe_amd.kv_cache import RopeTable
+    t = RopeTable.host_table(n_pos, rope_dim, base, scale)
+    ref = oracle.rope_table(n_pos, rope_dim, base, scale)
+    assert np.array_equal(t.view(np.uint32), ref.view(np.uint32))
+
+
+def test_host_rope_table_rejects_bad_args():
+    L = airframe_amd.load()
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data_as(ctypes.c_void_p)
+    assert L.ts_rope_table_host(p, 4, 7, 10000.0, 1.0) == _lib.TS_ERR_INVALID
+    assert L.ts_rope_table_host(p, 4, 8, 10000.0, 0.5) == _lib.TS_ERR_UNSUPPORTED
+    assert L.ts_rope_table_host(None, 4, 8, 10000.0, 1.0) == _lib.TS_ERR_INVALID
+
+
+def test_kv_bytes_sizing():
+    from airframe_amd.kv_cache import KVCache
+    # Qwen3-8B shape, 36 layers, 32 sequences of 8192+128: packed K+V (hd/2 each) + 2 f32 scales
+    b = KVCache.bytes_for(36, 8, 128, 8192 + 128, 32)
+    P = (8192 + 128 + 63) // 64 * 64
+    assert b == 36 * 32 * 8 * P * (64 + 64 + 4 + 4)
+    assert b < 288e9
+    # 7.5x smaller than the f32 cache the reference also allocates (kv_cache.rs:121-145)
+    assert abs((36 * 32 * 8 * P * 128 * 4 * 2) / b - 7.53) < 0.01
+
+
+def test_create_validates_before_touching_the_device():
+    L = airframe_amd.load()
+    h = ctypes.c_void_p()
+    bad = [(0, 1, 1, 64, 16), (1, 1, 1, 60, 16), (1, 0, 1, 64, 16), (1, 1, 1, 64, 0)]
+    for d in bad:
+        assert L.ts_kv_create(ctypes.byref(_lib.KvDesc(*d)), ctypes.byref(h)) == _lib.TS_ERR_INVALID
+    # multiple of 8 but no kernel built for it (the reference accepts any multiple of 8)
+    assert L.ts_kv_create(ctypes.byref(_lib.KvDesc(1, 1, 1, 96, 16)), ctypes.byref(h)) == _lib.TS_ERR_UNSUPPORTED
+    assert L.ts_kv_create(None, ctypes.byref(h)) == _lib.TS_ERR_INVALID
+    # null handles are rejected everywhere
+    assert L.ts_kv_increment(None, 1, None) == _lib.TS_ERR_INVALID
+    assert L.ts_attn_decode(None, 0, None, 32, None, 0.0, None, None, 0, None) == _lib.TS_ERR_INVALID
+    assert L.ts_append_quant(None, 0, None, None, 1, None, None) == _lib.TS_ERR_INVALID

@@ -1,0 +1,199 @@
+"""GPU parity of the split-K INT4 decode attention against the CPU oracle (attention.rs:236-313
+over the dequantized INT4 cache), within |err| <= 2e-3 + 1e-3*|ref|, plus the codes of every
+token appended on the way (bit-exact)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from airframe_amd import synth
+from oracle import oracle
+from tests.gpu_util import Pair, assert_close, dev, say
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def decode_step(p: Pair, rng, n_head, scale_kv=None, scale_q=None, softcap=0.0, check=True):
+    n_seq, n_kv, hd = p.n_seq, p.n_kv, p.hd
+    k = synth.normal(rng, (n_seq, 1, n_kv, hd), scale_kv)
+    v = synth.normal(rng, (n_seq, 1, n_kv, hd), scale_kv)
+    q = synth.normal(rng, (n_seq, n_head, hd), scale_q)
+    p.append(k, v)
+    out = p.gpu.attn_decode(0, dev(q), p.rope, softcap=softcap).cpu().numpy()
+    ref = p.ora.attend(q[:, None], 1, softcap=softcap, threads=8)[:, 0] if check else None
+    p.advance(1)
+    return out, ref
+
+
+def prefill_cache(p: Pair, rng, n, scale_kv=None, step=512):
+    done = 0
+    while done < n:
+        m = min(step, n - done)
+        k = synth.normal(rng, (p.n_seq, m, p.n_kv, p.hd), scale_kv)
+        v = synth.normal(rng, (p.n_seq, m, p.n_kv, p.hd), scale_kv)
+        p.append(k, v)
+        p.advance(m)
+        done += m
+
+
+def test_config1_llama32_1b_single_layer(gpu):
+    """32 q / 8 kv heads, hd 64, batch 1, 512 cached + 1 appended, theta 5e5."""
+    say("decode cfg1")
+    rng = np.random.default_rng(1)
+    p = Pair(1, 8, 64, 513, 500000.0)
+    prefill_cache(p, rng, 512)
+    out, ref = decode_step(p, rng, 32)
+    assert_close(out, ref, "cfg1 out")
+    p.check_codes()
+
+
+def test_gqa3_hd128_llama32_3b_shape(gpu):
+    """Config 2's head shape (24 q / 8 kv, group 3) at a shorter context, several steps."""
+    say("decode gqa3")
+    rng = np.random.default_rng(2)
+    p = Pair(1, 8, 128, 800, 500000.0)
+    prefill_cache(p, rng, 700)
+    for _ in range(3):
+        out, ref = decode_step(p, rng, 24)
+        assert_close(out, ref, "gqa3 out")
+    p.check_codes()
+
+
+def test_batch_outliers_qwen3_shape(gpu):
+    """Config 3's shape (32/8, hd 128, theta 1e6, x8 outlier channels on 2% of dims) at
+    batch 4 and context 3000."""
+    say("decode outliers")
+    rng = np.random.default_rng(3)
+    n_kv, n_head, hd = 8, 32, 128
+    dims = synth.outlier_dims(n_kv, hd, 3)
+    skv = synth.channel_scale(n_kv, n_kv, hd, dims)
+    sq = synth.channel_scale(n_head, n_kv, hd, dims)
+    p = Pair(4, n_kv, hd, 3100, 1e6)
+    prefill_cache(p, rng, 3000, skv[None, None])
+    for _ in range(2):
+        out, ref = decode_step(p, rng, n_head, skv[None, None], sq[None])
+        assert_close(out, ref, "outlier out")
+
+
+def test_ragged_lengths_and_split_boundaries(gpu):
+    """Per-sequence lengths around every window/split edge, including an empty cache."""
+    say("decode ragged")
+    rng = np.random.default_rng(4)
+    lens = [0, 1, 31, 63, 64, 65, 127, 128, 255, 256, 257, 1000, 1087, 1088, 1089, 2047]
+    n_seq, n_kv, hd = len(lens), 2, 128
+    p = Pair(n_seq, n_kv, hd, 2100, 1e6)
+    # fill each sequence to its own length: fill all to max, then cut lengths back
+    prefill_cache(p, rng, max(lens))
+    p.set_lens(lens)
+    for _ in range(2):
+        out, ref = decode_step(p, rng, 8)
+        assert_close(out, ref, "ragged out")
+    p.check_codes()
+
+
+def test_softcap(gpu):
+    say("decode softcap")
+    rng = np.random.default_rng(5)
+    p = Pair(2, 4, 64, 400, 10000.0)
+    prefill_cache(p, rng, 300, np.float32(3.0))
+    out, ref = decode_step(p, rng, 16, np.float32(3.0), np.float32(3.0), softcap=5.0)
+    assert_close(out, ref, "softcap out")
+
+
+def test_group8_and_group1(gpu):
+    say("decode group 8 / 1")
+    rng = np.random.default_rng(6)
+    for n_kv, n_head in ((2, 16), (4, 4)):
+        p = Pair(2, n_kv, 128, 600, 500000.0)
+        prefill_cache(p, rng, 513)
+        out, ref = decode_step(p, rng, n_head)
+        assert_close(out, ref, f"G={n_head // n_kv} out")
+
+
+def test_golden_fixture_through_gpu(gpu):
+    """tests/golden/oracle_small.npz: append 40, chunk 24 (prefill kernel), decode 1."""
+    say("golden fixture")
+    g = np.load(os.path.join(GOLD, "oracle_small.npz"))
+    c = json.loads(str(g["config"]))
+    P, C = c["prefill"], c["chunk"]
+    p = Pair(c["n_seq"], c["n_kv"], c["hd"], P + C + 1, c["base"])
+    p.gpu.append_quant(0, dev(g["k0"]), dev(g["v0"]), p.rope)
+    p.gpu.increment(P)
+    p.gpu.append_quant(0, dev(g["k1"]), dev(g["v1"]), p.rope)
+    o1 = p.gpu.attn_prefill(0, dev(g["q1"]), p.rope).cpu().numpy()
+    assert_close(o1, g["o_prefill"], "golden prefill")
+    p.gpu.increment(C)
+    p.gpu.append_quant(0, dev(g["k2"]), dev(g["v2"]), p.rope)
+    o2 = p.gpu.attn_decode(0, dev(g["q2"][:, 0]), p.rope).cpu().numpy()
+    assert_close(o2, g["o_decode"][:, 0], "golden decode")
+    torch.cuda.synchronize()
+    for s in range(c["n_seq"]):
+        kp, vp, ks, vs = p.gpu.export(0, s, 0, P + C + 1)
+        assert np.array_equal(kp.cpu().numpy().view(np.uint32), g["k_packed"][s])
+        assert np.array_equal(vp.cpu().numpy().view(np.uint32), g["v_packed"][s])
+        assert np.array_equal(ks.cpu().numpy(), g["k_scale"][s])
+        assert np.array_equal(vs.cpu().numpy(), g["v_scale"][s])
+
+
+def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, sample, outliers):
+    """One layer at the full BASELINE shape: the GPU runs every sequence; the oracle checks a
+    sample of (sequence, head) pairs on identical inputs (copied back from the device)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    dims = synth.outlier_dims(n_kv, hd, seed) if outliers else None
+    skv = torch.as_tensor(synth.channel_scale(n_kv, n_kv, hd, dims)).cuda()
+    sq = torch.as_tensor(synth.channel_scale(n_head, n_kv, hd, dims)).cuda()
+    max_len = max(lens)
+    p = Pair(n_seq, n_kv, hd, max_len + 1, base)
+    seqs = sorted({s for s, _ in sample})
+    host_k = {s: [] for s in seqs}
+    host_v = {s: [] for s in seqs}
+    step = 2048
+    for t0 in range(0, max_len, step):
+        m = min(step, max_len - t0)
+        k = torch.randn((n_seq, m, n_kv, hd), generator=gen, device="cuda") * skv
+        v = torch.randn((n_seq, m, n_kv, hd), generator=gen, device="cuda") * skv
+        p.gpu.append_quant(0, k, v, p.rope)
+        p.gpu.increment(m)
+        for s in seqs:
+            host_k[s].append(k[s].cpu().numpy())
+            host_v[s].append(v[s].cpu().numpy())
+    p.set_lens(lens)
+    k1 = torch.randn((n_seq, 1, n_kv, hd), generator=gen, device="cuda") * skv
+    v1 = torch.randn((n_seq, 1, n_kv, hd), generator=gen, device="cuda") * skv
+    q = torch.randn((n_seq, n_head, hd), generator=gen, device="cuda") * sq
+    p.gpu.append_quant(0, k1, v1, p.rope)
+    out = p.gpu.attn_decode(0, q, p.rope).cpu().numpy()
+    qh, k1h, v1h = q.cpu().numpy(), k1.cpu().numpy(), v1.cpu().numpy()
+    for s in seqs:
+        kk = np.concatenate(host_k[s])[:lens[s]]
+        vv = np.concatenate(host_v[s])[:lens[s]]
+        kk = np.concatenate([kk, k1h[s]])
+        vv = np.concatenate([vv, v1h[s]])
+        ora = oracle.OracleKV(1, lens[s] + 1, n_kv, hd, p.ora.table)
+        ora.append(kk[None], vv[None])
+        ora.lens[:] = lens[s]
+        for s2, h in sample:
+            if s2 != s:
+                continue
+            ref = ora.attend_one(qh[s][None], 0, h)[0]
+            assert_close(out[s, h], ref, f"full-size seq {s} head {h} (len {lens[s]})")
+
+
+def test_full_size_config3_one_layer(gpu):
+    """Config 3 at full size (batch 32, ctx 8192, outliers), one layer; sample of heads."""
+    say("decode full cfg3")
+    sample = [(0, 0), (0, 31), (17, 5), (31, 12), (31, 30)]
+    _full_size(32, 8, 32, 128, [8192] * 32, 1e6, 33, sample, True)
+
+
+def test_full_size_config4_ragged_one_layer(gpu):
+    """Config 4 at full size: batch 8, lengths ~U[16K, 32K] (seeded), one layer."""
+    say("decode full cfg4")
+    rng = np.random.default_rng(44)
+    lens = [int(x) for x in rng.integers(16384, 32768, size=8)]
+    sample = [(0, 0), (3, 17), (7, 31)]
+    _full_size(8, 8, 32, 128, lens, 500000.0, 44, sample, False)

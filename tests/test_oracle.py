@@ -1,0 +1,303 @@
+"""Pins the CPU oracle (oracle/ts_oracle.c) before anything is compared against it.
+
+Each check is chosen so that a plausible mistake in the oracle fails it: the reference's own
+known answers (test_int4_parity.rs), closed forms of RoPE and attention, and an independent
+numpy restatement (oracle/np_oracle.py) on small inputs.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import np_oracle, oracle
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _kat():
+    with open(os.path.join(GOLD, "reference_kat.json")) as f:
+        return {c["name"]: c for c in json.load(f)["cases"]}
+
+
+# ---- quantizer: reference known answers (test_int4_parity.rs) ---------------------------------
+
+def test_kat_zero_vector():  # :489-520
+    c = _kat()["zero_vector_no_nan"]
+    s, w = oracle.quantize_row(np.array(c["x"], np.float32))
+    assert s == np.float32(1.0) and np.isfinite(s)
+    assert list(w) == c["expect_words"] == [0x88888888]
+
+
+def test_kat_extreme_all_positive():  # :525-572
+    c = _kat()["extreme_all_positive"]
+    s, w = oracle.quantize_row(np.array(c["x"], np.float32))
+    assert list(w) == [0xFFFFFFFF]
+    assert s == np.float32(1000.0) / np.float32(7.0)
+
+
+@pytest.mark.parametrize("name,bound_abs", [
+    ("extreme_alternating", 1.0), ("single_head_ramp_k", 1e-5), ("single_head_sinusoid_v", 1e-5)]
+    + [(f"multi_head_k_amp{a}", 1e-5) for a in (1.0, 2.0, 0.5, 7.0)]
+    + [(f"multi_head_v_amp{a}", 1e-5) for a in (1.0, 2.0, 0.5, 7.0)])
+def test_kat_roundtrip_bound(name, bound_abs):  # :370-385, :455-473, :575-581
+    c = _kat()[name]
+    x = np.array(c["x"], np.float32)
+    s, w = oracle.quantize_row(x)
+    err = np.abs(oracle.dequantize_row(w, s) - x).max()
+    assert err <= s / 2 + bound_abs
+    if "expect_scale_close" in c:  # multi-head: independent per-head scales amp*max|..|/7
+        assert abs(s - c["expect_scale_close"]) < 1e-5
+    if "expect_max_abs" in c:  # ramp: max_abs 3.15 -> scale ~0.45
+        assert abs(s * 7 - c["expect_max_abs"]) < 1e-5
+
+
+def test_kat_ramp_words_by_hand():
+    # ramp d*0.1-3.15, scale = 3.15/7 = 0.45: element 0 is -3.15/0.45 = -7 -> code 1;
+    # element 31 is -0.05/0.45 -> round(-0.111) = 0 -> code 8; element 63 -> +7 -> 15.
+    x = np.array(_kat()["single_head_ramp_k"]["x"], np.float32)
+    s, w = oracle.quantize_row(x)
+    nib = lambda i: (int(w[i // 8]) >> (4 * (i % 8))) & 0xF  # noqa: E731
+    assert nib(0) == 1 and nib(31) == 8 and nib(63) == 15
+    # d=4: -2.75/0.45 = -6.11 -> -6 -> 2 ;  d=5: -2.65/0.45=-5.89 -> -6 -> 2
+    assert nib(4) == 2 and nib(5) == 2
+
+
+def test_quantizer_layout_and_rounding_by_hand():
+    # scale = 7/7 = 1: codes are round_half_away(x) + 8, element n of a word at bits 4n.
+    x = np.array([7, -7, 0.5, -0.5, 1.5, -1.5, 2.49, 0], np.float32)
+    s, w = oracle.quantize_row(x)
+    assert s == 1.0
+    # half away from zero: 0.5 -> 1, -0.5 -> -1, 1.5 -> 2, -1.5 -> -2
+    codes = [15, 1, 9, 7, 10, 6, 10, 8]
+    assert int(w[0]) == sum(c << (4 * n) for n, c in enumerate(codes))
+
+
+def test_quantizer_special_values():
+    # NaN is skipped by the max (f32::max) and encodes as code 8 (NaN as i32 == 0);
+    # +inf makes scale inf: finite/inf = 0 -> 8, inf/inf = NaN -> 8.
+    x = np.array([np.nan, 2.0, -3.5, 0, 0, 0, 0, 1.0], np.float32)
+    s, w = oracle.quantize_row(x)
+    assert s == np.float32(3.5) / np.float32(7.0)
+    assert int(w[0]) & 0xF == 8
+    x = np.array([np.inf, 1.0, -1.0, 0, 0, 0, 0, 0], np.float32)
+    s, w = oracle.quantize_row(x)
+    assert np.isinf(s) and int(w[0]) == 0x88888888
+    # subnormal max: scale stays subnormal, codes still span [1,15]
+    x = np.array([1e-40, -1e-40, 5e-41, 0, 0, 0, 0, 0], np.float32)
+    s, w = oracle.quantize_row(x)
+    assert 0 < s < np.finfo(np.float32).tiny
+    assert (int(w[0]) & 0xF) == 15 and ((int(w[0]) >> 4) & 0xF) == 1
+
+
+def test_quantizer_invariants_random():
+    rng = np.random.default_rng(5)
+    for hd in (8, 64, 128):
+        x = (rng.standard_normal((200, hd)) * rng.uniform(0.01, 100, (200, 1))).astype(np.float32)
+        for row in x:
+            s, w = oracle.quantize_row(row)
+            nib = (w[:, None] >> (np.arange(8, dtype=np.uint32) * 4)) & 0xF
+            assert nib.min() >= 1 and nib.max() <= 15
+            assert np.abs(oracle.dequantize_row(w, s) - row).max() <= s / 2 * (1 + 1e-6)
+
+
+def test_quantizer_matches_numpy_restatement():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((500, 128)).astype(np.float32)
+    x[::7] *= 1000
+    x[3, 5] = 0.5 * 7 / 7  # ties appear naturally too; both use half-away rounding
+    ref_s, ref_w = np_oracle.quantize(x)
+    for i, row in enumerate(x):
+        s, w = oracle.quantize_row(row)
+        assert s == ref_s[i] and (w == ref_w[i]).all()
+
+
+def test_tie_rounding_half_away():
+    # x/scale == +-2.5 exactly: half away gives +-3 (codes 11 and 5); half-even would give +-2.
+    x = np.array([7.0, 2.5, -2.5, 0, 0, 0, 0, 0], np.float32)
+    s, w = oracle.quantize_row(x)
+    assert ((int(w[0]) >> 4) & 0xF) == 11 and ((int(w[0]) >> 8) & 0xF) == 5
+    s2, w2 = np_oracle.quantize(x)
+    assert (w2 == w).all()
+
+
+# ---- RoPE ---------------------------------------------------------------------------------------
+
+def test_rope_table_closed_forms():
+    t = oracle.rope_table(64, 128, 500000.0)
+    assert (t[0, :, 0] == 1.0).all() and (t[0, :, 1] == 0.0).all()  # preflight.rs:267-285
+    # pair 0 has theta 1: angle = pos
+    assert np.allclose(t[:, 0, 0], np.cos(np.arange(64)), atol=1e-6)
+    # theta_i = base^(-2i/d) in float64 within f32 rounding (closed form)
+    i = np.arange(64)
+    theta = 500000.0 ** (-2.0 * i / 128)
+    assert np.allclose(t[5, :, 0], np.cos(5 * theta), atol=2e-6)
+    assert np.allclose(t[5, :, 1], np.sin(5 * theta), atol=2e-6)
+    # linear scale multiplies theta (preflight.rs:288-303)
+    t2 = oracle.rope_table(8, 8, 10000.0, 2.0)
+    assert np.allclose(t2[3, 0], [np.cos(6.0), np.sin(6.0)], atol=1e-6)
+    with pytest.raises(ValueError):
+        oracle.rope_table(8, 8, 10000.0, 0.5)  # YaRN branch is not part of this path
+
+
+def test_rope_rotation_is_pairwise_rotation():
+    rng = np.random.default_rng(2)
+    t = oracle.rope_table(100, 64, 10000.0)
+    x = rng.standard_normal(64).astype(np.float32)
+    y = oracle.rope_rotate(x, t[37])
+    # norm per pair preserved, angle advanced by 37*theta_i
+    for i in range(32):
+        a, b = x[2 * i], x[2 * i + 1]
+        c, s = t[37, i]
+        assert abs(y[2 * i] - (a * c - b * s)) < 1e-6 and abs(y[2 * i + 1] - (a * s + b * c)) < 1e-6
+        assert abs(math.hypot(y[2 * i], y[2 * i + 1]) - math.hypot(a, b)) < 1e-5
+    # adjacent pairs (2i, 2i+1), not halves: rotating e0 only moves dims 0 and 1
+    e0 = np.zeros(64, np.float32)
+    e0[0] = 1
+    y = oracle.rope_rotate(e0, t[3])
+    assert np.count_nonzero(y) <= 2 and y[1] != 0
+    # relative-position identity used by the reference GPU kernel (sh_layer_v1_int4.wgsl:1112)
+    q = rng.standard_normal(64).astype(np.float32)
+    k = rng.standard_normal(64).astype(np.float32)
+    d1 = np.dot(oracle.rope_rotate(q, t[50]), oracle.rope_rotate(k, t[20]))
+    d2 = np.dot(oracle.rope_rotate(q, t[31]), oracle.rope_rotate(k, t[1]))
+    assert abs(d1 - d2) < 1e-4
+
+
+# ---- attention ------------------------------------------------------------------------------------
+
+def _cache(n_seq, max_seq, n_kv, hd, base=10000.0):
+    return oracle.OracleKV(n_seq, max_seq, n_kv, hd, oracle.rope_table(max_seq, hd, base))
+
+
+def test_attention_single_position_is_v():
+    kv = _cache(1, 4, 2, 64)
+    rng = np.random.default_rng(0)
+    k = rng.standard_normal((1, 1, 2, 64), dtype=np.float32)
+    v = rng.standard_normal((1, 1, 2, 64), dtype=np.float32)
+    kv.append(k, v)
+    q = rng.standard_normal((1, 1, 4, 64), dtype=np.float32)
+    out = kv.attend(q, 1)
+    for h in range(4):
+        vd = oracle.dequantize_row(kv.v_packed[0, 0, h // 2], kv.v_scale[0, 0, h // 2])
+        assert (out[0, 0, h] == vd).all()  # p == 1 exactly, f64 sum of 1*v
+
+
+def test_attention_equal_keys_give_mean_and_gqa_mapping():
+    n_kv, G, hd, L = 2, 3, 64, 10
+    kv = _cache(1, L, n_kv, hd)
+    rng = np.random.default_rng(1)
+    k = np.zeros((1, L, n_kv, hd), np.float32)  # all keys zero -> all scores equal
+    v = rng.standard_normal((1, L, n_kv, hd), dtype=np.float32)
+    v[0, :, 1] += 100.0  # kv head 1 clearly distinct from head 0
+    kv.append(k, v)
+    kv.advance(L - 1)
+    kv.lens[:] = L - 1
+    q = rng.standard_normal((1, 1, n_kv * G, hd), dtype=np.float32)
+    out = kv.attend(q, 1)
+    for h in range(n_kv * G):
+        kvh = h // G  # attention.rs:237
+        vd = np.stack([oracle.dequantize_row(kv.v_packed[0, j, kvh], kv.v_scale[0, j, kvh]) for j in range(L)])
+        assert np.allclose(out[0, 0, h], vd.mean(0), atol=1e-5)
+
+
+def test_attention_two_keys_closed_form():
+    # scores s0, s1 -> weights sigmoid(s0-s1); check the 1/sqrt(hd) factor and the softmax.
+    hd = 64
+    kv = _cache(1, 2, 1, hd, base=1e30)  # base so large every angle is ~0 beyond pair 0
+    t = kv.table
+    t[:] = 0
+    t[:, :, 0] = 1.0  # identity rotation
+    k = np.zeros((1, 2, 1, hd), np.float32)
+    k[0, 0, 0, 0] = 7.0
+    k[0, 1, 0, 0] = -7.0
+    v = np.zeros((1, 2, 1, hd), np.float32)
+    v[0, 0, 0, :] = 7.0
+    v[0, 1, 0, :] = -7.0
+    kv.append(k, v)
+    kv.lens[:] = 1
+    q = np.zeros((1, 1, 1, hd), np.float32)
+    q[0, 0, 0, 0] = 2.0
+    out = kv.attend(q, 1)
+    s0, s1 = 2 * 7 / math.sqrt(hd), -2 * 7 / math.sqrt(hd)
+    w0 = 1 / (1 + math.exp(s1 - s0))
+    assert abs(out[0, 0, 0, 3] - (7 * w0 - 7 * (1 - w0))) < 1e-5
+
+
+def test_attention_decode_equals_last_prefill_row():  # kvcache.rs:363-416
+    rng = np.random.default_rng(3)
+    n_kv, n_head, hd, L = 2, 4, 64, 33
+    a = _cache(1, L, n_kv, hd)
+    b = _cache(1, L, n_kv, hd)
+    k = rng.standard_normal((1, L, n_kv, hd), dtype=np.float32)
+    v = rng.standard_normal((1, L, n_kv, hd), dtype=np.float32)
+    q = rng.standard_normal((1, L, n_head, hd), dtype=np.float32)
+    a.append(k, v)
+    full = a.attend(q, L)
+    b.append(k[:, :-1], v[:, :-1])
+    b.advance(L - 1)
+    b.append(k[:, -1:], v[:, -1:])
+    last = b.attend(q[:, -1:], 1)
+    assert np.array_equal(full[:, -1:], last)
+    # causal: the first query only sees key 0 -> output is V[0]
+    vd0 = oracle.dequantize_row(a.v_packed[0, 0, 0], a.v_scale[0, 0, 0])
+    assert (full[0, 0, 0] == vd0).all()
+
+
+def test_attention_matches_numpy_restatement():
+    rng = np.random.default_rng(4)
+    n_kv, n_head, hd, L, T = 2, 6, 128, 50, 7
+    kv = _cache(2, L + T, n_kv, hd, base=1e6)
+    k = rng.standard_normal((2, L + T, n_kv, hd), dtype=np.float32)
+    v = rng.standard_normal((2, L + T, n_kv, hd), dtype=np.float32)
+    kv.append(k[:, :L], v[:, :L])
+    kv.advance(L)
+    kv.append(k[:, L:], v[:, L:])
+    q = rng.standard_normal((2, T, n_head, hd), dtype=np.float32)
+    for softcap in (0.0, 5.0):
+        out = kv.attend(q, T, softcap=softcap)
+        out_mt = kv.attend(q, T, softcap=softcap, threads=4)
+        assert np.array_equal(out, out_mt)
+        t = kv.table
+        for s in range(2):
+            kd = np_oracle.dequantize(kv.k_packed[s, :L + T], kv.k_scale[s, :L + T])
+            vd = np_oracle.dequantize(kv.v_packed[s, :L + T], kv.v_scale[s, :L + T])
+            qr = np_oracle.rotate(q[s], t[L:L + T, None, :, 0], t[L:L + T, None, :, 1])
+            ref = np_oracle.attend(qr, kd, vd, L, softcap)
+            assert np.abs(ref - out[s]).max() < 2e-6
+
+
+def test_append_matches_numpy_restatement_and_keeps_v_unrotated():
+    rng = np.random.default_rng(8)
+    kv = _cache(1, 20, 3, 128, base=500000.0)
+    k = rng.standard_normal((1, 20, 3, 128), dtype=np.float32)
+    v = rng.standard_normal((1, 20, 3, 128), dtype=np.float32)
+    kv.append(k, v)
+    t = kv.table
+    kr = np_oracle.rotate(k[0], t[:20, None, :, 0], t[:20, None, :, 1])
+    ks, kw = np_oracle.quantize(kr)
+    vs, vw = np_oracle.quantize(v[0])
+    assert (kw == kv.k_packed[0]).all() and (ks == kv.k_scale[0]).all()
+    assert (vw == kv.v_packed[0]).all() and (vs == kv.v_scale[0]).all()
+    # position 0 rotation is the identity
+    s0, w0 = oracle.quantize_row(k[0, 0, 1])
+    assert (w0 == kv.k_packed[0, 0, 1]).all()
+
+
+# ---- golden fixture -------------------------------------------------------------------------------
+
+def test_oracle_reproduces_golden_fixture():
+    g = np.load(os.path.join(GOLD, "oracle_small.npz"))
+    c = json.loads(str(g["config"]))
+    P, C = c["prefill"], c["chunk"]
+    kv = _cache(c["n_seq"], P + C + 1, c["n_kv"], c["hd"], c["base"])
+    kv.append(g["k0"], g["v0"])
+    kv.advance(P)
+    kv.append(g["k1"], g["v1"])
+    assert np.array_equal(kv.attend(g["q1"], C), g["o_prefill"])
+    kv.advance(C)
+    kv.append(g["k2"], g["v2"])
+    assert np.array_equal(kv.attend(g["q2"], 1), g["o_decode"])
+    for name in ("k_packed", "v_packed", "k_scale", "v_scale"):
+        assert np.array_equal(getattr(kv, name), g[name])
