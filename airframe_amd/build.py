@@ -26,11 +26,15 @@ COMMON = [
 # Files whose arithmetic must round exactly like the CPU reference get no FMA contraction.
 EXACT = ["-ffp-contract=off"]
 
+# MFMA accumulators in VGPRs: the attention kernels rescale them with VALU ops, which would
+# otherwise cost two AGPR<->VGPR moves per accumulator register and window.
+MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+
 SOURCES = {
     "ts_kv.cpp": EXACT,
     "ts_append.hip": EXACT,
-    "ts_decode.hip": [],
-    "ts_prefill.hip": [],
+    "ts_decode.hip": MFMA_VGPR,
+    "ts_prefill.hip": MFMA_VGPR,
 }
 HEADERS = ["ts_internal.h", "ts_mfma.h", os.path.join("..", "..", "include", "turboshimmy.h")]
 

@@ -17,13 +17,23 @@
 //   a byte is taken as 1024+16*nibble and fixed with one packed f16 FMA), so K and V enter the
 //   MFMA exactly.  The per-position scales are applied in f32 outside the MFMA: s_k on the
 //   scores, s_v folded into the probabilities.
-// * q and p are split hi + lo in f16 (x = hi + lo to ~22 bits), so the f32-accumulated MFMA
-//   results carry f32-level accuracy: QK issues two MFMAs (hi, lo) into one accumulator; for
-//   PV the lo part rides in the spare accumulator columns G..2G-1.
-// * online softmax in the exp2 domain with one cross-lane max per 64 positions; the 4 waves
-//   merge through LDS; splits merge in a second kernel (log-sum-exp combine) unless a
-//   sequence fits one split.
+// * q is split hi + lo in f16 (q = hi + lo to ~22 bits) and QK^T issues two MFMAs (hi, lo)
+//   into one f32 accumulator, so scores carry f32-level accuracy; the probabilities enter PV
+//   as f16 (relative error 2^-11, well inside the output tolerance).
+// * online softmax in the exp2 domain with one cross-lane max per 64 positions and lazy
+//   rescaling; s_v is folded into the probabilities under a per-window exponent bound so they
+//   never leave f16 range.  The 4 waves merge through LDS; splits merge in a second kernel
+//   (log-sum-exp combine) unless a sequence fits one split.
+#include <stdlib.h>
+
 #include "ts_mfma.h"
+
+#ifndef TS_DECODE_WAVES
+#define TS_DECODE_WAVES 2
+#endif
+#ifndef TS_DECODE_DEPTH
+#define TS_DECODE_DEPTH 2
+#endif
 
 namespace ts {
 namespace {
@@ -44,11 +54,200 @@ struct DecodeArgs {
     float *ws;  // partial o [S][n_head][n_split][hd], then m [..][n_split], l [..][n_split]
 };
 
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// One 64-position window of one (sequence, kv head) stream, as held by one lane in registers
+// while it is in flight: K rows (tile kt, row n, the words of lane group g), V blocks (block b,
+// words lane*NTD..), and one K and one V scale (position base + lane).
 template <int HD>
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
+struct Window {
+    static constexpr int WPG = HD / 32, NTD = HD / 16;
+    uint32_t kw[4][WPG];
+    uint32_t vw[2][NTD];
+    float sk, sv;
+};
+
+// Buffer resources of one (sequence, kv head) stream, bounded to the positions of one split:
+// loads past the bound return zeros without touching memory, so prefetches can be issued
+// unconditionally (which keeps the compiler's load counters static, so the wait before each
+// window only covers that window's own loads).
+struct Streams {
+    __amdgpu_buffer_rsrc_t k, v;
+    const float *ksb, *vsb;
+    int last;  // last position of the split
+};
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int HD>
+__device__ __forceinline__ void load_window(Window<HD> &w, const Streams &st, int base, int n,
+                                            int g, int lane) {
+    constexpr int WPG = HD / 32, NTD = HD / 16, ROWB = HD / 2;
+    const int koff = n * ROWB + g * (WPG * 4);
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+        if constexpr (WPG == 4) {
+            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, koff + kt * 16 * ROWB, base * ROWB, 0);
+            w.kw[kt][0] = t4[0]; w.kw[kt][1] = t4[1]; w.kw[kt][2] = t4[2]; w.kw[kt][3] = t4[3];
+        } else {
+            const u32x2 t2 = __builtin_amdgcn_raw_buffer_load_b64(st.k, koff + kt * 16 * ROWB, base * ROWB, 0);
+            w.kw[kt][0] = t2[0]; w.kw[kt][1] = t2[1];
+        }
+    }
+    const int voff = lane * NTD * 4;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+#pragma unroll
+        for (int q4 = 0; q4 < NTD / 4; q4++) {
+            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.v, voff + 16 * q4 + b * (HD * 16), (base / 32) * (HD * 16), 0);
+            w.vw[b][4 * q4 + 0] = t4[0]; w.vw[b][4 * q4 + 1] = t4[1];
+            w.vw[b][4 * q4 + 2] = t4[2]; w.vw[b][4 * q4 + 3] = t4[3];
+        }
+    }
+    // Scales: plain loads with the index clamped into the split (4-byte raw buffer loads of
+    // this stream measured ~20% slower); windows past the end re-read valid, unused scales.
+    const int sp = min(base + lane, st.last);
+    w.sk = st.ksb[sp];
+    w.sv = st.vsb[sp];
+}
+
+// Max of v over the four lane groups g (lanes n, n+16, n+32, n+48): two permlane swaps.
+__device__ inline float group_max(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ inline float group_sum(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Running state of one wave: O^T accumulators (column n = head, rows = dims 16td+4g+r), the
+// reference exponent m (exp2 domain) and the softmax sum l.
+template <int HD>
+struct WaveState {
+    floatx4 o[HD / 16];
+    float m, l;
+};
+
+// q operands in LDS: [k-step t][lane] = (hi, lo), shared by the four waves of a workgroup.
+template <int HD>
+struct QLds {
+    half8 hi[HD / 32][64];
+    half8 lo[HD / 32][64];
+};
+
+template <int HD, bool SOFTCAP, bool TAIL>
+__device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD> &st,
+                                               const QLds<HD> &qs, float *stage, int base, int end,
+                                               int lane, int g, bool live, float softcap,
+                                               const DeqConst &dc) {
+    constexpr int WPG = HD / 32, NTD = HD / 16;
+    // Scales: one per lane in registers -> this wave's LDS stage -> the 4 positions each lane
+    // holds per tile (16kt + 4g + r).  Same-wave LDS traffic is ordered: no barrier needed.
+    stage[lane] = w.sk;
+    stage[64 + lane] = w.sv;
+    // ---- S^T = K Q^T (rows: positions, columns: heads), hi + lo q in one accumulator --------
+    floatx4 sc[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) sc[kt] = (floatx4)0.0f;
+#pragma unroll
+    for (int t = 0; t < WPG; t++) {
+        const half8 qh = qs.hi[t][lane], ql = qs.lo[t][lane];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            const half8 ka = dequant8(w.kw[kt][t], dc);
+            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh, sc[kt], 0, 0, 0);
+            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql, sc[kt], 0, 0, 0);
+        }
+    }
+    // ---- softmax ----------------------------------------------------------------------------
+    // x = score * log2(e).  s_v is folded into the probabilities: P = 2^(x - m) * s_v, with the
+    // window reference m >= max(x) + log2(max s_v), so P <= 1 always fits f16.
+    float x[16], sv[16];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+        const floatx4 sk4 = *reinterpret_cast<const floatx4 *>(stage + 16 * kt + 4 * g);
+        const floatx4 sv4 = *reinterpret_cast<const floatx4 *>(stage + 64 + 16 * kt + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float v = sc[kt][r] * sk4[r];
+            if constexpr (SOFTCAP) v = tanhf(v * (1.0f / kLog2e) / softcap) * softcap * kLog2e;
+            x[4 * kt + r] = v;
+            sv[4 * kt + r] = sv4[r];
+        }
+    }
+    if constexpr (TAIL) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int pos = base + 16 * (i >> 2) + 4 * g + (i & 3);
+            if (pos >= end) {
+                x[i] = -INFINITY;
+                sv[i] = 0.0f;
+            }
+        }
+    }
+    float xm = x[0], sm = sv[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) {
+        xm = fmaxf(xm, x[i]);
+        sm = fmaxf(sm, sv[i]);
+    }
+    xm = group_max(xm);
+    sm = group_max(sm);
+    float mw = xm + __builtin_amdgcn_logf(sm);
+    mw = fminf(fmaxf(mw, xm - 64.0f), xm + 64.0f);
+    // Rescale only when the reference would grow by more than 2^8; in between P stays below
+    // 2^8 (fine for f16) and no accumulator is touched.
+    if (__any(live && mw > st.m + 8.0f)) {
+        asm volatile("" ::: "memory");  // keep this a branch: the multiply is the rare case
+        const float m_new = fmaxf(st.m, mw);
+        const float alpha = fast_exp2(st.m - m_new);
+        st.l *= alpha;
+#pragma unroll
+        for (int td = 0; td < NTD; td++) st.o[td] *= alpha;
+        st.m = m_new;
+    }
+    float psum = 0.0f, pv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float p = fast_exp2(x[i] - st.m);
+        psum += p;
+        pv[i] = p * sv[i];
+    }
+    st.l += psum;
+    // ---- O^T += V^T P^T ---------------------------------------------------------------------
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        half8 pb;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            // slots (2r, 2r+1) = positions 4g+r of tiles 2b and 2b+1
+            // (columns past G hold finite garbage; they only feed output columns never read)
+            half2_t pr = {(_Float16)pv[4 * (2 * b) + r], (_Float16)pv[4 * (2 * b + 1) + r]};
+            pb[2 * r] = pr[0];
+            pb[2 * r + 1] = pr[1];
+        }
+#pragma unroll
+        for (int td = 0; td < NTD; td++) {
+            const half8 va = dequant8(w.vw[b][td], dc);
+            st.o[td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, st.o[td], 0, 0, 0);
+        }
+    }
+}
+
+template <int HD, bool SOFTCAP>
+__global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(DecodeArgs a) {
     constexpr int WPG = HD / 32;   // K words per lane group = MFMA k-steps per 16-row tile
     constexpr int NTD = HD / 16;   // 16-dim output tiles
     constexpr int ROWB = HD / 2;   // bytes per K row
+    constexpr int OST = HD + 1;
     const KvLayerView &L = a.L;
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int qpos = a.len[s];
@@ -58,26 +257,27 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     const int end = min(start + a.chunk, n_ctx);
     const int n_split_s = (n_ctx + a.chunk - 1) / a.chunk;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave index in an SGPR: window bases are then provably wave-uniform and feed the scalar
+    // offset of the buffer loads directly
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
     const int G = a.G;
+    const bool live = n < G;  // accumulator column n = query head h*G + n
+    const DeqConst dc;
 
-    // q operands (B of the QK MFMA): column n holds head n % G for n < 2G.
-    half8 qh[WPG], ql[WPG];
-    {
-        const bool live = n < 2 * G;
-        const int head = h * G + (live ? n % G : 0);
-        const float *qrow = a.q + ((size_t)s * a.n_head + head) * HD;
-#pragma unroll
-        for (int t = 0; t < WPG; t++) {
-            load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qpos, qh[t], ql[t]);
-            if (!live) {
-                qh[t] = (half8)(_Float16)0.0f;
-                ql[t] = (half8)(_Float16)0.0f;
-            }
-        }
-    }
-    const bool col_hi = n < G, col_lo = (n >= G) && (n < 2 * G);
+    // LDS: q operands, per-wave scale stages; reused for the final merge.
+    union Smem {
+        struct {
+            QLds<HD> q;
+            float stage[4][128];
+        } run;
+        struct {
+            float o[4][8 * OST];
+            float m[4][8], l[4][8];
+        } merge;
+    };
+    __shared__ Smem sm;
 
     const size_t row = (size_t)s * L.H + h;
     const uint8_t *kbase = L.kp + row * L.P * ROWB;
@@ -85,135 +285,114 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     const float *ksb = L.ks + row * L.P;
     const float *vsb = L.vs + row * L.P;
 
-    floatx4 o[NTD];
-#pragma unroll
-    for (int td = 0; td < NTD; td++) o[td] = (floatx4)0.0f;
-    float m_run = kMinit, l_run = 0.0f;
-    const float qk_scale = a.inv_sqrt_hd;
+    Streams str;
+    str.k = make_rsrc(kbase, (uint32_t)end * ROWB);
+    str.v = make_rsrc(vbase, (uint32_t)((end + 31) / 32) * (HD * 16));
+    str.ksb = ksb;
+    str.vsb = vsb;
+    str.last = end - 1;
 
-    for (int base = start + wave * 64; base < end; base += 256) {
-        // ---- loads -----------------------------------------------------------------------
-        uint32_t kw[4][WPG];
-        floatx4 skv[4], svv[4];
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-            const uint8_t *kr = kbase + (size_t)(base + 16 * kt + n) * ROWB + g * (WPG * 4);
-            if constexpr (WPG == 4) {
-                const uint4 t4 = *reinterpret_cast<const uint4 *>(kr);
-                kw[kt][0] = t4.x; kw[kt][1] = t4.y; kw[kt][2] = t4.z; kw[kt][3] = t4.w;
-            } else {
-                const uint2 t2 = *reinterpret_cast<const uint2 *>(kr);
-                kw[kt][0] = t2.x; kw[kt][1] = t2.y;
-            }
-            skv[kt] = *reinterpret_cast<const floatx4 *>(ksb + base + 16 * kt + 4 * g);
-            svv[kt] = *reinterpret_cast<const floatx4 *>(vsb + base + 16 * kt + 4 * g);
+    // First window in flight before anything else.
+    Window<HD> w0, w1;
+#if TS_DECODE_DEPTH == 3
+    Window<HD> w2;
+#endif
+    int base = start + wave * 64;
+    load_window<HD>(w0, str, base, n, g, lane);
+
+    // q operands: wave w builds k-step t = w (rotated, scaled by log2(e)/sqrt(hd), split hi/lo)
+    // for all 64 lanes; zero in the columns past G.
+    for (int t = wave; t < WPG; t += 4) {
+        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (live ? n : 0)) * HD;
+        half8 qh, ql;
+        load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qpos, a.inv_sqrt_hd * kLog2e, qh, ql);
+        if (!live) {
+            qh = (half8)(_Float16)0.0f;
+            ql = (half8)(_Float16)0.0f;
         }
-        uint32_t vw[2][NTD];
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const uint32_t *vr = reinterpret_cast<const uint32_t *>(vbase + (size_t)(base / 32 + b) * (HD * 16)) + lane * NTD;
-#pragma unroll
-            for (int q4 = 0; q4 < NTD / 4; q4++) {
-                const uint4 t4 = reinterpret_cast<const uint4 *>(vr)[q4];
-                vw[b][4 * q4 + 0] = t4.x; vw[b][4 * q4 + 1] = t4.y;
-                vw[b][4 * q4 + 2] = t4.z; vw[b][4 * q4 + 3] = t4.w;
-            }
-        }
-        // ---- S^T = K Q^T (rows: positions, columns: heads) --------------------------------------
-        floatx4 sc[4];
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-            floatx4 acc = (floatx4)0.0f;
-#pragma unroll
-            for (int t = 0; t < WPG; t++) {
-                const half8 ka = dequant8(kw[kt][t]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[t], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[t], acc, 0, 0, 0);
-            }
-            sc[kt] = acc;
-        }
-        // ---- online softmax (exp2 domain) ------------------------------------------------------
-        float mloc = kMinit;
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int pos = base + 16 * kt + 4 * g + r;
-                float x = sc[kt][r] * (skv[kt][r] * qk_scale);
-                if (a.softcap > 0.0f) x = tanhf(x / a.softcap) * a.softcap;
-                x = (pos < end) ? x * kLog2e : -INFINITY;
-                sc[kt][r] = x;
-                mloc = fmaxf(mloc, x);
-            }
-        }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = exp2f(m_run - m_new);
-        m_run = m_new;
-        float psum = 0.0f;
-        half2_t pp[4][2];  // [r][block]: (tile 2b, tile 2b+1) pair for slot r
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int pos = base + 16 * kt + 4 * g + r;
-                const float p = exp2f(sc[kt][r] - m_new);
-                psum += p;
-                const float pv = (pos < end) ? p * svv[kt][r] : 0.0f;
-                const _Float16 ph = (_Float16)pv;
-                const _Float16 pl = (_Float16)(pv - (float)ph);
-                const _Float16 sel = col_hi ? ph : (col_lo ? pl : (_Float16)0.0f);
-                pp[r][kt >> 1][kt & 1] = sel;
-            }
-        }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int td = 0; td < NTD; td++) o[td] *= alpha;
-        // ---- O^T += V^T P^T ------------------------------------------------------------------
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            half8 pb;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                pb[2 * r] = pp[r][b][0];
-                pb[2 * r + 1] = pp[r][b][1];
-            }
-#pragma unroll
-            for (int td = 0; td < NTD; td++) {
-                const half8 va = dequant8(vw[b][td]);
-                o[td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[td], 0, 0, 0);
-            }
-        }
+        sm.run.q.hi[t][lane] = qh;
+        sm.run.q.lo[t][lane] = ql;
     }
+    __syncthreads();
+
+    WaveState<HD> st;
+#pragma unroll
+    for (int td = 0; td < NTD; td++) st.o[td] = (floatx4)0.0f;
+    st.m = kMinit;
+    st.l = 0.0f;
+    float *stage = sm.run.stage[wave];
+
+#if TS_DECODE_DEPTH == 3
+    // Register triple buffering: windows i+1 and i+2 are in flight while window i is computed.
+    load_window<HD>(w1, str, base + 256, n, g, lane);
+#define TS_STEP(CUR, NXT)                                                                       \
+    {                                                                                          \
+        load_window<HD>(NXT, str, base + 512, n, g, lane);                                     \
+        /* keep the prefetch here: the scheduler would otherwise sink it below CUR's use */     \
+        asm volatile("" ::: "memory");                                                         \
+        __builtin_amdgcn_sched_barrier(0);                                                     \
+        if (base + 64 <= end)                                                                  \
+            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
+        else                                                                                   \
+            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
+        base += 256;                                                                           \
+        if (base >= end) break;                                                                \
+    }
+    while (base < end) {
+        TS_STEP(w0, w2)
+        TS_STEP(w1, w0)
+        TS_STEP(w2, w1)
+    }
+#undef TS_STEP
+#else
+    // Register double buffering: window i+1 is in flight while window i is computed.  Full
+    // windows take the unmasked path; only the window that crosses `end` is masked.
+#define TS_STEP(CUR, NXT)                                                                       \
+    {                                                                                          \
+        load_window<HD>(NXT, str, base + 256, n, g, lane);                                     \
+        /* keep the prefetch here: the scheduler would otherwise sink it below CUR's use */     \
+        asm volatile("" ::: "memory");                                                         \
+        __builtin_amdgcn_sched_barrier(0);                                                     \
+        if (base + 64 <= end)                                                                  \
+            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
+        else                                                                                   \
+            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
+        base += 256;                                                                           \
+        if (base >= end) break;                                                                \
+    }
+    while (base < end) {
+        TS_STEP(w0, w1)
+        TS_STEP(w1, w0)
+    }
+#undef TS_STEP
+#endif
 
     // ---- merge the 4 waves through LDS ---------------------------------------------------------
-    l_run += __shfl_xor(l_run, 16, 64);
-    l_run += __shfl_xor(l_run, 32, 64);
-    constexpr int OST = HD + 1;
-    __shared__ float s_o[4][16 * OST];
-    __shared__ float s_m[4][16], s_l[4][16];
-    if (g == 0) {
-        s_m[wave][n] = m_run;
-        s_l[wave][n] = l_run;
+    const float l_run = group_sum(st.l);
+    __syncthreads();  // all waves are done with the q operands and stages
+    if (live) {
+        if (g == 0) {
+            sm.merge.m[wave][n] = st.m;
+            sm.merge.l[wave][n] = l_run;
+        }
+#pragma unroll
+        for (int td = 0; td < NTD; td++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sm.merge.o[wave][n * OST + 16 * td + 4 * g + r] = st.o[td][r];
     }
-#pragma unroll
-    for (int td = 0; td < NTD; td++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) s_o[wave][n * OST + 16 * td + 4 * g + r] = o[td][r];
     __syncthreads();
 
     for (int idx = tid; idx < G * HD; idx += 256) {
         const int hh = idx / HD, d = idx % HD;
         float M = kMinit;
 #pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w][hh]);
+        for (int w = 0; w < 4; w++) M = fmaxf(M, sm.merge.m[w][hh]);
         float acc = 0.0f, lsum = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            const float e = exp2f(s_m[w][hh] - M);
-            acc += e * (s_o[w][hh * OST + d] + s_o[w][(hh + G) * OST + d]);
-            lsum += e * s_l[w][hh];
+            const float e = exp2f(sm.merge.m[w][hh] - M);
+            acc += e * sm.merge.o[w][hh * OST + d];
+            lsum += e * sm.merge.l[w][hh];
         }
         const size_t head = (size_t)s * a.n_head + h * G + hh;
         if (n_split_s == 1) {
@@ -256,7 +435,12 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(DecodeArgs a) {
 // Split plan: aim for ~kTargetWG workgroups in total so all 256 CUs get several, with each
 // split a multiple of 64 positions.  n_split is non-decreasing in max_ctx.
 DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx) {
-    constexpr int kTargetWG = 2048;
+    // TS_DECODE_WG overrides the workgroup target (a tuning knob; read once).
+    static const int kTargetWG = [] {
+        const char *e = getenv("TS_DECODE_WG");
+        const int v = e ? atoi(e) : 0;
+        return v > 0 ? v : 1024;
+    }();
     const int units = n_seq * n_kv;
     int want = (kTargetWG + units - 1) / units;
     if (want < 1) want = 1;
@@ -290,10 +474,16 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.ws = ws;
     dim3 grid(plan.n_split, L.H, L.S);
     if (L.hd == 128) {
-        decode_split_kernel<128><<<grid, 256, 0, st>>>(a);
+        if (softcap > 0.0f)
+            decode_split_kernel<128, true><<<grid, 256, 0, st>>>(a);
+        else
+            decode_split_kernel<128, false><<<grid, 256, 0, st>>>(a);
         if (plan.n_split > 1) decode_combine_kernel<128><<<dim3(n_head, L.S), 128, 0, st>>>(a);
     } else if (L.hd == 64) {
-        decode_split_kernel<64><<<grid, 256, 0, st>>>(a);
+        if (softcap > 0.0f)
+            decode_split_kernel<64, true><<<grid, 256, 0, st>>>(a);
+        else
+            decode_split_kernel<64, false><<<grid, 256, 0, st>>>(a);
         if (plan.n_split > 1) decode_combine_kernel<64><<<dim3(n_head, L.S), 64, 0, st>>>(a);
     } else {
         return hipErrorInvalidValue;

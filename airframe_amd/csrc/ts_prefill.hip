@@ -54,6 +54,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     const int c_wave = cblk * kColsPerBlock + wave * kColsPerWave;
     if (c_wave >= n_cols) return;
     const int len0 = a.len[s];
+    const DeqConst dc;
 
     // Per column tile: this lane's column, its token, query position and q operands.
     half8 qh[2][WPG], ql[2][WPG];
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
         const float *qrow = a.q + (((size_t)s * a.n_tok + tok) * a.n_head + head) * HD;
 #pragma unroll
         for (int t = 0; t < WPG; t++) {
-            load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, len0 + tok, qh[nt][t], ql[nt][t]);
+            load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, len0 + tok, 1.0f, qh[nt][t], ql[nt][t]);
             if (!live[nt]) {
                 qh[nt][t] = (half8)(_Float16)0.0f;
                 ql[nt][t] = (half8)(_Float16)0.0f;
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
         for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
             for (int t = 0; t < WPG; t++) {
-                const half8 ka = dequant8(kw[kt][t]);
+                const half8 ka = dequant8(kw[kt][t], dc);
 #pragma unroll
                 for (int nt = 0; nt < 2; nt++) {
                     sc[nt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[nt][t], sc[nt][kt], 0, 0, 0);
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
         }
 #pragma unroll
         for (int td = 0; td < NTD; td++) {
-            const half8 va = dequant8(vw[td]);
+            const half8 va = dequant8(vw[td], dc);
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
                 o[nt][td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[nt], o[nt][td], 0, 0, 0);

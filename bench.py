@@ -1,0 +1,349 @@
+"""Benchmark of the INT4 KV decode path on one MI355X.
+
+Default workload (the headline): Qwen3-8B attention shape, 36 layers,
+32 query / 8 kv heads, head_dim 128, batch 32, each sequence with 8192 cached INT4 tokens,
+seeded f32 N(0,1) Q/K/V with x8 outlier channels on 2% of dims, RoPE theta 1e6.  A step is one
+decode token for all 32 sequences: per layer, RoPE-fused quantize-on-append of the new K/V
+(ts_append_quant) and split-K GQA attention over the INT4 cache (ts_attn_decode); then the
+lengths advance (ts_kv_increment).  All inputs are generated on the device before timing.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+
+Prints one JSON line.  `value` = algorithmic HBM bytes of the whole step / step time (GB/s);
+`roofline` = the decode attention kernel (bytes per launch / its average launch time from HIP
+events recorded around every launch in the timed region); `cpu_baseline` = the C oracle on a
+bounded sample of the same workload (same device-generated inputs copied to the host).
+Other configs (--config 1,2,4 decode; 5 chunked prefill) print their own line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+CONFIGS = {
+    1: dict(name="llama3.2-1b_b1_ctx512_1layer", layers=1, n_head=32, n_kv=8, hd=64, batch=1,
+            ctx=512, theta=500000.0, steps=64, outliers=False),
+    2: dict(name="llama3.2-3b_b1_prefill4096_28layers", layers=28, n_head=24, n_kv=8, hd=128,
+            batch=1, ctx=4096, theta=500000.0, steps=256, outliers=False),
+    3: dict(name="qwen3-8b_b32_ctx8192_36layers", layers=36, n_head=32, n_kv=8, hd=128,
+            batch=32, ctx=8192, theta=1000000.0, steps=128, outliers=True),
+    4: dict(name="llama3-8b_b8_ctx16k-32k_ragged_32layers", layers=32, n_head=32, n_kv=8, hd=128,
+            batch=8, ctx=32768, theta=500000.0, steps=1, outliers=False, ragged=(16384, 32768)),
+    5: dict(name="qwen3-4b_b4_prefill_4x512_36layers", layers=36, n_head=32, n_kv=8, hd=128,
+            batch=4, chunk=512, n_chunks=4, theta=1000000.0, outliers=False),
+}
+
+
+def attn_bytes(batch_ctx, n_kv, n_head, hd, batch):
+    """Algorithmic bytes of one decode-attention launch: packed K+V (hd/2 bytes each) and two
+    f32 scales for every attended position of every (sequence, kv head), plus q in and o out
+    in f32."""
+    return sum(batch_ctx) * n_kv * (hd + 8) + 2 * batch * n_head * hd * 4
+
+
+def append_bytes(batch, n_kv, hd):
+    """One appended token per sequence: f32 K and V read, packed rows and scales written."""
+    return batch * n_kv * (2 * hd * 4 + hd + 8)
+
+
+def cpu_baseline(kv, cfg, qs, ks, vs, lens, max_seq, table, layers_mt=2, seqs_st=2):
+    """Time the C oracle (oracle/ts_oracle.c) on a bounded sample of the same step: append the
+    step's token and attend, for every sequence of `layers_mt` layers (OpenMP over
+    (sequence, head)) and for `seqs_st` sequences of one layer single-threaded."""
+    import torch
+
+    from oracle import oracle
+    n_kv, hd, n_head, B = cfg["n_kv"], cfg["hd"], cfg["n_head"], cfg["batch"]
+    threads = min(16, os.cpu_count() or 1)
+    t_mt = 0.0
+    t_st = 0.0
+    for layer in range(layers_mt):
+        ora = oracle.OracleKV(B, max_seq, n_kv, hd, table)
+        for s in range(B):
+            kp, vp, kss, vss = kv.export(layer, s, 0, lens[s])
+            torch.cuda.synchronize()
+            ora.k_packed[s, :lens[s]] = kp.cpu().numpy().view(np.uint32)
+            ora.v_packed[s, :lens[s]] = vp.cpu().numpy().view(np.uint32)
+            ora.k_scale[s, :lens[s]] = kss.cpu().numpy()
+            ora.v_scale[s, :lens[s]] = vss.cpu().numpy()
+        ora.lens[:] = np.asarray(lens, np.int32)
+        k = ks[layer].cpu().numpy()
+        v = vs[layer].cpu().numpy()
+        q = qs[layer].cpu().numpy()[:, None]
+        t0 = time.perf_counter()
+        ora.append(k, v)
+        ora.attend(q, 1, threads=threads)
+        t_mt += time.perf_counter() - t0
+        if layer == 0:
+            sub = oracle.OracleKV(seqs_st, max_seq, n_kv, hd, table)
+            for name in ("k_packed", "v_packed", "k_scale", "v_scale"):
+                getattr(sub, name)[:] = getattr(ora, name)[:seqs_st]
+            sub.lens[:] = ora.lens[:seqs_st]
+            t0 = time.perf_counter()
+            sub.append(k[:seqs_st], v[:seqs_st])
+            sub.attend(q[:seqs_st], 1, threads=1)
+            t_st = time.perf_counter() - t0
+    step_mt = t_mt / layers_mt * cfg["layers"]
+    step_st = t_st / seqs_st * B * cfg["layers"]
+    return step_mt, threads, step_st
+
+
+def run_decode(args, cfg):
+    import torch
+
+    from airframe_amd import synth
+    from airframe_amd.kv_cache import KVCache, RopeTable
+
+    dev = torch.device("cuda:0")
+    L, n_head, n_kv, hd, B = cfg["layers"], cfg["n_head"], cfg["n_kv"], cfg["hd"], cfg["batch"]
+    steps, warmup = args.steps, args.warmup
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    if "ragged" in cfg:
+        rng = np.random.default_rng(args.seed)
+        lens0 = [int(x) for x in rng.integers(cfg["ragged"][0], cfg["ragged"][1], size=B)]
+    else:
+        lens0 = [cfg["ctx"]] * B
+    max_seq = max(lens0) + max(steps, warmup) + 1
+    rope = RopeTable(max_seq, hd, cfg["theta"])
+    kv = KVCache.new_int4(L, n_kv, hd, max_seq, B)
+    dims = synth.outlier_dims(n_kv, hd, args.seed) if cfg["outliers"] else None
+    skv = torch.as_tensor(synth.channel_scale(n_kv, n_kv, hd, dims), device=dev)
+    sq = torch.as_tensor(synth.channel_scale(n_head, n_kv, hd, dims), device=dev)
+
+    # Fill every layer's cache to its starting length with the fused append.
+    fill = max(lens0)
+    chunk = 1024
+    for layer in range(L):
+        kv.reset()
+        for t0 in range(0, fill, chunk):
+            m = min(chunk, fill - t0)
+            k = torch.randn((B, m, n_kv, hd), generator=gen, device=dev).mul_(skv)
+            v = torch.randn((B, m, n_kv, hd), generator=gen, device=dev).mul_(skv)
+            kv.append_quant(layer, k, v, rope)
+            kv.increment(m)
+        del k, v
+    for s, l in enumerate(lens0):
+        kv.set_seq_len(l, seq=s)
+
+    # Per-step inputs, resident before timing: one set per step (warmup reuses the first).
+    n_sets = max(steps, 1)
+    qs = [[torch.randn((B, n_head, hd), generator=gen, device=dev).mul_(sq) for _ in range(L)] for _ in range(n_sets)]
+    ks = [[torch.randn((B, 1, n_kv, hd), generator=gen, device=dev).mul_(skv) for _ in range(L)] for _ in range(n_sets)]
+    vs = [[torch.randn((B, 1, n_kv, hd), generator=gen, device=dev).mul_(skv) for _ in range(L)] for _ in range(n_sets)]
+    out = torch.empty((B, n_head, hd), device=dev)
+    ws = kv.workspace(n_head)
+    torch.cuda.synchronize()
+
+    def step(i, events=None):
+        for layer in range(L):
+            kv.append_quant(layer, ks[i][layer], vs[i][layer], rope)
+            if events is not None:
+                events[layer][0].record()
+            kv.attn_decode(layer, qs[i][layer], rope, out=out, workspace=ws)
+            if events is not None:
+                events[layer][1].record()
+        kv.increment(1)
+
+    for i in range(warmup):
+        step(i % n_sets)
+    for s, l in enumerate(lens0):
+        kv.set_seq_len(l, seq=s)
+    torch.cuda.synchronize()
+
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)] for _ in range(steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for i in range(steps):
+        step(i, ev[i] if args.kernel_events else None)
+    t_end.record()
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    ms_step = total_ms / steps
+
+    step_bytes = 0
+    kern_bytes = []
+    for i in range(steps):
+        ctx = [l + i + 1 for l in lens0]
+        b = attn_bytes(ctx, n_kv, n_head, hd, B)
+        kern_bytes.append(b)
+        step_bytes += L * (b + append_bytes(B, n_kv, hd))
+    step_bytes /= steps
+    result = dict(total_ms=total_ms, ms_step=ms_step, step_bytes=step_bytes)
+    if args.kernel_events:
+        kt = [ev[i][l][0].elapsed_time(ev[i][l][1]) for i in range(steps) for l in range(L)]
+        kb = [kern_bytes[i] for i in range(steps) for _ in range(L)]
+        result["kernel_ms"] = float(np.mean(kt))
+        result["kernel_bytes"] = float(np.mean(kb))
+    lens_now = [l + steps for l in lens0]
+
+    cpu = None
+    if not args.no_cpu:
+        for s, l in enumerate(lens0):
+            kv.set_seq_len(l, seq=s)
+        torch.cuda.synchronize()
+        from oracle import oracle
+        table = oracle.rope_table(max_seq, hd, cfg["theta"])
+        # The oracle appends at lens0 (same token the GPU appended in timed step 0).
+        t_mt, cores, t_st = cpu_baseline(kv, cfg, qs[0], ks[0], vs[0], lens0, max_seq, table,
+                                         layers_mt=min(2, L), seqs_st=min(2, B))
+        cpu = dict(step_s_mt=t_mt, cores=cores, step_s_st=t_st)
+    del lens_now
+    return result, cpu
+
+
+def run_prefill(args, cfg):
+    import torch
+
+    from airframe_amd.kv_cache import KVCache, RopeTable
+
+    dev = torch.device("cuda:0")
+    L, n_head, n_kv, hd, B = cfg["layers"], cfg["n_head"], cfg["n_kv"], cfg["hd"], cfg["batch"]
+    C, NC = cfg["chunk"], cfg["n_chunks"]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    max_seq = C * NC
+    rope = RopeTable(max_seq, hd, cfg["theta"])
+    kv = KVCache.new_int4(L, n_kv, hd, max_seq, B)
+    qs = [[torch.randn((B, C, n_head, hd), generator=gen, device=dev) for _ in range(L)] for _ in range(NC)]
+    ks = [[torch.randn((B, C, n_kv, hd), generator=gen, device=dev) for _ in range(L)] for _ in range(NC)]
+    vs = [[torch.randn((B, C, n_kv, hd), generator=gen, device=dev) for _ in range(L)] for _ in range(NC)]
+    out = torch.empty((B, C, n_head, hd), device=dev)
+
+    def run(events=None):
+        kv.reset()
+        for c in range(NC):
+            for layer in range(L):
+                kv.append_quant(layer, ks[c][layer], vs[c][layer], rope)
+                if events is not None:
+                    events[c][layer][0].record()
+                kv.attn_prefill(layer, qs[c][layer], rope, out=out)
+                if events is not None:
+                    events[c][layer][1].record()
+            kv.increment(C)
+
+    for _ in range(max(args.warmup, 1)):
+        run()
+    torch.cuda.synchronize()
+    reps = max(args.steps, 1)
+    evs = [[[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)] for _ in range(NC)] for _ in range(reps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for r in range(reps):
+        run(evs[r])
+    t1.record()
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1) / reps
+    kt = [evs[r][c][l][0].elapsed_time(evs[r][c][l][1]) for r in range(reps) for c in range(NC) for l in range(L)]
+    # causal-exact flops per layer: QK^T and PV, 2 flops per MAC, over all chunks
+    n_tot = C * NC
+    flops_layer = 4 * hd * n_head * B * (n_tot * (n_tot + 1) // 2)
+    kernel_ms_layer = float(np.sum(kt)) / reps / L
+    return dict(total_ms=total_ms, kernel_ms_layer=kernel_ms_layer, flops_layer=flops_layer)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-kernel-events", dest="kernel_events", action="store_false")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the INT4 KV path shards "
+                          "by sequence or kv head with no exchange (see DESIGN.md), but "
+                          "multi-GPU runs are not part of it", "n_gpus": args.gpus}))
+        sys.exit(2)
+    cfg = CONFIGS[args.config]
+    if args.steps is None:
+        args.steps = cfg.get("steps", 3) if args.config != 5 else 3
+
+    import torch
+    import airframe_amd
+    airframe_amd.load()
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    torch.cuda.set_device(0)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"decode_traffic_cfg{args.config}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
+
+    if args.config == 5:
+        r = run_prefill(args, cfg)
+        achieved = r["flops_layer"] / (r["kernel_ms_layer"] * 1e-3) / 1e12
+        line = {
+            "metric": "INT4-KV chunked-prefill attention MFMA TFLOP/s (% of f16 dense peak)",
+            "value": round(r["flops_layer"] * cfg["layers"] / (r["total_ms"] * 1e-3) / 1e12, 3),
+            "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(r["total_ms"], 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f16-mfma(hi/lo split)+int4", "data": "synthetic",
+            "config": {"workload": cfg["name"], "global_batch": cfg["batch"],
+                       "seq_len": cfg["chunk"] * cfg["n_chunks"], "parallelism": "none"},
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                         "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+            "cpu_baseline": None,
+        }
+        print(json.dumps(line), flush=True)
+        return
+
+    r, cpu = run_decode(args, cfg)
+    B, L = cfg["batch"], cfg["layers"]
+    gbs = r["step_bytes"] / (r["ms_step"] * 1e-3) / 1e9
+    tok_s = B / (r["ms_step"] * 1e-3)
+    roof = None
+    if "kernel_ms" in r:
+        ach = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "decode_split_kernel<128>+decode_combine_kernel (ts_attn_decode)",
+                "bytes_per_launch": int(r["kernel_bytes"]),
+                "avg_launch_us": round(r["kernel_ms"] * 1e3, 2)}
+    cpu_line = None
+    if cpu:
+        cpu_gbs = r["step_bytes"] / cpu["step_s_mt"] / 1e9
+        cpu_line = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": cpu["cores"],
+                    "kind": "port",
+                    "tokens_per_s": round(B / cpu["step_s_mt"], 4),
+                    "single_thread_tokens_per_s": round(B / cpu["step_s_st"], 5),
+                    "sample": f"C oracle: append + attention of step 0 for all {B} sequences of "
+                              f"2 layers (OpenMP, {cpu['cores']} threads), and of 2 sequences of "
+                              f"1 layer single-threaded; scaled to {L} layers x {B} sequences"}
+    line = {
+        "metric": "INT4-KV decode-attn HBM GB/s (% of peak) + tokens/s, 8B shape ctx 8K b32",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(r["ms_step"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int4-kv/f32-io (f16 mfma, hi/lo split)",
+        "data": "synthetic (seeded N(0,1), x8 outlier channels)" if cfg["outliers"] else "synthetic (seeded N(0,1))",
+        "tokens_per_s": round(tok_s, 1), "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "config": {"workload": cfg["name"], "global_batch": B, "seq_len": cfg.get("ctx"),
+                   "layers": L, "n_head": cfg["n_head"], "n_head_kv": cfg["n_kv"],
+                   "head_dim": cfg["hd"], "parallelism": "none"},
+        "roofline": roof,
+        "cpu_baseline": cpu_line,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
