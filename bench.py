@@ -157,19 +157,55 @@ def run_decode(args, cfg):
                 events[layer][1].record()
         kv.increment(1)
 
-    for i in range(warmup):
+    def reset_lens():
+        for s, l in enumerate(lens0):
+            kv.set_seq_len(l, seq=s)
+
+    # Kernel timing pass (no graph): HIP events around every ts_attn_decode launch.
+    n_kt = min(steps, 16)
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)] for _ in range(n_kt)]
+    for i in range(min(warmup, 2)):
         step(i % n_sets)
-    for s, l in enumerate(lens0):
-        kv.set_seq_len(l, seq=s)
+    reset_lens()
+    for i in range(n_kt):
+        step(i, ev[i])
+    torch.cuda.synchronize()
+    reset_lens()
     torch.cuda.synchronize()
 
-    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)] for _ in range(steps)]
+    # The timed steps.  With graphs, each step (36 x (append, decode split, combine) + the
+    # length increment) is captured once with its own split plan and replayed; device lengths
+    # advance inside the graphs exactly as in eager execution.
+    graphs = None
+    if args.graph:
+        graphs = []
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        for i in range(steps):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=cap):
+                step(i)
+            graphs.append(gr)
+        torch.cuda.synchronize()
+        for i in range(warmup):
+            graphs[i % steps].replay()
+        torch.cuda.synchronize()
+        reset_lens()
+    else:
+        for i in range(warmup):
+            step(i % n_sets)
+        reset_lens()
+    torch.cuda.synchronize()
+
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record()
     for i in range(steps):
-        step(i, ev[i] if args.kernel_events else None)
+        if graphs is not None:
+            graphs[i].replay()
+        else:
+            step(i)
     t_end.record()
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
@@ -184,25 +220,22 @@ def run_decode(args, cfg):
         step_bytes += L * (b + append_bytes(B, n_kv, hd))
     step_bytes /= steps
     result = dict(total_ms=total_ms, ms_step=ms_step, step_bytes=step_bytes)
-    if args.kernel_events:
-        kt = [ev[i][l][0].elapsed_time(ev[i][l][1]) for i in range(steps) for l in range(L)]
-        kb = [kern_bytes[i] for i in range(steps) for _ in range(L)]
-        result["kernel_ms"] = float(np.mean(kt))
-        result["kernel_bytes"] = float(np.mean(kb))
-    lens_now = [l + steps for l in lens0]
+    kt = [ev[i][l][0].elapsed_time(ev[i][l][1]) for i in range(n_kt) for l in range(L)]
+    kb = [kern_bytes[i] for i in range(n_kt) for _ in range(L)]
+    result["kernel_ms"] = float(np.mean(kt))
+    result["kernel_bytes"] = float(np.mean(kb))
 
     cpu = None
+    reset_lens()
+    torch.cuda.synchronize()
+    del graphs
     if not args.no_cpu:
-        for s, l in enumerate(lens0):
-            kv.set_seq_len(l, seq=s)
-        torch.cuda.synchronize()
         from oracle import oracle
         table = oracle.rope_table(max_seq, hd, cfg["theta"])
         # The oracle appends at lens0 (same token the GPU appended in timed step 0).
         t_mt, cores, t_st = cpu_baseline(kv, cfg, qs[0], ks[0], vs[0], lens0, max_seq, table,
                                          layers_mt=min(2, L), seqs_st=min(2, B))
         cpu = dict(step_s_mt=t_mt, cores=cores, step_s_st=t_st)
-    del lens_now
     return result, cpu
 
 
@@ -265,7 +298,11 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--no-kernel-events", dest="kernel_events", action="store_false")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run a plain 1 GiB device copy (4 launches) so rocprofv3 HBM counters "
+                         "can be scaled by what they read for a copy of known size")
+    ap.add_argument("--no-graph", dest="graph", action="store_false",
+                    help="launch every kernel eagerly instead of replaying captured HIP graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the INT4 KV path shards "
@@ -282,11 +319,23 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
     torch.cuda.set_device(0)
+    # HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated) for
+    # this configuration, as recorded in its profile summary; null when none was taken.
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"decode_traffic_cfg{args.config}.json")
+    tpath = os.path.join(ROOT, "profiles", f"decode_cfg{args.config}.md")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("traffic_bytes_per_launch")
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    traffic = int(float(line.split(":")[1]))
+
+    if args.copy_calib:
+        x = torch.empty(2**28, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(4):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        del x, y
 
     if args.config == 5:
         r = run_prefill(args, cfg)
@@ -312,13 +361,15 @@ def main():
     gbs = r["step_bytes"] / (r["ms_step"] * 1e-3) / 1e9
     tok_s = B / (r["ms_step"] * 1e-3)
     roof = None
-    if "kernel_ms" in r:
+    if True:
         ach = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": f"profiles/decode_cfg{args.config}.md" if traffic else None,
                 "kernel": "decode_split_kernel<128>+decode_combine_kernel (ts_attn_decode)",
                 "bytes_per_launch": int(r["kernel_bytes"]),
-                "avg_launch_us": round(r["kernel_ms"] * 1e3, 2)}
+                "avg_launch_us": round(r["kernel_ms"] * 1e3, 2),
+                "timing": "HIP events around each ts_attn_decode launch, eager pass of 16 steps"}
     cpu_line = None
     if cpu:
         cpu_gbs = r["step_bytes"] / cpu["step_s_mt"] / 1e9
@@ -336,6 +387,7 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "int4-kv/f32-io (f16 mfma, hi/lo split)",
         "data": "synthetic (seeded N(0,1), x8 outlier channels)" if cfg["outliers"] else "synthetic (seeded N(0,1))",
         "tokens_per_s": round(tok_s, 1), "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "launch": "hip-graph replay per step" if args.graph else "eager",
         "config": {"workload": cfg["name"], "global_batch": B, "seq_len": cfg.get("ctx"),
                    "layers": L, "n_head": cfg["n_head"], "n_head_kv": cfg["n_kv"],
                    "head_dim": cfg["hd"], "parallelism": "none"},
