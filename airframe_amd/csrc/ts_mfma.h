@@ -18,6 +18,12 @@ constexpr float kMinit = -1.0e30f;
 
 // (w & mask) | add in one VALU op.  gfx9 VOP3 encodings take no literal constants and read at
 // most one SGPR, so the masks are passed in VGPRs (see DeqConst).
+//
+// Inline asm is invisible to the compiler's hazard recognizer, so its result must never feed a
+// matrix-core instruction directly: every use below goes through a compiler-visible packed f16
+// op first, which carries the required wait states.  (Written as plain C, the compiler picks
+// the same v_and_or_b32 but reschedules the decode loop into spills, ~20% slower; both builds
+// give bit-identical attention outputs.)
 __device__ inline uint32_t and_or(uint32_t w, uint32_t mask, uint32_t add) {
     uint32_t r;
     asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(mask), "v"(add));
