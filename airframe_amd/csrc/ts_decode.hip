@@ -31,6 +31,9 @@
 #ifndef TS_DECODE_WAVES
 #define TS_DECODE_WAVES 2
 #endif
+#ifndef TS_DECODE_NW
+#define TS_DECODE_NW 4
+#endif
 #ifndef TS_DECODE_DEPTH
 #define TS_DECODE_DEPTH 2
 #endif
@@ -243,7 +246,9 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
 }
 
 template <int HD, bool SOFTCAP>
-__global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_split_kernel(DecodeArgs a) {
+    constexpr int NW = TS_DECODE_NW;  // waves per workgroup
+    constexpr int SPAN = 64 * NW;     // positions one round of windows covers
     constexpr int WPG = HD / 32;   // K words per lane group = MFMA k-steps per 16-row tile
     constexpr int NTD = HD / 16;   // 16-dim output tiles
     constexpr int ROWB = HD / 2;   // bytes per K row
@@ -270,11 +275,11 @@ __global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(Deco
     union Smem {
         struct {
             QLds<HD> q;
-            float stage[4][128];
+            float stage[NW][128];
         } run;
         struct {
-            float o[4][8 * OST];
-            float m[4][8], l[4][8];
+            float o[NW][8 * OST];
+            float m[NW][8], l[NW][8];
         } merge;
     };
     __shared__ Smem sm;
@@ -302,7 +307,7 @@ __global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(Deco
 
     // q operands: wave w builds k-step t = w (rotated, scaled by log2(e)/sqrt(hd), split hi/lo)
     // for all 64 lanes; zero in the columns past G.
-    for (int t = wave; t < WPG; t += 4) {
+    for (int t = wave; t < WPG; t += NW) {
         const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (live ? n : 0)) * HD;
         half8 qh, ql;
         load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qpos, a.inv_sqrt_hd * kLog2e, qh, ql);
@@ -324,10 +329,10 @@ __global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(Deco
 
 #if TS_DECODE_DEPTH == 3
     // Register triple buffering: windows i+1 and i+2 are in flight while window i is computed.
-    load_window<HD>(w1, str, base + 256, n, g, lane);
+    load_window<HD>(w1, str, base + SPAN, n, g, lane);
 #define TS_STEP(CUR, NXT)                                                                       \
     {                                                                                          \
-        load_window<HD>(NXT, str, base + 512, n, g, lane);                                     \
+        load_window<HD>(NXT, str, base + 2 * SPAN, n, g, lane);                                     \
         /* keep the prefetch here: the scheduler would otherwise sink it below CUR's use */     \
         asm volatile("" ::: "memory");                                                         \
         __builtin_amdgcn_sched_barrier(0);                                                     \
@@ -335,7 +340,7 @@ __global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(Deco
             process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
         else                                                                                   \
             process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
-        base += 256;                                                                           \
+        base += SPAN;                                                                           \
         if (base >= end) break;                                                                \
     }
     while (base < end) {
@@ -349,7 +354,7 @@ __global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(Deco
     // windows take the unmasked path; only the window that crosses `end` is masked.
 #define TS_STEP(CUR, NXT)                                                                       \
     {                                                                                          \
-        load_window<HD>(NXT, str, base + 256, n, g, lane);                                     \
+        load_window<HD>(NXT, str, base + SPAN, n, g, lane);                                     \
         /* keep the prefetch here: the scheduler would otherwise sink it below CUR's use */     \
         asm volatile("" ::: "memory");                                                         \
         __builtin_amdgcn_sched_barrier(0);                                                     \
@@ -357,7 +362,7 @@ __global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(Deco
             process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
         else                                                                                   \
             process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
-        base += 256;                                                                           \
+        base += SPAN;                                                                           \
         if (base >= end) break;                                                                \
     }
     while (base < end) {
@@ -382,14 +387,14 @@ __global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(Deco
     }
     __syncthreads();
 
-    for (int idx = tid; idx < G * HD; idx += 256) {
+    for (int idx = tid; idx < G * HD; idx += SPAN) {
         const int hh = idx / HD, d = idx % HD;
         float M = kMinit;
 #pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, sm.merge.m[w][hh]);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sm.merge.m[w][hh]);
         float acc = 0.0f, lsum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
+        for (int w = 0; w < NW; w++) {
             const float e = exp2f(sm.merge.m[w][hh] - M);
             acc += e * sm.merge.o[w][hh * OST + d];
             lsum += e * sm.merge.l[w][hh];
@@ -408,10 +413,16 @@ __global__ __launch_bounds__(256, TS_DECODE_WAVES) void decode_split_kernel(Deco
     }
 }
 
-// Log-sum-exp merge of the splits of one (sequence, head); one thread per dim.
+// Log-sum-exp merge of the splits of one (sequence, head).  256 threads: HD/4 threads (one
+// float4 of dims each) per split row, 1024/HD row groups striding over the splits, then an
+// LDS reduction over the groups, so the dependent-load chain is ns/groups long, not ns.
 template <int HD>
-__global__ __launch_bounds__(HD) void decode_combine_kernel(DecodeArgs a) {
-    const int head = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+    constexpr int V4 = HD / 4, NG = 256 / V4;
+    __shared__ float4 part[NG][V4];
+    __shared__ float lpart[NG];
+    __shared__ float wmax[4];
+    const int head = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
     const int n_ctx = a.len[s] + 1;
     const int ns = (n_ctx + a.chunk - 1) / a.chunk;
     if (ns <= 1) return;
@@ -419,21 +430,58 @@ __global__ __launch_bounds__(HD) void decode_combine_kernel(DecodeArgs a) {
     const float *ml = a.ws + (size_t)a.L.S * a.n_head * a.n_split * HD;
     const float *mm = ml + hidx * a.n_split;
     const float *ll = ml + (size_t)a.L.S * a.n_head * a.n_split + hidx * a.n_split;
+
     float M = kMinit;
-    for (int i = 0; i < ns; i++) M = fmaxf(M, mm[i]);
-    float acc = 0.0f, lsum = 0.0f;
-    for (int i = 0; i < ns; i++) {
+    for (int i = tid; i < ns; i += 256) M = fmaxf(M, mm[i]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if ((tid & 63) == 0) wmax[tid >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+
+    const int g = tid / V4, j = tid % V4;
+    const float4 *o4 = reinterpret_cast<const float4 *>(a.ws + hidx * a.n_split * HD);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float lsum = 0.0f;
+#pragma unroll 4
+    for (int i = g; i < ns; i += NG) {
         const float e = exp2f(mm[i] - M);
-        acc += e * a.ws[(hidx * a.n_split + i) * HD + d];
+        const float4 x = o4[(size_t)i * V4 + j];
+        acc.x += e * x.x;
+        acc.y += e * x.y;
+        acc.z += e * x.z;
+        acc.w += e * x.w;
         lsum += e * ll[i];
     }
-    a.out[hidx * HD + d] = lsum > 0.0f ? acc / lsum : 0.0f;
+    part[g][j] = acc;
+    if (j == 0) lpart[g] = lsum;
+    __syncthreads();
+    if (tid < V4) {
+        float4 r = part[0][tid];
+        float l = lpart[0];
+#pragma unroll
+        for (int k = 1; k < NG; k++) {
+            const float4 x = part[k][tid];
+            r.x += x.x;
+            r.y += x.y;
+            r.z += x.z;
+            r.w += x.w;
+            l += lpart[k];
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        float *o = a.out + hidx * HD + 4 * tid;  // d_out is only 4-byte aligned
+        o[0] = r.x * inv;
+        o[1] = r.y * inv;
+        o[2] = r.z * inv;
+        o[3] = r.w * inv;
+    }
 }
 
 }  // namespace
 
 // Split plan: aim for ~kTargetWG workgroups in total so all 256 CUs get several, with each
-// split a multiple of 64 positions.  n_split is non-decreasing in max_ctx.
+// split a multiple of 64 positions and at least 256 when the context allows.  n_split is
+// non-decreasing in max_ctx.
 DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx) {
     // TS_DECODE_WG overrides the workgroup target (a tuning knob; read once).
     static const int kTargetWG = [] {
@@ -444,8 +492,10 @@ DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx) {
     const int units = n_seq * n_kv;
     int want = (kTargetWG + units - 1) / units;
     if (want < 1) want = 1;
-    const int max_split_64 = (max_ctx + 63) / 64;
-    if (want > max_split_64) want = max_split_64;
+    // Every wave of a workgroup takes 64-position windows round robin: a split shorter than
+    // 4 windows leaves waves idle, so short contexts get fewer, fuller splits.
+    const int max_split = (max_ctx + 64 * TS_DECODE_NW - 1) / (64 * TS_DECODE_NW);
+    if (want > max_split) want = max_split;
     int chunk = (max_ctx + want - 1) / want;
     chunk = (chunk + 63) / 64 * 64;
     DecodePlan p;
@@ -475,16 +525,16 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     dim3 grid(plan.n_split, L.H, L.S);
     if (L.hd == 128) {
         if (softcap > 0.0f)
-            decode_split_kernel<128, true><<<grid, 256, 0, st>>>(a);
+            decode_split_kernel<128, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
         else
-            decode_split_kernel<128, false><<<grid, 256, 0, st>>>(a);
-        if (plan.n_split > 1) decode_combine_kernel<128><<<dim3(n_head, L.S), 128, 0, st>>>(a);
+            decode_split_kernel<128, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
+        if (plan.n_split > 1) decode_combine_kernel<128><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else if (L.hd == 64) {
         if (softcap > 0.0f)
-            decode_split_kernel<64, true><<<grid, 256, 0, st>>>(a);
+            decode_split_kernel<64, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
         else
-            decode_split_kernel<64, false><<<grid, 256, 0, st>>>(a);
-        if (plan.n_split > 1) decode_combine_kernel<64><<<dim3(n_head, L.S), 64, 0, st>>>(a);
+            decode_split_kernel<64, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
+        if (plan.n_split > 1) decode_combine_kernel<64><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else {
         return hipErrorInvalidValue;
     }

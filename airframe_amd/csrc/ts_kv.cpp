@@ -297,6 +297,7 @@ int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_h
     ts_attn_decode_workspace(kv, n_head, &need);
     ts::DecodePlan plan = ts::decode_plan(kv->d.n_seq, kv->d.n_head_kv, max_len + 1);
     if (plan.n_split > 1 && (!d_workspace || workspace_bytes < need)) return TS_ERR_WORKSPACE;
+    if (plan.n_split > 1 && ((uintptr_t)d_workspace & 15u)) return TS_ERR_INVALID;
     // plan.n_split <= cap(max_seq), the count the workspace was sized for.
     return hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
                                         rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,

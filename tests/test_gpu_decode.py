@@ -197,3 +197,40 @@ def test_full_size_config4_ragged_one_layer(gpu):
     lens = [int(x) for x in rng.integers(16384, 32768, size=8)]
     sample = [(0, 0), (3, 17), (7, 31)]
     _full_size(8, 8, 32, 128, lens, 500000.0, 44, sample, False)
+
+
+def test_config2_batch1_long_context_unaligned_out(gpu):
+    """Config 2's decode shape at its full context (batch 1, 24/8 heads, hd 128, 4352 keys):
+    one sequence spread over many splits, so the split merge carries the result.  The output
+    goes to a buffer offset by one float (4-byte aligned only)."""
+    say("decode cfg2 full context")
+    rng = np.random.default_rng(22)
+    p = Pair(1, 8, 128, 4353, 500000.0)
+    prefill_cache(p, rng, 4351, step=1024)
+    for _ in range(2):
+        k = synth.normal(rng, (1, 1, 8, 128))
+        v = synth.normal(rng, (1, 1, 8, 128))
+        q = synth.normal(rng, (1, 24, 128))
+        p.append(k, v)
+        buf = torch.empty(24 * 128 + 1, device="cuda")
+        out = buf[1:].view(1, 24, 128)
+        p.gpu.attn_decode(0, dev(q), p.rope, out=out)
+        ref = p.ora.attend(q[:, None], 1, threads=8)[:, 0]
+        assert_close(out.cpu().numpy(), ref, "cfg2 out")
+        p.advance(1)
+
+
+def test_misaligned_workspace_rejected(gpu):
+    say("decode misaligned workspace")
+    from airframe_amd._lib import TsError
+    p = Pair(1, 2, 64, 2048, 10000.0)
+    prefill_cache(p, np.random.default_rng(7), 1500)
+    k = synth.normal(np.random.default_rng(8), (1, 1, 2, 64))
+    p.gpu.append_quant(0, dev(k), dev(k), p.rope)
+    ws = p.gpu.workspace(8)
+    buf = torch.empty(ws.numel() + 16, dtype=torch.uint8, device="cuda")
+    q = torch.zeros((1, 8, 64), device="cuda")
+    with pytest.raises(TsError):
+        p.gpu.attn_decode(0, q, p.rope, workspace=buf[4:4 + ws.numel()])
+    p.gpu.attn_decode(0, q, p.rope, workspace=buf[16:16 + ws.numel()])
+    torch.cuda.synchronize()
