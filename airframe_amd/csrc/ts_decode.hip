@@ -116,21 +116,6 @@ __device__ __forceinline__ void load_window(Window<HD> &w, const Streams &st, in
     w.sv = st.vsb[sp];
 }
 
-// Max of v over the four lane groups g (lanes n, n+16, n+32, n+48): two permlane swaps.
-__device__ inline float group_max(float v) {
-    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-__device__ inline float group_sum(float v) {
-    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
 // Running state of one wave: O^T accumulators (column n = head, rows = dims 16td+4g+r), the
 // reference exponent m (exp2 domain) and the softmax sum l.
 template <int HD>

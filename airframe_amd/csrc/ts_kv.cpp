@@ -238,9 +238,13 @@ static int check_rope(const ts_rope *rope, int hd, int64_t max_pos_exclusive) {
     return TS_OK;
 }
 
+// The kernels move f32 rows in 16-byte pieces.
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
 int ts_append_quant(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v, int32_t n_tok,
                     const ts_rope *rope, void *stream) {
-    if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_k || !d_v || n_tok < 0)
+    if (!kv || layer < 0 || layer >= kv->d.n_layers || !aligned16(d_k) || !aligned16(d_v) || !d_k ||
+        !d_v || n_tok < 0)
         return TS_ERR_INVALID;
     int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
     if ((int64_t)max_len + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;
@@ -257,7 +261,7 @@ int ts_append_quant(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v
 int ts_requant_all(ts_kv *kv, int32_t layer, const float *d_k_cache, const float *d_v_cache,
                    int32_t seq_len, int32_t ld_pos, const ts_rope *rope, void *stream) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_k_cache || !d_v_cache || seq_len < 0 ||
-        ld_pos < seq_len)
+        ld_pos < seq_len || !aligned16(d_k_cache) || !aligned16(d_v_cache))
         return TS_ERR_INVALID;
     if (seq_len > kv->d.max_seq) return TS_ERR_OVERFLOW;
     if (rope) {
@@ -287,7 +291,7 @@ int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_h
                    const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
                    uint64_t workspace_bytes, void *stream) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_q || !d_out || !heads_ok(kv, n_head) ||
-        !(softcap >= 0.0f))
+        !(softcap >= 0.0f) || !aligned16(d_q) || !aligned16(d_out))
         return TS_ERR_INVALID;
     int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
     if (max_len + 1 > kv->d.max_seq) return TS_ERR_OVERFLOW;
@@ -297,7 +301,7 @@ int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_h
     ts_attn_decode_workspace(kv, n_head, &need);
     ts::DecodePlan plan = ts::decode_plan(kv->d.n_seq, kv->d.n_head_kv, max_len + 1);
     if (plan.n_split > 1 && (!d_workspace || workspace_bytes < need)) return TS_ERR_WORKSPACE;
-    if (plan.n_split > 1 && ((uintptr_t)d_workspace & 15u)) return TS_ERR_INVALID;
+    if (plan.n_split > 1 && !aligned16(d_workspace)) return TS_ERR_INVALID;
     // plan.n_split <= cap(max_seq), the count the workspace was sized for.
     return hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
                                         rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
@@ -308,7 +312,7 @@ int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_
                     int32_t n_tok, const ts_rope *rope, float softcap, float *d_out,
                     void *stream) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_q || !d_out || !heads_ok(kv, n_head) ||
-        n_tok < 0 || !(softcap >= 0.0f))
+        n_tok < 0 || !(softcap >= 0.0f) || !aligned16(d_q) || !aligned16(d_out))
         return TS_ERR_INVALID;
     int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
     if ((int64_t)max_len + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;

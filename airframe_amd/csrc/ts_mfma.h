@@ -62,6 +62,21 @@ __device__ inline half8 dequant8(uint32_t w, const DeqConst &k) {
     return r;
 }
 
+// Max of v over the four lane groups g (lanes n, n+16, n+32, n+48): two permlane swaps.
+__device__ inline float group_max(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ inline float group_sum(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // dims held in slot j of a dequantized word: 8u + kPerm[j]
 __device__ constexpr int kPerm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 

@@ -114,6 +114,10 @@ int ts_kv_export(const ts_kv *kv, int32_t layer, int32_t seq, int32_t pos0, int3
 
 /* ---- hot path ------------------------------------------------------------------------------ */
 
+/* Every device array these entry points read or write (k, v, q, out, workspace) must be
+ * 16-byte aligned, as hipMalloc and torch allocations are; otherwise the call returns
+ * TS_ERR_INVALID and launches nothing. */
+
 /* RoPE-fused quantize-on-append.  Replaces quantize_kv (sh_quantize_kv.wgsl:39-90, dispatched
  * at layer.rs:1092-1099) plus the RoPE step of attention.rs:196-199.
  * d_k, d_v: [n_seq][n_tok][n_head_kv][head_dim] raw f32.  Token t of sequence s is written
@@ -141,8 +145,7 @@ int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes);
  * ts_append_quant and ts_kv_increment, like CacheParams{current_pos, seq_len+1}).
  * d_out: [n_seq][n_head][head_dim] f32.  n_head must be a multiple of n_head_kv with
  * n_head/n_head_kv <= 8.  softcap > 0 applies tanh(s/softcap)*softcap to the scaled scores
- * (sh_layer_v1_int4.wgsl:1116-1118).  d_workspace: ts_attn_decode_workspace bytes, 16-byte
- * aligned (hipMalloc memory is); a misaligned workspace returns TS_ERR_INVALID. */
+ * (sh_layer_v1_int4.wgsl:1116-1118).  d_workspace: ts_attn_decode_workspace bytes. */
 int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
                    const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
                    uint64_t workspace_bytes, void *stream);

@@ -199,10 +199,9 @@ def test_full_size_config4_ragged_one_layer(gpu):
     _full_size(8, 8, 32, 128, lens, 500000.0, 44, sample, False)
 
 
-def test_config2_batch1_long_context_unaligned_out(gpu):
+def test_config2_batch1_long_context(gpu):
     """Config 2's decode shape at its full context (batch 1, 24/8 heads, hd 128, 4352 keys):
-    one sequence spread over many splits, so the split merge carries the result.  The output
-    goes to a buffer offset by one float (4-byte aligned only)."""
+    one sequence spread over many splits, so the split merge carries the result."""
     say("decode cfg2 full context")
     rng = np.random.default_rng(22)
     p = Pair(1, 8, 128, 4353, 500000.0)
@@ -212,16 +211,16 @@ def test_config2_batch1_long_context_unaligned_out(gpu):
         v = synth.normal(rng, (1, 1, 8, 128))
         q = synth.normal(rng, (1, 24, 128))
         p.append(k, v)
-        buf = torch.empty(24 * 128 + 1, device="cuda")
-        out = buf[1:].view(1, 24, 128)
-        p.gpu.attn_decode(0, dev(q), p.rope, out=out)
+        out = p.gpu.attn_decode(0, dev(q), p.rope)
         ref = p.ora.attend(q[:, None], 1, threads=8)[:, 0]
         assert_close(out.cpu().numpy(), ref, "cfg2 out")
         p.advance(1)
 
 
-def test_misaligned_workspace_rejected(gpu):
-    say("decode misaligned workspace")
+def test_misaligned_buffers_rejected(gpu):
+    """Device arrays must be 16-byte aligned: a misaligned workspace, q or out is refused
+    before anything is launched."""
+    say("decode misaligned buffers")
     from airframe_amd._lib import TsError
     p = Pair(1, 2, 64, 2048, 10000.0)
     prefill_cache(p, np.random.default_rng(7), 1500)
@@ -232,5 +231,12 @@ def test_misaligned_workspace_rejected(gpu):
     q = torch.zeros((1, 8, 64), device="cuda")
     with pytest.raises(TsError):
         p.gpu.attn_decode(0, q, p.rope, workspace=buf[4:4 + ws.numel()])
+    flat = torch.zeros(8 * 64 + 4, device="cuda")
+    with pytest.raises(TsError):
+        p.gpu.attn_decode(0, flat[1:1 + 8 * 64].view(1, 8, 64), p.rope)
+    with pytest.raises(TsError):
+        p.gpu.attn_decode(0, q, p.rope, out=flat[2:2 + 8 * 64].view(1, 8, 64))
+    with pytest.raises(TsError):
+        p.gpu.append_quant(0, flat[1:1 + 2 * 64].view(1, 1, 2, 64), dev(k), p.rope)
     p.gpu.attn_decode(0, q, p.rope, workspace=buf[16:16 + ws.numel()])
     torch.cuda.synchronize()
