@@ -36,7 +36,7 @@ SOURCES = {
     "ts_decode.hip": MFMA_VGPR,
     "ts_prefill.hip": MFMA_VGPR,
 }
-HEADERS = ["ts_internal.h", "ts_mfma.h", os.path.join("..", "..", "include", "turboshimmy.h")]
+HEADERS = ["ts_internal.h", "ts_mfma.h", "ts_quant.h", os.path.join("..", "..", "include", "turboshimmy.h")]
 
 
 def _compile(src: str, extra: list[str], objdir: str) -> str:

@@ -13,27 +13,12 @@
 // quantizes every position of the block that falls in the append range, stages the codes in
 // LDS, and writes whole words with 128-bit stores.  Owning the block means no two workgroups
 // ever write the same V word, although a word interleaves 8 positions.
-#include "ts_internal.h"
+#include "ts_quant.h"
 
 namespace ts {
 namespace {
 
 constexpr int kBlk = 32;
-
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-// Rust `f32::round() as i32` followed by +8 and clamp(1, 15); NaN maps to 0 -> code 8.
-__device__ inline uint32_t encode(float x, float scale) {
-    float r = roundf(__fdiv_rn(x, scale));
-    int q = (r != r) ? 0 : (int)fminf(fmaxf(r, -64.0f), 64.0f);
-    q += 8;
-    q = q < 1 ? 1 : (q > 15 ? 15 : q);
-    return (uint32_t)q;
-}
 
 // start: first position written for this sequence (d_start[s] if d_start, else fixed_start).
 // Source row of position p: src[((s*ld_tok) + (p - start)) * H + h][hd].
@@ -77,13 +62,8 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
                 b = kk.y;
                 c = vv.x;
                 d = vv.y;
-                if (rope && pi < rope_pairs) {
-                    float2 cs = *reinterpret_cast<const float2 *>(rope + ((size_t)p * rope_pairs + pi) * 2);
-                    float xc = __fmul_rn(a, cs.x), ys = __fmul_rn(b, cs.y);
-                    float xs = __fmul_rn(a, cs.y), yc = __fmul_rn(b, cs.x);
-                    a = __fsub_rn(xc, ys);
-                    b = __fadd_rn(xs, yc);
-                }
+                if (rope && pi < rope_pairs)
+                    rope_rotate(a, b, *reinterpret_cast<const float2 *>(rope + ((size_t)p * rope_pairs + pi) * 2));
             }
             kx[2 * j] = a;
             kx[2 * j + 1] = b;
@@ -94,8 +74,8 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
         }
         km = wave_max(km);
         vm = wave_max(vm);
-        const float ks = (km == 0.0f) ? 1.0f : __fdiv_rn(km, 7.0f);
-        const float vs = (vm == 0.0f) ? 1.0f : __fdiv_rn(vm, 7.0f);
+        const float ks = quant_scale(km);
+        const float vs = quant_scale(vm);
 #pragma unroll
         for (int j = 0; j < (PAIRS + 63) / 64; j++) {
             const int pi = lane + 64 * j;

@@ -17,9 +17,10 @@
 //   a byte is taken as 1024+16*nibble and fixed with one packed f16 FMA), so K and V enter the
 //   MFMA exactly.  The per-position scales are applied in f32 outside the MFMA: s_k on the
 //   scores, s_v folded into the probabilities.
-// * q is split hi + lo in f16 (q = hi + lo to ~22 bits) and QK^T issues two MFMAs (hi, lo)
-//   into one f32 accumulator, so scores carry f32-level accuracy; the probabilities enter PV
-//   as f16 (relative error 2^-11, well inside the output tolerance).
+// * q is split hi + lo in f16 (q = hi + lo to ~22 bits).  With G = n_head/n_kv <= 8 query
+//   heads per kv head, 2G of the 16 MFMA columns carry the hi parts of the G heads and their
+//   lo parts, so one MFMA gives both halves of every score (summed across lanes afterwards)
+//   and scores carry f32-level accuracy; the probabilities enter PV split the same way.
 // * online softmax in the exp2 domain with one cross-lane max per 64 positions and lazy
 //   rescaling; s_v is folded into the probabilities under a per-window exponent bound so they
 //   never leave f16 range.  The 4 waves merge through LDS; splits merge in a second kernel
@@ -27,6 +28,7 @@
 #include <stdlib.h>
 
 #include "ts_mfma.h"
+#include "ts_quant.h"
 
 #ifndef TS_DECODE_WAVES
 #define TS_DECODE_WAVES 2
@@ -55,6 +57,8 @@ struct DecodeArgs {
     float softcap;
     float *out;
     float *ws;  // partial o [S][n_head][n_split][hd], then m [..][n_split], l [..][n_split]
+    // Fused append (ts_attn_decode_append): the new token's raw K and V, [S][H][hd], or null.
+    const float *k_new, *v_new;
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -124,18 +128,22 @@ struct WaveState {
     float m, l;
 };
 
-// q operands in LDS: [k-step t][lane] = (hi, lo), shared by the four waves of a workgroup.
+// q operands in LDS, [k-step t][lane], shared by the waves of a workgroup.  Column n of the
+// MFMA (lane group n = lane & 15) carries the f16 high part of head n for n < G and the low
+// part (q - hi) of head n - G for G <= n < 2G, so one MFMA computes both halves of every
+// score; G <= 8 keeps 2G within the 16 columns.
 template <int HD>
 struct QLds {
-    half8 hi[HD / 32][64];
-    half8 lo[HD / 32][64];
+    half8 p[HD / 32][64];
 };
 
+// live: this lane's column carries a head (n < 2G); lo_col: it carries the low parts (G <= n);
+// partner4: byte address (for ds_bpermute) of the lane holding the other part of its scores.
 template <int HD, bool SOFTCAP, bool TAIL>
 __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD> &st,
                                                const QLds<HD> &qs, float *stage, int base, int end,
-                                               int lane, int g, bool live, float softcap,
-                                               const DeqConst &dc) {
+                                               int lane, int g, bool live, bool lo_col, int partner4,
+                                               float softcap, const DeqConst &dc) {
     constexpr int WPG = HD / 32, NTD = HD / 16;
     // Scales: one per lane in registers -> this wave's LDS stage -> the 4 positions each lane
     // holds per tile (16kt + 4g + r).  Same-wave LDS traffic is ordered: no barrier needed.
@@ -147,14 +155,20 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
     for (int kt = 0; kt < 4; kt++) sc[kt] = (floatx4)0.0f;
 #pragma unroll
     for (int t = 0; t < WPG; t++) {
-        const half8 qh = qs.hi[t][lane], ql = qs.lo[t][lane];
+        const half8 qp = qs.p[t][lane];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             const half8 ka = dequant8(w.kw[kt][t], dc);
-            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh, sc[kt], 0, 0, 0);
-            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql, sc[kt], 0, 0, 0);
+            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qp, sc[kt], 0, 0, 0);
         }
     }
+    // hi column + lo column: lanes n and n +- G swap partial scores and both hold the same sum
+    // (a + b == b + a exactly), so the two columns run identical softmax arithmetic below.
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            sc[kt][r] += __int_as_float(__builtin_amdgcn_ds_bpermute(partner4, __float_as_int(sc[kt][r])));
     // ---- softmax ----------------------------------------------------------------------------
     // x = score * log2(e).  s_v is folded into the probabilities: P = 2^(x - m) * s_v, with the
     // window reference m >= max(x) + log2(max s_v), so P <= 1 always fits f16.
@@ -211,14 +225,22 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
     }
     st.l += psum;
     // ---- O^T += V^T P^T ---------------------------------------------------------------------
+    // P = hi + lo in f16 (~22 bits, like q): the hi columns feed f16(P), the lo columns
+    // P - f16(P); a single f16 P would carry a relative error of 2^-11 straight into the output
+    // whenever one position dominates the softmax.  Columns past 2G hold finite garbage that
+    // only feeds output columns never read.
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float hi = (float)(_Float16)pv[i];
+        pv[i] = lo_col ? pv[i] - hi : pv[i];
+    }
 #pragma unroll
     for (int b = 0; b < 2; b++) {
         half8 pb;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             // slots (2r, 2r+1) = positions 4g+r of tiles 2b and 2b+1
-            // (columns past G hold finite garbage; they only feed output columns never read)
-            half2_t pr = {(_Float16)pv[4 * (2 * b) + r], (_Float16)pv[4 * (2 * b + 1) + r]};
+            const half2_t pr = {(_Float16)pv[4 * (2 * b) + r], (_Float16)pv[4 * (2 * b + 1) + r]};
             pb[2 * r] = pr[0];
             pb[2 * r + 1] = pr[1];
         }
@@ -227,6 +249,60 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
             const half8 va = dequant8(w.vw[b][td], dc);
             st.o[td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, st.o[td], 0, 0, 0);
         }
+    }
+}
+
+// Fused append, run by one wave of the workgroup whose split holds position p = len[s]: the
+// quantize-on-append of ts_append.hip for one (sequence, kv head) and one position, with the
+// same arithmetic (ts_quant.h), so codes and scales are bit-identical.  Lane i owns the
+// rotation pair (2i, 2i+1).  Writes the K row, both scales and the position's nibble of every
+// V word (read-modify-write: only this workgroup touches the block), and leaves the
+// dequantized row ((code - 8) * scale, the values the cache now holds) in kd / vd.
+template <int HD>
+__device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, float *kd, float *vd) {
+    constexpr int NTD = HD / 16, ROWB = HD / 2;
+    const KvLayerView &L = a.L;
+    const size_t row = (size_t)s * L.H + h;
+    const bool on = lane < HD / 2;
+    const int i = on ? lane : 0;
+    const size_t src = row * HD + 2 * i;
+    float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+    if (on) {
+        const float2 kk = *reinterpret_cast<const float2 *>(a.k_new + src);
+        const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
+        k0 = kk.x; k1 = kk.y; v0 = vv.x; v1 = vv.y;
+        if (i < a.rope_pairs)
+            rope_rotate(k0, k1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)p * a.rope_pairs + i) * 2));
+    }
+    const float ks = quant_scale(wave_max(fmaxf(fabsf(k0), fabsf(k1))));
+    const float vs = quant_scale(wave_max(fmaxf(fabsf(v0), fabsf(v1))));
+    const uint32_t c0 = encode(k0, ks), c1 = encode(k1, ks);
+    const uint32_t e0 = encode(v0, vs), e1 = encode(v1, vs);
+    // K row: word u holds dims 8u..8u+7 at bits 4*(d - 8u); pairs 4u..4u+3 share word u.
+    uint32_t kw = on ? (c0 | (c1 << 4)) << (8 * (i & 3)) : 0u;
+    kw |= __shfl_xor(kw, 1, 64);
+    kw |= __shfl_xor(kw, 2, 64);
+    if (on && (i & 3) == 0)
+        reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * ROWB)[i >> 2] = kw;
+    if (lane == 0) {
+        L.ks[row * L.P + p] = ks;
+        L.vs[row * L.P + p] = vs;
+    }
+    // V block p/32: dim d of key group gq sits in word (gq*16 + d%16)*NTD + d/16, position
+    // 4gq + r of tile t at nibble r + 4t.
+    const int q = p & 31, t = q >> 4, gq = (q & 15) >> 2, nib = (q & 3) + 4 * t;
+    uint32_t *vb = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / 32) + (p >> 5)) * (HD * 16));
+    if (on) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int d = 2 * i + j;
+            uint32_t *w = vb + (gq * 16 + (d & 15)) * NTD + (d >> 4);
+            *w = (*w & ~(0xFu << (4 * nib))) | ((j ? e1 : e0) << (4 * nib));
+        }
+        kd[2 * i] = (float)((int)c0 - 8) * ks;
+        kd[2 * i + 1] = (float)((int)c1 - 8) * ks;
+        vd[2 * i] = (float)((int)e0 - 8) * vs;
+        vd[2 * i + 1] = (float)((int)e1 - 8) * vs;
     }
 }
 
@@ -244,8 +320,11 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     const int n_ctx = qpos + 1;
     const int start = split * a.chunk;
     if (start >= n_ctx) return;
-    const int end = min(start + a.chunk, n_ctx);
     const int n_split_s = (n_ctx + a.chunk - 1) / a.chunk;
+    // With the fused append, this split's workgroup writes position qpos itself and adds its
+    // score from registers; the window loop then stops short of it.
+    const bool fused = a.k_new != nullptr && split == n_split_s - 1;
+    const int end = fused ? qpos : min(start + a.chunk, n_ctx);
 
     const int tid = threadIdx.x, lane = tid & 63;
     // wave index in an SGPR: window bases are then provably wave-uniform and feed the scalar
@@ -253,7 +332,10 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
     const int G = a.G;
-    const bool live = n < G;  // accumulator column n = query head h*G + n
+    // accumulator column n: high parts of head h*G + n (n < G), low parts of head
+    // h*G + n - G (G <= n < 2G), unused beyond
+    const bool live = n < 2 * G, lo_col = n >= G;
+    const int partner4 = 4 * (n < G ? lane + G : (live ? lane - G : lane));
     const DeqConst dc;
 
     // LDS: q operands, per-wave scale stages; reused for the final merge.
@@ -263,11 +345,13 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
             float stage[NW][128];
         } run;
         struct {
-            float o[NW][8 * OST];
+            float o[NW][16 * OST];
             float m[NW][8], l[NW][8];
         } merge;
     };
     __shared__ Smem sm;
+    // fused append: the new position's dequantized K and V rows and its score per head
+    __shared__ float kd[HD], vd[HD], xnew[8];
 
     const size_t row = (size_t)s * L.H + h;
     const uint8_t *kbase = L.kp + row * L.P * ROWB;
@@ -280,7 +364,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     str.v = make_rsrc(vbase, (uint32_t)((end + 31) / 32) * (HD * 16));
     str.ksb = ksb;
     str.vsb = vsb;
-    str.last = end - 1;
+    str.last = max(end - 1, 0);
 
     // First window in flight before anything else.
     Window<HD> w0, w1;
@@ -293,17 +377,30 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     // q operands: wave w builds k-step t = w (rotated, scaled by log2(e)/sqrt(hd), split hi/lo)
     // for all 64 lanes; zero in the columns past G.
     for (int t = wave; t < WPG; t += NW) {
-        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (live ? n : 0)) * HD;
+        const int head = n < G ? n : (live ? n - G : 0);
+        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + head) * HD;
         half8 qh, ql;
         load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qpos, a.inv_sqrt_hd * kLog2e, qh, ql);
-        if (!live) {
-            qh = (half8)(_Float16)0.0f;
-            ql = (half8)(_Float16)0.0f;
-        }
-        sm.run.q.hi[t][lane] = qh;
-        sm.run.q.lo[t][lane] = ql;
+        sm.run.q.p[t][lane] = !live ? (half8)(_Float16)0.0f : (lo_col ? ql : qh);
     }
+    if (fused && wave == 0) append_one<HD>(a, s, h, qpos, lane, kd, vd);
     __syncthreads();
+    if (fused) {
+        // score of the new position for head h*G + hh, from the rotated f32 q (as load_q8)
+        for (int hh = wave; hh < G; hh += NW) {
+            const int i = lane < HD / 2 ? lane : 0;
+            const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
+            float q0 = qq.x, q1 = qq.y;
+            if (i < a.rope_pairs)
+                rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qpos * a.rope_pairs + i) * 2));
+            float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+            float x = dot * a.inv_sqrt_hd;
+            if constexpr (SOFTCAP) x = tanhf(x / a.softcap) * a.softcap;
+            if (lane == 0) xnew[hh] = x * kLog2e;
+        }
+    }
 
     WaveState<HD> st;
 #pragma unroll
@@ -322,9 +419,9 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
         asm volatile("" ::: "memory");                                                         \
         __builtin_amdgcn_sched_barrier(0);                                                     \
         if (base + 64 <= end)                                                                  \
-            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
+            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, a.softcap, dc); \
         else                                                                                   \
-            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
+            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, a.softcap, dc); \
         base += SPAN;                                                                           \
         if (base >= end) break;                                                                \
     }
@@ -344,9 +441,9 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
         asm volatile("" ::: "memory");                                                         \
         __builtin_amdgcn_sched_barrier(0);                                                     \
         if (base + 64 <= end)                                                                  \
-            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
+            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, a.softcap, dc); \
         else                                                                                   \
-            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, a.softcap, dc); \
+            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, a.softcap, dc); \
         base += SPAN;                                                                           \
         if (base >= end) break;                                                                \
     }
@@ -361,7 +458,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     const float l_run = group_sum(st.l);
     __syncthreads();  // all waves are done with the q operands and stages
     if (live) {
-        if (g == 0) {
+        if (g == 0 && !lo_col) {
             sm.merge.m[wave][n] = st.m;
             sm.merge.l[wave][n] = l_run;
         }
@@ -377,12 +474,19 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
         float M = kMinit;
 #pragma unroll
         for (int w = 0; w < NW; w++) M = fmaxf(M, sm.merge.m[w][hh]);
+        if (fused) M = fmaxf(M, xnew[hh]);
         float acc = 0.0f, lsum = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
             const float e = exp2f(sm.merge.m[w][hh] - M);
-            acc += e * sm.merge.o[w][hh * OST + d];
+            acc += e * (sm.merge.o[w][hh * OST + d] + sm.merge.o[w][(hh + G) * OST + d]);
             lsum += e * sm.merge.l[w][hh];
+        }
+        if (fused) {
+            // the new position as one more partial: m = its score, l = 1, o = its V row
+            const float e = exp2f(xnew[hh] - M);
+            acc += e * vd[d];
+            lsum += e;
         }
         const size_t head = (size_t)s * a.n_head + h * G + hh;
         if (n_split_s == 1) {
@@ -492,7 +596,8 @@ DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx) {
 
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
-                         float *ws, const DecodePlan &plan, hipStream_t st) {
+                         float *ws, const DecodePlan &plan, const float *k_new,
+                         const float *v_new, hipStream_t st) {
     DecodeArgs a;
     a.L = L;
     a.len = d_len;
@@ -507,6 +612,8 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.softcap = softcap;
     a.out = out;
     a.ws = ws;
+    a.k_new = k_new;
+    a.v_new = v_new;
     dim3 grid(plan.n_split, L.H, L.S);
     if (L.hd == 128) {
         if (softcap > 0.0f)

@@ -88,7 +88,8 @@ struct DecodePlan {
 DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx);
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
-                         float *ws, const DecodePlan &plan, hipStream_t st);
+                         float *ws, const DecodePlan &plan, const float *k_new,
+                         const float *v_new, hipStream_t st);
 hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const float *q,
                           int n_head, int n_tok, const float *rope, int rope_pairs,
                           float softcap, float *out, hipStream_t st);

@@ -287,9 +287,11 @@ int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes) {
     return TS_OK;
 }
 
-int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
-                   const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
-                   uint64_t workspace_bytes, void *stream) {
+// Shared by ts_attn_decode and ts_attn_decode_append (k_new/v_new null for the former).
+static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
+                       const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
+                       uint64_t workspace_bytes, const float *k_new, const float *v_new,
+                       void *stream) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_q || !d_out || !heads_ok(kv, n_head) ||
         !(softcap >= 0.0f) || !aligned16(d_q) || !aligned16(d_out))
         return TS_ERR_INVALID;
@@ -305,7 +307,22 @@ int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_h
     // plan.n_split <= cap(max_seq), the count the workspace was sized for.
     return hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
                                         rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
-                                        plan, as_stream(stream)));
+                                        plan, k_new, v_new, as_stream(stream)));
+}
+
+int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
+                   const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
+                   uint64_t workspace_bytes, void *stream) {
+    return attn_decode(kv, layer, d_q, n_head, rope, softcap, d_out, d_workspace, workspace_bytes,
+                       nullptr, nullptr, stream);
+}
+
+int ts_attn_decode_append(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
+                          const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
+                          float *d_out, void *d_workspace, uint64_t workspace_bytes, void *stream) {
+    if (!d_k || !d_v || !aligned16(d_k) || !aligned16(d_v)) return TS_ERR_INVALID;
+    return attn_decode(kv, layer, d_q, n_head, rope, softcap, d_out, d_workspace, workspace_bytes,
+                       d_k, d_v, stream);
 }
 
 int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,

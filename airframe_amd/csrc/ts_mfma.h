@@ -2,7 +2,7 @@
 // conversion in the slot order the v_mfma_f32_16x16x32_f16 operands use, and the rotated,
 // hi/lo-split query operand.
 #pragma once
-#include "ts_internal.h"
+#include "ts_quant.h"
 
 namespace ts {
 namespace {
@@ -84,6 +84,7 @@ __device__ constexpr int kPerm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 // `mul`, split x = hi + lo into f16 and arranged in the slot order of dequant8.
 __device__ inline void load_q8(const float *rope, int rope_pairs, const float *qrow, int u,
                                int qpos, float mul, half8 &hi, half8 &lo) {
+#pragma clang fp contract(off)
     float x[8];
     const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * u);
     const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * u + 4);
@@ -94,9 +95,7 @@ __device__ inline void load_q8(const float *rope, int rope_pairs, const float *q
         const int pair = 4 * u + i;
         if (pair < rope_pairs) {
             const float2 cs = *reinterpret_cast<const float2 *>(rope + ((size_t)qpos * rope_pairs + pair) * 2);
-            const float xa = x[2 * i], xb = x[2 * i + 1];
-            x[2 * i] = __fsub_rn(__fmul_rn(xa, cs.x), __fmul_rn(xb, cs.y));
-            x[2 * i + 1] = __fadd_rn(__fmul_rn(xa, cs.y), __fmul_rn(xb, cs.x));
+            rope_rotate(x[2 * i], x[2 * i + 1], cs);
         }
     }
 #pragma unroll

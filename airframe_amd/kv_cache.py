@@ -167,6 +167,29 @@ class KVCache:
                                     ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
         return out
 
+    def attn_decode_append(self, layer: int, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
+                           rope: RopeTable, out: torch.Tensor = None, softcap: float = 0.0,
+                           workspace: torch.Tensor = None, stream=None):
+        """append_quant(layer, k, v) + attn_decode(layer, q) in one launch (the quantize_kv +
+        main_attn_out_int4 pair of run_layer_with_cache_int4).  k, v: [n_seq, 1, n_head_kv,
+        head_dim] or [n_seq, n_head_kv, head_dim]; q: [n_seq, n_head, head_dim]."""
+        n_head = q.shape[1]
+        if q.dim() != 3 or q.shape[0] != self.n_seq or q.shape[2] != self.head_dim:
+            raise ValueError("q must be [n_seq, n_head, head_dim]")
+        self._check_kv(k.reshape(self.n_seq, 1, self.n_head_kv, self.head_dim),
+                       v.reshape(self.n_seq, 1, self.n_head_kv, self.head_dim), 1)
+        if out is None:
+            out = torch.empty_like(q)
+        ws = workspace if workspace is not None else self.workspace(n_head)
+        check("ts_attn_decode_append",
+              load().ts_attn_decode_append(self._h, layer, _ptr(k, torch.float32, "k"),
+                                           _ptr(v, torch.float32, "v"), _ptr(q, torch.float32, "q"),
+                                           n_head, rope.handle, softcap,
+                                           _ptr(out, torch.float32, "out"),
+                                           ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                           _stream(stream)))
+        return out
+
     def attn_prefill(self, layer: int, q: torch.Tensor, rope: RopeTable, out: torch.Tensor = None,
                      softcap: float = 0.0, stream=None):
         """Chunked-prefill causal attention.  q: [n_seq, n_tok, n_head, head_dim]."""

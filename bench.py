@@ -4,8 +4,9 @@ Default workload (the headline): Qwen3-8B attention shape, 36
 32 query / 8 kv heads, head_dim 128, batch 32, each sequence with 8192 cached INT4 tokens,
 seeded f32 N(0,1) Q/K/V with x8 outlier channels on 2% of dims, RoPE theta 1e6.  A step is one
 decode token for all 32 sequences: per layer, RoPE-fused quantize-on-append of the new K/V
-(ts_append_quant) and split-K GQA attention over the INT4 cache (ts_attn_decode); then the
-lengths advance (ts_kv_increment).  All inputs are generated on the device before timing.
+and split-K GQA attention over the INT4 cache in one launch (ts_attn_decode_append; with
+--separate, ts_append_quant then ts_attn_decode); then the lengths advance (ts_kv_increment).
+All inputs are generated on the device before timing.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 
@@ -149,10 +150,15 @@ def run_decode(args, cfg):
 
     def step(i, events=None):
         for layer in range(L):
-            kv.append_quant(layer, ks[i][layer], vs[i][layer], rope)
+            if args.separate:
+                kv.append_quant(layer, ks[i][layer], vs[i][layer], rope)
             if events is not None:
                 events[layer][0].record()
-            kv.attn_decode(layer, qs[i][layer], rope, out=out, workspace=ws)
+            if args.separate:
+                kv.attn_decode(layer, qs[i][layer], rope, out=out, workspace=ws)
+            else:  # quantize_kv + main_attn_out_int4 in one launch
+                kv.attn_decode_append(layer, ks[i][layer], vs[i][layer], qs[i][layer], rope,
+                                      out=out, workspace=ws)
             if events is not None:
                 events[layer][1].record()
         kv.increment(1)
@@ -216,7 +222,8 @@ def run_decode(args, cfg):
     for i in range(steps):
         ctx = [l + i + 1 for l in lens0]
         b = attn_bytes(ctx, n_kv, n_head, hd, B)
-        kern_bytes.append(b)
+        # the timed launch also does the append unless the two calls are separate
+        kern_bytes.append(b if args.separate else b + append_bytes(B, n_kv, hd))
         step_bytes += L * (b + append_bytes(B, n_kv, hd))
     step_bytes /= steps
     result = dict(total_ms=total_ms, ms_step=ms_step, step_bytes=step_bytes)
@@ -298,6 +305,8 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--separate", action="store_true",
+                    help="decode: ts_append_quant + ts_attn_decode instead of the fused launch")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 1 GiB device copy (4 launches) so rocprofv3 HBM counters "
                          "can be scaled by what they read for a copy of known size")
@@ -366,10 +375,11 @@ def main():
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "traffic_source": f"profiles/decode_cfg{args.config}.md" if traffic else None,
-                "kernel": "decode_split_kernel<128>+decode_combine_kernel (ts_attn_decode)",
+                "kernel": ("decode_split_kernel<128>+decode_combine_kernel (ts_attn_decode)" if args.separate
+                           else "decode_split_kernel<128> with fused append + decode_combine_kernel (ts_attn_decode_append)"),
                 "bytes_per_launch": int(r["kernel_bytes"]),
                 "avg_launch_us": round(r["kernel_ms"] * 1e3, 2),
-                "timing": "HIP events around each ts_attn_decode launch, eager pass of 16 steps"}
+                "timing": "HIP events around each decode launch, eager pass of 16 steps"}
     cpu_line = None
     if cpu:
         cpu_gbs = r["step_bytes"] / cpu["step_s_mt"] / 1e9

@@ -150,6 +150,16 @@ int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_h
                    const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
                    uint64_t workspace_bytes, void *stream);
 
+/* ts_append_quant(kv, layer, d_k, d_v, 1, rope) followed by ts_attn_decode(...), in one launch:
+ * the quantize_kv + main_attn_out_int4 pair that run_layer_with_cache_int4 dispatches back to
+ * back for every decode token (layer.rs:1092-1107).  Writes the same codes and scales as
+ * ts_append_quant; the new position's score is taken from its dequantized row directly.
+ * d_k, d_v: [n_seq][n_head_kv][head_dim] raw f32; other arguments as ts_attn_decode.
+ * Lengths do not change. */
+int ts_attn_decode_append(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
+                          const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
+                          float *d_out, void *d_workspace, uint64_t workspace_bytes, void *stream);
+
 /* Chunked-prefill attention over the INT4 cache.  Stands in for the f32 main_attn_out of
  * batched prefill (sh_layer_v1.wgsl:662-762, inference.rs:1160-1166) with the INT4 cache as
  * its source.  d_q: [n_seq][n_tok][n_head][head_dim] raw f32 for the n_tok tokens just
