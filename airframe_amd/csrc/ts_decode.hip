@@ -143,11 +143,11 @@ template <int HD, bool SOFTCAP, bool TAIL>
 __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD> &st,
                                                const QLds<HD> &qs, float *stage, int base, int end,
                                                int lane, int g, bool live, bool lo_col, int partner4,
-                                               float softcap, const DeqConst &dc) {
+                                               float inv_s, float softcap, const DeqConst &dc) {
     constexpr int WPG = HD / 32, NTD = HD / 16;
     // Scales: one per lane in registers -> this wave's LDS stage -> the 4 positions each lane
     // holds per tile (16kt + 4g + r).  Same-wave LDS traffic is ordered: no barrier needed.
-    stage[lane] = w.sk;
+    stage[lane] = w.sk * inv_s;  // undo the q operand scale (a power of two: exact)
     stage[64 + lane] = w.sv;
     // ---- S^T = K Q^T (rows: positions, columns: heads), hi + lo q in one accumulator --------
     floatx4 sc[4];
@@ -221,7 +221,7 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
     for (int i = 0; i < 16; i++) {
         const float p = fast_exp2(x[i] - st.m);
         psum += p;
-        pv[i] = p * sv[i];
+        pv[i] = opaque(p * sv[i]);  // hi and lo columns must split the same f32 value
     }
     st.l += psum;
     // ---- O^T += V^T P^T ---------------------------------------------------------------------
@@ -376,11 +376,18 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
 
     // q operands: wave w builds k-step t = w (rotated, scaled by log2(e)/sqrt(hd), split hi/lo)
     // for all 64 lanes; zero in the columns past G.
+    // One power-of-two scale for the G heads: every wave reads the bound of all of them.
+    const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (n < G ? n : (live ? n - G : 0))) * HD;
+    float q_s, inv_s;
+    {
+        float qb = 0.0f;
+#pragma unroll
+        for (int t = 0; t < WPG; t++) qb = fmaxf(qb, q_bound8(qrow, WPG * g + t));
+        q_scale(wave_max(qb) * (a.inv_sqrt_hd * kLog2e), q_s, inv_s);
+    }
     for (int t = wave; t < WPG; t += NW) {
-        const int head = n < G ? n : (live ? n - G : 0);
-        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + head) * HD;
         half8 qh, ql;
-        load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qpos, a.inv_sqrt_hd * kLog2e, qh, ql);
+        load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qpos, a.inv_sqrt_hd * kLog2e * q_s, qh, ql);
         sm.run.q.p[t][lane] = !live ? (half8)(_Float16)0.0f : (lo_col ? ql : qh);
     }
     if (fused && wave == 0) append_one<HD>(a, s, h, qpos, lane, kd, vd);
@@ -419,9 +426,9 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
         asm volatile("" ::: "memory");                                                         \
         __builtin_amdgcn_sched_barrier(0);                                                     \
         if (base + 64 <= end)                                                                  \
-            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, a.softcap, dc); \
+            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
         else                                                                                   \
-            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, a.softcap, dc); \
+            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
         base += SPAN;                                                                           \
         if (base >= end) break;                                                                \
     }
@@ -441,9 +448,9 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
         asm volatile("" ::: "memory");                                                         \
         __builtin_amdgcn_sched_barrier(0);                                                     \
         if (base + 64 <= end)                                                                  \
-            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, a.softcap, dc); \
+            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
         else                                                                                   \
-            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, a.softcap, dc); \
+            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
         base += SPAN;                                                                           \
         if (base >= end) break;                                                                \
     }

@@ -80,6 +80,38 @@ __device__ inline float group_sum(float v) {
 // dims held in slot j of a dequantized word: 8u + kPerm[j]
 __device__ constexpr int kPerm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 
+// x as an opaque f32 register value.  Splitting v = a*b into hi = f16(v), lo = f16(v - hi)
+// needs both halves taken from the same rounded v: left visible, the compiler may turn one use
+// of f16(a*b) into a fused multiply-convert (one rounding of the exact product) and the other
+// into a convert of the f32 product (two roundings), and the halves then disagree by an f16
+// ulp.  The empty asm pins v.  (Its result only feeds VALU conversions, never an MFMA.)
+__device__ inline float opaque(float x) {
+    asm("" : "+v"(x));
+    return x;
+}
+
+// Bound on |rotated q| over the 8 dims 8u..8u+7 of one head: |a cos - b sin| <= |a| + |b|.
+__device__ inline float q_bound8(const float *qrow, int u) {
+    const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * u);
+    const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * u + 4);
+    return fmaxf(fmaxf(fabsf(x0.x) + fabsf(x0.y), fabsf(x0.z) + fabsf(x0.w)),
+                 fmaxf(fabsf(x1.x) + fabsf(x1.y), fabsf(x1.z) + fabsf(x1.w)));
+}
+
+// Power-of-two scale S for q operands bounded by m: m*S lands in [2^13, 2^14), so both halves
+// of the hi/lo split stay normal f16 numbers (the matrix cores flush f16 subnormals, which
+// would drop the low half of every small element).  Scores come out times S; callers fold
+// inv_s = 1/S into the per-key scale.
+__device__ inline void q_scale(float m, float &s, float &inv_s) {
+    if (!(m > 0.0f) || !(m < 3.0e38f)) {
+        s = inv_s = 1.0f;
+        return;
+    }
+    const int e = min(max(ilogbf(m), -100), 100);
+    s = ldexpf(1.0f, 13 - e);
+    inv_s = ldexpf(1.0f, e - 13);
+}
+
 // Rotated q for the 8 dims 8u..8u+7 of one head (rope.rs:186-196, table row qpos), times
 // `mul`, split x = hi + lo into f16 and arranged in the slot order of dequant8.
 __device__ inline void load_q8(const float *rope, int rope_pairs, const float *qrow, int u,
@@ -100,7 +132,7 @@ __device__ inline void load_q8(const float *rope, int rope_pairs, const float *q
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        const float v = x[kPerm[j]] * mul;
+        const float v = opaque(x[kPerm[j]] * mul);
         const _Float16 h = (_Float16)v;
         hi[j] = h;
         lo[j] = (_Float16)(v - (float)h);

@@ -16,8 +16,8 @@
 // * S^T = K Q^T with q split hi + lo (two f16 MFMAs into one f32 accumulator) and
 //   1/sqrt(hd)*log2(e) folded into q; the score is scaled by s_k in f32, masked only in
 //   windows that cross the causal diagonal, and enters an online softmax in the exp2 domain
-//   whose running max is raised lazily; p*s_v goes to O^T += V^T P^T in f16 under an exponent
-//   bound that keeps it below 2^15.
+//   whose running max is raised lazily; p*s_v goes to O^T += V^T P^T split hi + lo in f16
+//   (two MFMAs) under an exponent bound that keeps it below 2^15.
 // * Each wave owns whole output rows, so the result is written straight from registers.
 #include "ts_mfma.h"
 
@@ -135,7 +135,7 @@ __device__ inline void fetch_window(Pending<HD, NW> &pd, const uint8_t *kbase, c
 
 template <int HD, int NW>
 __device__ inline void stage_window(PrefillLds<HD> &sm, int buf, const Pending<HD, NW> &pd, int tid,
-                                    int wave, const DeqConst &dc) {
+                                    int wave, float inv_s, const DeqConst &dc) {
     using P = Pending<HD, NW>;
     constexpr int NTD = HD / 16;
     auto put_k = [&](int c, const uint4 &x) {
@@ -170,7 +170,7 @@ __device__ inline void stage_window(PrefillLds<HD> &sm, int buf, const Pending<H
         for (int i = 0; i < P::NK; i++) put_v(tid + P::NT * i, pd.v[i]);
     }
     if (tid < kWin) {
-        sm.sk[buf][tid] = pd.scale;
+        sm.sk[buf][tid] = pd.scale * inv_s;  // undo the q operand scale (a power of two: exact)
     } else if (tid < 2 * kWin) {
         sm.sv[buf][tid - kWin] = pd.scale;
         float m = pd.scale;
@@ -187,7 +187,7 @@ template <int NTD, bool SOFTCAP>
 __device__ inline void window_softmax(floatx4 (&sc)[4], const float *sk, const float *sv, float svl,
                                       float softcap, bool mask, int base, int g, int qpos,
                                       float &m_run, float &l_run, floatx4 (&o)[NTD],
-                                      half8 (&pb)[2]) {
+                                      half8 (&pb)[2], half8 (&pl)[2]) {
     // sk, sv: the window's scales in LDS; this lane's keys are 16kt + 4g + r.
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
@@ -233,7 +233,12 @@ __device__ inline void window_softmax(floatx4 (&sc)[4], const float *sk, const f
         for (int r = 0; r < 4; r++) {
             const float p = __builtin_amdgcn_exp2f(sc[kt][r] - m_run);
             psum += p;
-            pb[kt >> 1][2 * r + (kt & 1)] = (_Float16)(p * sv4[r]);
+            // p * s_v = hi + lo in f16 (~22 bits): one f16 would carry a relative error of 2^-11
+            // into the output whenever a few keys dominate the row
+            const float pv = opaque(p * sv4[r]);
+            const _Float16 hi = (_Float16)pv;
+            pb[kt >> 1][2 * r + (kt & 1)] = hi;
+            pl[kt >> 1][2 * r + (kt & 1)] = (_Float16)(pv - (float)hi);
         }
     }
     l_run += psum;
@@ -271,6 +276,7 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     const int len0 = a.len[s];
     const DeqConst dc;
     __shared__ PrefillLds<HD> sm;
+    __shared__ float sm_qb[NW];
 
     const size_t row = (size_t)s * L.H + h;
     const uint8_t *kbase = L.kp + row * L.P * ROWB;
@@ -287,6 +293,24 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
 
         // Per column tile: this lane's column, its query position and q operands (rotated,
         // times 1/sqrt(hd) and, without softcap, log2(e); split hi/lo).
+        // One power-of-two q scale per workgroup, from a bound over all its columns.
+        float q_s, inv_s;
+        {
+            float qb = 0.0f;
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                const int c = min(c_wave + 16 * nt + n, n_cols - 1);
+                const float *qrow = a.q + (((size_t)s * a.n_tok + c / G) * a.n_head + h * G + c % G) * HD;
+#pragma unroll
+                for (int t = 0; t < WPG; t++) qb = fmaxf(qb, q_bound8(qrow, WPG * g + t));
+            }
+            qb = wave_max(qb);
+            if (lane == 0) sm_qb[wave] = qb;
+            __syncthreads();
+#pragma unroll
+            for (int w = 0; w < NW; w++) qb = fmaxf(qb, sm_qb[w]);
+            q_scale(qb * qmul, q_s, inv_s);
+        }
         half8 qh[2][WPG], ql[2][WPG];
         int qpos[2];
 #pragma unroll
@@ -299,7 +323,7 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
             const float *qrow = a.q + (((size_t)s * a.n_tok + tok) * a.n_head + head) * HD;
 #pragma unroll
             for (int t = 0; t < WPG; t++) {
-                load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, len0 + tok, qmul, qh[nt][t], ql[nt][t]);
+                load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, len0 + tok, qmul * q_s, qh[nt][t], ql[nt][t]);
                 if (!live) {
                     qh[nt][t] = (half8)(_Float16)0.0f;
                     ql[nt][t] = (half8)(_Float16)0.0f;
@@ -321,7 +345,7 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
 
         Pending<HD, NW> pd;
         fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, 0, tid, wave);
-        stage_window<HD, NW>(sm, 0, pd, tid, wave, dc);
+        stage_window<HD, NW>(sm, 0, pd, tid, wave, inv_s, dc);
         __syncthreads();
 
         for (int w = 0; w < n_win; w++) {
@@ -351,24 +375,26 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
                     }
                 }
                 const float svl = sm.svlog[buf];
-                half8 pb[2][2];  // [nt][32-key half]
+                half8 pb[2][2], pl[2][2];  // [nt][32-key half]: p*s_v high and low f16 parts
                 const bool mask = base + kWin - 1 > qmin_w;  // some key of the window is masked
 #pragma unroll
                 for (int nt = 0; nt < 2; nt++)
                     window_softmax<NTD, SOFTCAP>(sc[nt], sm.sk[buf], sm.sv[buf], svl, a.softcap, mask, base,
-                                                 g, qpos[nt], m_run[nt], l_run[nt], o[nt], pb[nt]);
+                                                 g, qpos[nt], m_run[nt], l_run[nt], o[nt], pb[nt], pl[nt]);
 #pragma unroll
                 for (int b = 0; b < 2; b++) {
 #pragma unroll
                     for (int td = 0; td < NTD; td++) {
                         const half8 va = sm.v[buf][16 * td + n][v_slot(n, 4 * b + g)];
 #pragma unroll
-                        for (int nt = 0; nt < 2; nt++)
+                        for (int nt = 0; nt < 2; nt++) {
                             o[nt][td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[nt][b], o[nt][td], 0, 0, 0);
+                            o[nt][td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[nt][b], o[nt][td], 0, 0, 0);
+                        }
                     }
                 }
             }
-            if (more) stage_window<HD, NW>(sm, buf ^ 1, pd, tid, wave, dc);
+            if (more) stage_window<HD, NW>(sm, buf ^ 1, pd, tid, wave, inv_s, dc);
             __syncthreads();
         }
 

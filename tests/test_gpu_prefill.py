@@ -77,3 +77,17 @@ def test_full_size_config5(gpu):
     run_chunks(p, rng, 32, [512] * 4, check_heads=[(0, 0), (1, 9), (2, 22), (3, 31)])
     p.check_codes()
     torch.cuda.synchronize()
+
+
+def test_outlier_channels(gpu):
+    """x8 outlier channels on 2% of dims in q, k and v (the shape of config 3's data): peaked
+    softmax rows and large V values, where the precision of P matters."""
+    say("prefill outliers")
+    rng = np.random.default_rng(53)
+    n_kv, n_head, hd = 8, 32, 128
+    dims = synth.outlier_dims(n_kv, hd, 7)
+    skv = synth.channel_scale(n_kv, n_kv, hd, dims)
+    sq = synth.channel_scale(n_head, n_kv, hd, dims)
+    p = Pair(2, n_kv, hd, 700, 1e6)
+    run_chunks(p, rng, n_head, [256, 300, 100], skv[None, None], sq[None, None])
+    p.check_codes()
