@@ -8,16 +8,20 @@
 //
 // * The (query token, head) pairs that share one kv head form the columns of the MFMA
 //   N dimension: column c of a (sequence, kv head) is token c / G, head c % G.
-// * grid = (column block of 128, kv head, sequence); each of the 4 waves owns 32 columns
-//   (two 16-column tiles).  The workgroup walks the keys in 64-key windows: every thread
-//   loads one 16-byte piece of the next window's K rows / V blocks / scales while the current
-//   window is computed, then converts it to exact f16 integer codes in a double-buffered LDS
-//   tile, so each code is converted once per workgroup and read by all 4 waves.
+// * grid = (column block of 128, kv head, sequence); each of the 4 waves owns 32 columns,
+//   one N tile of v_mfma_f32_32x32x16_f16 (the shape that reaches the matrix cores' rate;
+//   16x16x32 tops out near 60% of it).  The workgroup walks the keys in 64-key windows:
+//   every thread loads one 16-byte piece of the next window's K rows / V blocks / scales
+//   while the current window is computed, then converts it to exact f16 integer codes in a
+//   double-buffered LDS tile, so each code is converted once per workgroup and read by all
+//   4 waves.
 // * S^T = K Q^T with q split hi + lo (two f16 MFMAs into one f32 accumulator) and
-//   1/sqrt(hd)*log2(e) folded into q; the score is scaled by s_k in f32, masked only in
-//   windows that cross the causal diagonal, and enters an online softmax in the exp2 domain
-//   whose running max is raised lazily; p*s_v goes to O^T += V^T P^T split hi + lo in f16
-//   (two MFMAs) under an exponent bound that keeps it below 2^15.
+//   1/sqrt(hd)*log2(e) and a power-of-two range scale folded into q.  K rows enter the MFMA in
+//   the order that leaves every lane holding, per 16-key step, exactly the 8 keys it supplies
+//   to the PV operand, so P never moves between lanes.  The score is scaled by s_k in f32,
+//   masked only in windows that cross the causal diagonal, and enters an online softmax in
+//   the exp2 domain whose running max is raised lazily; p*s_v goes to O^T += V^T P^T split
+//   hi + lo in f16 (two MFMAs) under an exponent bound that keeps it below 2^15.
 // * Each wave owns whole output rows, so the result is written straight from registers.
 #include "ts_mfma.h"
 
@@ -45,10 +49,10 @@ struct PrefillArgs {
 constexpr int kColsPerWave = 32;
 constexpr int kWin = 64;  // keys per window
 
-// Double-buffered window tiles.  K: [key][word] f16 codes; V^T: [dim][8-key group] f16 codes
-// in the PV operand's key order.  Rows are unpadded; the 16-byte slots inside a row are
-// rotated per row (k_slot, v_slot) so that the MFMA operand reads of a wave hit distinct LDS
-// banks (measured on gfx950: 2x the read rate of padded rows).
+// Double-buffered window tiles.  K: [key][word] f16 codes; V^T: [dim][8-key group] f16
+// codes, each group in the PV operand's key order.  Rows are unpadded; the 16-byte slots
+// inside a row are rotated per row (k_slot, v_slot) so that the MFMA operand reads of a wave
+// hit distinct LDS banks (chosen by measurement on gfx950: 2x the rate of unrotated rows).
 template <int HD>
 struct PrefillLds {
     half8 k[2][kWin][HD / 8];
@@ -71,16 +75,19 @@ struct Pending {
     float scale;
 };
 
-// Slot of word w in the K row of `key`, and of 8-key group cg in the V^T row `row`.
+// Slot of word w in the K row of `key`, and of 8-key group sl in the V^T row `row`.
 template <int HD>
-__device__ inline int k_slot(int key, int w) {
-    const int k = key & 15;
-    if constexpr (HD == 128)
-        return (w + k + 4 * (k >> 2)) & 15;
-    else
-        return ((w >> 1) + 4 * (w & 1) + k) & 7;
+__device__ inline int k_slot(int key, int w) { return (w + key) & (HD / 8 - 1); }
+__device__ inline int v_slot(int row, int sl) { return (sl + (row >> 1)) & 7; }
+
+// Key (within a 32-key tile) that accumulator row R of the QK MFMA stands for.  Lane half h
+// holds rows 8q + 4h + r (q, r = 0..3); mapping them to keys 16(q/2) + 8h + 4(q%2) + r gives
+// each lane half the 8 consecutive keys 16s + 8h .. +7 of 16-key step s, which is what the PV
+// MFMA's B operand wants from it.
+__device__ inline int qk_row_key(int R) {
+    const int q = R >> 3, h = (R >> 2) & 1, r = R & 3;
+    return 16 * (q >> 1) + 8 * h + 4 * (q & 1) + r;
 }
-__device__ inline int v_slot(int row, int cg) { return (cg + row) & 7; }
 
 // Which 16-byte piece of the window a staging thread owns.  The maps are chosen so that 16
 // consecutive lanes write 16 different LDS bank groups:
@@ -145,17 +152,25 @@ __device__ inline void stage_window(PrefillLds<HD> &sm, int buf, const Pending<H
 #pragma unroll
         for (int j = 0; j < 4; j++) sm.k[buf][key][k_slot<HD>(key, 4 * part + j)] = dequant8(w[j], dc);
     };
+    // V: lane L holds 4 words of packed lane group ln = L (key group g = ln/16, dim row dl =
+    // ln%16); lane L^16 holds the same words of key group g^1.  Words of groups 2p and 2p+1
+    // hold keys 8p..8p+7 in their low halves (nibbles 0-3) and 16+8p..16+8p+7 in their high
+    // halves, so the even lane builds the dword of low halves, the odd lane the one of high
+    // halves: one 8-key group of the V^T row each.
     auto put_v = [&](int c, const uint4 &x) {
         const uint32_t w[4] = {x.x, x.y, x.z, x.w};
         int b, piece;
         v_piece<HD>(c, b, piece);
+        const int ln = c % 64, dl = ln & 15, odd = (ln >> 4) & 1, pair = ln >> 5;
+        const int td0 = (c % HD) / 64 * 4;
+        const int sl = 4 * b + 2 * odd + pair;
+        const int src = 4 * (threadIdx.x ^ 16);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            // word (gg*16 + dl)*NTD + td of the block holds dim 16td+dl, key group gg
-            const int widx = 4 * piece + j;
-            const int ln = widx / NTD, td = widx % NTD;
-            const int row = 16 * td + (ln & 15);
-            sm.v[buf][row][v_slot(row, 4 * b + (ln >> 4))] = dequant8(w[j], dc);
+            const uint32_t pw = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)w[j]);
+            const uint32_t d = odd ? (pw >> 16) | (w[j] & 0xFFFF0000u) : (w[j] & 0xFFFFu) | (pw << 16);
+            const int row = 16 * (td0 + j) + dl;
+            sm.v[buf][row][v_slot(row, sl)] = dequant8(d, dc);
         }
     };
     if constexpr (P::SPLIT) {
@@ -180,40 +195,55 @@ __device__ inline void stage_window(PrefillLds<HD> &sm, int buf, const Pending<H
     }
 }
 
-// Scores of one 64-key window for one 16-column tile -> f16 probabilities (times s_v) in PV
-// operand order, with the online-softmax state update.  MASK: the window crosses the causal
-// diagonal of some column.
-template <int NTD, bool SOFTCAP>
-__device__ inline void window_softmax(floatx4 (&sc)[4], const float *sk, const float *sv, float svl,
-                                      float softcap, bool mask, int base, int g, int qpos,
-                                      float &m_run, float &l_run, floatx4 (&o)[NTD],
-                                      half8 (&pb)[2], half8 (&pl)[2]) {
-    // sk, sv: the window's scales in LDS; this lane's keys are 16kt + 4g + r.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Max / sum over the two lane halves (lanes l and l^32) that hold one column.
+__device__ inline float half_max(float v) {
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float half_sum(float v) {
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Scores of one 64-key window for this lane's column, in place (sc[kb][4q + r] is key
+// 32kb + qk_row_key(8q + 4h + r)): times s_k, softcap, causal mask, then the online-softmax
+// state update.  Leaves sc - m_run ready for exp2.
+template <int NDB, bool SOFTCAP>
+__device__ inline void window_scores(floatx16 (&sc)[2], const float *sk, float svl, float softcap,
+                                     bool mask, int base, int h, int qpos, float &m_run,
+                                     float &l_run, floatx16 (&o)[NDB]) {
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++) {
-        const floatx4 sk4 = *reinterpret_cast<const floatx4 *>(sk + 16 * kt + 4 * g);
+    for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float x = sc[kt][r] * sk4[r];
-            if (SOFTCAP) x = tanhf(x / softcap) * softcap * kLog2e;
-            sc[kt][r] = x;
+        for (int q = 0; q < 4; q++) {
+            const floatx4 sk4 = *reinterpret_cast<const floatx4 *>(sk + 32 * kb + 16 * (q >> 1) + 8 * h + 4 * (q & 1));
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float x = sc[kb][4 * q + r] * sk4[r];
+                if (SOFTCAP) x = tanhf(x / softcap) * softcap * kLog2e;
+                sc[kb][4 * q + r] = x;
+            }
         }
     }
     if (mask) {
         // a real branch: only windows on the causal diagonal pay for the compares
         asm volatile("");
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
+        for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                if (base + 16 * kt + 4 * g + r > qpos) sc[kt][r] = -INFINITY;
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (base + 32 * kb + 16 * (q >> 1) + 8 * h + 4 * (q & 1) + r > qpos) sc[kb][4 * q + r] = -INFINITY;
     }
     float mloc = kMinit;
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++)
+    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) mloc = fmaxf(mloc, sc[kt][r]);
-    mloc = group_max(mloc);
+        for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, sc[kb][i]);
+    mloc = half_max(mloc);
     // Keep p <= 2^8 and p*s_v <= 2^15 (f16 range); raise the running max only when the window
     // breaks either bound.
     const float need = fmaxf(mloc - 8.0f, mloc + svl - 15.0f);
@@ -223,32 +253,39 @@ __device__ inline void window_softmax(floatx4 (&sc)[4], const float *sk, const f
         m_run = m_new;
         l_run *= alpha;
 #pragma unroll
-        for (int td = 0; td < NTD; td++) o[td] *= alpha;
+        for (int db = 0; db < NDB; db++) o[db] *= alpha;
     }
-    float psum = 0.0f;
+}
+
+// Probabilities of 16-key step st (keys 16st + 8h + 0..7 of the window) times s_v, split
+// hi + lo in f16 in the PV operand's slot order; adds the p to l_run.  p*s_v = hi + lo keeps
+// ~22 bits: one f16 would carry a relative error of 2^-11 into the output whenever a few
+// keys dominate the row.
+__device__ inline void step_probs(const floatx16 (&sc)[2], const float *sv, int st, int h,
+                                  float m_run, float &l_run, half8 &pb, half8 &pl) {
+    const int kb = st >> 1;
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++) {
-        const floatx4 sv4 = *reinterpret_cast<const floatx4 *>(sv + 16 * kt + 4 * g);
+    for (int qq = 0; qq < 2; qq++) {
+        const int q = 2 * (st & 1) + qq;
+        const floatx4 sv4 = *reinterpret_cast<const floatx4 *>(sv + 32 * kb + 16 * (q >> 1) + 8 * h + 4 * (q & 1));
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float p = __builtin_amdgcn_exp2f(sc[kt][r] - m_run);
-            psum += p;
-            // p * s_v = hi + lo in f16 (~22 bits): one f16 would carry a relative error of 2^-11
-            // into the output whenever a few keys dominate the row
+            const float p = __builtin_amdgcn_exp2f(sc[kb][4 * q + r] - m_run);
+            l_run += p;
             const float pv = opaque(p * sv4[r]);
             const _Float16 hi = (_Float16)pv;
-            pb[kt >> 1][2 * r + (kt & 1)] = hi;
-            pl[kt >> 1][2 * r + (kt & 1)] = (_Float16)(pv - (float)hi);
+            // key 16st + 8h + 4(q&1) + r: slot 2r + (q&1)
+            pb[2 * r + (q & 1)] = hi;
+            pl[2 * r + (q & 1)] = (_Float16)(pv - (float)hi);
         }
     }
-    l_run += psum;
 }
 
 template <int HD, bool SOFTCAP>
 __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillArgs a) {
     constexpr int NW = TS_PREFILL_NW;
-    constexpr int WPG = HD / 32;
-    constexpr int NTD = HD / 16;
+    constexpr int NKS = HD / 16;   // MFMA k-steps over the head dim
+    constexpr int NDB = HD / 32;   // 32-dim output tiles
     constexpr int ROWB = HD / 2;
     constexpr int COLS = NW * kColsPerWave;  // columns per block
     const KvLayerView &L = a.L;
@@ -272,7 +309,7 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     const int n_blk = (n_cols + COLS - 1) / COLS;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n = lane & 15, g = lane >> 4;
+    const int j = lane & 31, hf = lane >> 5;  // MFMA column / lane half
     const int len0 = a.len[s];
     const DeqConst dc;
     __shared__ PrefillLds<HD> sm;
@@ -284,135 +321,113 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     const float *ksb = L.ks + row * L.P;
     const float *vsb = L.vs + row * L.P;
     const float qmul = SOFTCAP ? a.inv_sqrt_hd : a.inv_sqrt_hd * kLog2e;
+    const int krow = qk_row_key(j);  // K row this lane feeds to the QK MFMA (within 32 keys)
 
     // Heavier column blocks (later tokens) first.
+    const int cblk = n_blk - 1 - xb;
+    const int c_blk = cblk * COLS;
+    const int c_wave = c_blk + wave * kColsPerWave;
+    const int c = c_wave + j;
+    const bool live = c < n_cols;
+    const int cc = live ? c : n_cols - 1;
+    const int tok = cc / G;
+    const float *qrow = a.q + (((size_t)s * a.n_tok + tok) * a.n_head + h * G + cc % G) * HD;
+    const int qpos = live ? len0 + tok : -1;
+
+    // One power-of-two q scale per workgroup, from a bound over all its columns.
+    float q_s, inv_s;
     {
-        const int cblk = n_blk - 1 - xb;
-        const int c_blk = cblk * COLS;
-        const int c_wave = c_blk + wave * kColsPerWave;
-
-        // Per column tile: this lane's column, its query position and q operands (rotated,
-        // times 1/sqrt(hd) and, without softcap, log2(e); split hi/lo).
-        // One power-of-two q scale per workgroup, from a bound over all its columns.
-        float q_s, inv_s;
-        {
-            float qb = 0.0f;
+        float qb = 0.0f;
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                const int c = min(c_wave + 16 * nt + n, n_cols - 1);
-                const float *qrow = a.q + (((size_t)s * a.n_tok + c / G) * a.n_head + h * G + c % G) * HD;
-#pragma unroll
-                for (int t = 0; t < WPG; t++) qb = fmaxf(qb, q_bound8(qrow, WPG * g + t));
-            }
-            qb = wave_max(qb);
-            if (lane == 0) sm_qb[wave] = qb;
-            __syncthreads();
-#pragma unroll
-            for (int w = 0; w < NW; w++) qb = fmaxf(qb, sm_qb[w]);
-            q_scale(qb * qmul, q_s, inv_s);
-        }
-        half8 qh[2][WPG], ql[2][WPG];
-        int qpos[2];
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const int c = c_wave + 16 * nt + n;
-            const bool live = c < n_cols;
-            const int cc = live ? c : 0;
-            const int tok = cc / G, head = h * G + cc % G;
-            qpos[nt] = live ? len0 + tok : -1;
-            const float *qrow = a.q + (((size_t)s * a.n_tok + tok) * a.n_head + head) * HD;
-#pragma unroll
-            for (int t = 0; t < WPG; t++) {
-                load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, len0 + tok, qmul * q_s, qh[nt][t], ql[nt][t]);
-                if (!live) {
-                    qh[nt][t] = (half8)(_Float16)0.0f;
-                    ql[nt][t] = (half8)(_Float16)0.0f;
-                }
-            }
-        }
-        // Query positions this wave covers (inclusive); qmax < 0 for a wave with no columns.
-        const int qmin_w = len0 + c_wave / G;
-        const int qmax_w = c_wave < n_cols ? len0 + (min(c_wave + kColsPerWave, n_cols) - 1) / G : -1;
-        const int key_end = len0 + (min(c_blk + COLS, n_cols) - 1) / G + 1;
-        const int n_win = (key_end + kWin - 1) / kWin;
-
-        floatx4 o[2][NTD];
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-            for (int td = 0; td < NTD; td++) o[nt][td] = (floatx4)0.0f;
-        float m_run[2] = {kMinit, kMinit}, l_run[2] = {0.0f, 0.0f};
-
-        Pending<HD, NW> pd;
-        fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, 0, tid, wave);
-        stage_window<HD, NW>(sm, 0, pd, tid, wave, inv_s, dc);
+        for (int t = 0; t < NKS; t++) qb = fmaxf(qb, q_bound8(qrow, 2 * t + hf));
+        qb = wave_max(qb);
+        if (lane == 0) sm_qb[wave] = qb;
         __syncthreads();
+#pragma unroll
+        for (int w = 0; w < NW; w++) qb = fmaxf(qb, sm_qb[w]);
+        q_scale(qb * qmul, q_s, inv_s);
+    }
+    // q operands of this lane's column: k-step t holds dims 8(2t + hf) .. +7.
+    half8 qh[NKS], ql[NKS];
+#pragma unroll
+    for (int t = 0; t < NKS; t++) {
+        load_q8(a.rope, a.rope_pairs, qrow, 2 * t + hf, len0 + tok, qmul * q_s, qh[t], ql[t]);
+        if (!live) {
+            qh[t] = (half8)(_Float16)0.0f;
+            ql[t] = (half8)(_Float16)0.0f;
+        }
+    }
+    // Query positions this wave covers (inclusive); qmax < 0 for a wave with no columns.
+    const int qmin_w = len0 + c_wave / G;
+    const int qmax_w = c_wave < n_cols ? len0 + (min(c_wave + kColsPerWave, n_cols) - 1) / G : -1;
+    const int key_end = len0 + (min(c_blk + COLS, n_cols) - 1) / G + 1;
+    const int n_win = (key_end + kWin - 1) / kWin;
 
-        for (int w = 0; w < n_win; w++) {
-            const int buf = w & 1, base = w * kWin;
-            const bool more = w + 1 < n_win;
-            if (more) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, base + kWin, tid, wave);
-            // keep the prefetch ahead of the compute below
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
+    floatx16 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; db++) o[db] = (floatx16)0.0f;
+    float m_run = kMinit, l_run = 0.0f;
 
-            if (base <= qmax_w) {
-                floatx4 sc[2][4];
+    Pending<HD, NW> pd;
+    fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, 0, tid, wave);
+    stage_window<HD, NW>(sm, 0, pd, tid, wave, inv_s, dc);
+    __syncthreads();
+
+    for (int w = 0; w < n_win; w++) {
+        const int buf = w & 1, base = w * kWin;
+        const bool more = w + 1 < n_win;
+        if (more) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, base + kWin, tid, wave);
+        // keep the prefetch ahead of the compute below
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+
+        if (base <= qmax_w) {
+            floatx16 sc[2];
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++)
+            for (int kb = 0; kb < 2; kb++) {
+                sc[kb] = (floatx16)0.0f;
+                const int key = 32 * kb + krow;
 #pragma unroll
-                    for (int kt = 0; kt < 4; kt++) sc[nt][kt] = (floatx4)0.0f;
-#pragma unroll
-                for (int kt = 0; kt < 4; kt++) {
-#pragma unroll
-                    for (int t = 0; t < WPG; t++) {
-                        const half8 ka = sm.k[buf][16 * kt + n][k_slot<HD>(n, WPG * g + t)];
-#pragma unroll
-                        for (int nt = 0; nt < 2; nt++) {
-                            sc[nt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[nt][t], sc[nt][kt], 0, 0, 0);
-                            sc[nt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[nt][t], sc[nt][kt], 0, 0, 0);
-                        }
-                    }
-                }
-                const float svl = sm.svlog[buf];
-                half8 pb[2][2], pl[2][2];  // [nt][32-key half]: p*s_v high and low f16 parts
-                const bool mask = base + kWin - 1 > qmin_w;  // some key of the window is masked
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++)
-                    window_softmax<NTD, SOFTCAP>(sc[nt], sm.sk[buf], sm.sv[buf], svl, a.softcap, mask, base,
-                                                 g, qpos[nt], m_run[nt], l_run[nt], o[nt], pb[nt], pl[nt]);
-#pragma unroll
-                for (int b = 0; b < 2; b++) {
-#pragma unroll
-                    for (int td = 0; td < NTD; td++) {
-                        const half8 va = sm.v[buf][16 * td + n][v_slot(n, 4 * b + g)];
-#pragma unroll
-                        for (int nt = 0; nt < 2; nt++) {
-                            o[nt][td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[nt][b], o[nt][td], 0, 0, 0);
-                            o[nt][td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[nt][b], o[nt][td], 0, 0, 0);
-                        }
-                    }
+                for (int t = 0; t < NKS; t++) {
+                    const half8 ka = sm.k[buf][key][k_slot<HD>(key, 2 * t + hf)];
+                    sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[t], sc[kb], 0, 0, 0);
+                    sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[t], sc[kb], 0, 0, 0);
                 }
             }
-            if (more) stage_window<HD, NW>(sm, buf ^ 1, pd, tid, wave, inv_s, dc);
-            __syncthreads();
-        }
-
+            const bool mask = base + kWin - 1 > qmin_w;  // some key of the window is masked
+            window_scores<NDB, SOFTCAP>(sc, sm.sk[buf], sm.svlog[buf], a.softcap, mask, base, hf, qpos,
+                                        m_run, l_run, o);
+            // O^T += V^T P^T one 16-key step at a time: the exps of step st+1 overlap the
+            // MFMAs of step st.
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const float l = group_sum(l_run[nt]);
-            if (qpos[nt] < 0) continue;
-            const int c = c_wave + 16 * nt + n;
-            const int tok = c / G, head = h * G + c % G;
-            float *orow = a.out + (((size_t)s * a.n_tok + tok) * a.n_head + head) * HD;
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            for (int st = 0; st < 4; st++) {
+                half8 pb, pl;  // p*s_v high and low f16 parts
+                step_probs(sc, sm.sv[buf], st, hf, m_run, l_run, pb, pl);
 #pragma unroll
-            for (int td = 0; td < NTD; td++) {
-                float4 v4 = make_float4(o[nt][td][0] * inv, o[nt][td][1] * inv, o[nt][td][2] * inv,
-                                        o[nt][td][3] * inv);
-                *reinterpret_cast<float4 *>(orow + 16 * td + 4 * g) = v4;
+                for (int db = 0; db < NDB; db++) {
+                    const int vr = 32 * db + j;
+                    const half8 va = sm.v[buf][vr][v_slot(vr, 2 * st + hf)];
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, o[db], 0, 0, 0);
+                }
             }
         }
+        if (more) stage_window<HD, NW>(sm, buf ^ 1, pd, tid, wave, inv_s, dc);
+        __syncthreads();
+    }
+
+    const float l = half_sum(l_run);
+    if (live) {
+        float *orow = a.out + (((size_t)s * a.n_tok + tok) * a.n_head + h * G + c % G) * HD;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float4 v4 = make_float4(o[db][4 * q] * inv, o[db][4 * q + 1] * inv,
+                                        o[db][4 * q + 2] * inv, o[db][4 * q + 3] * inv);
+                *reinterpret_cast<float4 *>(orow + 32 * db + 8 * q + 4 * hf) = v4;
+            }
     }
 }
 
