@@ -221,7 +221,7 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
     for (int i = 0; i < 16; i++) {
         const float p = fast_exp2(x[i] - st.m);
         psum += p;
-        pv[i] = opaque(p * sv[i]);  // hi and lo columns must split the same f32 value
+        pv[i] = p * sv[i];
     }
     st.l += psum;
     // ---- O^T += V^T P^T ---------------------------------------------------------------------
@@ -231,8 +231,8 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
     // only feeds output columns never read.
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        const float hi = (float)(_Float16)pv[i];
-        pv[i] = lo_col ? pv[i] - hi : pv[i];
+        const float hi = split_hi(pv[i]);
+        pv[i] = lo_col ? pv[i] - hi : hi;
     }
 #pragma unroll
     for (int b = 0; b < 2; b++) {

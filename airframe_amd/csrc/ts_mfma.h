@@ -90,6 +90,12 @@ __device__ inline float opaque(float x) {
     return x;
 }
 
+// Split of v >= 0 into hi + lo, both then converted to f16: hi = v with the low 13 mantissa
+// bits cleared (exact in f16 for v in f16's normal range), lo = v - hi (exact in f32, below
+// 2^-10 v, so f16 keeps it to 2^-11 of itself: ~21 bits in all).  Bit operations on one
+// register: the halves cannot come from different roundings of v.
+__device__ inline float split_hi(float v) { return __uint_as_float(__float_as_uint(v) & 0xFFFFE000u); }
+
 // Bound on |rotated q| over the 8 dims 8u..8u+7 of one head: |a cos - b sin| <= |a| + |b|.
 __device__ inline float q_bound8(const float *qrow, int u) {
     const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * u);

@@ -9,8 +9,8 @@
 // * The (query token, head) pairs that share one kv head form the columns of the MFMA
 //   N dimension: column c of a (sequence, kv head) is token c / G, head c % G.
 // * grid = (column block of 128, kv head, sequence); each of the 4 waves owns 32 columns,
-//   one N tile of v_mfma_f32_32x32x16_f16 (the shape that reaches the matrix cores' rate;
-//   16x16x32 tops out near 60% of it).  The workgroup walks the keys in 64-key windows:
+//   one N tile of v_mfma_f32_32x32x16_f16 (half the instructions of 16x16x32 for the same
+//   work).  The workgroup walks the keys in 64-key windows:
 //   every thread loads one 16-byte piece of the next window's K rows / V blocks / scales
 //   while the current window is computed, then converts it to exact f16 integer codes in a
 //   double-buffered LDS tile, so each code is converted once per workgroup and read by all
@@ -272,11 +272,11 @@ __device__ inline void step_probs(const floatx16 (&sc)[2], const float *sv, int 
         for (int r = 0; r < 4; r++) {
             const float p = __builtin_amdgcn_exp2f(sc[kb][4 * q + r] - m_run);
             l_run += p;
-            const float pv = opaque(p * sv4[r]);
-            const _Float16 hi = (_Float16)pv;
+            const float pv = p * sv4[r];
+            const float hi = split_hi(pv);
             // key 16st + 8h + 4(q&1) + r: slot 2r + (q&1)
-            pb[2 * r + (q & 1)] = hi;
-            pl[2 * r + (q & 1)] = (_Float16)(pv - (float)hi);
+            pb[2 * r + (q & 1)] = (_Float16)hi;
+            pl[2 * r + (q & 1)] = (_Float16)(pv - hi);
         }
     }
 }
@@ -382,18 +382,21 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
         __builtin_amdgcn_sched_barrier(0);
 
         if (base <= qmax_w) {
-            floatx16 sc[2];
+            // QK^T for both 32-key tiles, the two tiles' MFMAs alternating so that no MFMA
+            // waits on the one just before it.  The matrix cores get the wave's priority while
+            // it issues them, so the other wave on the SIMD fills in with VALU work.
+            floatx16 sc[2] = {(floatx16)0.0f, (floatx16)0.0f};
+            __builtin_amdgcn_s_setprio(3);
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-                sc[kb] = (floatx16)0.0f;
-                const int key = 32 * kb + krow;
-#pragma unroll
-                for (int t = 0; t < NKS; t++) {
-                    const half8 ka = sm.k[buf][key][k_slot<HD>(key, 2 * t + hf)];
-                    sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[t], sc[kb], 0, 0, 0);
-                    sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[t], sc[kb], 0, 0, 0);
-                }
+            for (int t = 0; t < NKS; t++) {
+                const half8 ka0 = sm.k[buf][krow][k_slot<HD>(krow, 2 * t + hf)];
+                const half8 ka1 = sm.k[buf][32 + krow][k_slot<HD>(32 + krow, 2 * t + hf)];
+                sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0, qh[t], sc[0], 0, 0, 0);
+                sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1, qh[t], sc[1], 0, 0, 0);
+                sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0, ql[t], sc[0], 0, 0, 0);
+                sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1, ql[t], sc[1], 0, 0, 0);
             }
+            __builtin_amdgcn_s_setprio(0);
             const bool mask = base + kWin - 1 > qmin_w;  // some key of the window is masked
             window_scores<NDB, SOFTCAP>(sc, sm.sk[buf], sm.svlog[buf], a.softcap, mask, base, hf, qpos,
                                         m_run, l_run, o);
@@ -403,15 +406,20 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
             for (int st = 0; st < 4; st++) {
                 half8 pb, pl;  // p*s_v high and low f16 parts
                 step_probs(sc, sm.sv[buf], st, hf, m_run, l_run, pb, pl);
+                __builtin_amdgcn_s_setprio(2);
+                half8 va[NDB];
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
                     const int vr = 32 * db + j;
-                    const half8 va = sm.v[buf][vr][v_slot(vr, 2 * st + hf)];
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, o[db], 0, 0, 0);
+                    va[db] = sm.v[buf][vr][v_slot(vr, 2 * st + hf)];
                 }
+#pragma unroll
+                for (int db = 0; db < NDB; db++) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db], pb, o[db], 0, 0, 0);
+#pragma unroll
+                for (int db = 0; db < NDB; db++) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db], pl, o[db], 0, 0, 0);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         if (more) stage_window<HD, NW>(sm, buf ^ 1, pd, tid, wave, inv_s, dc);
         __syncthreads();
     }
