@@ -20,8 +20,22 @@ namespace {
 
 constexpr int kBlk = 32;
 
+// Nibble n of the result = byte n of x (every byte < 16).
+__device__ inline uint32_t pack8(uint64_t x) {
+    x = (x | (x >> 4)) & 0x00FF00FF00FF00FFull;
+    x = (x | (x >> 8)) & 0x0000FFFF0000FFFFull;
+    x = (x | (x >> 16)) & 0x00000000FFFFFFFFull;
+    return (uint32_t)x;
+}
+
 // start: first position written for this sequence (d_start[s] if d_start, else fixed_start).
 // Source row of position p: src[((s*ld_tok) + (p - start)) * H + h][hd].
+//
+// Wave w quantizes positions w, w+4, ... of the block.  Every load of the wave is issued
+// before any reduction (positions outside the append range load a valid neighbour's row and
+// are never written), reductions use DPP and permlane swaps, and the quotient takes the
+// reciprocal fast path of encode_fast.  Codes are staged in LDS as K [position][dim] and V
+// [dim][position] bytes, so each output word is one 8-byte (K) or two 4-byte (V) LDS reads.
 template <int HD>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const float *__restrict__ k,
                                                              const float *__restrict__ v,
@@ -31,11 +45,13 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
                                                              const float *__restrict__ rope,
                                                              int32_t rope_pairs) {
     constexpr int PAIRS = HD / 2;
-    constexpr int NTD = HD / 16;  // 16-dim tiles of the V block layout
-    __shared__ uint8_t kc[kBlk][HD];
-    __shared__ uint8_t vc[kBlk][HD];
+    constexpr int NTD = HD / 16;          // 16-dim tiles of the V block layout
+    constexpr int PPW = kBlk / 4;         // positions per wave
+    constexpr int NJ = (PAIRS + 63) / 64; // pairs per lane
+    constexpr int VROW = kBlk + 4;        // V staging row (bytes): 36 keeps lane writes 2-way
+    __shared__ __align__(16) uint8_t kc[kBlk][HD];
+    __shared__ __align__(16) uint8_t vc[HD][VROW];
     __shared__ float ksc[kBlk], vsc[kBlk];
-
     const int s = blockIdx.z, h = blockIdx.y;
     const int start = d_start ? d_start[s] : fixed_start;
     const int end = start + count;
@@ -43,47 +59,59 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
     const int p0 = blk * kBlk;
     if (p0 >= end) return;
     const int lo = max(p0, start), hi = min(p0 + kBlk, end);
-
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int i = wave; i < kBlk; i += 4) {
-        const int p = p0 + i;
-        if (p < lo || p >= hi) continue;
-        const size_t src = (((size_t)s * ld_tok + (p - start)) * L.H + h) * HD;
-        float kx[2 * ((PAIRS + 63) / 64)], vx[2 * ((PAIRS + 63) / 64)];
-        float km = 0.0f, vm = 0.0f;
+
+    float kx[PPW][2 * NJ], vx[PPW][2 * NJ];
 #pragma unroll
-        for (int j = 0; j < (PAIRS + 63) / 64; j++) {
-            const int pi = lane + 64 * j;
-            float a = 0.f, b = 0.f, c = 0.f, d = 0.f;
-            if (pi < PAIRS) {
-                float2 kk = *reinterpret_cast<const float2 *>(k + src + 2 * pi);
-                float2 vv = *reinterpret_cast<const float2 *>(v + src + 2 * pi);
-                a = kk.x;
-                b = kk.y;
-                c = vv.x;
-                d = vv.y;
-                if (rope && pi < rope_pairs)
-                    rope_rotate(a, b, *reinterpret_cast<const float2 *>(rope + ((size_t)p * rope_pairs + pi) * 2));
-            }
-            kx[2 * j] = a;
-            kx[2 * j + 1] = b;
-            vx[2 * j] = c;
-            vx[2 * j + 1] = d;
-            km = fmaxf(km, fmaxf(fabsf(a), fabsf(b)));
-            vm = fmaxf(vm, fmaxf(fabsf(c), fabsf(d)));
+    for (int ii = 0; ii < PPW; ii++) {
+        const int pc = min(max(p0 + wave + 4 * ii, lo), hi - 1);
+        const size_t src = (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int pi = min(lane + 64 * j, PAIRS - 1);  // lanes past the row repeat its end
+            const float2 kk = *reinterpret_cast<const float2 *>(k + src + 2 * pi);
+            const float2 vv = *reinterpret_cast<const float2 *>(v + src + 2 * pi);
+            kx[ii][2 * j] = kk.x;
+            kx[ii][2 * j + 1] = kk.y;
+            vx[ii][2 * j] = vv.x;
+            vx[ii][2 * j + 1] = vv.y;
         }
-        km = wave_max(km);
-        vm = wave_max(vm);
-        const float ks = quant_scale(km);
-        const float vs = quant_scale(vm);
+    }
+    float km[PPW], vm[PPW];
 #pragma unroll
-        for (int j = 0; j < (PAIRS + 63) / 64; j++) {
+    for (int ii = 0; ii < PPW; ii++) {
+        const int pc = min(max(p0 + wave + 4 * ii, lo), hi - 1);
+        km[ii] = 0.0f;
+        vm[ii] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int pi = min(lane + 64 * j, PAIRS - 1);
+            if (rope && pi < rope_pairs)
+                rope_rotate(kx[ii][2 * j], kx[ii][2 * j + 1],
+                            *reinterpret_cast<const float2 *>(rope + ((size_t)pc * rope_pairs + pi) * 2));
+            km[ii] = fmaxf(km[ii], fmaxf(fabsf(kx[ii][2 * j]), fabsf(kx[ii][2 * j + 1])));
+            vm[ii] = fmaxf(vm[ii], fmaxf(fabsf(vx[ii][2 * j]), fabsf(vx[ii][2 * j + 1])));
+        }
+    }
+#pragma unroll
+    for (int ii = 0; ii < PPW; ii++) {
+        km[ii] = wave_max_nonneg(km[ii]);
+        vm[ii] = wave_max_nonneg(vm[ii]);
+    }
+#pragma unroll
+    for (int ii = 0; ii < PPW; ii++) {
+        const int i = wave + 4 * ii;
+        const float ks = quant_scale(km[ii]);
+        const float vs = quant_scale(vm[ii]);
+        const float kr = __builtin_amdgcn_rcpf(ks), vr = __builtin_amdgcn_rcpf(vs);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
             const int pi = lane + 64 * j;
             if (pi < PAIRS) {
-                kc[i][2 * pi] = (uint8_t)encode(kx[2 * j], ks);
-                kc[i][2 * pi + 1] = (uint8_t)encode(kx[2 * j + 1], ks);
-                vc[i][2 * pi] = (uint8_t)encode(vx[2 * j], vs);
-                vc[i][2 * pi + 1] = (uint8_t)encode(vx[2 * j + 1], vs);
+                *reinterpret_cast<uint16_t *>(&kc[i][2 * pi]) =
+                    (uint16_t)(encode_fast(kx[ii][2 * j], ks, kr) | (encode_fast(kx[ii][2 * j + 1], ks, kr) << 8));
+                vc[2 * pi][i] = (uint8_t)encode_fast(vx[ii][2 * j], vs, vr);
+                vc[2 * pi + 1][i] = (uint8_t)encode_fast(vx[ii][2 * j + 1], vs, vr);
             }
         }
         if (lane == 0) {
@@ -99,49 +127,201 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
         constexpr int QPP = HD / 32;
         const int i = tid / QPP, quad = tid % QPP;
         if (tid < kBlk * QPP && p0 + i >= lo && p0 + i < hi) {
-            uint32_t w[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                uint32_t word = 0;
-#pragma unroll
-                for (int n = 0; n < 8; n++) word |= (uint32_t)kc[i][(quad * 4 + u) * 8 + n] << (4 * n);
-                w[u] = word;
-            }
-            uint4 *dst = reinterpret_cast<uint4 *>(L.kp + (row * L.P + p0 + i) * (HD / 2)) + quad;
-            *dst = make_uint4(w[0], w[1], w[2], w[3]);
+            const uint64_t *src = reinterpret_cast<const uint64_t *>(&kc[i][quad * 32]);
+            const uint4 w = make_uint4(pack8(src[0]), pack8(src[1]), pack8(src[2]), pack8(src[3]));
+            reinterpret_cast<uint4 *>(L.kp + (row * L.P + p0 + i) * (HD / 2))[quad] = w;
         }
     }
     if (tid < kBlk && p0 + tid >= lo && p0 + tid < hi) {
         L.ks[row * L.P + p0 + tid] = ksc[tid];
         L.vs[row * L.P + p0 + tid] = vsc[tid];
     }
-    // V block: HD*4 words, 4 consecutive words per thread.
-    {
+    // V block: HD*4 words, 4 consecutive words per thread.  Word (g, dl, td) holds dim
+    // 16 td + dl at positions 4g..4g+3 (nibbles 0-3) and 16+4g..16+4g+3 (nibbles 4-7).
+    if (tid < HD) {
         const bool full = (lo == p0 && hi == p0 + kBlk);
-        if (tid < HD) {
-            uint4 *dst = reinterpret_cast<uint4 *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16)) + tid;
-            uint4 old = make_uint4(0, 0, 0, 0);
-            if (!full) old = *dst;
-            uint32_t w[4] = {old.x, old.y, old.z, old.w};
+        uint4 *dst = reinterpret_cast<uint4 *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16)) + tid;
+        uint4 old = make_uint4(0, 0, 0, 0);
+        if (!full) old = *dst;
+        uint32_t w[4] = {old.x, old.y, old.z, old.w};
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int widx = tid * 4 + u;
-                const int lanei = widx / NTD, td = widx % NTD;
-                const int g = lanei >> 4, dl = lanei & 15;
-                const int d = 16 * td + dl;
-                uint32_t word = w[u];
+        for (int u = 0; u < 4; u++) {
+            const int widx = tid * 4 + u;
+            const int lanei = widx / NTD, td = widx % NTD;
+            const int g = lanei >> 4, dl = lanei & 15;
+            const int d = 16 * td + dl;
+            const uint64_t x = (uint64_t)*reinterpret_cast<const uint32_t *>(&vc[d][4 * g]) |
+                               ((uint64_t)*reinterpret_cast<const uint32_t *>(&vc[d][16 + 4 * g]) << 32);
+            const uint32_t fresh = pack8(x);
+            uint32_t keep = 0;  // nibbles of positions outside [lo, hi)
 #pragma unroll
-                for (int n = 0; n < 8; n++) {
-                    const int i = (n < 4) ? (4 * g + n) : (16 + 4 * g + (n - 4));
-                    if (p0 + i >= lo && p0 + i < hi) {
-                        word &= ~(0xFu << (4 * n));
-                        word |= (uint32_t)vc[i][d] << (4 * n);
-                    }
-                }
-                w[u] = word;
+            for (int n = 0; n < 8; n++) {
+                const int i = (n < 4) ? (4 * g + n) : (16 + 4 * g + (n - 4));
+                if (p0 + i < lo || p0 + i >= hi) keep |= 0xFu << (4 * n);
             }
-            *dst = make_uint4(w[0], w[1], w[2], w[3]);
+            w[u] = (w[u] & keep) | (fresh & ~keep);
         }
+        *dst = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// Code of x (= clamp(round_half_away(x/scale) + 8, 1, 15)) from y = x * rcp(scale), for
+// |x| <= 7 scale: t = y + 8.5 lies in [1.5, 15.5] and trunc(t) is the code unless y is within
+// 1e-5 of a half-integer (|y - x/scale| <= ~1.3e-6, and the add rounds by < 1e-6), which sets
+// `need` (as does NaN); the caller then recomputes with encode().
+__device__ inline uint32_t code_fast(float y, bool &need) {
+    const float t = y + 8.5f;
+    const uint32_t c = (uint32_t)t;
+    const float d = t - (float)c;
+    need |= !(fabsf(d - 0.5f) <= 0.49999f);
+    return c;
+}
+
+// hd = 128: 16 lanes per position, lane l holding dims 8l..8l+7 -- exactly K word l.  Wave w
+// takes positions 4w + r and 16 + 4w + r (r = lane / 16): the two halves of V words with
+// g = w, so the V words are assembled across the wave's 4 rows with permlane swaps and
+// written by the wave itself.  No LDS.  Max reductions: 4 DPP steps within a 16-lane row.
+__global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, const float *__restrict__ k,
+                                                                const float *__restrict__ v,
+                                                                const int32_t *__restrict__ d_start,
+                                                                int32_t fixed_start, int32_t count,
+                                                                int32_t ld_tok,
+                                                                const float *__restrict__ rope,
+                                                                int32_t rope_pairs) {
+    constexpr int HD = 128;
+    const int s = blockIdx.z, h = blockIdx.y;
+    const int start = d_start ? d_start[s] : fixed_start;
+    const int end = start + count;
+    const int blk = start / kBlk + blockIdx.x;
+    const int p0 = blk * kBlk;
+    if (p0 >= end) return;
+    const int lo = max(p0, start), hi = min(p0 + kBlk, end);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane >> 4, l = lane & 15;
+    const size_t row = (size_t)s * L.H + h;
+
+    float kx[2][8], vx[2][8];
+    float2 cs[2][4];  // rotation of each pair (identity without a table or past rope_dim)
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        const int pc = min(max(p0 + 16 * rd + 4 * wave + r, lo), hi - 1);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int pair = 4 * l + m;
+            cs[rd][m] = (rope && pair < rope_pairs)
+                            ? *reinterpret_cast<const float2 *>(rope + ((size_t)pc * rope_pairs + pair) * 2)
+                            : make_float2(1.0f, 0.0f);
+        }
+        const float4 *ks4 = reinterpret_cast<const float4 *>(k + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD + 8 * l);
+        const float4 *vs4 = reinterpret_cast<const float4 *>(v + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD + 8 * l);
+        const float4 a = ks4[0], b = ks4[1], c = vs4[0], d = vs4[1];
+        kx[rd][0] = a.x; kx[rd][1] = a.y; kx[rd][2] = a.z; kx[rd][3] = a.w;
+        kx[rd][4] = b.x; kx[rd][5] = b.y; kx[rd][6] = b.z; kx[rd][7] = b.w;
+        vx[rd][0] = c.x; vx[rd][1] = c.y; vx[rd][2] = c.z; vx[rd][3] = c.w;
+        vx[rd][4] = d.x; vx[rd][5] = d.y; vx[rd][6] = d.z; vx[rd][7] = d.w;
+    }
+    float km[2], vm[2];
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        if (rope) {
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                if (4 * l + m < rope_pairs) rope_rotate(kx[rd][2 * m], kx[rd][2 * m + 1], cs[rd][m]);
+        }
+        km[rd] = 0.0f;
+        vm[rd] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            km[rd] = fmaxf(km[rd], fabsf(kx[rd][e]));
+            vm[rd] = fmaxf(vm[rd], fabsf(vx[rd][e]));
+        }
+    }
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        km[rd] = fmaxf(km[rd], dpp_f<0xB1>(km[rd]));
+        vm[rd] = fmaxf(vm[rd], dpp_f<0xB1>(vm[rd]));
+    }
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        km[rd] = fmaxf(km[rd], dpp_f<0x4E>(km[rd]));
+        vm[rd] = fmaxf(vm[rd], dpp_f<0x4E>(vm[rd]));
+    }
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        km[rd] = fmaxf(km[rd], dpp_f<0x141>(km[rd]));
+        vm[rd] = fmaxf(vm[rd], dpp_f<0x141>(vm[rd]));
+    }
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        km[rd] = fmaxf(km[rd], dpp_f<0x140>(km[rd]));
+        vm[rd] = fmaxf(vm[rd], dpp_f<0x140>(vm[rd]));
+    }
+
+    uint32_t vpart[8];  // this row's nibbles of V words (dims 8l + e)
+#pragma unroll
+    for (int e = 0; e < 8; e++) vpart[e] = 0;
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        const int p = p0 + 16 * rd + 4 * wave + r;
+        const bool in = p >= lo && p < hi;
+        const float ks = quant_scale(km[rd]), vs = quant_scale(vm[rd]);
+        const float kr = __builtin_amdgcn_rcpf(ks), vr = __builtin_amdgcn_rcpf(vs);
+        const bool k_ok = ks >= 1.17549435e-38f && ks <= 4.25352959e37f;
+        const bool v_ok = vs >= 1.17549435e-38f && vs <= 4.25352959e37f;
+        uint32_t kc[8], vc[8];
+        bool kneed = !k_ok, vneed = !v_ok;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            kc[e] = code_fast(kx[rd][e] * kr, kneed);
+            vc[e] = code_fast(vx[rd][e] * vr, vneed);
+        }
+        if (__builtin_amdgcn_ballot_w64(kneed) != 0) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) kc[e] = encode(kx[rd][e], ks);
+        }
+        if (__builtin_amdgcn_ballot_w64(vneed) != 0) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) vc[e] = encode(vx[rd][e], vs);
+        }
+        uint32_t kw = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            kw |= kc[e] << (4 * e);
+            vpart[e] |= vc[e] << (4 * r + 16 * rd);
+        }
+        if (in) {
+            reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[l] = kw;
+            if (l == 0) {
+                L.ks[row * L.P + p] = ks;
+                L.vs[row * L.P + p] = vs;
+            }
+        }
+    }
+    // OR the 4 rows' parts: lanes l, l+16, l+32, l+48 end up with the same 8 words
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        auto a = __builtin_amdgcn_permlane16_swap(vpart[e], vpart[e], false, false);
+        vpart[e] = a[0] | a[1];
+        auto b = __builtin_amdgcn_permlane32_swap(vpart[e], vpart[e], false, false);
+        vpart[e] = b[0] | b[1];
+    }
+    // row r writes dims 8l + 2r and 8l + 2r + 1: word (g = wave, dl, td) of the block
+    uint32_t keep = 0;  // nibbles of positions outside [lo, hi)
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const int p = p0 + 4 * wave + (n & 3) + 16 * (n >> 2);
+        if (p < lo || p >= hi) keep |= 0xFu << (4 * n);
+    }
+    uint32_t *vb = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16));
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int e = 2 * r + q;
+        const uint32_t w = r == 0 ? (q ? vpart[1] : vpart[0])
+                         : r == 1 ? (q ? vpart[3] : vpart[2])
+                         : r == 2 ? (q ? vpart[5] : vpart[4])
+                                  : (q ? vpart[7] : vpart[6]);
+        const int d = 8 * l + e, td = d >> 4, dl = d & 15;
+        uint32_t *dst = vb + (wave * 16 + dl) * (HD / 16) + td;
+        *dst = keep ? (*dst & keep) | (w & ~keep) : w;
     }
 }
 
@@ -190,7 +370,7 @@ hipError_t launch_quantize_rows(const KvLayerView &L, const float *k, const floa
                                 int32_t max_blocks, hipStream_t st) {
     dim3 grid(max_blocks, L.H, L.S);
     if (L.hd == 128)
-        quantize_rows_kernel<128><<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
+        quantize_rows128_kernel<<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
     else if (L.hd == 64)
         quantize_rows_kernel<64><<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
     else

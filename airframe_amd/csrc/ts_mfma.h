@@ -77,6 +77,31 @@ __device__ inline float group_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// dequant8 written in plain C: the same instructions, but visible to the scheduler, so it can
+// be interleaved with matrix-core work (prefill staging).
+__device__ inline half8 dequant8_c(uint32_t w) {
+    const uint32_t w8 = w >> 8;
+    const uint32_t a = (w & 0x000F000Fu) | 0x64006400u;
+    const uint32_t b = (w & 0x00F000F0u) | 0x64006400u;
+    const uint32_t c = (w8 & 0x000F000Fu) | 0x64006400u;
+    const uint32_t d = (w8 & 0x00F000F0u) | 0x64006400u;
+    half2_t ha = __builtin_bit_cast(half2_t, a), hb = __builtin_bit_cast(half2_t, b);
+    half2_t hc = __builtin_bit_cast(half2_t, c), hd = __builtin_bit_cast(half2_t, d);
+    const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const half2_t off2 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    ha = ha - off;
+    hb = hb * sixteenth + off2;
+    hc = hc - off;
+    hd = hd * sixteenth + off2;
+    half8 r;
+    r[0] = ha[0]; r[1] = ha[1];
+    r[2] = hb[0]; r[3] = hb[1];
+    r[4] = hc[0]; r[5] = hc[1];
+    r[6] = hd[0]; r[7] = hd[1];
+    return r;
+}
+
 // dims held in slot j of a dequantized word: 8u + kPerm[j]
 __device__ constexpr int kPerm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 

@@ -140,50 +140,90 @@ __device__ inline void fetch_window(Pending<HD, NW> &pd, const uint8_t *kbase, c
         pd.scale = vsb[base + tid - kWin];
 }
 
+// Staging of one window's codes, as 8 * NK parts of one 32-bit word each per thread (parts
+// [0, 4 NK): K words, [4 NK, 8 NK): V words), so the caller can spread them over other work.
+// Only for the layout where every thread holds NK K pieces and NK V pieces (!SPLIT).
 template <int HD, int NW>
-__device__ inline void stage_window(PrefillLds<HD> &sm, int buf, const Pending<HD, NW> &pd, int tid,
-                                    int wave, float inv_s, const DeqConst &dc) {
+__device__ inline void stage_part(PrefillLds<HD> &sm, int buf, const Pending<HD, NW> &pd, int tid,
+                                  int part) {
     using P = Pending<HD, NW>;
-    constexpr int NTD = HD / 16;
-    auto put_k = [&](int c, const uint4 &x) {
-        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-        int key, part;
-        k_piece<HD>(c, key, part);
-#pragma unroll
-        for (int j = 0; j < 4; j++) sm.k[buf][key][k_slot<HD>(key, 4 * part + j)] = dequant8(w[j], dc);
-    };
-    // V: lane L holds 4 words of packed lane group ln = L (key group g = ln/16, dim row dl =
-    // ln%16); lane L^16 holds the same words of key group g^1.  Words of groups 2p and 2p+1
-    // hold keys 8p..8p+7 in their low halves (nibbles 0-3) and 16+8p..16+8p+7 in their high
-    // halves, so the even lane builds the dword of low halves, the odd lane the one of high
-    // halves: one 8-key group of the V^T row each.
-    auto put_v = [&](int c, const uint4 &x) {
-        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+    static_assert(!P::SPLIT, "per-part staging needs whole K and V pieces per thread");
+    const int i = (part % (4 * P::NK)) / 4, j = part % 4;
+    const int c = tid + P::NT * i;
+    if (part < 4 * P::NK) {
+        const uint4 &x = pd.k[i];
+        const uint32_t wj = j == 0 ? x.x : j == 1 ? x.y : j == 2 ? x.z : x.w;
+        int key, kpart;
+        k_piece<HD>(c, key, kpart);
+        sm.k[buf][key][k_slot<HD>(key, 4 * kpart + j)] = dequant8_c(wj);
+    } else {
+        // V: lane L holds 4 words of packed lane group ln = L (key group g = ln/16, dim row dl
+        // = ln%16); lane L^16 holds the same words of key group g^1.  Words of groups 2p and
+        // 2p+1 hold keys 8p..8p+7 in their low halves (nibbles 0-3) and 16+8p..16+8p+7 in
+        // their high halves, so the even lane builds the dword of low halves, the odd lane the
+        // one of high halves: one 8-key group of the V^T row each.
+        const uint4 &x = pd.v[i];
+        const uint32_t wj = j == 0 ? x.x : j == 1 ? x.y : j == 2 ? x.z : x.w;
         int b, piece;
         v_piece<HD>(c, b, piece);
         const int ln = c % 64, dl = ln & 15, odd = (ln >> 4) & 1, pair = ln >> 5;
         const int td0 = (c % HD) / 64 * 4;
         const int sl = 4 * b + 2 * odd + pair;
-        const int src = 4 * (threadIdx.x ^ 16);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t pw = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)w[j]);
-            const uint32_t d = odd ? (pw >> 16) | (w[j] & 0xFFFF0000u) : (w[j] & 0xFFFFu) | (pw << 16);
-            const int row = 16 * (td0 + j) + dl;
-            sm.v[buf][row][v_slot(row, sl)] = dequant8(d, dc);
-        }
-    };
+        // byte selects of v_perm_b32(pw, w): even lanes low(w) | low(pw) << 16, odd lanes
+        // high(pw) | high(w) << 16 (one instruction, no lane-divergent branch)
+        const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+        const uint32_t pw = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (threadIdx.x ^ 16), (int)wj);
+        const uint32_t d = __builtin_amdgcn_perm(pw, wj, sel);
+        const int row = 16 * (td0 + j) + dl;
+        sm.v[buf][row][v_slot(row, sl)] = dequant8_c(d);
+    }
+}
+
+// All of one window's codes into LDS.
+template <int HD, int NW>
+__device__ inline void stage_codes(PrefillLds<HD> &sm, int buf, const Pending<HD, NW> &pd, int tid,
+                                   int wave) {
+    using P = Pending<HD, NW>;
     if constexpr (P::SPLIT) {
+        // V staging as in stage_part, for a thread that holds one V piece
+        auto put_k = [&](int c, const uint4 &x) {
+            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+            int key, part;
+            k_piece<HD>(c, key, part);
+#pragma unroll
+            for (int j = 0; j < 4; j++) sm.k[buf][key][k_slot<HD>(key, 4 * part + j)] = dequant8_c(w[j]);
+        };
+        auto put_v = [&](int c, const uint4 &x) {
+            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+            int b, piece;
+            v_piece<HD>(c, b, piece);
+            const int ln = c % 64, dl = ln & 15, odd = (ln >> 4) & 1, pair = ln >> 5;
+            const int td0 = (c % HD) / 64 * 4;
+            const int sl = 4 * b + 2 * odd + pair;
+            const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t pw = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (threadIdx.x ^ 16), (int)w[j]);
+                const uint32_t d = __builtin_amdgcn_perm(pw, w[j], sel);
+                const int row = 16 * (td0 + j) + dl;
+                sm.v[buf][row][v_slot(row, sl)] = dequant8_c(d);
+            }
+        };
         if (wave < P::KCH / 64)
             put_k(tid, pd.k[0]);
         else
             put_v(tid - P::KCH, pd.k[0]);
     } else {
 #pragma unroll
-        for (int i = 0; i < P::NK; i++) put_k(tid + P::NT * i, pd.k[i]);
-#pragma unroll
-        for (int i = 0; i < P::NK; i++) put_v(tid + P::NT * i, pd.v[i]);
+        for (int part = 0; part < 8 * P::NK; part++) stage_part<HD, NW>(sm, buf, pd, tid, part);
     }
+}
+
+// The window's scales into LDS (kept apart from the code staging, which is branch-free so it
+// can be scheduled in between the QK matrix-core instructions).
+template <int HD, int NW>
+__device__ inline void stage_scales(PrefillLds<HD> &sm, int buf, const Pending<HD, NW> &pd, int tid,
+                                    float inv_s) {
     if (tid < kWin) {
         sm.sk[buf][tid] = pd.scale * inv_s;  // undo the q operand scale (a power of two: exact)
     } else if (tid < 2 * kWin) {
@@ -311,7 +351,6 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, hf = lane >> 5;  // MFMA column / lane half
     const int len0 = a.len[s];
-    const DeqConst dc;
     __shared__ PrefillLds<HD> sm;
     __shared__ float sm_qb[NW];
 
@@ -368,35 +407,46 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     for (int db = 0; db < NDB; db++) o[db] = (floatx16)0.0f;
     float m_run = kMinit, l_run = 0.0f;
 
+    // Window w+1 is staged into LDS while window w's QK^T runs on the matrix cores (the
+    // staging is VALU and LDS-write work); its global loads were issued one iteration earlier.
     Pending<HD, NW> pd;
     fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, 0, tid, wave);
-    stage_window<HD, NW>(sm, 0, pd, tid, wave, inv_s, dc);
+    stage_codes<HD, NW>(sm, 0, pd, tid, wave);
+    stage_scales<HD, NW>(sm, 0, pd, tid, inv_s);
+    if (n_win > 1) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, kWin, tid, wave);
     __syncthreads();
 
     for (int w = 0; w < n_win; w++) {
         const int buf = w & 1, base = w * kWin;
         const bool more = w + 1 < n_win;
-        if (more) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, base + kWin, tid, wave);
-        // keep the prefetch ahead of the compute below
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-
-        if (base <= qmax_w) {
-            // QK^T for both 32-key tiles, the two tiles' MFMAs alternating so that no MFMA
-            // waits on the one just before it.  The matrix cores get the wave's priority while
-            // it issues them, so the other wave on the SIMD fills in with VALU work.
-            floatx16 sc[2] = {(floatx16)0.0f, (floatx16)0.0f};
-            __builtin_amdgcn_s_setprio(3);
+        // QK^T for both 32-key tiles, the two tiles' MFMAs alternating so that no MFMA waits
+        // on the one just before it, with the next window's staging in between.  (A wave whose
+        // columns all lie before the window computes scores it then drops: on the diagonal
+        // only, and it keeps the staging in the MFMAs' basic block.)
+        floatx16 sc[2] = {(floatx16)0.0f, (floatx16)0.0f};
+        __builtin_amdgcn_s_setprio(3);
+        using PD = Pending<HD, NW>;
+        constexpr int NPART = PD::SPLIT ? 0 : 8 * PD::NK;  // staging parts, spread over k-steps
 #pragma unroll
-            for (int t = 0; t < NKS; t++) {
-                const half8 ka0 = sm.k[buf][krow][k_slot<HD>(krow, 2 * t + hf)];
-                const half8 ka1 = sm.k[buf][32 + krow][k_slot<HD>(32 + krow, 2 * t + hf)];
-                sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0, qh[t], sc[0], 0, 0, 0);
-                sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1, qh[t], sc[1], 0, 0, 0);
-                sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0, ql[t], sc[0], 0, 0, 0);
-                sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1, ql[t], sc[1], 0, 0, 0);
+        for (int t = 0; t < NKS; t++) {
+            const half8 ka0 = sm.k[buf][krow][k_slot<HD>(krow, 2 * t + hf)];
+            const half8 ka1 = sm.k[buf][32 + krow][k_slot<HD>(32 + krow, 2 * t + hf)];
+            sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0, qh[t], sc[0], 0, 0, 0);
+            sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1, qh[t], sc[1], 0, 0, 0);
+            sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0, ql[t], sc[0], 0, 0, 0);
+            sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1, ql[t], sc[1], 0, 0, 0);
+            // (after the last window this writes the unused buffer)
+            if constexpr (NPART > 0) {
+#pragma unroll
+                for (int part = t * NPART / NKS; part < (t + 1) * NPART / NKS; part++)
+                    stage_part<HD, NW>(sm, buf ^ 1, pd, tid, part);
             }
-            __builtin_amdgcn_s_setprio(0);
+        }
+        if constexpr (NPART == 0) stage_codes<HD, NW>(sm, buf ^ 1, pd, tid, wave);
+        __builtin_amdgcn_s_setprio(0);
+        if (more) stage_scales<HD, NW>(sm, buf ^ 1, pd, tid, inv_s);
+        if (w + 2 < n_win) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, base + 2 * kWin, tid, wave);
+        if (base <= qmax_w) {
             const bool mask = base + kWin - 1 > qmin_w;  // some key of the window is masked
             window_scores<NDB, SOFTCAP>(sc, sm.sk[buf], sm.svlog[buf], a.softcap, mask, base, hf, qpos,
                                         m_run, l_run, o);
@@ -418,9 +468,8 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
 #pragma unroll
                 for (int db = 0; db < NDB; db++) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db], pl, o[db], 0, 0, 0);
             }
+            __builtin_amdgcn_s_setprio(0);
         }
-        __builtin_amdgcn_s_setprio(0);
-        if (more) stage_window<HD, NW>(sm, buf ^ 1, pd, tid, wave, inv_s, dc);
         __syncthreads();
     }
 

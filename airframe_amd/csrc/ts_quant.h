@@ -43,5 +43,40 @@ __device__ inline uint32_t encode(float x, float scale) {
     return (uint32_t)q;
 }
 
+// Max over the 64 lanes of a wave for values >= 0 (or NaN, ignored like fmaxf): DPP within each
+// 16-lane row, then two permlane swaps across rows.  No LDS traffic.
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ inline float wave_max_nonneg(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm(1,0,3,2)
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm(2,3,0,1)
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// encode(x, scale) with the quotient taken as x * rcp(scale) wherever that cannot change the
+// rounded result: |x| <= 7 scale here (scale = max|x| / 7), so the product is within ~1.3e-6
+// of the correctly rounded x / scale, and only a quotient within 1e-5 of a half-integer (the
+// rounding boundaries) or a scale outside [2^-126, 2^125] (denormal or overflowing reciprocal)
+// takes the correctly rounded division.  Bit-identical to encode for every input.
+__device__ inline uint32_t encode_fast(float x, float scale, float rinv) {
+    float q = x * rinv;
+    const float a = fabsf(q);
+    const float f = a - floorf(a);  // exact for a < 8
+    if (fabsf(f - 0.5f) < 1.0e-5f || !(scale >= 1.17549435e-38f && scale <= 4.25352959e37f))
+        q = __fdiv_rn(x, scale);
+    const float r = roundf(q);
+    int c = (r != r) ? 0 : (int)fminf(fmaxf(r, -64.0f), 64.0f);
+    c += 8;
+    c = c < 1 ? 1 : (c > 15 ? 15 : c);
+    return (uint32_t)c;
+}
+
 }  // namespace
 }  // namespace ts

@@ -69,6 +69,38 @@ def test_append_special_values_bit_exact(gpu):
     assert (vp[0, 1] == 0xFFFFFFFF).all()
 
 
+def test_append_quotients_at_rounding_boundaries(gpu):
+    """Quotients x/scale within a few ulps of the half-integers (where round() flips) under
+    scales that are not powers of two, and scales at the ends of f32's range: the device's
+    reciprocal shortcut must fall back to the correctly rounded division there."""
+    say("append rounding boundaries")
+    n_kv, hd, n_tok = 4, 128, 64
+    rng = np.random.default_rng(11)
+    v = np.empty((1, n_tok, n_kv, hd), np.float32)
+    for t in range(n_tok):
+        for h in range(n_kv):
+            exp = [-120, -60, -3, 0, 5, 40, 100, 124][(t + h) % 8]
+            m = np.float32(7.0 * (1.0 + rng.random()) * 2.0 ** exp)
+            sc = np.float32(m / np.float32(7.0))
+            half = (rng.integers(0, 7, hd) + 0.5) * rng.choice([-1.0, 1.0], hd)
+            x = (half * sc).astype(np.float32)
+            ulps = rng.integers(-3, 4, hd)
+            for _ in range(3):  # step each value by -3..3 ulps
+                x = np.where(ulps > 0, np.nextafter(x, np.float32(np.inf)), x)
+                x = np.where(ulps < 0, np.nextafter(x, np.float32(-np.inf)), x)
+                ulps = ulps - np.sign(ulps)
+            x[0] = m
+            v[0, t, h] = np.clip(x, -m, m)
+    v[0, 0, 0] = np.float32(3.3e38) * np.sign(v[0, 0, 0])  # reciprocal would overflow
+    v[0, 1, 0, 0] = np.float32(2e-38)                          # denormal scale
+    v[0, 1, 0, 1:] = v[0, 1, 0, 1:] * np.float32(0.0)
+    k = v.copy()
+    p = Pair(1, n_kv, hd, n_tok + 8, 10000.0)
+    p.append(k, v)
+    p.advance(n_tok)
+    p.check_codes()
+
+
 def test_reference_known_answers_through_gpu(gpu):
     """test_int4_parity.rs cases, run through the GPU append at position 0 (rotation = identity)
     as V (never rotated) and K."""
