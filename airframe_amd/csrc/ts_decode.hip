@@ -36,6 +36,12 @@
 #ifndef TS_DECODE_NW
 #define TS_DECODE_NW 4
 #endif
+#ifndef TS_DECODE4_WAVES
+#define TS_DECODE4_WAVES 2
+#endif
+#ifndef TS_DECODE_FORCE16
+#define TS_DECODE_FORCE16 0
+#endif
 #ifndef TS_DECODE_DEPTH
 #define TS_DECODE_DEPTH 2
 #endif
@@ -573,6 +579,354 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     }
 }
 
+
+// ---- G <= 4: QK^T on v_mfma_f32_4x4x4_16b_f16 -------------------------------------------------
+//
+// The 16x16 tiles above leave 8 of 16 columns empty for G <= 4 and give each lane 16 scores,
+// most of them copies.  Here QK^T runs on the 16-block 4x4x4 matrix instruction: block b takes
+// positions 4b..4b+3 of the window (B operand: lane = position, its own K row), the A operand
+// (4 heads x 4 dims of q) is broadcast to all 16 blocks from block `abid`, so one q register
+// pair holds 16 k-steps.  The result leaves lane L with the scores of position base + L for
+// heads 0..3: softmax is 4 values per lane, with the lane's own scales.  p * s_v goes through
+// a per-wave LDS tile into the PV operand layout of the 16x16x32 instruction (as above).
+
+template <int HD>
+struct Window4 {
+    static constexpr int NKW = HD / 8, NTD = HD / 16;
+    uint32_t kw[NKW];     // K row of position base + lane
+    uint32_t vw[2][NTD];  // V words, as Window
+    float sk, sv;         // scales of position base + lane
+};
+
+template <int HD>
+__device__ __forceinline__ void load_window4(Window4<HD> &w, const Streams &st, int base, int lane) {
+    constexpr int NKW = HD / 8, NTD = HD / 16, ROWB = HD / 2;
+#pragma unroll
+    for (int j = 0; j < NKW / 4; j++) {
+        const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, lane * ROWB + 16 * j, base * ROWB, 0);
+        w.kw[4 * j + 0] = t4[0]; w.kw[4 * j + 1] = t4[1]; w.kw[4 * j + 2] = t4[2]; w.kw[4 * j + 3] = t4[3];
+    }
+    const int voff = lane * NTD * 4;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+#pragma unroll
+        for (int q4 = 0; q4 < NTD / 4; q4++) {
+            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.v, voff + 16 * q4 + b * (HD * 16), (base / 32) * (HD * 16), 0);
+            w.vw[b][4 * q4 + 0] = t4[0]; w.vw[b][4 * q4 + 1] = t4[1];
+            w.vw[b][4 * q4 + 2] = t4[2]; w.vw[b][4 * q4 + 3] = t4[3];
+        }
+    }
+    const int sp = min(base + lane, st.last);
+    w.sk = st.ksb[sp];
+    w.sv = st.vsb[sp];
+}
+
+// Wave state: O^T accumulators (column n < 4: head n from the high parts of p*s_v, 4 <= n < 8:
+// head n - 4 from the low parts), per-head exponent reference (wave-uniform) and this lane's
+// share of the per-head softmax sums.
+template <int HD>
+struct WaveState4 {
+    floatx4 o[HD / 16];
+    float m[4], l[4];
+};
+
+template <int CTRL>
+__device__ inline float dpp_any(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ inline float wave_max_all(float v) {
+    v = fmaxf(v, dpp_any<0xB1>(v));
+    v = fmaxf(v, dpp_any<0x4E>(v));
+    v = fmaxf(v, dpp_any<0x141>(v));
+    v = fmaxf(v, dpp_any<0x140>(v));
+    return group_max(v);
+}
+__device__ inline float wave_sum_all(float v) {
+    v += dpp_any<0xB1>(v);
+    v += dpp_any<0x4E>(v);
+    v += dpp_any<0x141>(v);
+    v += dpp_any<0x140>(v);
+    return group_sum(v);
+}
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+// LDS slot of position `key` (0..63) of a window in the PV operand order: lane (n, g) of the
+// 16x16x32 B operand reads slots 32b + 8g .. +7 = positions 32b + 16t + 4g + r at 2r + t.
+__device__ inline int p_slot(int key) {
+    return 32 * (key >> 5) + 8 * ((key >> 2) & 3) + 2 * (key & 3) + ((key >> 4) & 1);
+}
+
+// The QK^T matrix instructions of one window: word U of the lane's K row gives k-steps 2U and
+// 2U + 1, broadcast operand block (k-step % 16) of q pair (k-step / 16).  The broadcast block
+// is an immediate, hence the compile-time recursion over words.
+template <int HD, int U>
+struct QkWords {
+    static __device__ __forceinline__ void run(const Window4<HD> &w, const half4_t (&qh)[HD / 64],
+                                               const half4_t (&ql)[HD / 64], floatx4 (&acc)[2],
+                                               const DeqConst &dc) {
+        const half8 kd = dequant8(w.kw[U], dc);
+        const half4_t k0 = {kd[0], kd[1], kd[2], kd[3]};
+        const half4_t k1 = {kd[4], kd[5], kd[6], kd[7]};
+        constexpr int T0 = 2 * U, T1 = 2 * U + 1;
+        acc[0] = __builtin_amdgcn_mfma_f32_4x4x4f16(qh[T0 / 16], k0, acc[0], 4, T0 % 16, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_4x4x4f16(ql[T0 / 16], k0, acc[1], 4, T0 % 16, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_4x4x4f16(qh[T1 / 16], k1, acc[0], 4, T1 % 16, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_4x4x4f16(ql[T1 / 16], k1, acc[1], 4, T1 % 16, 0);
+        QkWords<HD, U + 1>::run(w, qh, ql, acc, dc);
+    }
+};
+template <int HD>
+struct QkWords<HD, HD / 8> {
+    static __device__ __forceinline__ void run(const Window4<HD> &, const half4_t (&)[HD / 64],
+                                               const half4_t (&)[HD / 64], floatx4 (&)[2],
+                                               const DeqConst &) {}
+};
+
+template <int HD, bool SOFTCAP, bool TAIL>
+__device__ __forceinline__ void process_window4(const Window4<HD> &w, WaveState4<HD> &st,
+                                                const half4_t (&qh)[HD / 64], const half4_t (&ql)[HD / 64],
+                                                _Float16 (*pt)[64], int base, int end, int lane, int G,
+                                                float inv_s, float softcap, const DeqConst &dc) {
+    constexpr int NKW = HD / 8, NTD = HD / 16;
+    // ---- S = Q K^T --------------------------------------------------------------------------------
+    floatx4 acc[2] = {(floatx4)0.0f, (floatx4)0.0f};  // hi and lo parts of q
+    QkWords<HD, 0>::run(w, qh, ql, acc, dc);
+    const floatx4 sc = acc[0] + acc[1];
+    // ---- softmax on this lane's position for heads 0..3 ---------------------------------------
+    const float sk = w.sk * inv_s;  // undo the q operand scale (a power of two: exact)
+    float sv = w.sv;
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float v = sc[i] * sk;
+        if constexpr (SOFTCAP) v = tanhf(v * (1.0f / kLog2e) / softcap) * softcap * kLog2e;
+        x[i] = v;
+    }
+    if constexpr (TAIL) {
+        if (base + lane >= end) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[i] = -INFINITY;
+            sv = 0.0f;
+        }
+    }
+    // P = 2^(x - m) * s_v must stay <= 2^8 (f16 range for its two parts, with room).  The
+    // per-head reference m moves only when some position of the window breaks that: a ballot
+    // in the common case, wave reductions only then (to m = max(x) + log2(max s_v), P <= 1).
+    float p[4], pv[4];
+    bool need = false;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        p[i] = i < G ? fast_exp2(x[i] - st.m[i]) : 0.0f;
+        pv[i] = p[i] * sv;
+        need |= !(pv[i] <= 256.0f);
+    }
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        asm volatile("" ::: "memory");  // keep this a branch: the rescale is the rare case
+        const float svl = __builtin_amdgcn_logf(wave_max_all(sv));
+        float al[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float xm = wave_max_all(x[i]);
+            const float mw = fminf(fmaxf(xm + svl, xm - 64.0f), xm + 64.0f);
+            const float m_new = fmaxf(st.m[i], mw);
+            al[i] = fast_exp2(st.m[i] - m_new);
+            st.l[i] *= al[i];
+            st.m[i] = m_new;
+            p[i] = i < G ? fast_exp2(x[i] - st.m[i]) : 0.0f;
+            pv[i] = p[i] * sv;
+        }
+        const int n = lane & 3;
+        const float a = n == 0 ? al[0] : n == 1 ? al[1] : n == 2 ? al[2] : al[3];
+#pragma unroll
+        for (int td = 0; td < NTD; td++) st.o[td] *= a;
+    }
+    const int slot = p_slot(lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        st.l[i] += p[i];
+        const float hi = split_hi(pv[i]);
+        pt[i][slot] = (_Float16)hi;
+        pt[4 + i][slot] = (_Float16)(pv[i] - hi);
+    }
+    // ---- O^T += V^T P^T (the wave's own LDS writes are ordered before its reads) -------------
+    const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        // columns 8..15 read real p values: their outputs are never used
+        const half8 pb = *reinterpret_cast<const half8 *>(&pt[n & 7][32 * b + 8 * g]);
+#pragma unroll
+        for (int td = 0; td < NTD; td++) {
+            const half8 va = dequant8(w.vw[b][td], dc);
+            st.o[td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, st.o[td], 0, 0, 0);
+        }
+    }
+}
+
+template <int HD, bool SOFTCAP>
+__global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_split4_kernel(DecodeArgs a) {
+    constexpr int NW = TS_DECODE_NW;
+    constexpr int SPAN = 64 * NW;
+    constexpr int NTD = HD / 16;
+    constexpr int NQ = HD / 64;  // q register pairs (16 k-steps each)
+    constexpr int OST = HD + 1;
+    const KvLayerView &L = a.L;
+    const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+    const int qpos = a.len[s];
+    const int n_ctx = qpos + 1;
+    const int start = split * a.chunk;
+    if (start >= n_ctx) return;
+    const int n_split_s = (n_ctx + a.chunk - 1) / a.chunk;
+    const bool fused = a.k_new != nullptr && split == n_split_s - 1;
+    const int end = fused ? qpos : min(start + a.chunk, n_ctx);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.G;
+    const DeqConst dc;
+
+    union Smem {
+        _Float16 pt[NW][8][64];  // per-wave p*s_v tile, [column][slot]
+        struct {
+            float o[NW][8 * OST];
+            float m[NW][4], l[NW][4];
+        } merge;
+    };
+    __shared__ Smem sm;
+    __shared__ float kd[HD], vd[HD], xnew[8];
+
+    const size_t row = (size_t)s * L.H + h;
+    constexpr int ROWB = HD / 2;
+    Streams str;
+    str.k = make_rsrc(L.kp + row * L.P * ROWB, (uint32_t)end * ROWB);
+    str.v = make_rsrc(L.vp + row * (L.P / 32) * (HD * 16), (uint32_t)((end + 31) / 32) * (HD * 16));
+    str.ksb = L.ks + row * L.P;
+    str.vsb = L.vs + row * L.P;
+    str.last = max(end - 1, 0);
+
+    Window4<HD> w0, w1;
+    int base = start + wave * 64;
+    load_window4<HD>(w0, str, base, lane);
+
+    // q operands: lane 4 blk + i holds head i (zero past G) for k-step 16 c + blk of pair c; a
+    // k-step is half of a dequantized word's slots: word t/2, slots 4 (t%2) .. +3.
+    half4_t qh[NQ], ql[NQ];
+    float q_s, inv_s;
+    {
+        const int blk = lane >> 2, i = lane & 3;
+        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (i < G ? i : 0)) * HD;
+        float qb = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NQ; c++) qb = fmaxf(qb, q_bound8(qrow, (16 * c + blk) >> 1));
+        q_scale(wave_max_all(qb) * (a.inv_sqrt_hd * kLog2e), q_s, inv_s);
+#pragma unroll
+        for (int c = 0; c < NQ; c++) {
+            const int t = 16 * c + blk;
+            half8 hh8, ll8;
+            load_q8(a.rope, a.rope_pairs, qrow, t >> 1, qpos, a.inv_sqrt_hd * kLog2e * q_s, hh8, ll8);
+            const int o4 = 4 * (t & 1);
+            half4_t hv = {hh8[o4], hh8[o4 + 1], hh8[o4 + 2], hh8[o4 + 3]};
+            half4_t lv = {ll8[o4], ll8[o4 + 1], ll8[o4 + 2], ll8[o4 + 3]};
+            qh[c] = i < G ? hv : (half4_t)(_Float16)0.0f;
+            ql[c] = i < G ? lv : (half4_t)(_Float16)0.0f;
+        }
+    }
+    if (fused && wave == 0) append_one<HD>(a, s, h, qpos, lane, kd, vd);
+    __syncthreads();
+    if (fused) {
+        for (int hh = wave; hh < G; hh += NW) {
+            const int i = lane < HD / 2 ? lane : 0;
+            const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
+            float q0 = qq.x, q1 = qq.y;
+            if (i < a.rope_pairs)
+                rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qpos * a.rope_pairs + i) * 2));
+            float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+            float x = dot * a.inv_sqrt_hd;
+            if constexpr (SOFTCAP) x = tanhf(x / a.softcap) * a.softcap;
+            if (lane == 0) xnew[hh] = x * kLog2e;
+        }
+    }
+
+    WaveState4<HD> st;
+#pragma unroll
+    for (int td = 0; td < NTD; td++) st.o[td] = (floatx4)0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        st.m[i] = kMinit;
+        st.l[i] = 0.0f;
+    }
+    _Float16 (*pt)[64] = sm.pt[wave];
+
+#define TS_STEP4(CUR, NXT)                                                                      \
+    {                                                                                          \
+        load_window4<HD>(NXT, str, base + SPAN, lane);                                          \
+        asm volatile("" ::: "memory");                                                         \
+        __builtin_amdgcn_sched_barrier(0);                                                     \
+        if (base + 64 <= end)                                                                  \
+            process_window4<HD, SOFTCAP, false>(CUR, st, qh, ql, pt, base, end, lane, G, inv_s, a.softcap, dc); \
+        else                                                                                   \
+            process_window4<HD, SOFTCAP, true>(CUR, st, qh, ql, pt, base, end, lane, G, inv_s, a.softcap, dc); \
+        base += SPAN;                                                                          \
+        if (base >= end) break;                                                                \
+    }
+    while (base < end) {
+        TS_STEP4(w0, w1)
+        TS_STEP4(w1, w0)
+    }
+#undef TS_STEP4
+
+    // ---- merge the waves through LDS ------------------------------------------------------------
+    float l_run[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) l_run[i] = wave_sum_all(st.l[i]);
+    __syncthreads();  // all waves are done with their P tiles
+    const int n = lane & 15, g = lane >> 4;
+    if (lane < 4) {
+        const int i = lane;
+        sm.merge.m[wave][i] = i == 0 ? st.m[0] : i == 1 ? st.m[1] : i == 2 ? st.m[2] : st.m[3];
+        sm.merge.l[wave][i] = i == 0 ? l_run[0] : i == 1 ? l_run[1] : i == 2 ? l_run[2] : l_run[3];
+    }
+    if (n < 8) {
+#pragma unroll
+        for (int td = 0; td < NTD; td++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sm.merge.o[wave][n * OST + 16 * td + 4 * g + r] = st.o[td][r];
+    }
+    __syncthreads();
+
+    for (int idx = tid; idx < G * HD; idx += SPAN) {
+        const int hh = idx / HD, d = idx % HD;
+        float M = kMinit;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sm.merge.m[w][hh]);
+        if (fused) M = fmaxf(M, xnew[hh]);
+        float acc = 0.0f, lsum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float e = exp2f(sm.merge.m[w][hh] - M);
+            acc += e * (sm.merge.o[w][hh * OST + d] + sm.merge.o[w][(hh + 4) * OST + d]);
+            lsum += e * sm.merge.l[w][hh];
+        }
+        if (fused) {
+            const float e = exp2f(xnew[hh] - M);
+            acc += e * vd[d];
+            lsum += e;
+        }
+        const size_t head = (size_t)s * a.n_head + h * G + hh;
+        if (n_split_s == 1) {
+            a.out[head * HD + d] = lsum > 0.0f ? acc / lsum : 0.0f;
+        } else {
+            a.ws[(head * a.n_split + split) * HD + d] = acc;
+            if (d == 0) {
+                float *ml = a.ws + (size_t)L.S * a.n_head * a.n_split * HD;
+                ml[head * a.n_split + split] = M;
+                ml[(size_t)L.S * a.n_head * a.n_split + head * a.n_split + split] = lsum;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // Split plan: aim for ~kTargetWG workgroups in total so all 256 CUs get several, with each
@@ -622,14 +976,23 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.k_new = k_new;
     a.v_new = v_new;
     dim3 grid(plan.n_split, L.H, L.S);
+    const bool g4 = a.G <= 4 && !TS_DECODE_FORCE16;
     if (L.hd == 128) {
-        if (softcap > 0.0f)
+        if (g4 && softcap > 0.0f)
+            decode_split4_kernel<128, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
+        else if (g4)
+            decode_split4_kernel<128, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
+        else if (softcap > 0.0f)
             decode_split_kernel<128, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
         else
             decode_split_kernel<128, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
         if (plan.n_split > 1) decode_combine_kernel<128><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else if (L.hd == 64) {
-        if (softcap > 0.0f)
+        if (g4 && softcap > 0.0f)
+            decode_split4_kernel<64, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
+        else if (g4)
+            decode_split4_kernel<64, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
+        else if (softcap > 0.0f)
             decode_split_kernel<64, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
         else
             decode_split_kernel<64, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
