@@ -976,7 +976,10 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.k_new = k_new;
     a.v_new = v_new;
     dim3 grid(plan.n_split, L.H, L.S);
-    const bool g4 = a.G <= 4 && !TS_DECODE_FORCE16;
+    // The 4x4x4 QK kernel does less VALU work per window but has the longer per-window
+    // dependency chain (QK chains of 32 MFMAs, P through LDS): measured faster once every wave
+    // streams at least 4 windows per split, slower for short splits (batch-1 shapes).
+    const bool g4 = a.G <= 4 && plan.chunk >= 4 * 64 * TS_DECODE_NW && !TS_DECODE_FORCE16;
     if (L.hd == 128) {
         if (g4 && softcap > 0.0f)
             decode_split4_kernel<128, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);

@@ -297,6 +297,18 @@ def run_prefill(args, cfg):
     return dict(total_ms=total_ms, kernel_ms_layer=kernel_ms_layer, flops_layer=flops_layer)
 
 
+def _split_kernel_name(cfg):
+    """Which split kernel the library launches for this shape: decode_plan and the dispatch
+    rule of launch_decode (ts_decode.hip), restated for the bench label."""
+    max_ctx = cfg["ctx"] + 1  # upper bound of the step's longest context
+    units = cfg["batch"] * cfg["n_kv"]
+    want = max(1, -(-1024 // units))
+    want = min(want, -(-max_ctx // 256))
+    chunk = -(-(-(-max_ctx // want)) // 64) * 64
+    g4 = cfg["n_head"] // cfg["n_kv"] <= 4 and chunk >= 1024
+    return "decode_split4_kernel" if g4 else "decode_split_kernel"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -372,11 +384,12 @@ def main():
     roof = None
     if True:
         ach = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+        split_name = _split_kernel_name(cfg)
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "traffic_source": f"profiles/decode_cfg{args.config}.md" if traffic else None,
-                "kernel": ("decode_split_kernel<128>+decode_combine_kernel (ts_attn_decode)" if args.separate
-                           else "decode_split_kernel<128> with fused append + decode_combine_kernel (ts_attn_decode_append)"),
+                "kernel": (f"{split_name}<{cfg['hd']}>+decode_combine_kernel (ts_attn_decode)" if args.separate
+                           else f"{split_name}<{cfg['hd']}> with fused append + decode_combine_kernel (ts_attn_decode_append)"),
                 "bytes_per_launch": int(r["kernel_bytes"]),
                 "avg_launch_us": round(r["kernel_ms"] * 1e3, 2),
                 "timing": "HIP events around each decode launch, eager pass of 16 steps"}

@@ -101,3 +101,24 @@ def test_fused_equals_separate_calls(gpu):
     for s in range(3):
         for x, y in zip(a.gpu.export(0, s, 0, 1001), b.gpu.export(0, s, 0, 1001)):
             assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+
+
+@pytest.mark.parametrize("n_head,softcap", [(32, 0.0), (24, 0.0), (8, 30.0)])
+def test_long_splits(gpu, n_head, softcap):
+    """Shapes whose splits are long enough (>= 4 windows per wave) for the 4x4x4 QK kernel:
+    16 sequences x 8 kv heads at up to 8200 positions (split length 1088), ragged lengths on
+    and around the split edges, outlier channels, G = 4, 3 and 1."""
+    say(f"fused long splits n_head={n_head} softcap={softcap}")
+    rng = np.random.default_rng(103 + n_head)
+    n_kv, hd = 8, 128
+    dims = synth.outlier_dims(n_kv, hd, 7)
+    skv = synth.channel_scale(n_kv, n_kv, hd, dims)
+    sq = synth.channel_scale(n_head, n_kv, hd, dims)
+    lens = [8199, 8198, 4351, 1087, 1088, 1089, 2176, 3263, 5440, 6527, 7614, 100, 0, 2000, 4000, 6000]
+    p = Pair(len(lens), n_kv, hd, 8210, 1e6)
+    fill(p, rng, max(lens), skv[None, None], step=2048)
+    p.set_lens(lens)
+    for _ in range(2):
+        out, ref = fused_step(p, rng, n_head, skv[None, None], sq[None], softcap=softcap)
+        assert_close(out, ref, "fused long-split out")
+    p.check_codes()
