@@ -45,18 +45,22 @@ def lib():
         L.or_dequantize_row.restype = None
         L.or_append_batch.argtypes = [_u32p, _u32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p,
-                                      _f32p, _i32p, ctypes.c_int]
+                                      _f32p, _i32p, ctypes.c_int, _i32p, _i32p]
         L.or_append_batch.restype = None
         L.or_attend_batch.argtypes = [_u32p, _u32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       _f32p, _f32p, _i32p, ctypes.c_int, ctypes.c_float, _f32p,
-                                      ctypes.c_int]
+                                      ctypes.c_int, _i32p]
         L.or_attend_batch.restype = None
         L.or_attend_one.argtypes = [_u32p, _u32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                    ctypes.c_float, _f32p]
+                                    ctypes.c_float, _f32p, ctypes.c_int]
         L.or_attend_one.restype = None
+        L.or_shift_seq.argtypes = [_u32p, _u32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_int]
+        L.or_shift_seq.restype = None
         _lib = L
     return _lib
 
@@ -105,6 +109,9 @@ class OracleKV:
         self.table = np.ascontiguousarray(rope_table_arr, np.float32)
         self.rope_dim = self.table.shape[1] * 2
         self.lens = np.zeros(n_seq, np.int32)
+        # sliding-window compaction state (kv_cache.rs:41-46): window base and sink count
+        self.rot = np.zeros(n_seq, np.int32)
+        self.n_sink = np.zeros(n_seq, np.int32)
 
     def append(self, k: np.ndarray, v: np.ndarray):
         """k, v: [n_seq, n_tok, n_kv, hd] raw f32; written at each sequence's length."""
@@ -112,10 +119,10 @@ class OracleKV:
         v = np.ascontiguousarray(v, np.float32)
         n_tok = k.shape[1]
         assert (self.lens + n_tok <= self.max_seq).all()
-        assert (self.lens + n_tok <= self.table.shape[0]).all()
+        assert (self.lens + self.rot + n_tok <= self.table.shape[0]).all()
         lib().or_append_batch(self.k_packed, self.v_packed, self.k_scale, self.v_scale,
                               self.n_seq, self.max_seq, self.n_kv, self.hd, self.rope_dim,
-                              self.table, k, v, self.lens, n_tok)
+                              self.table, k, v, self.lens, n_tok, self.rot, self.n_sink)
 
     def attend(self, q: np.ndarray, n_tok: int, softcap: float = 0.0, threads: int = 1):
         """q: [n_seq, n_tok, n_head, hd] raw f32 for the n_tok tokens just appended (query
@@ -126,7 +133,7 @@ class OracleKV:
         lib().or_attend_batch(self.k_packed, self.v_packed, self.k_scale, self.v_scale,
                               self.n_seq, self.max_seq, n_head, self.n_kv, self.hd,
                               self.rope_dim, self.table, q, self.lens, n_tok, float(softcap),
-                              out, int(threads))
+                              out, int(threads), self.rot)
         return out
 
     def attend_one(self, q_seq: np.ndarray, seq: int, head: int, softcap: float = 0.0):
@@ -137,9 +144,23 @@ class OracleKV:
         out = np.zeros_like(q_seq)
         lib().or_attend_one(self.k_packed, self.v_packed, self.k_scale, self.v_scale,
                             self.max_seq, n_head, self.n_kv, self.hd, self.rope_dim, self.table,
-                            q_seq, int(self.lens[seq]), n_tok, seq, head, float(softcap), out)
+                            q_seq, int(self.lens[seq]), n_tok, seq, head, float(softcap), out,
+                            int(self.rot[seq]))
         return out[:, head]
 
     def advance(self, n_tok: int):
         """complete_decode / complete_prefill: lengths advance after all layers."""
         self.lens += n_tok
+
+    def shift(self, seq: int, keep_sink: int, shift_amt: int):
+        """RopeShiftPipeline::execute_int4 (pipeline_shift.rs:360-566) for one sequence of this
+        single-layer cache: slots keep_sink+shift_amt.. move down by shift_amt.  The caller then
+        advances the window base and sets the length, as the reference's caller does."""
+        lib().or_shift_seq(self.k_packed, self.v_packed, self.k_scale, self.v_scale,
+                           self.max_seq, self.n_kv, self.hd, int(seq), int(keep_sink),
+                           int(shift_amt), int(self.lens[seq]))
+        self.n_sink[seq] = keep_sink
+
+    def advance_window_base(self, seq: int, shift_amt: int):
+        """KVCache::advance_window_base (kv_cache.rs:277-279)."""
+        self.rot[seq] += shift_amt

@@ -19,6 +19,10 @@
  *                       with the store replaced by the INT4 quantizer (layout
  *                       src/backend/bindless/kv_cache.rs:26-37: packed [pos][n_kv][hd/8] u32,
  *                       scales [pos][n_kv] f32)
+ *   or_shift            src/backend/bindless/sh_rope_shift_int4.wgsl:44-84 with
+ *                       pipeline_shift.rs:360-566 (execute_int4): slide the INT4 rows down
+ *   rot_pos             kv_cache.rs:41-46,277-279 (window_base) with the post-RoPE storage
+ *                       of the CPU path: where each cache slot's K was rotated
  *   or_attend_head      src/ops/reference/attention.rs:236-313 (per-head QK^T, scale,
  *                       causal softmax, PV), src/ops/reference/matmul.rs:91-104 (f32 products
  *                       accumulated in f64), src/ops/reference/softmax.rs:91-129 (mask to -inf,
@@ -125,10 +129,16 @@ typedef struct {
     float *v_scale;
 } or_cache;
 
+/* Rotation position of cache slot `pos` after sliding-window compaction: slots below n_sink
+ * (the sinks, never moved) keep their own position; every other slot is rotated at
+ * pos + rot, rot being the sequence's window base (kv_cache.rs:41-46, advanced by the shift
+ * amount of every compaction, :277-279).  Without compaction rot = 0. */
+static int rot_pos(int pos, int rot, int n_sink) { return pos < n_sink ? pos : pos + rot; }
+
 /* Append n_tok tokens at positions pos0..pos0+n_tok-1.  k, v: [n_tok][n_kv][hd] raw f32.
  * K is rotated at its absolute position with the table (rope_dim <= hd), V is not. */
 void or_append(or_cache c, int n_kv, int hd, int rope_dim, const float *table,
-               const float *k, const float *v, int pos0, int n_tok) {
+               const float *k, const float *v, int pos0, int n_tok, int rot, int n_sink) {
     float *tmp = (float *)malloc(sizeof(float) * hd);
     int n_pairs = rope_dim / 2;
     for (int t = 0; t < n_tok; t++) {
@@ -137,7 +147,7 @@ void or_append(or_cache c, int n_kv, int hd, int rope_dim, const float *table,
             size_t src = ((size_t)t * n_kv + h) * hd;
             size_t row = (size_t)pos * n_kv + h;
             memcpy(tmp, k + src, sizeof(float) * hd);
-            or_rope_rotate(tmp, rope_dim, table + (size_t)pos * n_pairs * 2);
+            or_rope_rotate(tmp, rope_dim, table + (size_t)rot_pos(pos, rot, n_sink) * n_pairs * 2);
             or_quantize_row(tmp, hd, &c.k_scale[row], c.k_packed + row * (hd / 8));
             or_quantize_row(v + src, hd, &c.v_scale[row], c.v_packed + row * (hd / 8));
         }
@@ -149,9 +159,10 @@ void or_append(or_cache c, int n_kv, int hd, int rope_dim, const float *table,
 
 /* One (sequence, query head) over n_q_tok query tokens at absolute positions
  * q_pos0..q_pos0+n_q_tok-1; keys 0..q_pos0+n_q_tok-1 (causal).  q: [n_q_tok][n_head][hd] raw
- * (rotated here at the query position), out: [n_q_tok][n_head][hd]. */
+ * (rotated here at the query position plus the window base `rot`), out: [n_q_tok][n_head][hd]. */
 void or_attend_head(or_cache c, int n_head, int n_kv, int hd, int rope_dim, const float *table,
-                    const float *q, int q_pos0, int n_q_tok, int head, float softcap, float *out) {
+                    const float *q, int q_pos0, int n_q_tok, int head, float softcap, float *out,
+                    int rot) {
     int group = n_head / n_kv;
     int kvh = head / group;
     int key_len = q_pos0 + n_q_tok;
@@ -170,7 +181,7 @@ void or_attend_head(or_cache c, int n_head, int n_kv, int hd, int rope_dim, cons
     for (int t = 0; t < n_q_tok; t++) {
         int qpos = q_pos0 + t;
         memcpy(qr, q + ((size_t)t * n_head + head) * hd, sizeof(float) * hd);
-        or_rope_rotate(qr, rope_dim, table + (size_t)qpos * n_pairs * 2);
+        or_rope_rotate(qr, rope_dim, table + (size_t)(qpos + rot) * n_pairs * 2);
         for (int j = 0; j < key_len; j++) {
             double acc = 0.0;
             for (int d = 0; d < hd; d++) acc += (double)(qr[d] * kd[(size_t)j * hd + d]);
@@ -219,14 +230,16 @@ static or_cache seq_cache(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int 
     return c;
 }
 
-/* Append n_tok tokens to every sequence at its own length lens[s].  k, v: [n_seq][n_tok][n_kv][hd]. */
+/* Append n_tok tokens to every sequence at its own length lens[s].  k, v: [n_seq][n_tok][n_kv][hd].
+ * rot, n_sink: per-sequence window base and sink count (NULL: no compaction). */
 void or_append_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq, int max_seq,
                      int n_kv, int hd, int rope_dim, const float *table, const float *k,
-                     const float *v, const int32_t *lens, int n_tok) {
+                     const float *v, const int32_t *lens, int n_tok, const int32_t *rot,
+                     const int32_t *n_sink) {
     for (int s = 0; s < n_seq; s++) {
         size_t off = (size_t)s * n_tok * n_kv * hd;
         or_append(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_kv, hd, rope_dim, table,
-                  k + off, v + off, lens[s], n_tok);
+                  k + off, v + off, lens[s], n_tok, rot ? rot[s] : 0, n_sink ? n_sink[s] : 0);
     }
 }
 
@@ -235,14 +248,16 @@ void or_append_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq
  * faithful single-threaded loop; otherwise OpenMP over (sequence, head). */
 void or_attend_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq, int max_seq,
                      int n_head, int n_kv, int hd, int rope_dim, const float *table, const float *q,
-                     const int32_t *lens, int n_tok, float softcap, float *out, int n_threads) {
+                     const int32_t *lens, int n_tok, float softcap, float *out, int n_threads,
+                     const int32_t *rot) {
     long total = (long)n_seq * n_head;
     if (n_threads <= 1) {
         for (long i = 0; i < total; i++) {
             int s = (int)(i / n_head), h = (int)(i % n_head);
             size_t off = (size_t)s * n_tok * n_head * hd;
             or_attend_head(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_head, n_kv, hd,
-                           rope_dim, table, q + off, lens[s], n_tok, h, softcap, out + off);
+                           rope_dim, table, q + off, lens[s], n_tok, h, softcap, out + off,
+                           rot ? rot[s] : 0);
         }
         return;
     }
@@ -253,7 +268,7 @@ void or_attend_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq
         int s = (int)(i / n_head), h = (int)(i % n_head);
         size_t off = (size_t)s * n_tok * n_head * hd;
         or_attend_head(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_head, n_kv, hd, rope_dim,
-                       table, q + off, lens[s], n_tok, h, softcap, out + off);
+                       table, q + off, lens[s], n_tok, h, softcap, out + off, rot ? rot[s] : 0);
     }
 }
 
@@ -261,7 +276,40 @@ void or_attend_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq
  * heads at sizes where running every head would take minutes. */
 void or_attend_one(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int max_seq, int n_head,
                    int n_kv, int hd, int rope_dim, const float *table, const float *q_seq,
-                   int q_pos0, int n_tok, int seq, int head, float softcap, float *out_seq) {
+                   int q_pos0, int n_tok, int seq, int head, float softcap, float *out_seq,
+                   int rot) {
     or_attend_head(seq_cache(kp, vp, ks, vs, seq, max_seq, n_kv, hd), n_head, n_kv, hd, rope_dim,
-                   table, q_seq, q_pos0, n_tok, head, softcap, out_seq);
+                   table, q_seq, q_pos0, n_tok, head, softcap, out_seq, rot);
+}
+
+/* ---- sliding-window compaction ---------------------------------------------------------- */
+
+/* RopeShiftPipeline::execute_int4 / sh_rope_shift_int4.wgsl:44-84 for one sequence: slots
+ * keep_sink + shift_amt .. old_len-1 move down by shift_amt (packed K/V words and both
+ * scales, copied from a snapshot of the sources, as the reference copies from frozen
+ * scratch buffers); the sinks 0..keep_sink-1 stay.  Nothing is moved when
+ * old_len <= keep_sink + shift_amt (elements_to_shift saturates at 0, pipeline_shift.rs:381). */
+void or_shift(or_cache c, int n_kv, int hd, int keep_sink, int shift_amt, int old_len) {
+    int src0 = keep_sink + shift_amt;
+    if (old_len <= src0) return;
+    size_t n_move = (size_t)(old_len - src0) * n_kv, wpr = hd / 8;
+    uint32_t *kw = (uint32_t *)malloc(n_move * wpr * 4), *vw = (uint32_t *)malloc(n_move * wpr * 4);
+    float *ksn = (float *)malloc(n_move * 4), *vsn = (float *)malloc(n_move * 4);
+    memcpy(kw, c.k_packed + (size_t)src0 * n_kv * wpr, n_move * wpr * 4);
+    memcpy(vw, c.v_packed + (size_t)src0 * n_kv * wpr, n_move * wpr * 4);
+    memcpy(ksn, c.k_scale + (size_t)src0 * n_kv, n_move * 4);
+    memcpy(vsn, c.v_scale + (size_t)src0 * n_kv, n_move * 4);
+    memcpy(c.k_packed + (size_t)keep_sink * n_kv * wpr, kw, n_move * wpr * 4);
+    memcpy(c.v_packed + (size_t)keep_sink * n_kv * wpr, vw, n_move * wpr * 4);
+    memcpy(c.k_scale + (size_t)keep_sink * n_kv, ksn, n_move * 4);
+    memcpy(c.v_scale + (size_t)keep_sink * n_kv, vsn, n_move * 4);
+    free(kw);
+    free(vw);
+    free(ksn);
+    free(vsn);
+}
+
+void or_shift_seq(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int max_seq, int n_kv, int hd,
+                  int seq, int keep_sink, int shift_amt, int old_len) {
+    or_shift(seq_cache(kp, vp, ks, vs, seq, max_seq, n_kv, hd), n_kv, hd, keep_sink, shift_amt, old_len);
 }

@@ -301,3 +301,106 @@ def test_oracle_reproduces_golden_fixture():
     assert np.array_equal(kv.attend(g["q2"], 1), g["o_decode"])
     for name in ("k_packed", "v_packed", "k_scale", "v_scale"):
         assert np.array_equal(getattr(kv, name), g[name])
+
+
+# ---- sliding-window compaction (pipeline_shift.rs, kv_cache.rs window_base) ----------------------
+
+def _reference_relative_attention(q, k_raw, v, compact_q, window_base, n_sink, table, sink_count=4):
+    """sh_layer_v1_int4.wgsl:1062-1143 restated in float64 for one head: the reference keeps
+    K unrotated and applies RoPE(rel) in the score, with rel the compacted distance, except for
+    the sink slots (pos < SINK_COUNT), which use the logical distance window_base + qpos - pos."""
+    hd = q.shape[0]
+    L = k_raw.shape[0]
+    logical_q = window_base + compact_q
+    scores = np.empty(L)
+    for pos in range(L):
+        rel = (logical_q - pos) if pos < sink_count else (compact_q - pos)
+        c = table[rel, :, 0].astype(np.float64)
+        s = table[rel, :, 1].astype(np.float64)
+        qr, qi = q[0::2].astype(np.float64), q[1::2].astype(np.float64)
+        kr, ki = k_raw[pos, 0::2], k_raw[pos, 1::2]
+        scores[pos] = np.sum((qr * kr + qi * ki) * c + (qr * ki - qi * kr) * s) / math.sqrt(hd)
+    p = np.exp(scores - scores.max())
+    return (p / p.sum()) @ v
+
+
+def test_compaction_matches_reference_relative_rope():
+    """Two compactions and appends around them.  The oracle stores K rotated at its slot
+    position plus the window base (sinks at their own position) and rotates q at its slot
+    plus the window base; its outputs must equal the reference's relative-RoPE attention over
+    the compacted slots (compacted distances for window slots, logical distances for the
+    four sinks), with each slot's raw K recovered by rotating its dequantized K back."""
+    rng = np.random.default_rng(21)
+    n_kv, hd, n_head, max_seq = 2, 64, 4, 256
+    table = oracle.rope_table(1024, hd, 10000.0)
+    kv = oracle.OracleKV(1, max_seq, n_kv, hd, table)
+    angle = np.zeros((1, max_seq), np.int64)  # rotation position of every slot's stored K
+
+    def append(n):
+        k = rng.standard_normal((1, n, n_kv, hd), dtype=np.float32)
+        v = rng.standard_normal((1, n, n_kv, hd), dtype=np.float32)
+        kv.append(k, v)
+        for t in range(n):
+            pos = kv.lens[0] + t
+            angle[0, pos] = pos if pos < kv.n_sink[0] else pos + kv.rot[0]
+        kv.advance(n)
+
+    def shift(keep, amt):
+        old = int(kv.lens[0])
+        kv.shift(0, keep, amt)
+        angle[0, keep:old - amt] = angle[0, keep + amt:old].copy()
+        kv.advance_window_base(0, amt)
+        kv.lens[0] = old - amt
+
+    def check():
+        L = int(kv.lens[0])
+        q = rng.standard_normal((1, 1, n_head, hd), dtype=np.float32)
+        kv.lens[0] = L - 1  # the query is the last slot: attend over 0..L-1
+        out = kv.attend(q, 1)[0, 0]
+        kv.lens[0] = L
+        for head in range(n_head):
+            h = head // (n_head // n_kv)
+            k_raw = np.empty((L, hd))
+            vd = np.empty((L, hd))
+            for j in range(L):
+                kd = oracle.dequantize_row(kv.k_packed[0, j, h], kv.k_scale[0, j, h]).astype(np.float64)
+                c = table[angle[0, j], :, 0].astype(np.float64)
+                s = table[angle[0, j], :, 1].astype(np.float64)
+                a, b = kd[0::2], kd[1::2]
+                k_raw[j, 0::2] = a * c + b * s     # inverse rotation
+                k_raw[j, 1::2] = -a * s + b * c
+                vd[j] = oracle.dequantize_row(kv.v_packed[0, j, h], kv.v_scale[0, j, h])
+            ref = _reference_relative_attention(q[0, 0, head], k_raw, vd, L - 1, int(kv.rot[0]),
+                                                int(kv.n_sink[0]), table)
+            np.testing.assert_allclose(out[head], ref, rtol=1e-4, atol=1e-5)
+
+    append(150)
+    check()
+    shift(4, 60)
+    append(1)
+    check()
+    append(40)
+    shift(4, 37)
+    append(1)
+    check()
+    assert kv.rot[0] == 97 and kv.n_sink[0] == 4
+
+
+def test_shift_is_a_copy():
+    """sh_rope_shift_int4.wgsl:44-84: slots keep_sink+shift.. move down unchanged, sinks and
+    nothing else change; a shift past the length moves nothing."""
+    rng = np.random.default_rng(22)
+    kv = oracle.OracleKV(2, 64, 2, 64, oracle.rope_table(128, 64, 10000.0))
+    k = rng.standard_normal((2, 50, 2, 64), dtype=np.float32)
+    kv.append(k, k * 2)
+    kv.advance(50)
+    before = [a.copy() for a in (kv.k_packed, kv.v_packed, kv.k_scale, kv.v_scale)]
+    kv.shift(0, 4, 10)
+    for a, b in zip((kv.k_packed, kv.v_packed, kv.k_scale, kv.v_scale), before):
+        assert (a[0, :4] == b[0, :4]).all()
+        assert (a[0, 4:40] == b[0, 14:50]).all()
+        assert (a[0, 40:50] == b[0, 40:50]).all()  # stale tail, beyond the new length
+        assert (a[1] == b[1]).all()                # other sequence untouched
+    snap = [a.copy() for a in (kv.k_packed, kv.v_packed)]
+    kv.shift(1, 30, 30)  # 50 <= 60: nothing moves
+    assert all((a == b).all() for a, b in zip((kv.k_packed, kv.v_packed), snap))
