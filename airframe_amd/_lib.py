@@ -47,6 +47,10 @@ SIGNATURES = {
     "ts_kv_set_seq_len": (ctypes.c_int, [_vp, _i32, _i32, _vp]),
     "ts_kv_reset": (ctypes.c_int, [_vp, _vp]),
     "ts_kv_export": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "ts_kv_window_base": (ctypes.c_int, [_vp, _i32, _i32p]),
+    "ts_kv_advance_window_base": (ctypes.c_int, [_vp, _i32, _i32, _vp]),
+    "ts_kv_shift_workspace": (ctypes.c_int, [_vp, _u64p]),
+    "ts_kv_shift": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, ctypes.c_uint64, _vp]),
     "ts_append_quant": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i32, _vp, _vp]),
     "ts_requant_all": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp]),
     "ts_attn_decode_workspace": (ctypes.c_int, [_vp, _i32, _u64p]),

@@ -88,7 +88,8 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
             const int pi = min(lane + 64 * j, PAIRS - 1);
             if (rope && pi < rope_pairs)
                 rope_rotate(kx[ii][2 * j], kx[ii][2 * j + 1],
-                            *reinterpret_cast<const float2 *>(rope + ((size_t)pc * rope_pairs + pi) * 2));
+                            *reinterpret_cast<const float2 *>(
+                                rope + ((size_t)rot_pos(pc, L.rot[s], L.sink[s]) * rope_pairs + pi) * 2));
             km[ii] = fmaxf(km[ii], fmaxf(fabsf(kx[ii][2 * j]), fabsf(kx[ii][2 * j + 1])));
             vm[ii] = fmaxf(vm[ii], fmaxf(fabsf(vx[ii][2 * j]), fabsf(vx[ii][2 * j + 1])));
         }
@@ -198,17 +199,19 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
     const int lo = max(p0, start), hi = min(p0 + kBlk, end);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane >> 4, l = lane & 15;
     const size_t row = (size_t)s * L.H + h;
+    const int rot = L.rot[s], sink = L.sink[s];
 
     float kx[2][8], vx[2][8];
     float2 cs[2][4];  // rotation of each pair (identity without a table or past rope_dim)
 #pragma unroll
     for (int rd = 0; rd < 2; rd++) {
         const int pc = min(max(p0 + 16 * rd + 4 * wave + r, lo), hi - 1);
+        const int pr = rot_pos(pc, rot, sink);
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const int pair = 4 * l + m;
             cs[rd][m] = (rope && pair < rope_pairs)
-                            ? *reinterpret_cast<const float2 *>(rope + ((size_t)pc * rope_pairs + pair) * 2)
+                            ? *reinterpret_cast<const float2 *>(rope + ((size_t)pr * rope_pairs + pair) * 2)
                             : make_float2(1.0f, 0.0f);
         }
         const float4 *ks4 = reinterpret_cast<const float4 *>(k + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD + 8 * l);
@@ -354,6 +357,55 @@ __global__ void export_kernel(KvLayerView L, int seq, int pos0, int n_pos, uint3
     }
 }
 
+// Inverse of export_kernel: positions pos0..pos0+n_pos-1 of one sequence and layer from the
+// reference layout.  K words and scales: one thread per (position, kv head, word).
+template <int HD>
+__global__ void import_k_kernel(KvLayerView L, int seq, int pos0, int n_pos, const uint32_t *kp,
+                                const float *ks, const float *vs) {
+    constexpr int WPR = HD / 8;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long total = (long)n_pos * L.H * WPR;
+    if (idx >= total) return;
+    const int u = idx % WPR;
+    const int h = (idx / WPR) % L.H;
+    const int p = pos0 + (int)(idx / (WPR * L.H));
+    const size_t row = (size_t)seq * L.H + h;
+    reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[u] = kp[idx];
+    if (u == 0) {
+        L.ks[row * L.P + p] = ks[idx / WPR];
+        L.vs[row * L.P + p] = vs[idx / WPR];
+    }
+}
+
+// V words of the 32-position blocks the range touches: one thread per (kv head, block, word);
+// each nibble comes from the reference-layout source if its position is in the range and is
+// kept otherwise.  Word (g, dl, td) of a block holds dim 16 td + dl at positions 4g + n
+// (n < 4) and 16 + 4g + n - 4 (n >= 4).
+template <int HD>
+__global__ void import_v_kernel(KvLayerView L, int seq, int pos0, int n_pos, const uint32_t *vp) {
+    constexpr int NTD = HD / 16, WPB = HD * 4;  // words per block
+    const int b0 = pos0 / 32, nb = (pos0 + n_pos - 1) / 32 - b0 + 1;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)L.H * nb * WPB) return;
+    const int w = idx % WPB;
+    const int b = b0 + (int)((idx / WPB) % nb);
+    const int h = (int)(idx / ((long)WPB * nb));
+    const int g = w / (16 * NTD), dl = (w / NTD) % 16, td = w % NTD;
+    const int d = 16 * td + dl;
+    const size_t row = (size_t)seq * L.H + h;
+    uint32_t *dst = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / 32) + b) * (HD * 16)) + w;
+    uint32_t word = *dst;
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const int p = 32 * b + (n < 4 ? 4 * g + n : 16 + 4 * g + n - 4);
+        if (p >= pos0 && p < pos0 + n_pos) {
+            const uint32_t src = vp[((size_t)(p - pos0) * L.H + h) * (HD / 8) + d / 8];
+            word = (word & ~(0xFu << (4 * n))) | (((src >> (4 * (d % 8))) & 0xFu) << (4 * n));
+        }
+    }
+    *dst = word;
+}
+
 // mode 0: all lengths += value; mode 1: set (seq < 0: all sequences).
 __global__ void len_update_kernel(int32_t *len, int n, int32_t seq, int32_t value, int mode) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -388,6 +440,23 @@ hipError_t launch_export(const KvLayerView &L, int seq, int pos0, int n_pos, uin
         export_kernel<64><<<blocks, 256, 0, st>>>(L, seq, pos0, n_pos, kp, vp, ks, vs);
     else
         return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_import(const KvLayerView &L, int seq, int pos0, int n_pos, const uint32_t *kp,
+                         const uint32_t *vp, const float *ks, const float *vs, hipStream_t st) {
+    const long nk = (long)n_pos * L.H * (L.hd / 8);
+    const int nb = (pos0 + n_pos - 1) / 32 - pos0 / 32 + 1;
+    const long nv = (long)L.H * nb * L.hd * 4;
+    if (L.hd == 128) {
+        import_k_kernel<128><<<(int)((nk + 255) / 256), 256, 0, st>>>(L, seq, pos0, n_pos, kp, ks, vs);
+        import_v_kernel<128><<<(int)((nv + 255) / 256), 256, 0, st>>>(L, seq, pos0, n_pos, vp);
+    } else if (L.hd == 64) {
+        import_k_kernel<64><<<(int)((nk + 255) / 256), 256, 0, st>>>(L, seq, pos0, n_pos, kp, ks, vs);
+        import_v_kernel<64><<<(int)((nv + 255) / 256), 256, 0, st>>>(L, seq, pos0, n_pos, vp);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

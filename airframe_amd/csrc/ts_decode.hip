@@ -278,7 +278,8 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
         const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
         k0 = kk.x; k1 = kk.y; v0 = vv.x; v1 = vv.y;
         if (i < a.rope_pairs)
-            rope_rotate(k0, k1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)p * a.rope_pairs + i) * 2));
+            rope_rotate(k0, k1, *reinterpret_cast<const float2 *>(
+                                    a.rope + ((size_t)rot_pos(p, L.rot[s], L.sink[s]) * a.rope_pairs + i) * 2));
     }
     const float ks = quant_scale(wave_max(fmaxf(fabsf(k0), fabsf(k1))));
     const float vs = quant_scale(wave_max(fmaxf(fabsf(v0), fabsf(v1))));
@@ -323,6 +324,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     const KvLayerView &L = a.L;
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int qpos = a.len[s];
+    const int qrot = rot_pos(qpos, a.L.rot[s], a.L.sink[s]);  // rotation position of the query
     const int n_ctx = qpos + 1;
     const int start = split * a.chunk;
     if (start >= n_ctx) return;
@@ -393,7 +395,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     }
     for (int t = wave; t < WPG; t += NW) {
         half8 qh, ql;
-        load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qpos, a.inv_sqrt_hd * kLog2e * q_s, qh, ql);
+        load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qrot, a.inv_sqrt_hd * kLog2e * q_s, qh, ql);
         sm.run.q.p[t][lane] = !live ? (half8)(_Float16)0.0f : (lo_col ? ql : qh);
     }
     if (fused && wave == 0) append_one<HD>(a, s, h, qpos, lane, kd, vd);
@@ -405,7 +407,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
             const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
             float q0 = qq.x, q1 = qq.y;
             if (i < a.rope_pairs)
-                rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qpos * a.rope_pairs + i) * 2));
+                rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + i) * 2));
             float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
@@ -773,6 +775,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     const KvLayerView &L = a.L;
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int qpos = a.len[s];
+    const int qrot = rot_pos(qpos, a.L.rot[s], a.L.sink[s]);  // rotation position of the query
     const int n_ctx = qpos + 1;
     const int start = split * a.chunk;
     if (start >= n_ctx) return;
@@ -822,7 +825,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
         for (int c = 0; c < NQ; c++) {
             const int t = 16 * c + blk;
             half8 hh8, ll8;
-            load_q8(a.rope, a.rope_pairs, qrow, t >> 1, qpos, a.inv_sqrt_hd * kLog2e * q_s, hh8, ll8);
+            load_q8(a.rope, a.rope_pairs, qrow, t >> 1, qrot, a.inv_sqrt_hd * kLog2e * q_s, hh8, ll8);
             const int o4 = 4 * (t & 1);
             half4_t hv = {hh8[o4], hh8[o4 + 1], hh8[o4 + 2], hh8[o4 + 3]};
             half4_t lv = {ll8[o4], ll8[o4 + 1], ll8[o4 + 2], ll8[o4 + 3]};
@@ -838,7 +841,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
             const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
             float q0 = qq.x, q1 = qq.y;
             if (i < a.rope_pairs)
-                rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qpos * a.rope_pairs + i) * 2));
+                rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + i) * 2));
             float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);

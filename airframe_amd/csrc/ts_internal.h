@@ -32,8 +32,14 @@ struct KvLayerView {
     uint8_t *vp;  // V packed
     float *ks;    // K scales
     float *vs;    // V scales
+    // Per sequence: window base (the shift total of all compactions) and sink count.  The K
+    // of slot p is stored rotated at rot_pos(p): p for the sinks, p + window base otherwise.
+    const int32_t *rot;
+    const int32_t *sink;
     int S, H, P, hd;
 };
+
+__device__ __host__ inline int rot_pos(int p, int rot, int sink) { return p < sink ? p : p + rot; }
 
 }  // namespace ts
 
@@ -42,8 +48,10 @@ struct ts_kv {
     int P;                    // padded positions per (seq, head)
     uint64_t layer_bytes;
     uint8_t *base;            // one allocation for all layers
-    int32_t *d_len;           // device mirror of lengths
-    std::vector<int32_t> h_len;
+    int32_t *d_len;           // device mirror of lengths [n_seq], then window bases [n_seq]
+                              // and sink counts [n_seq] (d_rot, d_sink)
+    int32_t *d_rot, *d_sink;
+    std::vector<int32_t> h_len, h_rot, h_sink;
     int device;
 
     ts::KvLayerView layer(int l) const {
@@ -54,6 +62,8 @@ struct ts_kv {
         v.vp = b + nrow * (d.head_dim / 2);
         v.ks = (float *)(b + nrow * d.head_dim);
         v.vs = v.ks + nrow;
+        v.rot = d_rot;
+        v.sink = d_sink;
         v.S = d.n_seq;
         v.H = d.n_head_kv;
         v.P = P;
@@ -77,6 +87,8 @@ hipError_t launch_quantize_rows(const KvLayerView &L, const float *k, const floa
                                 int32_t max_blocks, hipStream_t st);
 hipError_t launch_export(const KvLayerView &L, int seq, int pos0, int n_pos, uint32_t *kp,
                          uint32_t *vp, float *ks, float *vs, hipStream_t st);
+hipError_t launch_import(const KvLayerView &L, int seq, int pos0, int n_pos, const uint32_t *kp,
+                         const uint32_t *vp, const float *ks, const float *vs, hipStream_t st);
 hipError_t launch_len_update(int32_t *d_len, int n, int32_t seq, int32_t value, int mode,
                              hipStream_t st);
 

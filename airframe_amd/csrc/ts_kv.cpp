@@ -119,6 +119,17 @@ int ts_rope_info(const ts_rope *rope, const float **d_table, int32_t *n_pos, int
 
 // ---- cache -----------------------------------------------------------------------------------
 
+// The kernels move f32 rows in 16-byte pieces.
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Largest rotation position (exclusive) the next n_tok tokens of any sequence use: slots past
+// the sinks are rotated at slot + window base.
+static int64_t rot_end(const ts_kv *kv, int32_t n_tok) {
+    int64_t m = 0;
+    for (int s = 0; s < kv->d.n_seq; s++) m = std::max<int64_t>(m, (int64_t)kv->h_len[s] + kv->h_rot[s] + n_tok);
+    return m;
+}
+
 int ts_kv_bytes(const ts_kv_desc *desc, uint64_t *bytes) {
     if (!desc_valid(desc) || !bytes) return TS_ERR_INVALID;
     *bytes = layer_bytes_of(desc) * (uint64_t)desc->n_layers;
@@ -136,6 +147,8 @@ int ts_kv_create(const ts_kv_desc *desc, ts_kv **out) {
     kv->P = padded_positions(desc->max_seq);
     kv->layer_bytes = layer_bytes_of(desc);
     kv->h_len.assign(desc->n_seq, 0);
+    kv->h_rot.assign(desc->n_seq, 0);
+    kv->h_sink.assign(desc->n_seq, 0);
     if (hipGetDevice(&kv->device) != hipSuccess) {
         delete kv;
         return TS_ERR_HIP;
@@ -145,20 +158,22 @@ int ts_kv_create(const ts_kv_desc *desc, ts_kv **out) {
         delete kv;
         return TS_ERR_NOMEM;
     }
-    if (hipMalloc(&kv->d_len, sizeof(int32_t) * desc->n_seq) != hipSuccess) {
+    if (hipMalloc(&kv->d_len, sizeof(int32_t) * 3 * desc->n_seq) != hipSuccess) {
         hipFree(kv->base);
         delete kv;
         return TS_ERR_NOMEM;
     }
     // Zero fill once at creation: unwritten positions then dequantize to finite values.
     if (hipMemset(kv->base, 0, total) != hipSuccess ||
-        hipMemset(kv->d_len, 0, sizeof(int32_t) * desc->n_seq) != hipSuccess ||
+        hipMemset(kv->d_len, 0, sizeof(int32_t) * 3 * desc->n_seq) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         hipFree(kv->base);
         hipFree(kv->d_len);
         delete kv;
         return TS_ERR_HIP;
     }
+    kv->d_rot = kv->d_len + desc->n_seq;
+    kv->d_sink = kv->d_len + 2 * desc->n_seq;
     *out = kv;
     return TS_OK;
 }
@@ -211,10 +226,64 @@ int ts_kv_set_seq_len(ts_kv *kv, int32_t seq, int32_t len, void *stream) {
 
 int ts_kv_reset(ts_kv *kv, void *stream) {
     if (!kv) return TS_ERR_INVALID;
-    hipError_t e = ts::launch_len_update(kv->d_len, kv->d.n_seq, -1, 0, 1, as_stream(stream));
+    // lengths, window bases and sink counts: 3 n_seq consecutive ints
+    hipError_t e = ts::launch_len_update(kv->d_len, 3 * kv->d.n_seq, -1, 0, 1, as_stream(stream));
     if (e != hipSuccess) return TS_ERR_HIP;
     std::fill(kv->h_len.begin(), kv->h_len.end(), 0);
+    std::fill(kv->h_rot.begin(), kv->h_rot.end(), 0);
+    std::fill(kv->h_sink.begin(), kv->h_sink.end(), 0);
     return TS_OK;
+}
+
+int ts_kv_window_base(const ts_kv *kv, int32_t seq, int32_t *base) {
+    if (!kv || !base || seq < 0 || seq >= kv->d.n_seq) return TS_ERR_INVALID;
+    *base = kv->h_rot[seq];
+    return TS_OK;
+}
+
+int ts_kv_advance_window_base(ts_kv *kv, int32_t seq, int32_t shift_amt, void *stream) {
+    if (!kv || seq < 0 || seq >= kv->d.n_seq || shift_amt < 0) return TS_ERR_INVALID;
+    if ((int64_t)kv->h_rot[seq] + shift_amt > INT32_MAX / 2) return TS_ERR_OVERFLOW;
+    if (shift_amt == 0) return TS_OK;
+    hipError_t e = ts::launch_len_update(kv->d_rot, kv->d.n_seq, seq, shift_amt, 0, as_stream(stream));
+    if (e != hipSuccess) return TS_ERR_HIP;
+    kv->h_rot[seq] += shift_amt;
+    return TS_OK;
+}
+
+int ts_kv_shift_workspace(const ts_kv *kv, uint64_t *bytes) {
+    if (!kv || !bytes) return TS_ERR_INVALID;
+    // positions x heads x (K and V words, two scales), reference layout
+    *bytes = (uint64_t)kv->d.max_seq * kv->d.n_head_kv * (kv->d.head_dim + 8);
+    return TS_OK;
+}
+
+int ts_kv_shift(ts_kv *kv, int32_t layer, int32_t seq, int32_t keep_sink, int32_t shift_amt,
+                void *d_workspace, uint64_t workspace_bytes, void *stream) {
+    if (!kv || layer < 0 || layer >= kv->d.n_layers || seq < 0 || seq >= kv->d.n_seq ||
+        keep_sink < 0 || shift_amt < 0 || keep_sink > kv->d.max_seq)
+        return TS_ERR_INVALID;
+    // one sink count per sequence: the slots below it are never moved, so their K keeps the
+    // rotation of its own position
+    if ((kv->h_sink[seq] != 0 || kv->h_rot[seq] != 0) && kv->h_sink[seq] != keep_sink)
+        return TS_ERR_INVALID;
+    const int64_t n_move = (int64_t)kv->h_len[seq] - keep_sink - shift_amt;
+    if (n_move <= 0 || shift_amt == 0) return TS_OK;  // elements_to_shift == 0: nothing moves
+    const uint64_t wpp = (uint64_t)kv->d.n_head_kv * (kv->d.head_dim / 8);  // words per position
+    const uint64_t need = (uint64_t)n_move * kv->d.n_head_kv * (kv->d.head_dim + 8);
+    if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
+    if (!aligned16(d_workspace)) return TS_ERR_INVALID;
+    uint32_t *kp = (uint32_t *)d_workspace, *vp = kp + n_move * wpp;
+    float *ks = (float *)(vp + n_move * wpp), *vs = ks + n_move * kv->d.n_head_kv;
+    hipStream_t st = as_stream(stream);
+    const ts::KvLayerView L = kv->layer(layer);
+    hipError_t e = ts::launch_export(L, seq, keep_sink + shift_amt, (int)n_move, kp, vp, ks, vs, st);
+    if (e == hipSuccess) e = ts::launch_import(L, seq, keep_sink, (int)n_move, kp, vp, ks, vs, st);
+    if (e == hipSuccess && kv->h_sink[seq] != keep_sink) {
+        e = ts::launch_len_update(kv->d_sink, kv->d.n_seq, seq, keep_sink, 1, st);
+        if (e == hipSuccess) kv->h_sink[seq] = keep_sink;
+    }
+    return hip_status(e);
 }
 
 int ts_kv_export(const ts_kv *kv, int32_t layer, int32_t seq, int32_t pos0, int32_t n_pos,
@@ -238,8 +307,6 @@ static int check_rope(const ts_rope *rope, int hd, int64_t max_pos_exclusive) {
     return TS_OK;
 }
 
-// The kernels move f32 rows in 16-byte pieces.
-static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 int ts_append_quant(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v, int32_t n_tok,
                     const ts_rope *rope, void *stream) {
@@ -248,7 +315,7 @@ int ts_append_quant(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v
         return TS_ERR_INVALID;
     int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
     if ((int64_t)max_len + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;
-    int rc = check_rope(rope, kv->d.head_dim, (int64_t)max_len + n_tok);
+    int rc = check_rope(rope, kv->d.head_dim, rot_end(kv, n_tok));
     if (rc) return rc;
     if (n_tok == 0) return TS_OK;
     // Blocks of 32 positions touched by [len, len+n_tok): at most n_tok/32 + 2.
@@ -265,7 +332,8 @@ int ts_requant_all(ts_kv *kv, int32_t layer, const float *d_k_cache, const float
         return TS_ERR_INVALID;
     if (seq_len > kv->d.max_seq) return TS_ERR_OVERFLOW;
     if (rope) {
-        int rc = check_rope(rope, kv->d.head_dim, seq_len);
+        int32_t max_rot = *std::max_element(kv->h_rot.begin(), kv->h_rot.end());
+        int rc = check_rope(rope, kv->d.head_dim, (int64_t)seq_len + max_rot);
         if (rc) return rc;
     }
     if (seq_len == 0) return TS_OK;
@@ -297,7 +365,7 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
         return TS_ERR_INVALID;
     int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
     if (max_len + 1 > kv->d.max_seq) return TS_ERR_OVERFLOW;
-    int rc = check_rope(rope, kv->d.head_dim, (int64_t)max_len + 1);
+    int rc = check_rope(rope, kv->d.head_dim, rot_end(kv, 1));
     if (rc) return rc;
     uint64_t need = 0;
     ts_attn_decode_workspace(kv, n_head, &need);
@@ -333,7 +401,7 @@ int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_
         return TS_ERR_INVALID;
     int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
     if ((int64_t)max_len + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;
-    int rc = check_rope(rope, kv->d.head_dim, (int64_t)max_len + n_tok);
+    int rc = check_rope(rope, kv->d.head_dim, rot_end(kv, n_tok));
     if (rc) return rc;
     if (n_tok == 0) return TS_OK;
     return hip_status(ts::launch_prefill(kv->layer(layer), kv->d_len, d_q, n_head, n_tok,

@@ -119,6 +119,46 @@ class KVCache:
     def reset(self, stream=None):
         check("ts_kv_reset", load().ts_kv_reset(self._h, _stream(stream)))
 
+    # ---- sliding-window compaction (pipeline_shift.rs, kv_cache.rs window_base) ---------
+
+    def get_window_base(self, seq: int = 0) -> int:
+        """KVCache::get_window_base (kv_cache.rs:241-243)."""
+        v = ctypes.c_int32()
+        check("ts_kv_window_base", load().ts_kv_window_base(self._h, seq, ctypes.byref(v)))
+        return v.value
+
+    def advance_window_base(self, shift_amt: int, seq: int = 0, stream=None):
+        """KVCache::advance_window_base (kv_cache.rs:277-279)."""
+        check("ts_kv_advance_window_base",
+              load().ts_kv_advance_window_base(self._h, seq, shift_amt, _stream(stream)))
+
+    def shift_int4(self, layer: int, keep_sink: int, shift_amt: int, seq: int = 0,
+                   workspace: torch.Tensor = None, stream=None):
+        """RopeShiftPipeline::execute_int4 (pipeline_shift.rs:360-566) for one layer of one
+        sequence: slots keep_sink+shift_amt.. move down by shift_amt, sinks stay."""
+        if workspace is None:
+            if "shift" not in self._ws:
+                b = ctypes.c_uint64()
+                check("ts_kv_shift_workspace", load().ts_kv_shift_workspace(self._h, ctypes.byref(b)))
+                self._ws["shift"] = torch.empty(max(b.value, 16), dtype=torch.uint8, device="cuda")
+            workspace = self._ws["shift"]
+        check("ts_kv_shift",
+              load().ts_kv_shift(self._h, layer, seq, keep_sink, shift_amt,
+                                 ctypes.c_void_p(workspace.data_ptr()), workspace.numel(),
+                                 _stream(stream)))
+
+    def compact(self, keep_sink: int, shift_amt: int, seq: int = 0, stream=None):
+        """The helical-compaction sequence of the reference's caller for one sequence: every
+        layer shifted, then advance_window_base and set_seq_len(len - shift_amt).  Does nothing
+        when len <= keep_sink + shift_amt."""
+        n = self.get_seq_len(seq)
+        if n <= keep_sink + shift_amt or shift_amt == 0:
+            return
+        for layer in range(self.n_layers):
+            self.shift_int4(layer, keep_sink, shift_amt, seq, stream=stream)
+        self.advance_window_base(shift_amt, seq, stream)
+        self.set_seq_len(n - shift_amt, seq, stream)
+
     # ---- hot path ----------------------------------------------------------------------
 
     def append_quant(self, layer: int, k: torch.Tensor, v: torch.Tensor, rope: RopeTable,

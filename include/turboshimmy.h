@@ -101,7 +101,8 @@ int ts_kv_increment(ts_kv *kv, int32_t n_tok, void *stream);
  * the reference's panic).  Used for ragged batches. */
 int ts_kv_set_seq_len(ts_kv *kv, int32_t seq, int32_t len, void *stream);
 
-/* KVCache::reset (kv_cache.rs:256-259): all lengths to 0; buffers stay allocated. */
+/* KVCache::reset (kv_cache.rs:256-259): all lengths, window bases and sink counts to 0;
+ * buffers stay allocated. */
 int ts_kv_reset(ts_kv *kv, void *stream);
 
 /* Copy positions [pos0, pos0+n_pos) of one sequence and layer out of the cache into the
@@ -111,6 +112,31 @@ int ts_kv_reset(ts_kv *kv, void *stream);
 int ts_kv_export(const ts_kv *kv, int32_t layer, int32_t seq, int32_t pos0, int32_t n_pos,
                  uint32_t *d_k_packed, uint32_t *d_v_packed, float *d_k_scale, float *d_v_scale,
                  void *stream);
+
+/* ---- sliding-window compaction ------------------------------------------------------------- */
+
+/* KVCache::get_window_base / advance_window_base (kv_cache.rs:241-243, :277-279) for one
+ * sequence: the total shift of all compactions so far.  The K of every slot at or past the
+ * sequence's sink count is stored rotated at (slot + window base), so appends after a
+ * compaction rotate K there and queries are rotated at (position + window base): window keys
+ * then see the compacted distance and the sinks the logical one, as in
+ * sh_layer_v1_int4.wgsl:1062-1080.  Call advance after ts_kv_shift of every layer, then
+ * ts_kv_set_seq_len(len - shift_amt), as the reference's caller does. */
+int ts_kv_window_base(const ts_kv *kv, int32_t seq, int32_t *base);
+int ts_kv_advance_window_base(ts_kv *kv, int32_t seq, int32_t shift_amt, void *stream);
+
+/* Device bytes of scratch ts_kv_shift needs at most (a snapshot of the moved slots). */
+int ts_kv_shift_workspace(const ts_kv *kv, uint64_t *bytes);
+
+/* RopeShiftPipeline::execute_int4 (pipeline_shift.rs:360-566, sh_rope_shift_int4.wgsl:44-84)
+ * for one layer of one sequence: slots keep_sink + shift_amt .. len-1 move down by shift_amt
+ * (packed K and V and both scales, copied unchanged through a snapshot in d_workspace); the
+ * keep_sink sinks stay.  Nothing moves when len <= keep_sink + shift_amt.  The first call on a
+ * sequence records keep_sink as its sink count; a different keep_sink later is TS_ERR_INVALID
+ * (slots below the sink count keep the rotation of their own position).  Lengths and the
+ * window base do not change. */
+int ts_kv_shift(ts_kv *kv, int32_t layer, int32_t seq, int32_t keep_sink, int32_t shift_amt,
+                void *d_workspace, uint64_t workspace_bytes, void *stream);
 
 /* ---- hot path ------------------------------------------------------------------------------ */
 
