@@ -297,6 +297,47 @@ def run_prefill(args, cfg):
     return dict(total_ms=total_ms, kernel_ms_layer=kernel_ms_layer, flops_layer=flops_layer)
 
 
+def run_compact(args, cfg):
+    """Sliding-window compaction (ts_kv_shift) on a cache of the configuration's shape: every
+    sequence of every layer filled to ctx, then each sequence compacted (keep_sink 4, shift
+    ctx/2) layer by layer.  Returns the time of the shifts and the bytes they move: the moved
+    slots' K/V words and scales read once from the cache and written once into the workspace
+    snapshot, then read from the snapshot and written to their new slots."""
+    import torch
+
+    from airframe_amd.kv_cache import KVCache, RopeTable
+
+    dev = torch.device("cuda:0")
+    L, n_kv, hd, B, ctx = cfg["layers"], cfg["n_kv"], cfg["hd"], cfg["batch"], cfg["ctx"]
+    rope = RopeTable(2 * ctx + 8, hd, cfg["theta"])
+    kv = KVCache.new_int4(L, n_kv, hd, ctx + 8, B)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    for layer in range(L):
+        kv.reset()
+        for t0 in range(0, ctx, 1024):
+            m = min(1024, ctx - t0)
+            k = torch.randn((B, m, n_kv, hd), generator=gen, device=dev)
+            kv.append_quant(layer, k, k, rope)
+            kv.increment(m)
+    keep, amt = 4, ctx // 2
+    n_move = ctx - keep - amt
+    ws = torch.empty(kv.max_len() * n_kv * (hd + 8), dtype=torch.uint8, device=dev)
+    # warm-up shift on layer 0, sequence 0 (moves data, which is all this measures)
+    kv.shift_int4(0, keep, amt, 0, workspace=ws)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for s in range(B):
+        for layer in range(L):
+            kv.shift_int4(layer, keep, amt, s, workspace=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    per = n_move * n_kv * (hd + 8)  # one (sequence, layer): the moved slots' bytes
+    return ms, 4 * per * B * L, B * L
+
+
 def _split_kernel_name(cfg):
     """Which split kernel the library launches for this shape: decode_plan and the dispatch
     rule of launch_decode (ts_decode.hip), restated for the bench label."""
@@ -322,6 +363,9 @@ def main():
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 1 GiB device copy (4 launches) so rocprofv3 HBM counters "
                          "can be scaled by what they read for a copy of known size")
+    ap.add_argument("--compact", action="store_true",
+                    help="measure sliding-window compaction (ts_kv_shift) on the config's cache "
+                         "instead of the decode step")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="launch every kernel eagerly instead of replaying captured HIP graphs")
     args = ap.parse_args()
@@ -340,6 +384,23 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
     torch.cuda.set_device(0)
+    if args.compact:
+        if "ctx" not in cfg:
+            sys.exit("--compact needs a decode configuration (1-4)")
+        ms, moved, calls = run_compact(args, cfg)
+        gbs = moved / (ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "INT4 KV sliding-window compaction HBM GB/s", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+            "ms_total": round(ms, 3), "us_per_shift": round(ms * 1e3 / calls, 2),
+            "config": {"workload": cfg["name"] + "_compact_keep4_shift_half", "shifts": calls},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "bytes_per_shift": moved // calls,
+                         "counting": "moved slots' K/V words + scales: read, snapshot written, "
+                                     "snapshot read, written to the new slots (4x)"},
+            "data": "synthetic"}), flush=True)
+        return
     # HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated) for
     # this configuration, as recorded in its profile summary; null when none was taken.
     traffic = None
