@@ -45,24 +45,34 @@ def lib():
         L.or_dequantize_row.restype = None
         L.or_append_batch.argtypes = [_u32p, _u32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p,
-                                      _f32p, _i32p, ctypes.c_int, _i32p, _i32p]
+                                      _f32p, _i32p, ctypes.c_int, _i32p, _i32p, ctypes.c_void_p,
+                                      ctypes.c_float]
         L.or_append_batch.restype = None
         L.or_attend_batch.argtypes = [_u32p, _u32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       _f32p, _f32p, _i32p, ctypes.c_int, ctypes.c_float, _f32p,
-                                      ctypes.c_int, _i32p]
+                                      ctypes.c_int, _i32p, ctypes.c_void_p, ctypes.c_float]
         L.or_attend_batch.restype = None
         L.or_attend_one.argtypes = [_u32p, _u32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                    ctypes.c_float, _f32p, ctypes.c_int]
+                                    ctypes.c_float, _f32p, ctypes.c_int, ctypes.c_void_p, ctypes.c_float]
         L.or_attend_one.restype = None
+        L.or_qk_norm_row.argtypes = [_f32p, ctypes.c_int, _f32p, ctypes.c_float]
+        L.or_qk_norm_row.restype = None
         L.or_shift_seq.argtypes = [_u32p, _u32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_int]
         L.or_shift_seq.restype = None
         _lib = L
     return _lib
+
+
+def qk_norm_row(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """apply_qk_norm (attention.rs:92-108) of one head vector through the C oracle."""
+    out = np.ascontiguousarray(x, np.float32).copy()
+    lib().or_qk_norm_row(out, out.size, np.ascontiguousarray(w, np.float32), float(eps))
+    return out
 
 
 def rope_table(n_pos: int, rope_dim: int, base: float, scale: float = 1.0) -> np.ndarray:
@@ -112,6 +122,10 @@ class OracleKV:
         # sliding-window compaction state (kv_cache.rs:41-46): window base and sink count
         self.rot = np.zeros(n_seq, np.int32)
         self.n_sink = np.zeros(n_seq, np.int32)
+        # Qwen3 QK norm (attention.rs:92-108, :186-189): per-dim weights or None, eps 1e-6
+        self.q_norm = None
+        self.k_norm = None
+        self.norm_eps = 1e-6
 
     def append(self, k: np.ndarray, v: np.ndarray):
         """k, v: [n_seq, n_tok, n_kv, hd] raw f32; written at each sequence's length."""
@@ -122,7 +136,8 @@ class OracleKV:
         assert (self.lens + self.rot + n_tok <= self.table.shape[0]).all()
         lib().or_append_batch(self.k_packed, self.v_packed, self.k_scale, self.v_scale,
                               self.n_seq, self.max_seq, self.n_kv, self.hd, self.rope_dim,
-                              self.table, k, v, self.lens, n_tok, self.rot, self.n_sink)
+                              self.table, k, v, self.lens, n_tok, self.rot, self.n_sink,
+                              self._w(self.k_norm), float(self.norm_eps))
 
     def attend(self, q: np.ndarray, n_tok: int, softcap: float = 0.0, threads: int = 1):
         """q: [n_seq, n_tok, n_head, hd] raw f32 for the n_tok tokens just appended (query
@@ -133,7 +148,8 @@ class OracleKV:
         lib().or_attend_batch(self.k_packed, self.v_packed, self.k_scale, self.v_scale,
                               self.n_seq, self.max_seq, n_head, self.n_kv, self.hd,
                               self.rope_dim, self.table, q, self.lens, n_tok, float(softcap),
-                              out, int(threads), self.rot)
+                              out, int(threads), self.rot, self._w(self.q_norm),
+                              float(self.norm_eps))
         return out
 
     def attend_one(self, q_seq: np.ndarray, seq: int, head: int, softcap: float = 0.0):
@@ -145,8 +161,18 @@ class OracleKV:
         lib().or_attend_one(self.k_packed, self.v_packed, self.k_scale, self.v_scale,
                             self.max_seq, n_head, self.n_kv, self.hd, self.rope_dim, self.table,
                             q_seq, int(self.lens[seq]), n_tok, seq, head, float(softcap), out,
-                            int(self.rot[seq]))
+                            int(self.rot[seq]), self._w(self.q_norm), float(self.norm_eps))
         return out[:, head]
+
+    def _w(self, w):
+        """Norm weights as a C pointer (None: no norm); the array is kept alive on self."""
+        if w is None:
+            return None
+        w = np.ascontiguousarray(w, np.float32)
+        assert w.shape == (self.hd,)
+        self._keep = getattr(self, "_keep", []) + [w]
+        self._keep = self._keep[-4:]
+        return w.ctypes.data
 
     def advance(self, n_tok: int):
         """complete_decode / complete_prefill: lengths advance after all layers."""

@@ -8,6 +8,8 @@
  * Every function restates one piece of the reference (paths relative to the
  * reference repository root):
  *
+ *   or_qk_norm_row      src/ops/reference/attention.rs:92-108 (apply_qk_norm), applied to q and
+ *                       K before RoPE as at :186-199 (Qwen3)
  *   or_rope_table       src/backend/bindless/preflight.rs:71-111  (compute_rope_table,
  *                       plain/linear branch; theta as in src/ops/reference/rope.rs:150-152)
  *   or_rope_rotate      src/ops/reference/rope.rs:180-197          (adjacent-pair rotation)
@@ -129,6 +131,26 @@ typedef struct {
     float *v_scale;
 } or_cache;
 
+/* ---- QK norm ------------------------------------------------------------------------- */
+
+/* apply_qk_norm (src/ops/reference/attention.rs:92-108) for one head vector, in place:
+ * rms_sq = (sum of x*x, summed in order from 0 in f32) / hd, scale = 1 / sqrt(rms_sq + eps),
+ * x = x * scale * w (left to right).  w: [hd] (NULL: no norm). */
+void or_qk_norm_row(float *x, int hd, const float *w, float eps) {
+    if (!w) return;
+    float sum = 0.0f;
+    for (int d = 0; d < hd; d++) {
+        float sq = x[d] * x[d];
+        sum = sum + sq;
+    }
+    float rms_sq = sum / (float)hd;
+    float scale = 1.0f / sqrtf(rms_sq + eps);
+    for (int d = 0; d < hd; d++) {
+        float t = x[d] * scale;
+        x[d] = t * w[d];
+    }
+}
+
 /* Rotation position of cache slot `pos` after sliding-window compaction: slots below n_sink
  * (the sinks, never moved) keep their own position; every other slot is rotated at
  * pos + rot, rot being the sequence's window base (kv_cache.rs:41-46, advanced by the shift
@@ -138,7 +160,8 @@ static int rot_pos(int pos, int rot, int n_sink) { return pos < n_sink ? pos : p
 /* Append n_tok tokens at positions pos0..pos0+n_tok-1.  k, v: [n_tok][n_kv][hd] raw f32.
  * K is rotated at its absolute position with the table (rope_dim <= hd), V is not. */
 void or_append(or_cache c, int n_kv, int hd, int rope_dim, const float *table,
-               const float *k, const float *v, int pos0, int n_tok, int rot, int n_sink) {
+               const float *k, const float *v, int pos0, int n_tok, int rot, int n_sink,
+               const float *k_norm, float eps) {
     float *tmp = (float *)malloc(sizeof(float) * hd);
     int n_pairs = rope_dim / 2;
     for (int t = 0; t < n_tok; t++) {
@@ -147,6 +170,7 @@ void or_append(or_cache c, int n_kv, int hd, int rope_dim, const float *table,
             size_t src = ((size_t)t * n_kv + h) * hd;
             size_t row = (size_t)pos * n_kv + h;
             memcpy(tmp, k + src, sizeof(float) * hd);
+            or_qk_norm_row(tmp, hd, k_norm, eps);  /* attention.rs:186-189: norm before RoPE */
             or_rope_rotate(tmp, rope_dim, table + (size_t)rot_pos(pos, rot, n_sink) * n_pairs * 2);
             or_quantize_row(tmp, hd, &c.k_scale[row], c.k_packed + row * (hd / 8));
             or_quantize_row(v + src, hd, &c.v_scale[row], c.v_packed + row * (hd / 8));
@@ -162,7 +186,7 @@ void or_append(or_cache c, int n_kv, int hd, int rope_dim, const float *table,
  * (rotated here at the query position plus the window base `rot`), out: [n_q_tok][n_head][hd]. */
 void or_attend_head(or_cache c, int n_head, int n_kv, int hd, int rope_dim, const float *table,
                     const float *q, int q_pos0, int n_q_tok, int head, float softcap, float *out,
-                    int rot) {
+                    int rot, const float *q_norm, float eps) {
     int group = n_head / n_kv;
     int kvh = head / group;
     int key_len = q_pos0 + n_q_tok;
@@ -181,6 +205,7 @@ void or_attend_head(or_cache c, int n_head, int n_kv, int hd, int rope_dim, cons
     for (int t = 0; t < n_q_tok; t++) {
         int qpos = q_pos0 + t;
         memcpy(qr, q + ((size_t)t * n_head + head) * hd, sizeof(float) * hd);
+        or_qk_norm_row(qr, hd, q_norm, eps);
         or_rope_rotate(qr, rope_dim, table + (size_t)(qpos + rot) * n_pairs * 2);
         for (int j = 0; j < key_len; j++) {
             double acc = 0.0;
@@ -235,11 +260,12 @@ static or_cache seq_cache(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int 
 void or_append_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq, int max_seq,
                      int n_kv, int hd, int rope_dim, const float *table, const float *k,
                      const float *v, const int32_t *lens, int n_tok, const int32_t *rot,
-                     const int32_t *n_sink) {
+                     const int32_t *n_sink, const float *k_norm, float eps) {
     for (int s = 0; s < n_seq; s++) {
         size_t off = (size_t)s * n_tok * n_kv * hd;
         or_append(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_kv, hd, rope_dim, table,
-                  k + off, v + off, lens[s], n_tok, rot ? rot[s] : 0, n_sink ? n_sink[s] : 0);
+                  k + off, v + off, lens[s], n_tok, rot ? rot[s] : 0, n_sink ? n_sink[s] : 0,
+                  k_norm, eps);
     }
 }
 
@@ -249,7 +275,7 @@ void or_append_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq
 void or_attend_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq, int max_seq,
                      int n_head, int n_kv, int hd, int rope_dim, const float *table, const float *q,
                      const int32_t *lens, int n_tok, float softcap, float *out, int n_threads,
-                     const int32_t *rot) {
+                     const int32_t *rot, const float *q_norm, float eps) {
     long total = (long)n_seq * n_head;
     if (n_threads <= 1) {
         for (long i = 0; i < total; i++) {
@@ -257,7 +283,7 @@ void or_attend_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq
             size_t off = (size_t)s * n_tok * n_head * hd;
             or_attend_head(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_head, n_kv, hd,
                            rope_dim, table, q + off, lens[s], n_tok, h, softcap, out + off,
-                           rot ? rot[s] : 0);
+                           rot ? rot[s] : 0, q_norm, eps);
         }
         return;
     }
@@ -268,7 +294,8 @@ void or_attend_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq
         int s = (int)(i / n_head), h = (int)(i % n_head);
         size_t off = (size_t)s * n_tok * n_head * hd;
         or_attend_head(seq_cache(kp, vp, ks, vs, s, max_seq, n_kv, hd), n_head, n_kv, hd, rope_dim,
-                       table, q + off, lens[s], n_tok, h, softcap, out + off, rot ? rot[s] : 0);
+                       table, q + off, lens[s], n_tok, h, softcap, out + off, rot ? rot[s] : 0,
+                       q_norm, eps);
     }
 }
 
@@ -277,9 +304,9 @@ void or_attend_batch(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int n_seq
 void or_attend_one(uint32_t *kp, uint32_t *vp, float *ks, float *vs, int max_seq, int n_head,
                    int n_kv, int hd, int rope_dim, const float *table, const float *q_seq,
                    int q_pos0, int n_tok, int seq, int head, float softcap, float *out_seq,
-                   int rot) {
+                   int rot, const float *q_norm, float eps) {
     or_attend_head(seq_cache(kp, vp, ks, vs, seq, max_seq, n_kv, hd), n_head, n_kv, hd, rope_dim,
-                   table, q_seq, q_pos0, n_tok, head, softcap, out_seq, rot);
+                   table, q_seq, q_pos0, n_tok, head, softcap, out_seq, rot, q_norm, eps);
 }
 
 /* ---- sliding-window compaction ---------------------------------------------------------- */

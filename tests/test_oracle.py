@@ -404,3 +404,61 @@ def test_shift_is_a_copy():
     snap = [a.copy() for a in (kv.k_packed, kv.v_packed)]
     kv.shift(1, 30, 30)  # 50 <= 60: nothing moves
     assert all((a == b).all() for a, b in zip((kv.k_packed, kv.v_packed), snap))
+
+
+# ---- QK norm (Qwen3, attention.rs:92-108 and :186-189) --------------------------------------------
+
+def _qk_norm_py(x, w, eps):
+    """attention.rs:92-108 with every operation rounded to float32, in the reference's order."""
+    f = np.float32
+    s = f(0.0)
+    for v in x:
+        s = f(s + f(v * v))
+    scale = f(f(1.0) / f(np.sqrt(f(f(s / f(len(x))) + f(eps)))))
+    return np.array([f(f(v * scale) * wd) for v, wd in zip(x, w)], np.float32)
+
+
+@pytest.mark.parametrize("mag", [1e-3, 1.0, 37.0, 3e4])
+def test_qk_norm_row_matches_reference_order(mag):
+    rng = np.random.default_rng(int(mag * 10) + 5)
+    for hd in (64, 128):
+        x = (rng.standard_normal(hd) * mag).astype(np.float32)
+        w = (rng.standard_normal(hd) * 0.5 + 1.0).astype(np.float32)
+        got = oracle.qk_norm_row(x, w, 1e-6)
+        assert np.array_equal(got.view(np.uint32), _qk_norm_py(x, w, 1e-6).view(np.uint32))
+
+
+def test_qk_norm_closed_form():
+    hd = 128
+    w = np.linspace(0.5, 2.0, hd).astype(np.float32)
+    for c in (0.0, 1.0, -3.0):
+        got = oracle.qk_norm_row(np.full(hd, c, np.float32), w, 1e-6)
+        want = c / math.sqrt(c * c + 1e-6) * w.astype(np.float64)
+        np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-30)
+    # unit weights: the output has mean square 1 / (1 + eps / ms)
+    x = np.random.default_rng(9).standard_normal(hd).astype(np.float32) * 4
+    y = oracle.qk_norm_row(x, np.ones(hd, np.float32), 1e-6).astype(np.float64)
+    assert abs(np.mean(y * y) - 1.0) < 1e-5
+
+
+def test_qk_norm_sits_before_rope_in_append_and_attend():
+    """K is normalized before the rotation and quantization (codes equal those of appending the
+    normalized K), q before its rotation (outputs equal attending with normalized q)."""
+    rng = np.random.default_rng(41)
+    n_kv, hd, n_head = 2, 64, 4
+    table = oracle.rope_table(64, hd, 10000.0)
+    wq = (rng.standard_normal(hd) * 0.3 + 1).astype(np.float32)
+    wk = (rng.standard_normal(hd) * 0.3 + 1).astype(np.float32)
+    k = rng.standard_normal((1, 20, n_kv, hd), dtype=np.float32) * 3
+    v = rng.standard_normal((1, 20, n_kv, hd), dtype=np.float32)
+    a = oracle.OracleKV(1, 64, n_kv, hd, table)
+    a.k_norm, a.q_norm = wk, wq
+    a.append(k, v)
+    b = oracle.OracleKV(1, 64, n_kv, hd, table)
+    kn = np.stack([[[oracle.qk_norm_row(k[0, t, h], wk) for h in range(n_kv)] for t in range(20)]])
+    b.append(kn, v)
+    assert np.array_equal(a.k_packed, b.k_packed) and np.array_equal(a.k_scale, b.k_scale)
+    assert np.array_equal(a.v_packed, b.v_packed)
+    q = rng.standard_normal((1, 20, n_head, hd), dtype=np.float32)
+    qn = np.stack([[[oracle.qk_norm_row(q[0, t, h], wq) for h in range(n_head)] for t in range(20)]])
+    np.testing.assert_array_equal(a.attend(q, 20), b.attend(qn, 20))
