@@ -77,6 +77,22 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
             vx[ii][2 * j + 1] = vv.y;
         }
     }
+    if (L.kn) {
+        // QK norm of every K row before RoPE: lane 0 walks the row in order
+#pragma unroll
+        for (int ii = 0; ii < PPW; ii++) {
+            const int pc = min(max(p0 + wave + 4 * ii, lo), hi - 1);
+            float ns = 0.0f;
+            if (lane == 0) ns = qk_norm_scale(k + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD, HD, L.norm_eps);
+            ns = __shfl(ns, 0, 64);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int pi = min(lane + 64 * j, PAIRS - 1);
+                kx[ii][2 * j] = qk_norm_apply(kx[ii][2 * j], ns, L.kn[2 * pi]);
+                kx[ii][2 * j + 1] = qk_norm_apply(kx[ii][2 * j + 1], ns, L.kn[2 * pi + 1]);
+            }
+        }
+    }
     float km[PPW], vm[PPW];
 #pragma unroll
     for (int ii = 0; ii < PPW; ii++) {
@@ -221,6 +237,18 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
         kx[rd][4] = b.x; kx[rd][5] = b.y; kx[rd][6] = b.z; kx[rd][7] = b.w;
         vx[rd][0] = c.x; vx[rd][1] = c.y; vx[rd][2] = c.z; vx[rd][3] = c.w;
         vx[rd][4] = d.x; vx[rd][5] = d.y; vx[rd][6] = d.z; vx[rd][7] = d.w;
+    }
+    if (L.kn) {
+        // QK norm of every K row before RoPE: the row's first lane walks it in order
+#pragma unroll
+        for (int rd = 0; rd < 2; rd++) {
+            const int pc = min(max(p0 + 16 * rd + 4 * wave + r, lo), hi - 1);
+            float ns = 0.0f;
+            if (l == 0) ns = qk_norm_scale(k + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD, HD, L.norm_eps);
+            ns = __shfl(ns, lane & ~15, 64);
+#pragma unroll
+            for (int e = 0; e < 8; e++) kx[rd][e] = qk_norm_apply(kx[rd][e], ns, L.kn[8 * l + e]);
+        }
     }
     float km[2], vm[2];
 #pragma unroll

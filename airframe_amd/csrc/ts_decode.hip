@@ -264,19 +264,29 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
 // rotation pair (2i, 2i+1).  Writes the K row, both scales and the position's nibble of every
 // V word (read-modify-write: only this workgroup touches the block), and leaves the
 // dequantized row ((code - 8) * scale, the values the cache now holds) in kd / vd.
-template <int HD>
+template <int HD, bool NORM>
 __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, float *kd, float *vd) {
     constexpr int NTD = HD / 16, ROWB = HD / 2;
     const KvLayerView &L = a.L;
+    const float *const KN = NORM ? L.kn : nullptr;  // QK norm of K (compiled out when off)
     const size_t row = (size_t)s * L.H + h;
     const bool on = lane < HD / 2;
     const int i = on ? lane : 0;
     const size_t src = row * HD + 2 * i;
     float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+    float ns = 0.0f;  // QK norm scale of the new K row (lane 0 walks it in order)
+    if (KN) {
+        if (lane == 0) ns = qk_norm_scale(a.k_new + row * HD, HD, L.norm_eps);
+        ns = __shfl(ns, 0, 64);
+    }
     if (on) {
         const float2 kk = *reinterpret_cast<const float2 *>(a.k_new + src);
         const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
         k0 = kk.x; k1 = kk.y; v0 = vv.x; v1 = vv.y;
+        if (KN) {
+            k0 = qk_norm_apply(k0, ns, KN[2 * i]);
+            k1 = qk_norm_apply(k1, ns, KN[2 * i + 1]);
+        }
         if (i < a.rope_pairs)
             rope_rotate(k0, k1, *reinterpret_cast<const float2 *>(
                                     a.rope + ((size_t)rot_pos(p, L.rot[s], L.sink[s]) * a.rope_pairs + i) * 2));
@@ -313,7 +323,7 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
     }
 }
 
-template <int HD, bool SOFTCAP>
+template <int HD, bool SOFTCAP, bool NORM>
 __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_split_kernel(DecodeArgs a) {
     constexpr int NW = TS_DECODE_NW;  // waves per workgroup
     constexpr int SPAN = 64 * NW;     // positions one round of windows covers
@@ -322,6 +332,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     constexpr int ROWB = HD / 2;   // bytes per K row
     constexpr int OST = HD + 1;
     const KvLayerView &L = a.L;
+    const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int qpos = a.len[s];
     const int qrot = rot_pos(qpos, a.L.rot[s], a.L.sink[s]);  // rotation position of the query
@@ -385,20 +396,29 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     // q operands: wave w builds k-step t = w (rotated, scaled by log2(e)/sqrt(hd), split hi/lo)
     // for all 64 lanes; zero in the columns past G.
     // One power-of-two scale for the G heads: every wave reads the bound of all of them.
-    const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (n < G ? n : (live ? n - G : 0))) * HD;
+    const int qhead = n < G ? n : (live ? n - G : 0);
+    const float *qrow = a.q + ((size_t)s * a.n_head + h * G + qhead) * HD;
+    // QK norm scales of the G query heads (one thread walks each row in order)
+    __shared__ float qns[8];
+    if (QN) {
+        if (tid < G) qns[tid] = qk_norm_scale(a.q + ((size_t)s * a.n_head + h * G + tid) * HD, HD, L.norm_eps);
+        __syncthreads();
+    }
+    const float ns = QN ? qns[qhead] : 1.0f;
     float q_s, inv_s;
     {
         float qb = 0.0f;
 #pragma unroll
-        for (int t = 0; t < WPG; t++) qb = fmaxf(qb, q_bound8(qrow, WPG * g + t));
+        for (int t = 0; t < WPG; t++) qb = fmaxf(qb, q_bound8(qrow, WPG * g + t, QN, ns));
         q_scale(wave_max(qb) * (a.inv_sqrt_hd * kLog2e), q_s, inv_s);
     }
     for (int t = wave; t < WPG; t += NW) {
         half8 qh, ql;
-        load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qrot, a.inv_sqrt_hd * kLog2e * q_s, qh, ql);
+        load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qrot, a.inv_sqrt_hd * kLog2e * q_s, qh, ql,
+                QN, ns);
         sm.run.q.p[t][lane] = !live ? (half8)(_Float16)0.0f : (lo_col ? ql : qh);
     }
-    if (fused && wave == 0) append_one<HD>(a, s, h, qpos, lane, kd, vd);
+    if (fused && wave == 0) append_one<HD, NORM>(a, s, h, qpos, lane, kd, vd);
     __syncthreads();
     if (fused) {
         // score of the new position for head h*G + hh, from the rotated f32 q (as load_q8)
@@ -406,6 +426,10 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
             const int i = lane < HD / 2 ? lane : 0;
             const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
             float q0 = qq.x, q1 = qq.y;
+            if (QN) {
+                q0 = qk_norm_apply(q0, qns[hh], QN[2 * i]);
+                q1 = qk_norm_apply(q1, qns[hh], QN[2 * i + 1]);
+            }
             if (i < a.rope_pairs)
                 rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + i) * 2));
             float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
@@ -765,7 +789,7 @@ __device__ __forceinline__ void process_window4(const Window4<HD> &w, WaveState4
     }
 }
 
-template <int HD, bool SOFTCAP>
+template <int HD, bool SOFTCAP, bool NORM>
 __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_split4_kernel(DecodeArgs a) {
     constexpr int NW = TS_DECODE_NW;
     constexpr int SPAN = 64 * NW;
@@ -773,6 +797,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     constexpr int NQ = HD / 64;  // q register pairs (16 k-steps each)
     constexpr int OST = HD + 1;
     const KvLayerView &L = a.L;
+    const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int qpos = a.len[s];
     const int qrot = rot_pos(qpos, a.L.rot[s], a.L.sink[s]);  // rotation position of the query
@@ -796,6 +821,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     };
     __shared__ Smem sm;
     __shared__ float kd[HD], vd[HD], xnew[8];
+    __shared__ float qns[8];  // QK norm scales of the G query heads
 
     const size_t row = (size_t)s * L.H + h;
     constexpr int ROWB = HD / 2;
@@ -817,15 +843,21 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     {
         const int blk = lane >> 2, i = lane & 3;
         const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (i < G ? i : 0)) * HD;
+        if (QN) {
+            if (tid < G) qns[tid] = qk_norm_scale(a.q + ((size_t)s * a.n_head + h * G + tid) * HD, HD, L.norm_eps);
+            __syncthreads();
+        }
+        const float ns = QN ? qns[i < G ? i : 0] : 1.0f;
         float qb = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NQ; c++) qb = fmaxf(qb, q_bound8(qrow, (16 * c + blk) >> 1));
+        for (int c = 0; c < NQ; c++) qb = fmaxf(qb, q_bound8(qrow, (16 * c + blk) >> 1, QN, ns));
         q_scale(wave_max_all(qb) * (a.inv_sqrt_hd * kLog2e), q_s, inv_s);
 #pragma unroll
         for (int c = 0; c < NQ; c++) {
             const int t = 16 * c + blk;
             half8 hh8, ll8;
-            load_q8(a.rope, a.rope_pairs, qrow, t >> 1, qrot, a.inv_sqrt_hd * kLog2e * q_s, hh8, ll8);
+            load_q8(a.rope, a.rope_pairs, qrow, t >> 1, qrot, a.inv_sqrt_hd * kLog2e * q_s, hh8, ll8,
+                    QN, ns);
             const int o4 = 4 * (t & 1);
             half4_t hv = {hh8[o4], hh8[o4 + 1], hh8[o4 + 2], hh8[o4 + 3]};
             half4_t lv = {ll8[o4], ll8[o4 + 1], ll8[o4 + 2], ll8[o4 + 3]};
@@ -833,13 +865,17 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
             ql[c] = i < G ? lv : (half4_t)(_Float16)0.0f;
         }
     }
-    if (fused && wave == 0) append_one<HD>(a, s, h, qpos, lane, kd, vd);
+    if (fused && wave == 0) append_one<HD, NORM>(a, s, h, qpos, lane, kd, vd);
     __syncthreads();
     if (fused) {
         for (int hh = wave; hh < G; hh += NW) {
             const int i = lane < HD / 2 ? lane : 0;
             const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
             float q0 = qq.x, q1 = qq.y;
+            if (QN) {
+                q0 = qk_norm_apply(q0, qns[hh], QN[2 * i]);
+                q1 = qk_norm_apply(q1, qns[hh], QN[2 * i + 1]);
+            }
             if (i < a.rope_pairs)
                 rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + i) * 2));
             float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
@@ -983,29 +1019,24 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     // dependency chain (QK chains of 32 MFMAs, P through LDS): measured faster once every wave
     // streams at least 4 windows per split, slower for short splits (batch-1 shapes).
     const bool g4 = a.G <= 4 && plan.chunk >= 4 * 64 * TS_DECODE_NW && !TS_DECODE_FORCE16;
+    const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
+#define TS_SPLIT(HDV, SC, NM)                                                                 \
+    (g4 ? (decode_split4_kernel<HDV, SC, NM><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a), 0)       \
+        : (decode_split_kernel<HDV, SC, NM><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a), 0))
+#define TS_SPLIT_HD(HDV)                                                                      \
+    (cap ? (norm ? TS_SPLIT(HDV, true, true) : TS_SPLIT(HDV, true, false))                    \
+         : (norm ? TS_SPLIT(HDV, false, true) : TS_SPLIT(HDV, false, false)))
     if (L.hd == 128) {
-        if (g4 && softcap > 0.0f)
-            decode_split4_kernel<128, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
-        else if (g4)
-            decode_split4_kernel<128, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
-        else if (softcap > 0.0f)
-            decode_split_kernel<128, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
-        else
-            decode_split_kernel<128, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
+        TS_SPLIT_HD(128);
         if (plan.n_split > 1) decode_combine_kernel<128><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else if (L.hd == 64) {
-        if (g4 && softcap > 0.0f)
-            decode_split4_kernel<64, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
-        else if (g4)
-            decode_split4_kernel<64, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
-        else if (softcap > 0.0f)
-            decode_split_kernel<64, true><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
-        else
-            decode_split_kernel<64, false><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a);
+        TS_SPLIT_HD(64);
         if (plan.n_split > 1) decode_combine_kernel<64><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else {
         return hipErrorInvalidValue;
     }
+#undef TS_SPLIT_HD
+#undef TS_SPLIT
     return hipGetLastError();
 }
 

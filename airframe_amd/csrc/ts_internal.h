@@ -36,6 +36,9 @@ struct KvLayerView {
     // of slot p is stored rotated at rot_pos(p): p for the sinks, p + window base otherwise.
     const int32_t *rot;
     const int32_t *sink;
+    // QK norm of this layer (Qwen3): per-dim weights for q and K, or null (no norm), and eps
+    const float *qn, *kn;
+    float norm_eps;
     int S, H, P, hd;
 };
 
@@ -52,6 +55,8 @@ struct ts_kv {
                               // and sink counts [n_seq] (d_rot, d_sink)
     int32_t *d_rot, *d_sink;
     std::vector<int32_t> h_len, h_rot, h_sink;
+    std::vector<const float *> q_norm, k_norm;  // per layer, device pointers or null
+    std::vector<float> norm_eps;
     int device;
 
     ts::KvLayerView layer(int l) const {
@@ -64,6 +69,9 @@ struct ts_kv {
         v.vs = v.ks + nrow;
         v.rot = d_rot;
         v.sink = d_sink;
+        v.qn = q_norm[l];
+        v.kn = k_norm[l];
+        v.norm_eps = norm_eps[l];
         v.S = d.n_seq;
         v.H = d.n_head_kv;
         v.P = P;

@@ -149,6 +149,9 @@ int ts_kv_create(const ts_kv_desc *desc, ts_kv **out) {
     kv->h_len.assign(desc->n_seq, 0);
     kv->h_rot.assign(desc->n_seq, 0);
     kv->h_sink.assign(desc->n_seq, 0);
+    kv->q_norm.assign(desc->n_layers, nullptr);
+    kv->k_norm.assign(desc->n_layers, nullptr);
+    kv->norm_eps.assign(desc->n_layers, 1e-6f);
     if (hipGetDevice(&kv->device) != hipSuccess) {
         delete kv;
         return TS_ERR_HIP;
@@ -232,6 +235,17 @@ int ts_kv_reset(ts_kv *kv, void *stream) {
     std::fill(kv->h_len.begin(), kv->h_len.end(), 0);
     std::fill(kv->h_rot.begin(), kv->h_rot.end(), 0);
     std::fill(kv->h_sink.begin(), kv->h_sink.end(), 0);
+    return TS_OK;
+}
+
+int ts_kv_set_qk_norm(ts_kv *kv, int32_t layer, const float *d_q_norm, const float *d_k_norm,
+                      float eps) {
+    if (!kv || layer < 0 || layer >= kv->d.n_layers || !(eps >= 0.0f) || !(eps < 1e30f) ||
+        !aligned16(d_q_norm) || !aligned16(d_k_norm))
+        return TS_ERR_INVALID;
+    kv->q_norm[layer] = d_q_norm;
+    kv->k_norm[layer] = d_k_norm;
+    kv->norm_eps[layer] = eps;
     return TS_OK;
 }
 

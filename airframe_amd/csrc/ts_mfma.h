@@ -121,12 +121,25 @@ __device__ inline float opaque(float x) {
 // register: the halves cannot come from different roundings of v.
 __device__ inline float split_hi(float v) { return __uint_as_float(__float_as_uint(v) & 0xFFFFE000u); }
 
-// Bound on |rotated q| over the 8 dims 8u..8u+7 of one head: |a cos - b sin| <= |a| + |b|.
-__device__ inline float q_bound8(const float *qrow, int u) {
+// The 8 dims 8u..8u+7 of one head's q, normalized when nw is set (QK norm weights nw, the
+// row's scale ns: attention.rs:186-189 normalizes before RoPE).
+__device__ inline void q_read8(const float *qrow, int u, const float *nw, float ns, float (&x)[8]) {
     const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * u);
     const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * u + 4);
-    return fmaxf(fmaxf(fabsf(x0.x) + fabsf(x0.y), fabsf(x0.z) + fabsf(x0.w)),
-                 fmaxf(fabsf(x1.x) + fabsf(x1.y), fabsf(x1.z) + fabsf(x1.w)));
+    x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
+    x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+    if (nw) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = qk_norm_apply(x[e], ns, nw[8 * u + e]);
+    }
+}
+
+// Bound on |rotated q| over the 8 dims 8u..8u+7 of one head: |a cos - b sin| <= |a| + |b|.
+__device__ inline float q_bound8(const float *qrow, int u, const float *nw = nullptr, float ns = 1.0f) {
+    float x[8];
+    q_read8(qrow, u, nw, ns, x);
+    return fmaxf(fmaxf(fabsf(x[0]) + fabsf(x[1]), fabsf(x[2]) + fabsf(x[3])),
+                 fmaxf(fabsf(x[4]) + fabsf(x[5]), fabsf(x[6]) + fabsf(x[7])));
 }
 
 // Power-of-two scale S for q operands bounded by m: m*S lands in [2^13, 2^14), so both halves
@@ -143,16 +156,15 @@ __device__ inline void q_scale(float m, float &s, float &inv_s) {
     inv_s = ldexpf(1.0f, e - 13);
 }
 
-// Rotated q for the 8 dims 8u..8u+7 of one head (rope.rs:186-196, table row qpos), times
-// `mul`, split x = hi + lo into f16 and arranged in the slot order of dequant8.
+// Rotated q for the 8 dims 8u..8u+7 of one head (rope.rs:186-196, table row qpos), after the
+// optional QK norm, times `mul`, split x = hi + lo into f16 and arranged in the slot order of
+// dequant8.
 __device__ inline void load_q8(const float *rope, int rope_pairs, const float *qrow, int u,
-                               int qpos, float mul, half8 &hi, half8 &lo) {
+                               int qpos, float mul, half8 &hi, half8 &lo,
+                               const float *nw = nullptr, float ns = 1.0f) {
 #pragma clang fp contract(off)
     float x[8];
-    const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * u);
-    const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * u + 4);
-    x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
-    x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+    q_read8(qrow, u, nw, ns, x);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int pair = 4 * u + i;

@@ -321,7 +321,7 @@ __device__ inline void step_probs(const floatx16 (&sc)[2], const float *sv, int 
     }
 }
 
-template <int HD, bool SOFTCAP>
+template <int HD, bool SOFTCAP, bool NORM>
 __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillArgs a) {
     constexpr int NW = TS_PREFILL_NW;
     constexpr int NKS = HD / 16;   // MFMA k-steps over the head dim
@@ -329,6 +329,7 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     constexpr int ROWB = HD / 2;
     constexpr int COLS = NW * kColsPerWave;  // columns per block
     const KvLayerView &L = a.L;
+    const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     // Workgroups are dispatched round robin over the 8 XCDs by linear id.  Give XCD x the
     // contiguous range [x*N/8, (x+1)*N/8) of (column block, kv head, sequence) in row order, so
     // the 16-odd blocks that read one (sequence, kv head) stream share an L2 and every XCD gets
@@ -373,12 +374,14 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     const float *qrow = a.q + (((size_t)s * a.n_tok + tok) * a.n_head + h * G + cc % G) * HD;
     const int qpos = live ? len0 + tok : -1;
 
-    // One power-of-two q scale per workgroup, from a bound over all its columns.
+    // QK norm scale of this lane's column (its q row walked in order), then one power-of-two
+    // q scale per workgroup, from a bound over all its columns.
+    const float ns = QN ? qk_norm_scale(qrow, HD, L.norm_eps) : 1.0f;
     float q_s, inv_s;
     {
         float qb = 0.0f;
 #pragma unroll
-        for (int t = 0; t < NKS; t++) qb = fmaxf(qb, q_bound8(qrow, 2 * t + hf));
+        for (int t = 0; t < NKS; t++) qb = fmaxf(qb, q_bound8(qrow, 2 * t + hf, QN, ns));
         qb = wave_max(qb);
         if (lane == 0) sm_qb[wave] = qb;
         __syncthreads();
@@ -391,7 +394,7 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
 #pragma unroll
     for (int t = 0; t < NKS; t++) {
         load_q8(a.rope, a.rope_pairs, qrow, 2 * t + hf, rot_pos(len0 + tok, L.rot[s], L.sink[s]), qmul * q_s,
-                qh[t], ql[t]);
+                qh[t], ql[t], QN, ns);
         if (!live) {
             qh[t] = (half8)(_Float16)0.0f;
             ql[t] = (half8)(_Float16)0.0f;
@@ -510,17 +513,19 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
     const int cols = TS_PREFILL_NW * kColsPerWave;
     const int n_blk = (n_cols + cols - 1) / cols;
     dim3 grid(n_blk, L.H, L.S);
-    const bool cap = softcap > 0.0f;
-    if (L.hd == 128 && cap)
-        prefill_kernel<128, true><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a);
-    else if (L.hd == 128)
-        prefill_kernel<128, false><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a);
-    else if (L.hd == 64 && cap)
-        prefill_kernel<64, true><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a);
+    const bool cap = softcap > 0.0f, norm = L.qn != nullptr;
+#define TS_PF(HDV)                                                                                      \
+    (cap ? (norm ? (prefill_kernel<HDV, true, true><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a), 0)         \
+                 : (prefill_kernel<HDV, true, false><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a), 0))       \
+         : (norm ? (prefill_kernel<HDV, false, true><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a), 0)        \
+                 : (prefill_kernel<HDV, false, false><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a), 0)))
+    if (L.hd == 128)
+        TS_PF(128);
     else if (L.hd == 64)
-        prefill_kernel<64, false><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a);
+        TS_PF(64);
     else
         return hipErrorInvalidValue;
+#undef TS_PF
     return hipGetLastError();
 }
 

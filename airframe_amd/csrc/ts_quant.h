@@ -30,6 +30,30 @@ __device__ inline void rope_rotate(float &a, float &b, float2 cs) {
     b = xs + yc;
 }
 
+// apply_qk_norm (src/ops/reference/attention.rs:92-108), the scale of one head vector `row`
+// (hd f32): squares rounded, summed in order from 0 in f32, divided by hd, then
+// 1 / sqrt(mean + eps) with correctly rounded sqrt and division.  The caller applies
+// x = (x * scale) * w per element.  One thread walks the row (the order is the contract).
+__device__ inline float qk_norm_scale(const float *row, int hd, float eps) {
+#pragma clang fp contract(off)
+    float sum = 0.0f;
+    for (int d = 0; d < hd; d += 4) {
+        const float4 x = *reinterpret_cast<const float4 *>(row + d);
+        sum = sum + x.x * x.x;
+        sum = sum + x.y * x.y;
+        sum = sum + x.z * x.z;
+        sum = sum + x.w * x.w;
+    }
+    const float ms = sum / (float)hd;
+    return 1.0f / sqrtf(ms + eps);
+}
+
+__device__ inline float qk_norm_apply(float x, float scale, float w) {
+#pragma clang fp contract(off)
+    const float t = x * scale;
+    return t * w;
+}
+
 __device__ inline float quant_scale(float max_abs) {
     return (max_abs == 0.0f) ? 1.0f : __fdiv_rn(max_abs, 7.0f);
 }

@@ -119,6 +119,24 @@ class KVCache:
     def reset(self, stream=None):
         check("ts_kv_reset", load().ts_kv_reset(self._h, _stream(stream)))
 
+    # ---- QK norm (Qwen3: attention.rs:92-108 before RoPE, :186-189) ----------------------
+
+    def set_qk_norm(self, layer: int, q_norm: torch.Tensor | None, k_norm: torch.Tensor | None,
+                    eps: float = 1e-6):
+        """Per-head RMSNorm of q and K (weights [head_dim] f32 on the device, or None) for one
+        layer, applied by the append and attention calls before RoPE.  The tensors are kept
+        alive by the cache."""
+        for w in (q_norm, k_norm):
+            if w is not None and (w.dtype != torch.float32 or w.numel() != self.head_dim or
+                                  not w.is_cuda or not w.is_contiguous()):
+                raise ValueError("norm weights must be contiguous f32 [head_dim] on the device")
+        if not hasattr(self, "_norms"):
+            self._norms = {}
+        self._norms[layer] = (q_norm, k_norm)
+        ptr = lambda w: ctypes.c_void_p(w.data_ptr()) if w is not None else None
+        check("ts_kv_set_qk_norm",
+              load().ts_kv_set_qk_norm(self._h, layer, ptr(q_norm), ptr(k_norm), eps))
+
     # ---- sliding-window compaction (pipeline_shift.rs, kv_cache.rs window_base) ---------
 
     def get_window_base(self, seq: int = 0) -> int:

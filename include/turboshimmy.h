@@ -113,6 +113,20 @@ int ts_kv_export(const ts_kv *kv, int32_t layer, int32_t seq, int32_t pos0, int3
                  uint32_t *d_k_packed, uint32_t *d_v_packed, float *d_k_scale, float *d_v_scale,
                  void *stream);
 
+/* ---- QK norm (Qwen3) ------------------------------------------------------------------------ */
+
+/* Per-head RMSNorm of q and K before RoPE for one layer: apply_qk_norm
+ * (src/ops/reference/attention.rs:92-108, applied at :186-189; the GPU path's main_qk_norm,
+ * sh_layer_v1_int4.wgsl:577-640, runs at the same point).  From then on ts_append_quant and
+ * ts_attn_decode_append normalize each K head vector (x * 1/sqrt(mean(x^2) + eps) * w, the
+ * squares summed in order in f32) before rotating and quantizing it, and the attention entry
+ * points normalize q the same way before rotating it.  d_q_norm, d_k_norm: [head_dim] f32
+ * device arrays (16-byte aligned) that must stay valid while set, or NULL to leave that side
+ * unnormalized; eps as the reference (1e-6).  ts_requant_all takes K as given (the reference
+ * normalizes its f32 cache before requantizing). */
+int ts_kv_set_qk_norm(ts_kv *kv, int32_t layer, const float *d_q_norm, const float *d_k_norm,
+                      float eps);
+
 /* ---- sliding-window compaction ------------------------------------------------------------- */
 
 /* KVCache::get_window_base / advance_window_base (kv_cache.rs:241-243, :277-279) for one
