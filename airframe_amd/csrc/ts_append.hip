@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
             if (rope && pi < rope_pairs)
                 rope_rotate(kx[ii][2 * j], kx[ii][2 * j + 1],
                             *reinterpret_cast<const float2 *>(
-                                rope + ((size_t)rot_pos(pc, L.rot[s], L.sink[s]) * rope_pairs + pi) * 2));
+                                rope + ((size_t)rot_of(L, s, pc) * rope_pairs + pi) * 2));
             km[ii] = fmaxf(km[ii], fmaxf(fabsf(kx[ii][2 * j]), fabsf(kx[ii][2 * j + 1])));
             vm[ii] = fmaxf(vm[ii], fmaxf(fabsf(vx[ii][2 * j]), fabsf(vx[ii][2 * j + 1])));
         }
@@ -215,14 +215,13 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
     const int lo = max(p0, start), hi = min(p0 + kBlk, end);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane >> 4, l = lane & 15;
     const size_t row = (size_t)s * L.H + h;
-    const int rot = L.rot[s], sink = L.sink[s];
 
     float kx[2][8], vx[2][8];
     float2 cs[2][4];  // rotation of each pair (identity without a table or past rope_dim)
 #pragma unroll
     for (int rd = 0; rd < 2; rd++) {
         const int pc = min(max(p0 + 16 * rd + 4 * wave + r, lo), hi - 1);
-        const int pr = rot_pos(pc, rot, sink);
+        const int pr = rot_of(L, s, pc);
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const int pair = 4 * l + m;

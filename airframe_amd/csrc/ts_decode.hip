@@ -289,7 +289,7 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
         }
         if (i < a.rope_pairs)
             rope_rotate(k0, k1, *reinterpret_cast<const float2 *>(
-                                    a.rope + ((size_t)rot_pos(p, L.rot[s], L.sink[s]) * a.rope_pairs + i) * 2));
+                                    a.rope + ((size_t)rot_of(L, s, p) * a.rope_pairs + i) * 2));
     }
     const float ks = quant_scale(wave_max(fmaxf(fabsf(k0), fabsf(k1))));
     const float vs = quant_scale(wave_max(fmaxf(fabsf(v0), fabsf(v1))));
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int qpos = a.len[s];
-    const int qrot = rot_pos(qpos, a.L.rot[s], a.L.sink[s]);  // rotation position of the query
+    const int qrot = rot_of(a.L, s, qpos);  // rotation position of the query
     const int n_ctx = qpos + 1;
     const int start = split * a.chunk;
     if (start >= n_ctx) return;
@@ -800,7 +800,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int qpos = a.len[s];
-    const int qrot = rot_pos(qpos, a.L.rot[s], a.L.sink[s]);  // rotation position of the query
+    const int qrot = rot_of(a.L, s, qpos);  // rotation position of the query
     const int n_ctx = qpos + 1;
     const int start = split * a.chunk;
     if (start >= n_ctx) return;

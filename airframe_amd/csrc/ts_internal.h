@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "../../include/turboshimmy.h"
@@ -32,8 +33,9 @@ struct KvLayerView {
     uint8_t *vp;  // V packed
     float *ks;    // K scales
     float *vs;    // V scales
-    // Per sequence: window base (the shift total of all compactions) and sink count.  The K
-    // of slot p is stored rotated at rot_pos(p): p for the sinks, p + window base otherwise.
+    // Per sequence: window base (the shift total of all compactions) and sink count, or null
+    // while no sequence has been compacted.  The K of slot p is stored rotated at rot_pos(p):
+    // p for the sinks, p + window base otherwise.
     const int32_t *rot;
     const int32_t *sink;
     // QK norm of this layer (Qwen3): per-dim weights for q and K, or null (no norm), and eps
@@ -43,6 +45,12 @@ struct KvLayerView {
 };
 
 __device__ __host__ inline int rot_pos(int p, int rot, int sink) { return p < sink ? p : p + rot; }
+
+// Rotation position of slot p of sequence s (rot/sink are null while no sequence of the cache
+// has been compacted, which saves the kernels two loads).
+__device__ inline int rot_of(const KvLayerView &L, int s, int p) {
+    return L.rot ? rot_pos(p, L.rot[s], L.sink[s]) : p;
+}
 
 }  // namespace ts
 
@@ -67,8 +75,9 @@ struct ts_kv {
         v.vp = b + nrow * (d.head_dim / 2);
         v.ks = (float *)(b + nrow * d.head_dim);
         v.vs = v.ks + nrow;
-        v.rot = d_rot;
-        v.sink = d_sink;
+        const bool compacted = std::any_of(h_rot.begin(), h_rot.end(), [](int32_t r) { return r != 0; });
+        v.rot = compacted ? d_rot : nullptr;
+        v.sink = compacted ? d_sink : nullptr;
         v.qn = q_norm[l];
         v.kn = k_norm[l];
         v.norm_eps = norm_eps[l];

@@ -393,7 +393,7 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     half8 qh[NKS], ql[NKS];
 #pragma unroll
     for (int t = 0; t < NKS; t++) {
-        load_q8(a.rope, a.rope_pairs, qrow, 2 * t + hf, rot_pos(len0 + tok, L.rot[s], L.sink[s]), qmul * q_s,
+        load_q8(a.rope, a.rope_pairs, qrow, 2 * t + hf, rot_of(L, s, len0 + tok), qmul * q_s,
                 qh[t], ql[t], QN, ns);
         if (!live) {
             qh[t] = (half8)(_Float16)0.0f;
