@@ -78,13 +78,12 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
         }
     }
     if (L.kn) {
-        // QK norm of every K row before RoPE: lane 0 walks the row in order
+        // QK norm of every K row before RoPE, the squares summed in order across the lanes
 #pragma unroll
         for (int ii = 0; ii < PPW; ii++) {
-            const int pc = min(max(p0 + wave + 4 * ii, lo), hi - 1);
-            float ns = 0.0f;
-            if (lane == 0) ns = qk_norm_scale(k + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD, HD, L.norm_eps);
-            ns = __shfl(ns, 0, 64);
+            static_assert(NJ == 1, "the ordered sum reads one pair per lane");
+            const float ns = qk_norm_scale_from_sum(
+                ordered_sum_pairs(sq_rn(kx[ii][0]), sq_rn(kx[ii][1]), PAIRS), HD, L.norm_eps);
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
                 const int pi = min(lane + 64 * j, PAIRS - 1);
@@ -238,13 +237,14 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
         vx[rd][4] = d.x; vx[rd][5] = d.y; vx[rd][6] = d.z; vx[rd][7] = d.w;
     }
     if (L.kn) {
-        // QK norm of every K row before RoPE: the row's first lane walks it in order
+        // QK norm of every K row before RoPE, its squares summed in the row's order across the
+        // 16 lanes that hold it
 #pragma unroll
         for (int rd = 0; rd < 2; rd++) {
-            const int pc = min(max(p0 + 16 * rd + 4 * wave + r, lo), hi - 1);
-            float ns = 0.0f;
-            if (l == 0) ns = qk_norm_scale(k + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD, HD, L.norm_eps);
-            ns = __shfl(ns, lane & ~15, 64);
+            float sq[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) sq[e] = sq_rn(kx[rd][e]);
+            const float ns = qk_norm_scale_from_sum(ordered_sum_row16(sq, l), HD, L.norm_eps);
 #pragma unroll
             for (int e = 0; e < 8; e++) kx[rd][e] = qk_norm_apply(kx[rd][e], ns, L.kn[8 * l + e]);
         }

@@ -274,15 +274,15 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
     const int i = on ? lane : 0;
     const size_t src = row * HD + 2 * i;
     float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
-    float ns = 0.0f;  // QK norm scale of the new K row (lane 0 walks it in order)
-    if (KN) {
-        if (lane == 0) ns = qk_norm_scale(a.k_new + row * HD, HD, L.norm_eps);
-        ns = __shfl(ns, 0, 64);
-    }
     if (on) {
         const float2 kk = *reinterpret_cast<const float2 *>(a.k_new + src);
         const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
         k0 = kk.x; k1 = kk.y; v0 = vv.x; v1 = vv.y;
+    }
+    // QK norm scale of the new K row: its squares summed in dimension order across the lanes
+    float ns = 0.0f;
+    if (KN) ns = qk_norm_scale_from_sum(ordered_sum_pairs(sq_rn(k0), sq_rn(k1), HD / 2), HD, L.norm_eps);
+    if (on) {
         if (KN) {
             k0 = qk_norm_apply(k0, ns, KN[2 * i]);
             k1 = qk_norm_apply(k1, ns, KN[2 * i + 1]);
@@ -398,13 +398,9 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     // One power-of-two scale for the G heads: every wave reads the bound of all of them.
     const int qhead = n < G ? n : (live ? n - G : 0);
     const float *qrow = a.q + ((size_t)s * a.n_head + h * G + qhead) * HD;
-    // QK norm scales of the G query heads (one thread walks each row in order)
-    __shared__ float qns[8];
-    if (QN) {
-        if (tid < G) qns[tid] = qk_norm_scale(a.q + ((size_t)s * a.n_head + h * G + tid) * HD, HD, L.norm_eps);
-        __syncthreads();
-    }
-    const float ns = QN ? qns[qhead] : 1.0f;
+    // QK norm scale of this lane's query head (each wave computes it for itself)
+    const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, qhead, L.norm_eps)
+                        : 1.0f;
     float q_s, inv_s;
     {
         float qb = 0.0f;
@@ -427,8 +423,9 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
             const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
             float q0 = qq.x, q1 = qq.y;
             if (QN) {
-                q0 = qk_norm_apply(q0, qns[hh], QN[2 * i]);
-                q1 = qk_norm_apply(q1, qns[hh], QN[2 * i + 1]);
+                const float nh = q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, hh, L.norm_eps);
+                q0 = qk_norm_apply(q0, nh, QN[2 * i]);
+                q1 = qk_norm_apply(q1, nh, QN[2 * i + 1]);
             }
             if (i < a.rope_pairs)
                 rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + i) * 2));
@@ -821,7 +818,6 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     };
     __shared__ Smem sm;
     __shared__ float kd[HD], vd[HD], xnew[8];
-    __shared__ float qns[8];  // QK norm scales of the G query heads
 
     const size_t row = (size_t)s * L.H + h;
     constexpr int ROWB = HD / 2;
@@ -843,11 +839,9 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     {
         const int blk = lane >> 2, i = lane & 3;
         const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (i < G ? i : 0)) * HD;
-        if (QN) {
-            if (tid < G) qns[tid] = qk_norm_scale(a.q + ((size_t)s * a.n_head + h * G + tid) * HD, HD, L.norm_eps);
-            __syncthreads();
-        }
-        const float ns = QN ? qns[i < G ? i : 0] : 1.0f;
+        const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, i < G ? i : 0,
+                                                    L.norm_eps)
+                            : 1.0f;
         float qb = 0.0f;
 #pragma unroll
         for (int c = 0; c < NQ; c++) qb = fmaxf(qb, q_bound8(qrow, (16 * c + blk) >> 1, QN, ns));
@@ -873,8 +867,9 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
             const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
             float q0 = qq.x, q1 = qq.y;
             if (QN) {
-                q0 = qk_norm_apply(q0, qns[hh], QN[2 * i]);
-                q1 = qk_norm_apply(q1, qns[hh], QN[2 * i + 1]);
+                const float nh = q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, hh, L.norm_eps);
+                q0 = qk_norm_apply(q0, nh, QN[2 * i]);
+                q1 = qk_norm_apply(q1, nh, QN[2 * i + 1]);
             }
             if (i < a.rope_pairs)
                 rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + i) * 2));

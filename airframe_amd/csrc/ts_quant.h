@@ -34,16 +34,66 @@ __device__ inline void rope_rotate(float &a, float &b, float2 cs) {
 // (hd f32): squares rounded, summed in order from 0 in f32, divided by hd, then
 // 1 / sqrt(mean + eps) with correctly rounded sqrt and division.  The caller applies
 // x = (x * scale) * w per element.  One thread walks the row (the order is the contract).
+// The row is read in batches of 8 independent 16-byte loads (one memory latency per batch,
+// not one per load) and summed in order.
 __device__ inline float qk_norm_scale(const float *row, int hd, float eps) {
 #pragma clang fp contract(off)
     float sum = 0.0f;
-    for (int d = 0; d < hd; d += 4) {
-        const float4 x = *reinterpret_cast<const float4 *>(row + d);
-        sum = sum + x.x * x.x;
-        sum = sum + x.y * x.y;
-        sum = sum + x.z * x.z;
-        sum = sum + x.w * x.w;
+    for (int d0 = 0; d0 < hd; d0 += 32) {
+        float4 x[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) x[b] = *reinterpret_cast<const float4 *>(row + d0 + 4 * b);
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            sum = sum + x[b].x * x[b].x;
+            sum = sum + x[b].y * x[b].y;
+            sum = sum + x[b].z * x[b].z;
+            sum = sum + x[b].w * x[b].w;
+        }
     }
+    const float ms = sum / (float)hd;
+    return 1.0f / sqrtf(ms + eps);
+}
+
+// x * x rounded to f32 (never fused into a following add)
+__device__ inline float sq_rn(float x) {
+#pragma clang fp contract(off)
+    return x * x;
+}
+
+// The same sum over a row spread across lanes, without touching memory: lane l holds the
+// squares of dims 2l and 2l + 1 (sq0, sq1); lanes 0..n_lanes-1 are read in order.  Every lane
+// gets the ordered sum (of rounded squares, as qk_norm_scale).
+__device__ inline float ordered_sum_pairs(float sq0, float sq1, int n_lanes) {
+#pragma clang fp contract(off)
+    float sum = 0.0f;
+    for (int l = 0; l < n_lanes; l++) {
+        sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sq0), l));
+        sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sq1), l));
+    }
+    return sum;
+}
+
+// Ordered sum of a 128-dim row spread over the 16 lanes of a DPP row, lane l holding the 8
+// squares of dims 8l..8l+7 in order: the running sum walks the lanes with row_shr:1, so the
+// additions happen in the row's order.  Every lane of the row gets the total.
+__device__ inline float ordered_sum_row16(const float (&sq)[8], int l) {
+#pragma clang fp contract(off)
+    float run = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        // lane l receives lane l-1's running sum (0 for the row's first lane)
+        float t = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(run), 0x111, 0xF, 0xF, true));
+#pragma unroll
+        for (int e = 0; e < 8; e++) t = t + sq[e];
+        run = l == i ? t : run;
+    }
+    return __shfl(run, (__lane_id() & ~15) | 15, 64);
+}
+
+// 1 / sqrt(sum / hd + eps), the apply_qk_norm scale from a finished sum of squares.
+__device__ inline float qk_norm_scale_from_sum(float sum, int hd, float eps) {
+#pragma clang fp contract(off)
     const float ms = sum / (float)hd;
     return 1.0f / sqrtf(ms + eps);
 }
@@ -82,6 +132,48 @@ __device__ inline float wave_max_nonneg(float v) {
     v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
     auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Sum over the 64 lanes of a wave, every lane getting the same value (DPP within each 16-lane
+// row, then the two permlane swaps).  The additions pair lanes symmetrically, so the result is
+// identical in all lanes.
+__device__ inline float wave_sum(float v) {
+    v = v + dpp_f<0xB1>(v);   // quad_perm(1,0,3,2)
+    v = v + dpp_f<0x4E>(v);   // quad_perm(2,3,0,1)
+    v = v + dpp_f<0x141>(v);  // row_half_mirror
+    v = v + dpp_f<0x140>(v);  // row_mirror
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// apply_qk_norm scale of query head `mine` of the G (<= 8) consecutive head rows at q, computed
+// by the whole wave: every row's squares are summed as a tree across the lanes (the query side
+// only feeds the softmax, compared within tolerance, so the order of the sum is free) and no
+// LDS or barrier is involved.  All lanes must call it.
+template <int HD>
+__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps) {
+    static_assert(HD % 64 == 0, "whole float lanes per row");
+    constexpr int PER = HD / 64;
+    const int lane = __lane_id();
+    float x[8][PER];
+#pragma unroll
+    for (int g = 0; g < 8; g++)
+#pragma unroll
+        for (int e = 0; e < PER; e++) x[g][e] = g < G ? q[(size_t)g * HD + PER * lane + e] : 0.0f;
+    float out = 1.0f;
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        if (g < G) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < PER; e++) ss += x[g][e] * x[g][e];
+            const float sc = qk_norm_scale_from_sum(wave_sum(ss), HD, eps);
+            out = g == mine ? sc : out;
+        }
+    }
+    return out;
 }
 
 // encode(x, scale) with the quotient taken as x * rcp(scale) wherever that cannot change the

@@ -59,7 +59,7 @@ def append_bytes(batch, n_kv, hd):
     return batch * n_kv * (2 * hd * 4 + hd + 8)
 
 
-def cpu_baseline(kv, cfg, qs, ks, vs, lens, max_seq, table, layers_mt=2, seqs_st=2):
+def cpu_baseline(kv, cfg, qs, ks, vs, lens, max_seq, table, layers_mt=2, seqs_st=2, norms=None):
     """Time the C oracle (oracle/ts_oracle.c) on a bounded sample of the same step: append the
     step's token and attend, for every sequence of `layers_mt` layers (OpenMP over
     (sequence, head)) and for `seqs_st` sequences of one layer single-threaded."""
@@ -72,6 +72,8 @@ def cpu_baseline(kv, cfg, qs, ks, vs, lens, max_seq, table, layers_mt=2, seqs_st
     t_st = 0.0
     for layer in range(layers_mt):
         ora = oracle.OracleKV(B, max_seq, n_kv, hd, table)
+        if norms is not None:
+            ora.q_norm, ora.k_norm = norms[layer]
         for s in range(B):
             kp, vp, kss, vss = kv.export(layer, s, 0, lens[s])
             torch.cuda.synchronize()
@@ -89,6 +91,7 @@ def cpu_baseline(kv, cfg, qs, ks, vs, lens, max_seq, table, layers_mt=2, seqs_st
         t_mt += time.perf_counter() - t0
         if layer == 0:
             sub = oracle.OracleKV(seqs_st, max_seq, n_kv, hd, table)
+            sub.q_norm, sub.k_norm = ora.q_norm, ora.k_norm
             for name in ("k_packed", "v_packed", "k_scale", "v_scale"):
                 getattr(sub, name)[:] = getattr(ora, name)[:seqs_st]
             sub.lens[:] = ora.lens[:seqs_st]
@@ -123,6 +126,15 @@ def run_decode(args, cfg):
     dims = synth.outlier_dims(n_kv, hd, args.seed) if cfg["outliers"] else None
     skv = torch.as_tensor(synth.channel_scale(n_kv, n_kv, hd, dims), device=dev)
     sq = torch.as_tensor(synth.channel_scale(n_head, n_kv, hd, dims), device=dev)
+
+    norms = None
+    if args.qk_norm:  # Qwen3's per-head q/K RMSNorm before RoPE, random weights around 1
+        norms = []
+        for layer in range(L):
+            wq = (torch.randn(hd, generator=gen, device=dev) * 0.2 + 1.0).contiguous()
+            wk = (torch.randn(hd, generator=gen, device=dev) * 0.2 + 1.0).contiguous()
+            kv.set_qk_norm(layer, wq, wk)
+            norms.append((wq.cpu().numpy(), wk.cpu().numpy()))
 
     # Fill every layer's cache to its starting length with the fused append.
     fill = max(lens0)
@@ -241,7 +253,7 @@ def run_decode(args, cfg):
         table = oracle.rope_table(max_seq, hd, cfg["theta"])
         # The oracle appends at lens0 (same token the GPU appended in timed step 0).
         t_mt, cores, t_st = cpu_baseline(kv, cfg, qs[0], ks[0], vs[0], lens0, max_seq, table,
-                                         layers_mt=min(2, L), seqs_st=min(2, B))
+                                         layers_mt=min(2, L), seqs_st=min(2, B), norms=norms)
         cpu = dict(step_s_mt=t_mt, cores=cores, step_s_st=t_st)
     return result, cpu
 
@@ -295,6 +307,42 @@ def run_prefill(args, cfg):
     flops_layer = 4 * hd * n_head * B * (n_tot * (n_tot + 1) // 2)
     kernel_ms_layer = float(np.sum(kt)) / reps / L
     return dict(total_ms=total_ms, kernel_ms_layer=kernel_ms_layer, flops_layer=flops_layer)
+
+
+def run_append(args, cfg):
+    """Quantize-on-append of one 512-token prefill chunk per sequence (the configuration's
+    batch, kv heads and head dim), every layer, cache empty before each chunk.  Returns the
+    mean time of one ts_append_quant call and its algorithmic bytes: the f32 K and V read and
+    the packed rows and scales written."""
+    import torch
+
+    from airframe_amd.kv_cache import KVCache, RopeTable
+
+    dev = torch.device("cuda:0")
+    L, n_kv, hd, B = cfg["layers"], cfg["n_kv"], cfg["hd"], cfg["batch"]
+    n_tok = 512
+    rope = RopeTable(n_tok + 8, hd, cfg["theta"])
+    kv = KVCache.new_int4(L, n_kv, hd, n_tok + 8, B)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    ks = [torch.randn((B, n_tok, n_kv, hd), generator=gen, device=dev) for _ in range(L)]
+    vs = [torch.randn((B, n_tok, n_kv, hd), generator=gen, device=dev) for _ in range(L)]
+    if args.qk_norm:
+        for layer in range(L):
+            kv.set_qk_norm(layer, None, torch.randn(hd, generator=gen, device=dev) * 0.2 + 1.0)
+    for layer in range(L):
+        kv.append_quant(layer, ks[layer], vs[layer], rope)
+    torch.cuda.synchronize()
+    reps = 5
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for layer in range(L):
+            kv.append_quant(layer, ks[layer], vs[layer], rope)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * L)
+    return ms, B * n_tok * n_kv * (2 * hd * 4 + hd + 8), B * n_tok
 
 
 def run_compact(args, cfg):
@@ -363,6 +411,12 @@ def main():
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 1 GiB device copy (4 launches) so rocprofv3 HBM counters "
                          "can be scaled by what they read for a copy of known size")
+    ap.add_argument("--append", action="store_true",
+                    help="measure quantize-on-append (ts_append_quant) of a 512-token chunk per "
+                         "sequence at the config's shape instead of the decode step")
+    ap.add_argument("--qk-norm", action="store_true",
+                    help="turn on the fused Qwen3 QK norm (random weights) for the decode step or "
+                         "the append measurement")
     ap.add_argument("--compact", action="store_true",
                     help="measure sliding-window compaction (ts_kv_shift) on the config's cache "
                          "instead of the decode step")
@@ -384,6 +438,23 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
     torch.cuda.set_device(0)
+    if args.append:
+        if "ctx" not in cfg:
+            sys.exit("--append needs a decode configuration (1-4)")
+        ms, byts, toks = run_append(args, cfg)
+        gbs = byts / (ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "INT4 KV quantize-on-append HBM GB/s", "value": round(gbs, 1), "unit": "GB/s",
+            "n_gpus": 1, "higher_is_better": True, "us_per_call": round(ms * 1e3, 2),
+            "tokens_per_s": round(toks / (ms * 1e-3), 1),
+            "config": {"workload": cfg["name"] + "_append_512tok" + ("_qknorm" if args.qk_norm else ""),
+                       "tokens_per_call": toks},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "bytes_per_call": byts,
+                         "counting": "f32 K and V read, packed K/V rows and two scales written"},
+            "data": "synthetic"}), flush=True)
+        return
     if args.compact:
         if "ctx" not in cfg:
             sys.exit("--compact needs a decode configuration (1-4)")
@@ -472,7 +543,8 @@ def main():
         "data": "synthetic (seeded N(0,1), x8 outlier channels)" if cfg["outliers"] else "synthetic (seeded N(0,1))",
         "tokens_per_s": round(tok_s, 1), "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "launch": "hip-graph replay per step" if args.graph else "eager",
-        "config": {"workload": cfg["name"], "global_batch": B, "seq_len": cfg.get("ctx"),
+        "config": {"workload": cfg["name"] + ("_qknorm" if args.qk_norm else ""), "global_batch": B,
+                   "seq_len": cfg.get("ctx"),
                    "layers": L, "n_head": cfg["n_head"], "n_head_kv": cfg["n_kv"],
                    "head_dim": cfg["hd"], "parallelism": "none"},
         "roofline": roof,
