@@ -41,7 +41,7 @@ CONFIGS = {
     3: dict(name="qwen3-8b_b32_ctx8192_36layers", layers=36, n_head=32, n_kv=8, hd=128,
             batch=32, ctx=8192, theta=1000000.0, steps=128, outliers=True),
     4: dict(name="llama3-8b_b8_ctx16k-32k_ragged_32layers", layers=32, n_head=32, n_kv=8, hd=128,
-            batch=8, ctx=32768, theta=500000.0, steps=1, outliers=False, ragged=(16384, 32768)),
+            batch=8, ctx=32768, theta=500000.0, steps=16, outliers=False, ragged=(16384, 32768)),
     5: dict(name="qwen3-4b_b4_prefill_4x512_36layers", layers=36, n_head=32, n_kv=8, hd=128,
             batch=4, chunk=512, n_chunks=4, theta=1000000.0, outliers=False),
 }
