@@ -123,4 +123,16 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
                           int n_head, int n_tok, const float *rope, int rope_pairs,
                           float softcap, float *out, hipStream_t st);
 
+// Fused QKV projection + append (ts_qkv.hip): tiles and split of the reduction over dim.
+struct QkvPlan {
+    int RT, CT;           // row tiles, column tiles
+    int kps, n_split;     // reduction length per split, splits
+    uint64_t part_bytes;  // scratch for the split partials (0 without a split)
+};
+QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int dim, int n_tok);
+hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x, int dim, int n_tok,
+                      const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int n_head,
+                      float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,
+                      const QkvPlan &plan, float *part, hipStream_t st);
+
 }  // namespace ts

@@ -1,0 +1,181 @@
+// ts_store128.h -- the quantize-and-store step of the INT4 append for head_dim 128, shared
+// by the append kernel (rows loaded from f32 K/V) and the fused QKV projection (rows taken
+// from the projection's output tile), so both write bit-identical codes and scales.
+//
+// Quantiser (cpu_quantize, src/backend/bindless/test_int4_parity.rs:56-75): per head vector,
+// scale = max|x| / 7 (1 when max|x| == 0), code = clamp(round_half_away(x/scale) + 8, 1, 15),
+// after the optional QK norm (src/ops/reference/attention.rs:92-108) and the rotation of K at
+// its position (src/ops/reference/rope.rs:186-196).  Files that include it are compiled with
+// -ffp-contract=off: a product fused into a following add would change codes.
+#pragma once
+#include "ts_quant.h"
+
+namespace ts {
+namespace {
+
+constexpr int kBlk = 32;
+
+// Code of x (= clamp(round_half_away(x/scale) + 8, 1, 15)) from y = x * rcp(scale), for
+// |x| <= 7 scale: t = y + 8.5 lies in [1.5, 15.5] and trunc(t) is the code unless y is within
+// 1e-5 of a half-integer (|y - x/scale| <= ~1.3e-6, and the add rounds by < 1e-6), which sets
+// `need` (as does NaN); the caller then recomputes with encode().
+__device__ inline uint32_t code_fast(float y, bool &need) {
+    const float t = y + 8.5f;
+    const uint32_t c = (uint32_t)t;
+    const float d = t - (float)c;
+    need |= !(fabsf(d - 0.5f) <= 0.49999f);
+    return c;
+}
+
+// Rotation (cos, sin) of the 4 pairs 4l..4l+3 of slot p of sequence s (identity without a
+// table or past rope_pairs).
+__device__ inline void rope_cs4(const KvLayerView &L, int s, int p, const float *rope, int rope_pairs,
+                                int l, float2 (&cs)[4]) {
+    const int pr = rot_of(L, s, p);
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const int pair = 4 * l + m;
+        cs[m] = (rope && pair < rope_pairs)
+                    ? *reinterpret_cast<const float2 *>(rope + ((size_t)pr * rope_pairs + pair) * 2)
+                    : make_float2(1.0f, 0.0f);
+    }
+}
+
+// Quantizes and stores positions [lo, hi) of V block blk (positions p0 = 32 blk .. p0 + 31) of
+// one (sequence s, kv head h), hd = 128, from registers laid out as the append kernel loads
+// them: 4 waves, 16 lanes per position, lane l = lane % 16 holding dims 8l..8l+7 of positions
+// p0 + 16 rd + 4 wave + lane / 16 (rd = 0, 1) in kx[rd] / vx[rd] (raw K and V), and the
+// rotation of its 4 pairs at that position in cs[rd]; pairs at or past rot_pairs (0: no
+// rotation) are left as they are.  Rows outside [lo, hi) may hold
+// anything finite; they are never written.  Wave w assembles the V words with g = w from its
+// 4 rows with permlane swaps and writes them itself (keeping the nibbles of positions outside
+// [lo, hi)).  Reductions: 4 DPP steps within a 16-lane row.  Every lane of the workgroup
+// must call it.
+__device__ inline void store_block128(const KvLayerView &L, int s, int h, int blk, int lo, int hi,
+                                      float (&kx)[2][8], float (&vx)[2][8], const float2 (&cs)[2][4],
+                                      int rot_pairs, int wave, int lane) {
+    constexpr int HD = 128;
+    const int r = lane >> 4, l = lane & 15;
+    const int p0 = blk * kBlk;
+    const size_t row = (size_t)s * L.H + h;
+    if (L.kn) {
+        // QK norm of every K row before RoPE, its squares summed in the row's order across the
+        // 16 lanes that hold it
+#pragma unroll
+        for (int rd = 0; rd < 2; rd++) {
+            float sq[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) sq[e] = sq_rn(kx[rd][e]);
+            const float ns = qk_norm_scale_from_sum(ordered_sum_row16(sq, l), HD, L.norm_eps);
+#pragma unroll
+            for (int e = 0; e < 8; e++) kx[rd][e] = qk_norm_apply(kx[rd][e], ns, L.kn[8 * l + e]);
+        }
+    }
+    float km[2], vm[2];
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        {
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                if (4 * l + m < rot_pairs) rope_rotate(kx[rd][2 * m], kx[rd][2 * m + 1], cs[rd][m]);
+        }
+        km[rd] = 0.0f;
+        vm[rd] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            km[rd] = fmaxf(km[rd], fabsf(kx[rd][e]));
+            vm[rd] = fmaxf(vm[rd], fabsf(vx[rd][e]));
+        }
+    }
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        km[rd] = fmaxf(km[rd], dpp_f<0xB1>(km[rd]));
+        vm[rd] = fmaxf(vm[rd], dpp_f<0xB1>(vm[rd]));
+    }
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        km[rd] = fmaxf(km[rd], dpp_f<0x4E>(km[rd]));
+        vm[rd] = fmaxf(vm[rd], dpp_f<0x4E>(vm[rd]));
+    }
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        km[rd] = fmaxf(km[rd], dpp_f<0x141>(km[rd]));
+        vm[rd] = fmaxf(vm[rd], dpp_f<0x141>(vm[rd]));
+    }
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        km[rd] = fmaxf(km[rd], dpp_f<0x140>(km[rd]));
+        vm[rd] = fmaxf(vm[rd], dpp_f<0x140>(vm[rd]));
+    }
+
+    uint32_t vpart[8];  // this row's nibbles of V words (dims 8l + e)
+#pragma unroll
+    for (int e = 0; e < 8; e++) vpart[e] = 0;
+#pragma unroll
+    for (int rd = 0; rd < 2; rd++) {
+        const int p = p0 + 16 * rd + 4 * wave + r;
+        const bool in = p >= lo && p < hi;
+        const float ks = quant_scale(km[rd]), vs = quant_scale(vm[rd]);
+        const float kr = __builtin_amdgcn_rcpf(ks), vr = __builtin_amdgcn_rcpf(vs);
+        const bool k_ok = ks >= 1.17549435e-38f && ks <= 4.25352959e37f;
+        const bool v_ok = vs >= 1.17549435e-38f && vs <= 4.25352959e37f;
+        uint32_t kc[8], vc[8];
+        bool kneed = !k_ok, vneed = !v_ok;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            kc[e] = code_fast(kx[rd][e] * kr, kneed);
+            vc[e] = code_fast(vx[rd][e] * vr, vneed);
+        }
+        if (__builtin_amdgcn_ballot_w64(kneed) != 0) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) kc[e] = encode(kx[rd][e], ks);
+        }
+        if (__builtin_amdgcn_ballot_w64(vneed) != 0) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) vc[e] = encode(vx[rd][e], vs);
+        }
+        uint32_t kw = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            kw |= kc[e] << (4 * e);
+            vpart[e] |= vc[e] << (4 * r + 16 * rd);
+        }
+        if (in) {
+            reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[l] = kw;
+            if (l == 0) {
+                L.ks[row * L.P + p] = ks;
+                L.vs[row * L.P + p] = vs;
+            }
+        }
+    }
+    // OR the 4 rows' parts: lanes l, l+16, l+32, l+48 end up with the same 8 words
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        auto a = __builtin_amdgcn_permlane16_swap(vpart[e], vpart[e], false, false);
+        vpart[e] = a[0] | a[1];
+        auto b = __builtin_amdgcn_permlane32_swap(vpart[e], vpart[e], false, false);
+        vpart[e] = b[0] | b[1];
+    }
+    // row r writes dims 8l + 2r and 8l + 2r + 1: word (g = wave, dl, td) of the block
+    uint32_t keep = 0;  // nibbles of positions outside [lo, hi)
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const int p = p0 + 4 * wave + (n & 3) + 16 * (n >> 2);
+        if (p < lo || p >= hi) keep |= 0xFu << (4 * n);
+    }
+    uint32_t *vb = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16));
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int e = 2 * r + q;
+        const uint32_t w = r == 0 ? (q ? vpart[1] : vpart[0])
+                         : r == 1 ? (q ? vpart[3] : vpart[2])
+                         : r == 2 ? (q ? vpart[5] : vpart[4])
+                                  : (q ? vpart[7] : vpart[6]);
+        const int d = 8 * l + e, td = d >> 4, dl = d & 15;
+        uint32_t *dst = vb + (wave * 16 + dl) * (HD / 16) + td;
+        *dst = keep ? (*dst & keep) | (w & ~keep) : w;
+    }
+}
+
+}  // namespace
+}  // namespace ts

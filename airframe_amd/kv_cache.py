@@ -275,6 +275,47 @@ class KVCache:
                                   ctypes.c_void_p(vs.data_ptr()), _stream(stream)))
         return kp, vp, ks, vs
 
+    def qkv_workspace(self, dim: int, n_tok: int, n_head: int) -> torch.Tensor:
+        key = ("qkv", dim, n_tok, n_head)
+        if key not in self._ws:
+            b = ctypes.c_uint64()
+            check("ts_qkv_workspace",
+                  load().ts_qkv_workspace(self._h, dim, n_tok, n_head, ctypes.byref(b)))
+            self._ws[key] = torch.empty(max(b.value, 16), dtype=torch.uint8, device="cuda")
+        return self._ws[key]
+
+    def qkv_append(self, layer: int, x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor,
+                   wv: torch.Tensor, rope: RopeTable, q_out: torch.Tensor = None,
+                   kv_out: tuple | None = None, workspace: torch.Tensor = None, stream=None):
+        """main_qkv + quantize_kv in one pass: q = Wq x (returned), k = Wk x and v = Wv x
+        quantized into the cache at len[s] + t.  x: [n_seq, n_tok, dim] f32; wq: [n_head *
+        head_dim, dim], wk, wv: [n_head_kv * head_dim, dim] f16.  kv_out: optional (k, v)
+        tensors [n_seq, n_tok, n_head_kv, head_dim] f32 that receive the raw projections."""
+        if x.dim() != 3 or x.shape[0] != self.n_seq:
+            raise ValueError("x must be [n_seq, n_tok, dim]")
+        n_tok, dim = x.shape[1], x.shape[2]
+        n_head = wq.shape[0] // self.head_dim
+        kv_rows = self.n_head_kv * self.head_dim
+        if (wq.shape != (n_head * self.head_dim, dim) or wk.shape != (kv_rows, dim)
+                or wv.shape != (kv_rows, dim)):
+            raise ValueError("wq must be [n_head*head_dim, dim], wk/wv [n_head_kv*head_dim, dim]")
+        if q_out is None:
+            q_out = torch.empty((self.n_seq, n_tok, n_head, self.head_dim), dtype=torch.float32,
+                                device=x.device)
+        kp = vp = None
+        if kv_out is not None:
+            k_out, v_out = kv_out
+            self._check_kv(k_out, v_out, n_tok)
+            kp, vp = _ptr(k_out, torch.float32, "k_out"), _ptr(v_out, torch.float32, "v_out")
+        ws = workspace if workspace is not None else self.qkv_workspace(dim, n_tok, n_head)
+        check("ts_qkv_append",
+              load().ts_qkv_append(self._h, layer, _ptr(x, torch.float32, "x"), dim, n_tok,
+                                   _ptr(wq, torch.float16, "wq"), _ptr(wk, torch.float16, "wk"),
+                                   _ptr(wv, torch.float16, "wv"), n_head, rope.handle,
+                                   _ptr(q_out, torch.float32, "q_out"), kp, vp,
+                                   ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
+        return q_out
+
     def _check_kv(self, k, v, n_tok):
         want = (self.n_seq, n_tok, self.n_head_kv, self.head_dim)
         if tuple(k.shape) != want or tuple(v.shape) != want:

@@ -208,6 +208,29 @@ int ts_attn_decode_append(ts_kv *kv, int32_t layer, const float *d_k, const floa
 int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
                     int32_t n_tok, const ts_rope *rope, float softcap, float *d_out, void *stream);
 
+/* ---- QKV projection with the append as its epilogue ------------------------------------ */
+
+/* Bytes of scratch ts_qkv_append needs for this shape (0 when the projection is not split
+ * over dim).  Host only. */
+int ts_qkv_workspace(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head, uint64_t *bytes);
+
+/* main_qkv (sh_layer_v1_int4.wgsl:454-575, F16 weights: the formula slot 1 branch at :494-498)
+ * followed by quantize_kv (layer.rs:1092-1099), in one pass: for each token,
+ * q = Wq x, k = Wk x, v = Wv x, with k and v quantized straight into the cache as
+ * ts_append_quant would quantize them (QK norm of K when set, rotation of K, codes and
+ * scales), so the f32 K and V are never written unless asked for.
+ * d_x: [n_seq][n_tok][dim] f32 (the attention-normalized activations, |x| < 65504);
+ * d_wq: [n_head*head_dim][dim], d_wk, d_wv: [n_head_kv*head_dim][dim], f16 row-major (GGUF
+ * order: output row, then input column), 16-byte aligned.  Token t of sequence s goes to
+ * position len[s] + t.  d_q: [n_seq][n_tok][n_head][head_dim] raw q (the attention entry
+ * points apply the QK norm and rotation).  d_k, d_v: NULL, or [n_seq][n_tok][n_head_kv]
+ * [head_dim] to receive the raw projections as well (the reference's f32 staging cache).
+ * head_dim 128 (else TS_ERR_UNSUPPORTED), dim a multiple of 64.  Lengths do not change. */
+int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32_t n_tok,
+                  const uint16_t *d_wq, const uint16_t *d_wk, const uint16_t *d_wv, int32_t n_head,
+                  const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
+                  uint64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

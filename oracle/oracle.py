@@ -64,8 +64,31 @@ def lib():
                                    ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_int]
         L.or_shift_seq.restype = None
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_f16_to_f32.restype = ctypes.c_float
+        L.or_project.argtypes = [_f32p, ctypes.c_int, ctypes.c_int,
+                                 np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS"),
+                                 ctypes.c_int, _f32p]
+        L.or_project.restype = None
         _lib = L
     return _lib
+
+
+def f16_to_f32(bits: int) -> float:
+    return float(lib().or_f16_to_f32(int(bits)))
+
+
+def project(x: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
+    """main_qkv's f32 dot for every (row of x, row of w): x [n, dim] f32, w [n_out, dim] f16
+    bits (uint16) -> [n, n_out] f32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    n, dim = x.shape
+    n_out = w_bits.shape[0]
+    assert w_bits.shape[1] == dim
+    out = np.zeros((n, n_out), dtype=np.float32)
+    lib().or_project(x, n, dim, w_bits, n_out, out)
+    return out
 
 
 def qk_norm_row(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:

@@ -25,6 +25,10 @@
  *                       pipeline_shift.rs:360-566 (execute_int4): slide the INT4 rows down
  *   rot_pos             kv_cache.rs:41-46,277-279 (window_base) with the post-RoPE storage
  *                       of the CPU path: where each cache slot's K was rotated
+ *   or_f16_to_f32       sh_layer_v1_int4.wgsl:7-34 (f16_to_f32 behind dequant_f16_at,
+ *                       sh_dequant_any.wgsl:261-265)
+ *   or_project          sh_layer_v1_int4.wgsl:454-575 (main_qkv, F16 branch :494-498): one
+ *                       f32 dot per output, `dot += x[col] * w[row][col]` in column order
  *   or_attend_head      src/ops/reference/attention.rs:236-313 (per-head QK^T, scale,
  *                       causal softmax, PV), src/ops/reference/matmul.rs:91-104 (f32 products
  *                       accumulated in f64), src/ops/reference/softmax.rs:91-129 (mask to -inf,
@@ -130,6 +134,40 @@ typedef struct {
     float *k_scale; /* [max_seq][n_kv] */
     float *v_scale;
 } or_cache;
+
+/* ---- QKV projection ------------------------------------------------------------------ */
+
+/* IEEE half bits -> f32 as the reference shaders decode weights: zero, subnormal
+ * mant * 2^-24, normal (1 + mant/1024) * 2^(exp-15); inf and NaN decode to 0. */
+float or_f16_to_f32(uint16_t bits) {
+    uint32_t sign = (bits >> 15) & 1u, e = (bits >> 10) & 0x1fu, mant = bits & 0x3ffu;
+    float sign_f = sign ? -1.0f : 1.0f;
+    if (e == 0) return mant == 0 ? sign_f * 0.0f : sign_f * ((float)mant / 16777216.0f);
+    if (e == 0x1f) return 0.0f;
+    float fraction = 1.0f + (float)mant / 1024.0f;
+    return sign_f * ldexpf(fraction, (int)e - 15);
+}
+
+/* out[r][o] = sum over col of x[r][col] * w[o][col] for r < n_rows, o < n_out: one f32
+ * accumulator per output, each product rounded to f32 and added in column order (the
+ * reference's per-thread loop).  w: [n_out][dim] f16 bits.  OpenMP over outputs. */
+void or_project(const float *x, int n_rows, int dim, const uint16_t *w, int n_out, float *out) {
+    float *wf = (float *)malloc(sizeof(float) * (size_t)n_out * dim);
+    if (!wf) return;
+    for (size_t i = 0; i < (size_t)n_out * dim; i++) wf[i] = or_f16_to_f32(w[i]);
+#pragma omp parallel for schedule(static)
+    for (long ro = 0; ro < (long)n_rows * n_out; ro++) {
+        const long r = ro / n_out, o = ro % n_out;
+        const float *xr = x + (size_t)r * dim, *wr = wf + (size_t)o * dim;
+        float dot = 0.0f;
+        for (int c = 0; c < dim; c++) {
+            float prod = xr[c] * wr[c];
+            dot = dot + prod;
+        }
+        out[(size_t)r * n_out + o] = dot;
+    }
+    free(wf);
+}
 
 /* ---- QK norm ------------------------------------------------------------------------- */
 

@@ -462,3 +462,50 @@ def test_qk_norm_sits_before_rope_in_append_and_attend():
     q = rng.standard_normal((1, 20, n_head, hd), dtype=np.float32)
     qn = np.stack([[[oracle.qk_norm_row(q[0, t, h], wq) for h in range(n_head)] for t in range(20)]])
     np.testing.assert_array_equal(a.attend(q, 20), b.attend(qn, 20))
+
+
+# ---- QKV projection (main_qkv, F16 weights) --------------------------------------------------
+
+def test_f16_decode_every_bit_pattern():
+    """f16_to_f32 (sh_layer_v1_int4.wgsl:7-34) over all 65536 patterns: IEEE half for every
+    finite value (numpy's float16), 0 for inf and NaN as the shader returns."""
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16_to_f32(int(b)) for b in bits], dtype=np.float32)
+    fin = np.isfinite(ref)
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+    assert (got[~fin] == 0).all()
+
+
+def test_project_exact_on_integers():
+    """Small integers: every product and partial sum is exact in f32, so the dot is the
+    integer matrix product (a transposed operand or a dropped term would show)."""
+    rng = np.random.default_rng(1)
+    x = rng.integers(-8, 9, size=(5, 192)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(7, 192)).astype(np.float16)
+    got = oracle.project(x, w.view(np.uint16))
+    ref = x.astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(got, ref.astype(np.float32))
+
+
+def test_project_sequential_f32_order():
+    """The accumulation is one f32 sum in column order: against a float64 sum it is within the
+    sequential-rounding bound, and it equals a numpy restatement of the same order exactly."""
+    rng = np.random.default_rng(2)
+    dim = 1024
+    x = rng.standard_normal((3, dim)).astype(np.float32)
+    w = (rng.standard_normal((4, dim)) * 0.05).astype(np.float16)
+    got = oracle.project(x, w.view(np.uint16))
+    wf = w.astype(np.float32)
+    exact = x.astype(np.float64) @ wf.astype(np.float64).T
+    bound = dim * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(wf).astype(np.float64).T)
+    assert (np.abs(got - exact) <= bound).all()
+    seq = np.zeros((3, 4), np.float32)
+    for c in range(dim):            # order of the reference loop, one f32 rounding per step
+        seq = (seq + (x[:, c:c + 1] * wf[None, :, c])).astype(np.float32)
+    assert np.array_equal(got, seq)
+    # a cancelling pair: order matters, and the oracle keeps the reference's
+    xc = np.array([[1.0, 2.0 ** 24, -(2.0 ** 24)] + [0.0] * 61], np.float32)
+    wc = np.zeros((1, 64), np.float16)
+    wc[0, :3] = 1.0
+    assert oracle.project(xc, wc.view(np.uint16))[0, 0] == 0.0   # (1 + 2^24) rounds to 2^24
