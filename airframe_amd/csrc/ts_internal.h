@@ -127,6 +127,7 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
 struct QkvPlan {
     int RT, CT;           // row tiles, column tiles
     int kps, n_split;     // reduction length per split, splits
+    bool big;             // 128-row tiles (prefill chunks) instead of 32-row ones
     uint64_t part_bytes;  // scratch for the split partials (0 without a split)
 };
 QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int dim, int n_tok);

@@ -22,10 +22,12 @@
 //   * n_tok == 1 (decode): 32 sequences, one new token each, at position len[s];
 //   * n_tok > 1: the 32 positions of one V block of one sequence (the block owns its V words,
 //     as in the append kernel).
-// Small grids (decode) split the reduction over `dim` across workgroups: each writes an f32
-// partial tile, and a second kernel sums the partials in split order (deterministic) and runs
-// the epilogue.  The k-chunk loop double-buffers x (converted to hi/lo once per workgroup, in
-// LDS) and streams the weights straight into the B operands, one chunk ahead.
+// Large grids (prefill) run one workgroup per tile over all of dim: the k-chunk loop
+// double-buffers x (converted to hi/lo once per workgroup, in LDS) and streams the weights
+// straight into the B operands one chunk ahead, and the epilogue runs on the finished tile.
+// Small grids (decode) split the reduction over `dim` across workgroups: each loads its whole
+// slice in one round trip and writes an f32 partial tile, and a second kernel sums the
+// partials in split order (deterministic) and runs the epilogue.
 #include "ts_mfma.h"
 #include "ts_store128.h"
 
@@ -39,6 +41,12 @@ constexpr int kNT = 256;    // columns per tile
 constexpr int kKC = 64;     // k per chunk
 constexpr int kAStr = 72;   // LDS row stride of the x tiles (f16): 144 B spreads the rows' banks
 constexpr int kTStr = 260;  // LDS row stride of the output tile (f32)
+constexpr int kMaxSplit = 16;  // most splits of the reduction over dim
+#ifndef TS_QKV_BIG_BLOCKS
+#define TS_QKV_BIG_BLOCKS 2
+#endif
+constexpr int kBigBlocks = TS_QKV_BIG_BLOCKS;  // V blocks per row tile of the prefill kernel
+
 
 struct QkvArgs {
     KvLayerView L;
@@ -54,7 +62,7 @@ struct QkvArgs {
     int n_qt;              // q column tiles (ceil(n_head / 2))
     int RT, CT;            // row and column tiles
     int kps, n_split;      // k per split (multiple of kKC), splits
-    int n_wg;              // RT * CT * n_split
+    int n_wg;              // workgroups of the GEMM launch (before rounding up to 8)
 };
 
 // Rows of row tile rt.  n_tok == 1: sequences 32 rt .. 32 rt + 31.  Otherwise V block `blk` of
@@ -124,24 +132,26 @@ __device__ inline void split8(const float4 &u, const float4 &v, half8 &hi, half8
 }
 
 // Quantize-and-store of one new token per row (n_tok == 1): row i = sequence t.s + i at its
-// position len[s].  16 lanes per row (lane l = dims 8l..8l+7), rows 16 rd + 4 wave + lane/16.
+// position len[s], for tile rows r0 .. r0 + nr - 1 (nr a multiple of 4) held in tile[i - r0].
+// 16 lanes per row (lane l = dims 8l..8l+7), rows r0 + 16 m + 4 wave + lane/16.
 // Each row owns its sequence's K row, scales and the nibbles of its position in the V block.
 __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const float (*tile)[kTStr],
-                                  int h, int wave, int lane) {
+                                  int r0, int nr, int h, int wave, int lane) {
     constexpr int HD = 128, NTD = HD / 16;
     const KvLayerView &L = a.L;
     const int r = lane >> 4, l = lane & 15;
-#pragma unroll
-    for (int rd = 0; rd < 2; rd++) {
-        const int i = 16 * rd + 4 * wave + r;
+    for (int base = 0; base < nr; base += 16) {
+        if (base + 4 * wave >= nr) break;  // wave-uniform
+        const int i = r0 + base + 4 * wave + r;
+        const float *trow = tile[i - r0];
         const int s = min(t.s + i, L.S - 1);
         const bool live = t.s + i < L.S;
         const int p = a.len[s];
         float kx[8], vx[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            kx[e] = tile[i][8 * l + e];
-            vx[e] = tile[i][HD + 8 * l + e];
+            kx[e] = trow[8 * l + e];
+            vx[e] = trow[HD + 8 * l + e];
         }
         if (L.kn) {
             float sq[8];
@@ -213,19 +223,20 @@ __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const floa
     }
 }
 
-// The epilogue of one finished 32 x 256 tile held in LDS.
+// The epilogue of tile rows r0 .. r0 + nr - 1 of a finished 32 x 256 tile, held in LDS as
+// tile[i - r0].  Block rows (n_tok > 1) need the whole tile (r0 = 0, nr = 32).  256 threads.
 __device__ void qkv_epilogue(const QkvArgs &a, const RowTile &t, int ct, const float (*tile)[kTStr],
-                             int tid) {
+                             int r0, int nr, int tid) {
     const int wave = tid >> 6, lane = tid & 63;
     if (ct < a.n_qt) {
         // q: two heads side by side, contiguous in q_out
         const int c4 = tid & 63, i0 = tid >> 6;
         const int col = ct * kNT + 4 * c4;
         if (col >= a.n_head * 128) return;
-        for (int i = i0; i < kMT; i += 4) {
+        for (int i = r0 + i0; i < r0 + nr; i += 4) {
             const int xr = x_row(a, t, i);
             if (xr < 0) continue;
-            const float4 v = *reinterpret_cast<const float4 *>(&tile[i][4 * c4]);
+            const float4 v = *reinterpret_cast<const float4 *>(&tile[i - r0][4 * c4]);
             *reinterpret_cast<float4 *>(a.q_out + (size_t)xr * a.n_head * 128 + col) = v;
         }
         return;
@@ -235,15 +246,15 @@ __device__ void qkv_epilogue(const QkvArgs &a, const RowTile &t, int ct, const f
         const int c4 = tid & 63, i0 = tid >> 6;
         float *dst = c4 < 32 ? a.k_out : a.v_out;
         const int c = 4 * (c4 & 31);
-        for (int i = i0; i < kMT; i += 4) {
+        for (int i = r0 + i0; i < r0 + nr; i += 4) {
             const int xr = x_row(a, t, i);
             if (xr < 0) continue;
             *reinterpret_cast<float4 *>(dst + ((size_t)xr * a.L.H + h) * 128 + c) =
-                *reinterpret_cast<const float4 *>(&tile[i][4 * c4]);
+                *reinterpret_cast<const float4 *>(&tile[i - r0][4 * c4]);
         }
     }
     if (a.n_tok == 1) {
-        store_rows_single(a, t, tile, h, wave, lane);
+        store_rows_single(a, t, tile, r0, nr, h, wave, lane);
         return;
     }
     const int r = lane >> 4, l = lane & 15;
@@ -350,39 +361,277 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(QkvArgs a) {
     }
 
     // D layout: register 4q + r of column block cb is row 8q + 4hf + r, column 64 wave + 32 cb + j
-    if (a.n_split > 1) {
-        float *dst = a.part + (((size_t)sp * a.RT + rt) * a.CT + ct) * (kMT * kNT);
-#pragma unroll
-        for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-            for (int e = 0; e < 16; e++)
-                dst[(8 * (e >> 2) + 4 * hf + (e & 3)) * kNT + 64 * wave + 32 * cb + j] = acc[cb][e];
-        return;
-    }
 #pragma unroll
     for (int cb = 0; cb < 2; cb++)
 #pragma unroll
         for (int e = 0; e < 16; e++) tile[8 * (e >> 2) + 4 * hf + (e & 3)][64 * wave + 32 * cb + j] = acc[cb][e];
     __syncthreads();
-    qkv_epilogue(a, t, ct, tile, tid);
+    qkv_epilogue(a, t, ct, tile, 0, kMT, tid);
 }
 
-// Sum of the split partials of one tile, in split order, then the epilogue.
+// Block rows in tiles of 128 (prefill chunks): four consecutive V blocks blk0 .. blk0 + 3 of
+// one sequence.  8 waves: wave (wr, wc) computes rows 64 wr .. + 63, columns 64 wc .. + 63
+// (2 x 2 MFMA blocks), so each weight operand feeds two row blocks and each x operand two
+// column blocks: half the operand traffic per MFMA of the 32-row tiles.  x is staged per
+// chunk as hi/lo in LDS (double-buffered), the weights stream into registers one chunk ahead.
+// The epilogue runs block by block on a 32 x 256 LDS tile that reuses the x buffers.
+template <int WR>
+__global__ __launch_bounds__(256 * WR) void qkv_gemm128_kernel(QkvArgs a) {
+    constexpr int MT = 64 * WR, NBLK = MT / kBlk;
+    union Smem {
+        struct {
+            _Float16 hi[2][MT][kAStr];
+            _Float16 lo[2][MT][kAStr];
+        } x;
+        float tile[kMT][kTStr];
+    };
+    __shared__ __align__(16) Smem sm;
+
+    int rt, ct, sp;
+    tile_of(a, blockIdx.x, rt, ct, sp);
+    if (sp >= a.n_split) return;
+    const int nb4 = (a.n_tok / kBlk + 2 + NBLK - 1) / NBLK;
+    const int s = rt / nb4;
+    const int start = a.len[s], end = start + a.n_tok;
+    const int blk0 = start / kBlk + NBLK * (rt % nb4);
+    if (blk0 * kBlk >= end) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int wr = wave >> 2, wc = wave & 3;
+
+    // staging role: row si (0..MT-1), 16 floats at k offset 16 sc of each chunk
+    const int si = tid >> 2, sc = tid & 3;
+    const int ps = blk0 * kBlk + si;
+    const int xr = (ps >= start && ps < end) ? s * a.n_tok + (ps - start) : -1;
+    const float *xs = a.x + (size_t)max(xr, 0) * a.dim + 16 * sc;
+    const int nch = a.dim / kKC;
+
+    const _Float16 *wp[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) wp[cb] = w_row(a, ct, 64 * wc + 32 * cb + j) + 32 * hf;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[rb][cb][e] = 0.0f;
+
+    float4 xq[4];
+    auto load_x = [&](int c) {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            xq[u] = xr >= 0 ? *reinterpret_cast<const float4 *>(xs + c * kKC + 4 * u)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto store_x = [&](int buf) {
+        half8 h, l;
+        split8(xq[0], xq[1], h, l);
+        *reinterpret_cast<half8 *>(&sm.x.hi[buf][si][16 * sc]) = h;
+        *reinterpret_cast<half8 *>(&sm.x.lo[buf][si][16 * sc]) = l;
+        split8(xq[2], xq[3], h, l);
+        *reinterpret_cast<half8 *>(&sm.x.hi[buf][si][16 * sc + 8]) = h;
+        *reinterpret_cast<half8 *>(&sm.x.lo[buf][si][16 * sc + 8]) = l;
+    };
+    // weights two chunks ahead (wb: chunk c, wn: c + 1), x one chunk ahead (LDS double buffer)
+    half8 wb[2][4], wn[2][4];
+    auto load_w = [&](half8 (&w)[2][4], int c) {
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                w[cb][q] = c < nch ? *reinterpret_cast<const half8 *>(wp[cb] + c * kKC + 8 * q)
+                                   : (half8)(_Float16)0.0f;
+    };
+    load_x(0);
+    load_w(wb, 0);
+    load_w(wn, 1);
+    store_x(0);
+    __syncthreads();
+
+    for (int c = 0; c < nch; c++) {
+        const int buf = c & 1;
+        const bool more = c + 1 < nch;
+        half8 wf[2][4];
+        load_w(wf, c + 2);
+        if (more) load_x(c + 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++) {
+                const int row = 64 * wr + 32 * rb + j;
+                const half8 ah = *reinterpret_cast<const half8 *>(&sm.x.hi[buf][row][32 * hf + 8 * q]);
+                const half8 al = *reinterpret_cast<const half8 *>(&sm.x.lo[buf][row][32 * hf + 8 * q]);
+#pragma unroll
+                for (int cb = 0; cb < 2; cb++) {
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wb[cb][q], acc[rb][cb], 0, 0, 0);
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, wb[cb][q], acc[rb][cb], 0, 0, 0);
+                }
+            }
+        }
+        if (more) store_x(buf ^ 1);
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                wb[cb][q] = wn[cb][q];
+                wn[cb][q] = wf[cb][q];
+            }
+        __syncthreads();
+    }
+
+    // Epilogue, one 32-row block at a time: the waves holding it (wr = b / 2, row block b % 2)
+    // write it to the LDS tile, then the first 4 waves run the block's epilogue.
+    // (unrolled, so that acc is indexed with constants and stays in registers)
+#pragma unroll
+    for (int b = 0; b < NBLK; b++) {
+        const int p0 = (blk0 + b) * kBlk;
+        if (p0 >= end) continue;  // uniform
+        if (wr == (b >> 1)) {
+            const int rb = b & 1;
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    sm.tile[8 * (e >> 2) + 4 * hf + (e & 3)][64 * wc + 32 * cb + j] = acc[rb][cb][e];
+        }
+        __syncthreads();
+        if (tid < 256) {
+            RowTile t;
+            t.s = s;
+            t.start = start;
+            t.blk = blk0 + b;
+            t.lo = max(p0, start);
+            t.hi = min(p0 + kBlk, end);
+            t.live = true;
+            qkv_epilogue(a, t, ct, sm.tile, 0, kMT, tid);
+        }
+        __syncthreads();
+    }
+}
+
+// One split of the reduction for small grids (decode): the slice of dim, in batches of 4
+// chunks (256), is loaded in one go -- x for all 4 chunks into LDS as hi/lo (shared by the 4
+// waves), the weights straight into B operands (128 VGPRs) -- so a batch costs one memory
+// round trip, then 64 MFMAs per wave; the f32 partial tile goes to the scratch buffer.
+__global__ __launch_bounds__(256) void qkv_split_kernel(QkvArgs a) {
+    constexpr int NB = 4;  // chunks per batch
+    __shared__ __align__(16) _Float16 ahi[NB][kMT][kAStr];
+    __shared__ __align__(16) _Float16 alo[NB][kMT][kAStr];
+
+    int rt, ct, sp;
+    tile_of(a, blockIdx.x, rt, ct, sp);
+    if (sp >= a.n_split) return;
+    const RowTile t = row_tile(a, rt);
+    if (!t.live) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int si = tid >> 3, sc = tid & 7;
+    const int xr = x_row(a, t, si);
+    const int kb = sp * a.kps;
+    const int nbat = (min(kb + a.kps, a.dim) - kb) / (NB * kKC);
+    const float *xs = a.x + (size_t)max(xr, 0) * a.dim + kb + 8 * sc;
+    const _Float16 *wp[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) wp[cb] = w_row(a, ct, 64 * wave + 32 * cb + j) + kb + 32 * hf;
+
+    floatx16 acc[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[cb][e] = 0.0f;
+
+    for (int b = 0; b < nbat; b++) {
+        const int ko = b * NB * kKC;
+        float4 xu[NB], xv[NB];
+        half8 wb[NB][2][4];
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            xu[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[c] = xu[c];
+            if (xr >= 0) {
+                xu[c] = *reinterpret_cast<const float4 *>(xs + ko + c * kKC);
+                xv[c] = *reinterpret_cast<const float4 *>(xs + ko + c * kKC + 4);
+            }
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    wb[c][cb][q] = *reinterpret_cast<const half8 *>(wp[cb] + ko + c * kKC + 8 * q);
+        }
+        if (b > 0) __syncthreads();  // the previous batch's x tiles are no longer read
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            half8 h, l;
+            split8(xu[c], xv[c], h, l);
+            *reinterpret_cast<half8 *>(&ahi[c][si][8 * sc]) = h;
+            *reinterpret_cast<half8 *>(&alo[c][si][8 * sc]) = l;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NB; c++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const half8 ah = *reinterpret_cast<const half8 *>(&ahi[c][j][32 * hf + 8 * q]);
+                const half8 al = *reinterpret_cast<const half8 *>(&alo[c][j][32 * hf + 8 * q]);
+#pragma unroll
+                for (int cb = 0; cb < 2; cb++) {
+                    acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wb[c][cb][q], acc[cb], 0, 0, 0);
+                    acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, wb[c][cb][q], acc[cb], 0, 0, 0);
+                }
+            }
+    }
+    // D layout: register 4q + r of column block cb is row 8q + 4hf + r, column 64 wave + 32 cb + j
+    float *dst = a.part + (((size_t)sp * a.RT + rt) * a.CT + ct) * (kMT * kNT);
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            dst[(8 * (e >> 2) + 4 * hf + (e & 3)) * kNT + 64 * wave + 32 * cb + j] = acc[cb][e];
+}
+
+// Sum of the split partials of rows r0 .. r0 + NR - 1 of one tile, in split order, then their
+// epilogue.  Decode rows are independent, so a tile is spread over 32 / NR workgroups (NR = 8);
+// block rows share V words and take the whole tile (NR = 32).  Each thread issues the loads
+// of every split of two float4 before adding them.
+template <int NR>
 __global__ __launch_bounds__(256) void qkv_reduce_kernel(QkvArgs a) {
-    __shared__ __align__(16) float tile[kMT][kTStr];
-    const int rt = blockIdx.x % a.RT, ct = blockIdx.x / a.RT;
+    __shared__ __align__(16) float tile[NR][kTStr];
+    constexpr int G = kMT / NR;
+    const int tix = blockIdx.x / G, r0 = (blockIdx.x % G) * NR;
+    const int rt = tix % a.RT, ct = tix / a.RT;
     const RowTile t = row_tile(a, rt);
     if (!t.live) return;
     const int tid = threadIdx.x;
-    const size_t stride = (size_t)a.RT * a.CT * (kMT * kNT);
-    const float *src = a.part + ((size_t)rt * a.CT + ct) * (kMT * kNT);
-    for (int i = 0; i < kMT; i++) {
-        float v = src[i * kNT + tid];
-        for (int sp = 1; sp < a.n_split; sp++) v = v + src[sp * stride + i * kNT + tid];
-        tile[i][tid] = v;
+    const size_t stride = (size_t)a.RT * a.CT * (kMT * kNT) / 4;
+    const float4 *src = reinterpret_cast<const float4 *>(a.part) + ((size_t)rt * a.CT + ct) * (kMT * kNT / 4) +
+                        r0 * (kNT / 4);
+    constexpr int PER = NR / 4;            // float4 of the rows per thread
+    constexpr int U = PER < 2 ? PER : 2;   // float4 per pass
+#pragma unroll
+    for (int pass = 0; pass < PER / U; pass++) {
+        float4 v[U][kMaxSplit];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int sp = 0; sp < kMaxSplit; sp++)
+                if (sp < a.n_split) v[u][sp] = src[sp * stride + (U * pass + u) * 256 + tid];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float4 acc = v[u][0];
+#pragma unroll
+            for (int sp = 1; sp < kMaxSplit; sp++)
+                if (sp < a.n_split) {
+                    acc.x = acc.x + v[u][sp].x;
+                    acc.y = acc.y + v[u][sp].y;
+                    acc.z = acc.z + v[u][sp].z;
+                    acc.w = acc.w + v[u][sp].w;
+                }
+            const int e4 = (U * pass + u) * 256 + tid;
+            *reinterpret_cast<float4 *>(&tile[e4 / (kNT / 4)][4 * (e4 % (kNT / 4))]) = acc;
+        }
     }
     __syncthreads();
-    qkv_epilogue(a, t, ct, tile, tid);
+    qkv_epilogue(a, t, ct, tile, r0, NR, tid);
 }
 
 }  // namespace
@@ -391,14 +640,27 @@ QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int dim, int n_tok) {
     QkvPlan p;
     p.RT = n_tok == 1 ? (n_seq + kMT - 1) / kMT : n_seq * (n_tok / kBlk + 2);
     p.CT = (n_head + 1) / 2 + n_kv;
-    // Enough workgroups to cover the chip twice, each with at least 256 of the reduction.
     const int tiles = p.RT * p.CT;
-    const int want = std::max(1, (512 + tiles - 1) / tiles);
-    int kps = (dim + want - 1) / want;
-    kps = std::max(256, (kps + kKC - 1) / kKC * kKC);
-    p.kps = std::min(kps, dim);
-    p.n_split = (dim + p.kps - 1) / p.kps;
-    if (p.n_split == 1) p.kps = dim;
+    p.kps = dim;
+    p.n_split = 1;
+    p.big = false;
+    // Prefill chunks with enough work: 128-row tiles (four V blocks) over all of dim.
+    const int rt_big = n_seq * ((n_tok / kBlk + 2 + kBigBlocks - 1) / kBigBlocks);
+    if (n_tok > 1 && rt_big * p.CT >= 256) {
+        p.big = true;
+        p.RT = rt_big;
+        p.part_bytes = 0;
+        return p;
+    }
+    // Fewer tiles than CUs (decode): dim split into slices of whole 256s (at most kMaxSplit)
+    // so that about 512 workgroups stream the weights.
+    if (tiles < 256 && dim % 256 == 0 && dim >= 512) {
+        const int want = std::min(kMaxSplit, std::max(2, (512 + tiles - 1) / tiles));
+        const int nbat = dim / 256;
+        const int per = (nbat + want - 1) / want;  // 256s per split
+        p.kps = per * 256;
+        p.n_split = (nbat + per - 1) / per;
+    }
     p.part_bytes = p.n_split > 1 ? (uint64_t)p.n_split * tiles * kMT * kNT * sizeof(float) : 0;
     return p;
 }
@@ -431,8 +693,17 @@ hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x
     a.n_split = plan.n_split;
     a.n_wg = plan.RT * plan.CT * plan.n_split;
     const int grid = (a.n_wg + 7) / 8 * 8;
-    qkv_gemm_kernel<<<grid, 256, 0, st>>>(a);
-    if (plan.n_split > 1) qkv_reduce_kernel<<<plan.RT * plan.CT, 256, 0, st>>>(a);
+    if (plan.big) {
+        qkv_gemm128_kernel<kBigBlocks / 2><<<grid, 128 * kBigBlocks, 0, st>>>(a);
+    } else if (plan.n_split == 1) {
+        qkv_gemm_kernel<<<grid, 256, 0, st>>>(a);
+    } else {
+        qkv_split_kernel<<<grid, 256, 0, st>>>(a);
+        if (n_tok == 1)
+            qkv_reduce_kernel<8><<<plan.RT * plan.CT * (kMT / 8), 256, 0, st>>>(a);
+        else
+            qkv_reduce_kernel<kMT><<<plan.RT * plan.CT, 256, 0, st>>>(a);
+    }
     return hipGetLastError();
 }
 

@@ -35,15 +35,15 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 
 CONFIGS = {
     1: dict(name="llama3.2-1b_b1_ctx512_1layer", layers=1, n_head=32, n_kv=8, hd=64, batch=1,
-            ctx=512, theta=500000.0, steps=64, outliers=False),
+            ctx=512, theta=500000.0, steps=64, outliers=False, dim=2048),
     2: dict(name="llama3.2-3b_b1_prefill4096_28layers", layers=28, n_head=24, n_kv=8, hd=128,
-            batch=1, ctx=4096, theta=500000.0, steps=256, outliers=False),
+            batch=1, ctx=4096, theta=500000.0, steps=256, outliers=False, dim=3072),
     3: dict(name="qwen3-8b_b32_ctx8192_36layers", layers=36, n_head=32, n_kv=8, hd=128,
-            batch=32, ctx=8192, theta=1000000.0, steps=128, outliers=True),
+            batch=32, ctx=8192, theta=1000000.0, steps=128, outliers=True, dim=4096),
     4: dict(name="llama3-8b_b8_ctx16k-32k_ragged_32layers", layers=32, n_head=32, n_kv=8, hd=128,
-            batch=8, ctx=32768, theta=500000.0, steps=16, outliers=False, ragged=(16384, 32768)),
+            batch=8, ctx=32768, theta=500000.0, steps=16, outliers=False, ragged=(16384, 32768), dim=4096),
     5: dict(name="qwen3-4b_b4_prefill_4x512_36layers", layers=36, n_head=32, n_kv=8, hd=128,
-            batch=4, chunk=512, n_chunks=4, theta=1000000.0, outliers=False),
+            batch=4, chunk=512, n_chunks=4, theta=1000000.0, outliers=False, dim=2560),
 }
 
 
@@ -345,6 +345,55 @@ def run_append(args, cfg):
     return ms, B * n_tok * n_kv * (2 * hd * 4 + hd + 8), B * n_tok
 
 
+def run_qkv(args, cfg):
+    """The fused QKV projection + append (ts_qkv_append) of one step of the configuration:
+    one token per sequence for the decode configurations, one 512-token chunk per sequence
+    for config 5; every layer with its own f16 weights (so no layer's weights are still cached
+    when it runs again).  Returns the mean time of one call, its algorithmic bytes (weights,
+    x, q written, packed K/V rows and scales written) and its algorithmic flops (2 M N K)."""
+    import torch
+
+    from airframe_amd.kv_cache import KVCache, RopeTable
+
+    dev = torch.device("cuda:0")
+    L, n_head, n_kv, hd, B, dim = (cfg["layers"], cfg["n_head"], cfg["n_kv"], cfg["hd"],
+                                   cfg["batch"], cfg["dim"])
+    n_tok = cfg.get("chunk", 1)
+    reps = 5 if n_tok == 1 else 2
+    max_seq = n_tok * (reps + 1) + 8
+    rope = RopeTable(max_seq, hd, cfg["theta"])
+    kv = KVCache.new_int4(L, n_kv, hd, max_seq, B)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+
+    def w(rows):
+        return (torch.randn((rows, dim), generator=gen, device=dev) * 0.02).half()
+
+    ws = [(w(n_head * hd), w(n_kv * hd), w(n_kv * hd)) for _ in range(L)]
+    x = torch.randn((B, n_tok, dim), generator=gen, device=dev)
+    q = torch.empty((B, n_tok, n_head, hd), device=dev)
+    scratch = kv.qkv_workspace(dim, n_tok, n_head)
+    if args.qk_norm:
+        for layer in range(L):
+            kv.set_qk_norm(layer, None, torch.randn(hd, generator=gen, device=dev) * 0.2 + 1.0)
+    for layer in range(L):
+        kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch)
+    kv.increment(n_tok)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for layer in range(L):
+            kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch)
+        kv.increment(n_tok)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * L)
+    M, N = B * n_tok, (n_head + 2 * n_kv) * hd
+    byts = N * dim * 2 + M * dim * 4 + M * n_head * hd * 4 + M * n_kv * (hd + 8)
+    return ms, byts, 2.0 * M * N * dim, M
+
+
 def run_compact(args, cfg):
     """Sliding-window compaction (ts_kv_shift) on a cache of the configuration's shape: every
     sequence of every layer filled to ctx, then each sequence compacted (keep_sink 4, shift
@@ -417,6 +466,8 @@ def main():
     ap.add_argument("--qk-norm", action="store_true",
                     help="turn on the fused Qwen3 QK norm (random weights) for the decode step or "
                          "the append measurement")
+    ap.add_argument("--qkv", action="store_true",
+                    help="time the fused QKV projection + append (ts_qkv_append) instead")
     ap.add_argument("--compact", action="store_true",
                     help="measure sliding-window compaction (ts_kv_shift) on the config's cache "
                          "instead of the decode step")
@@ -454,6 +505,28 @@ def main():
                          "bytes_per_call": byts,
                          "counting": "f32 K and V read, packed K/V rows and two scales written"},
             "data": "synthetic"}), flush=True)
+        return
+    if args.qkv:
+        ms, byts, flops, toks = run_qkv(args, cfg)
+        decode = "ctx" in cfg
+        gbs = byts / (ms * 1e-3) / 1e9
+        tfs = flops / (ms * 1e-3) / 1e12
+        roof = ({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                 "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": byts,
+                 "counting": "f16 weights and f32 x read, f32 q, packed K/V rows and scales written"}
+                if decode else
+                {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                 "unit": "TFLOP/s", "frac": round(tfs / MFMA_F16_PEAK_TFLOPS, 4),
+                 "flops_per_call": flops, "counting": "2 M N K of the projection (the hi/lo split "
+                 "of x executes twice that on the matrix cores)"})
+        print(json.dumps({
+            "metric": "fused QKV projection + INT4 append " + ("HBM GB/s" if decode else "TFLOP/s"),
+            "value": round(gbs if decode else tfs, 2), "unit": "GB/s" if decode else "TFLOP/s",
+            "n_gpus": 1, "higher_is_better": True, "us_per_call": round(ms * 1e3, 2),
+            "tokens_per_s": round(toks / (ms * 1e-3), 1),
+            "config": {"workload": cfg["name"] + "_qkv" + ("_qknorm" if args.qk_norm else ""),
+                       "tokens_per_call": toks, "dim": cfg["dim"]},
+            "roofline": roof, "data": "synthetic (random f16 weights, N(0,1) x)"}), flush=True)
         return
     if args.compact:
         if "ctx" not in cfg:

@@ -8,7 +8,8 @@ F16 weights, followed by quantize_kv).
   it must write the same bits);
 * a run without the raw K/V outputs writes the same cache and q bits.
 Shapes cover the decode rows (one token per sequence, > 32 sequences), block rows (prefill
-chunks from ragged, unaligned lengths), the reduction split over dim and the unsplit one,
+chunks from ragged, unaligned lengths, in 32- and 128-row tiles), the reduction split over dim
+and the unsplit one,
 an odd number of query heads, the QK norm and a compacted sequence."""
 import numpy as np
 import pytest
@@ -59,11 +60,13 @@ def run_case(p: Pair, rng, n_tok, dim, n_head, x_scale=1.0):
     (3, 70, 1024, 8, 2),     # block rows, split
     (3, 70, 256, 8, 2),      # block rows, no split
     (2, 33, 512, 3, 1),      # odd query-head count: the last q tile is half empty
+    (4, 300, 256, 32, 8),    # prefill chunks: 128-row tiles (four V blocks per workgroup)
 ])
 def test_qkv_append(gpu, n_seq, n_tok, dim, n_head, n_kv):
     say(f"qkv n_seq={n_seq} n_tok={n_tok} dim={dim} n_head={n_head} n_kv={n_kv}")
     rng = np.random.default_rng(dim + n_tok + n_seq)
-    p = Pair(n_seq, n_kv, 128, 256, 1e6)
+    max_seq = 128 + 2 * n_tok + 16
+    p = Pair(n_seq, n_kv, 128, max_seq, 1e6)
     lens = rng.integers(0, 100, size=n_seq).astype(np.int32)
     lens[0] = 0
     p.set_lens(lens)
@@ -73,7 +76,7 @@ def test_qkv_append(gpu, n_seq, n_tok, dim, n_head, n_kv):
         run_case(p, rng, 5, dim, n_head)
 
     # the same call without the raw K/V outputs: identical q and cache bits
-    g2 = KVCache.new_int4(1, n_kv, 128, 256, n_seq)
+    g2 = KVCache.new_int4(1, n_kv, 128, max_seq, n_seq)
     for s, l in enumerate(lens_before):
         g2.set_seq_len(int(l), seq=s)
     q2 = g2.qkv_append(0, dev(x), dev(wq), dev(wk), dev(wv), p.rope).cpu().numpy()
