@@ -36,8 +36,9 @@ SOURCES = {
     "ts_decode.hip": MFMA_VGPR,
     "ts_prefill.hip": MFMA_VGPR,
     "ts_qkv.hip": EXACT,
+    "ts_proj.hip": EXACT,
 }
-HEADERS = ["ts_internal.h", "ts_mfma.h", "ts_quant.h", "ts_store128.h", os.path.join("..", "..", "include", "turboshimmy.h")]
+HEADERS = ["ts_internal.h", "ts_mfma.h", "ts_quant.h", "ts_store128.h", "ts_gemm.h", os.path.join("..", "..", "include", "turboshimmy.h")]
 
 
 def _compile(src: str, extra: list[str], objdir: str) -> str:

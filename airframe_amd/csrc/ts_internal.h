@@ -127,7 +127,7 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
 struct QkvPlan {
     int RT, CT;           // row tiles, column tiles
     int kps, n_split;     // reduction length per split, splits
-    bool big;             // 128-row tiles (prefill chunks) instead of 32-row ones
+    bool big;             // one workgroup per 64-row tile over all of dim (else split)
     uint64_t part_bytes;  // scratch for the split partials (0 without a split)
 };
 QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int dim, int n_tok);
@@ -135,5 +135,14 @@ hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x
                       const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int n_head,
                       float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,
                       const QkvPlan &plan, float *part, hipStream_t st);
+
+// Attention output projection (ts_proj.hip).
+struct ProjPlan {
+    int RT, CT, kps, n_split;
+    uint64_t part_bytes;
+};
+ProjPlan proj_plan(int M, int K, int N);
+hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, float *act, float *stash,
+                       const ProjPlan &plan, float *part, hipStream_t st);
 
 }  // namespace ts

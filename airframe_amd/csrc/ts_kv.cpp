@@ -458,4 +458,24 @@ int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32
                                      static_cast<float *>(d_workspace), as_stream(stream)));
 }
 
+int ts_attn_out_proj_workspace(int32_t n_tok, int32_t attn_dim, int32_t dim, uint64_t *bytes) {
+    if (!bytes || n_tok < 0 || attn_dim <= 0 || attn_dim % 64 != 0 || dim <= 0) return TS_ERR_INVALID;
+    *bytes = n_tok == 0 ? 0 : ts::proj_plan(n_tok, attn_dim, dim).part_bytes;
+    return TS_OK;
+}
+
+int ts_attn_out_proj(const float *d_attn, int32_t n_tok, int32_t attn_dim, const uint16_t *d_wo,
+                     int32_t dim, float *d_act, float *d_stash, void *d_workspace,
+                     uint64_t workspace_bytes, void *stream) {
+    if (!d_attn || !d_wo || !d_act || n_tok < 0 || attn_dim <= 0 || attn_dim % 64 != 0 || dim <= 0 ||
+        !aligned16(d_attn) || !aligned16(d_wo) || !aligned16(d_act) || !aligned16(d_stash))
+        return TS_ERR_INVALID;
+    if (n_tok == 0) return TS_OK;
+    const ts::ProjPlan plan = ts::proj_plan(n_tok, attn_dim, dim);
+    if (plan.part_bytes > 0 && (!d_workspace || workspace_bytes < plan.part_bytes || !aligned16(d_workspace)))
+        return TS_ERR_WORKSPACE;
+    return hip_status(ts::launch_proj(d_attn, n_tok, attn_dim, d_wo, dim, d_act, d_stash, plan,
+                                      static_cast<float *>(d_workspace), as_stream(stream)));
+}
+
 }  // extern "C"

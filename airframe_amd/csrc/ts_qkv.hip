@@ -16,30 +16,23 @@
 // are bounded by 2^-12 * sum|x w|, the same order as the f32 reference's own sequential
 // rounding over dim = 4096 terms (4096 * 2^-24).
 //
-// Tiles: 32 rows (tokens) x 256 columns, one workgroup of 4 waves, each wave 32 x 64 (two
-// MFMA column blocks).  A column tile is two q heads, or the K head h next to the V head h,
-// so the epilogue holds whole head rows.  Rows are
-//   * n_tok == 1 (decode): 32 sequences, one new token each, at position len[s];
-//   * n_tok > 1: the 32 positions of one V block of one sequence (the block owns its V words,
-//     as in the append kernel).
-// Large grids (prefill) run one workgroup per tile over all of dim: the k-chunk loop
-// double-buffers x (converted to hi/lo once per workgroup, in LDS) and streams the weights
-// straight into the B operands one chunk ahead, and the epilogue runs on the finished tile.
-// Small grids (decode) split the reduction over `dim` across workgroups: each loads its whole
-// slice in one round trip and writes an f32 partial tile, and a second kernel sums the
-// partials in split order (deterministic) and runs the epilogue.
-#include "ts_mfma.h"
+// Column tiles are 256 wide: two q heads, or the K head h next to the V head h, so the
+// epilogue holds whole head rows.  The epilogue works on 32-row units: for n_tok == 1 (decode)
+// 32 sequences, one new token each at position len[s]; for n_tok > 1 the 32 positions of one V
+// block of one sequence (the block owns its V words, as in the append kernel).
+//   * Enough tiles (prefill, large batches): one workgroup per 64-row tile over all of dim
+//     (gemm_tile_core), the epilogue on the finished tile.
+//   * Few tiles (decode): 32-row tiles with the reduction over dim split across workgroups
+//     (gemm_split_core, one memory round trip per slice), f32 partials, and a second kernel
+//     that sums them in split order (deterministic) and runs the epilogue.
+#include "ts_gemm.h"
 #include "ts_store128.h"
 
 namespace ts {
 namespace {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
 constexpr int kMT = 32;     // rows per tile
 constexpr int kNT = 256;    // columns per tile
-constexpr int kKC = 64;     // k per chunk
-constexpr int kAStr = 72;   // LDS row stride of the x tiles (f16): 144 B spreads the rows' banks
 constexpr int kTStr = 260;  // LDS row stride of the output tile (f32)
 constexpr int kMaxSplit = 16;  // most splits of the reduction over dim
 #ifndef TS_QKV_BIG_BLOCKS
@@ -118,17 +111,6 @@ __device__ inline void tile_of(const QkvArgs &a, int id, int &rt, int &ct, int &
     rt = lin % a.RT;
     ct = (lin / a.RT) % a.CT;
     sp = lin / (a.RT * a.CT);
-}
-
-// The 8 x values of one staging thread as hi and lo f16 halves.
-__device__ inline void split8(const float4 &u, const float4 &v, half8 &hi, half8 &lo) {
-    const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const _Float16 h = (_Float16)x[e];
-        hi[e] = h;
-        lo[e] = (_Float16)(x[e] - (float)h);
-    }
 }
 
 // Quantize-and-store of one new token per row (n_tok == 1): row i = sequence t.s + i at its
@@ -274,115 +256,16 @@ __device__ void qkv_epilogue(const QkvArgs &a, const RowTile &t, int ct, const f
     store_block128(a.L, t.s, h, t.blk, t.lo, t.hi, kx, vx, cs, a.rope ? a.rope_pairs : 0, wave, lane);
 }
 
-__global__ __launch_bounds__(256) void qkv_gemm_kernel(QkvArgs a) {
-    __shared__ __align__(16) _Float16 ahi[2][kMT][kAStr];
-    __shared__ __align__(16) _Float16 alo[2][kMT][kAStr];
-    __shared__ __align__(16) float tile[kMT][kTStr];
-
-    int rt, ct, sp;
-    tile_of(a, blockIdx.x, rt, ct, sp);
-    if (sp >= a.n_split) return;
-    const RowTile t = row_tile(a, rt);
-    if (!t.live) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-
-    // staging role: row si, 8 floats at k offset 8 sc of each chunk
-    const int si = tid >> 3, sc = tid & 7;
-    const int xr = x_row(a, t, si);
-    const int kb = sp * a.kps;
-    const int nch = (min(kb + a.kps, a.dim) - kb) / kKC;
-    const float *xs = a.x + (size_t)max(xr, 0) * a.dim + kb + 8 * sc;
-
-    // B role: columns 64 wave + 32 cb + j, 32 consecutive k (16 B per k-step) from 32 hf
-    const _Float16 *wp[2];
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++) wp[cb] = w_row(a, ct, 64 * wave + 32 * cb + j) + kb + 32 * hf;
-
-    floatx16 acc[2];
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[cb][e] = 0.0f;
-
-    float4 xu = make_float4(0.f, 0.f, 0.f, 0.f), xv = xu;
-    if (xr >= 0) {
-        xu = *reinterpret_cast<const float4 *>(xs);
-        xv = *reinterpret_cast<const float4 *>(xs + 4);
-    }
-    half8 wb[2][4];
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-        for (int q = 0; q < 4; q++) wb[cb][q] = *reinterpret_cast<const half8 *>(wp[cb] + 8 * q);
-    {
-        half8 h, l;
-        split8(xu, xv, h, l);
-        *reinterpret_cast<half8 *>(&ahi[0][si][8 * sc]) = h;
-        *reinterpret_cast<half8 *>(&alo[0][si][8 * sc]) = l;
-    }
-    __syncthreads();
-
-    for (int c = 0; c < nch; c++) {
-        const int buf = c & 1;
-        const bool more = c + 1 < nch;
-        half8 wn[2][4];
-        if (more) {
-            if (xr >= 0) {
-                xu = *reinterpret_cast<const float4 *>(xs + (c + 1) * kKC);
-                xv = *reinterpret_cast<const float4 *>(xs + (c + 1) * kKC + 4);
-            }
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-                    wn[cb][q] = *reinterpret_cast<const half8 *>(wp[cb] + (c + 1) * kKC + 8 * q);
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const half8 ah = *reinterpret_cast<const half8 *>(&ahi[buf][j][32 * hf + 8 * q]);
-            const half8 al = *reinterpret_cast<const half8 *>(&alo[buf][j][32 * hf + 8 * q]);
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++) {
-                acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wb[cb][q], acc[cb], 0, 0, 0);
-                acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, wb[cb][q], acc[cb], 0, 0, 0);
-            }
-        }
-        if (more) {
-            half8 h, l;
-            split8(xu, xv, h, l);
-            *reinterpret_cast<half8 *>(&ahi[buf ^ 1][si][8 * sc]) = h;
-            *reinterpret_cast<half8 *>(&alo[buf ^ 1][si][8 * sc]) = l;
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) wb[cb][q] = wn[cb][q];
-        }
-        __syncthreads();
-    }
-
-    // D layout: register 4q + r of column block cb is row 8q + 4hf + r, column 64 wave + 32 cb + j
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) tile[8 * (e >> 2) + 4 * hf + (e & 3)][64 * wave + 32 * cb + j] = acc[cb][e];
-    __syncthreads();
-    qkv_epilogue(a, t, ct, tile, 0, kMT, tid);
-}
-
-// Block rows in tiles of 128 (prefill chunks): four consecutive V blocks blk0 .. blk0 + 3 of
-// one sequence.  8 waves: wave (wr, wc) computes rows 64 wr .. + 63, columns 64 wc .. + 63
-// (2 x 2 MFMA blocks), so each weight operand feeds two row blocks and each x operand two
-// column blocks: half the operand traffic per MFMA of the 32-row tiles.  x is staged per
-// chunk as hi/lo in LDS (double-buffered), the weights stream into registers one chunk ahead.
-// The epilogue runs block by block on a 32 x 256 LDS tile that reuses the x buffers.
+// One workgroup per tile over all of dim (grids with enough tiles): MT = 64 WR rows -- for
+// block rows 2 WR consecutive V blocks of one sequence, for decode rows MT sequences -- through
+// gemm_tile_core (each wave 64 x 64, 2 x 2 MFMA blocks: every weight operand feeds two row
+// blocks and every x operand two column blocks).  The epilogue runs 32 rows at a time on a
+// 32 x 256 LDS tile that reuses the x buffers.
 template <int WR>
-__global__ __launch_bounds__(256 * WR) void qkv_gemm128_kernel(QkvArgs a) {
+__global__ __launch_bounds__(256 * WR) void qkv_tile_kernel(QkvArgs a) {
     constexpr int MT = 64 * WR, NBLK = MT / kBlk;
     union Smem {
-        struct {
-            _Float16 hi[2][MT][kAStr];
-            _Float16 lo[2][MT][kAStr];
-        } x;
+        XTiles<MT> x;
         float tile[kMT][kTStr];
     };
     __shared__ __align__(16) Smem sm;
@@ -390,95 +273,24 @@ __global__ __launch_bounds__(256 * WR) void qkv_gemm128_kernel(QkvArgs a) {
     int rt, ct, sp;
     tile_of(a, blockIdx.x, rt, ct, sp);
     if (sp >= a.n_split) return;
+    const bool single = a.n_tok == 1;  // decode rows: MT sequences, one token each
     const int nb4 = (a.n_tok / kBlk + 2 + NBLK - 1) / NBLK;
-    const int s = rt / nb4;
-    const int start = a.len[s], end = start + a.n_tok;
+    const int s = single ? MT * rt : rt / nb4;
+    const int start = single ? 0 : a.len[s], end = start + a.n_tok;
     const int blk0 = start / kBlk + NBLK * (rt % nb4);
-    if (blk0 * kBlk >= end) return;
+    if (!single && blk0 * kBlk >= end) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int wr = wave >> 2, wc = wave & 3;
 
     // staging role: row si (0..MT-1), 16 floats at k offset 16 sc of each chunk
     const int si = tid >> 2, sc = tid & 3;
     const int ps = blk0 * kBlk + si;
-    const int xr = (ps >= start && ps < end) ? s * a.n_tok + (ps - start) : -1;
-    const float *xs = a.x + (size_t)max(xr, 0) * a.dim + 16 * sc;
-    const int nch = a.dim / kKC;
-
-    const _Float16 *wp[2];
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++) wp[cb] = w_row(a, ct, 64 * wc + 32 * cb + j) + 32 * hf;
-
+    const int xr = single ? (s + si < a.L.S ? s + si : -1)
+                          : (ps >= start && ps < end) ? s * a.n_tok + (ps - start) : -1;
+    const float *xs = xr >= 0 ? a.x + (size_t)xr * a.dim + 16 * sc : nullptr;
+    const _Float16 *const wp[2] = {w_row(a, ct, 64 * wc + j) + 32 * hf, w_row(a, ct, 64 * wc + 32 + j) + 32 * hf};
     floatx16 acc[2][2];
-#pragma unroll
-    for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-        for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[rb][cb][e] = 0.0f;
-
-    float4 xq[4];
-    auto load_x = [&](int c) {
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-            xq[u] = xr >= 0 ? *reinterpret_cast<const float4 *>(xs + c * kKC + 4 * u)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-    };
-    auto store_x = [&](int buf) {
-        half8 h, l;
-        split8(xq[0], xq[1], h, l);
-        *reinterpret_cast<half8 *>(&sm.x.hi[buf][si][16 * sc]) = h;
-        *reinterpret_cast<half8 *>(&sm.x.lo[buf][si][16 * sc]) = l;
-        split8(xq[2], xq[3], h, l);
-        *reinterpret_cast<half8 *>(&sm.x.hi[buf][si][16 * sc + 8]) = h;
-        *reinterpret_cast<half8 *>(&sm.x.lo[buf][si][16 * sc + 8]) = l;
-    };
-    // weights two chunks ahead (wb: chunk c, wn: c + 1), x one chunk ahead (LDS double buffer)
-    half8 wb[2][4], wn[2][4];
-    auto load_w = [&](half8 (&w)[2][4], int c) {
-#pragma unroll
-        for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                w[cb][q] = c < nch ? *reinterpret_cast<const half8 *>(wp[cb] + c * kKC + 8 * q)
-                                   : (half8)(_Float16)0.0f;
-    };
-    load_x(0);
-    load_w(wb, 0);
-    load_w(wn, 1);
-    store_x(0);
-    __syncthreads();
-
-    for (int c = 0; c < nch; c++) {
-        const int buf = c & 1;
-        const bool more = c + 1 < nch;
-        half8 wf[2][4];
-        load_w(wf, c + 2);
-        if (more) load_x(c + 1);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-#pragma unroll
-            for (int rb = 0; rb < 2; rb++) {
-                const int row = 64 * wr + 32 * rb + j;
-                const half8 ah = *reinterpret_cast<const half8 *>(&sm.x.hi[buf][row][32 * hf + 8 * q]);
-                const half8 al = *reinterpret_cast<const half8 *>(&sm.x.lo[buf][row][32 * hf + 8 * q]);
-#pragma unroll
-                for (int cb = 0; cb < 2; cb++) {
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wb[cb][q], acc[rb][cb], 0, 0, 0);
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, wb[cb][q], acc[rb][cb], 0, 0, 0);
-                }
-            }
-        }
-        if (more) store_x(buf ^ 1);
-#pragma unroll
-        for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                wb[cb][q] = wn[cb][q];
-                wn[cb][q] = wf[cb][q];
-            }
-        __syncthreads();
-    }
+    gemm_tile_core<WR>(sm.x, xs, wp, a.dim / kKC, tid, acc);
 
     // Epilogue, one 32-row block at a time: the waves holding it (wr = b / 2, row block b % 2)
     // write it to the LDS tile, then the first 4 waves run the block's epilogue.
@@ -486,7 +298,7 @@ __global__ __launch_bounds__(256 * WR) void qkv_gemm128_kernel(QkvArgs a) {
 #pragma unroll
     for (int b = 0; b < NBLK; b++) {
         const int p0 = (blk0 + b) * kBlk;
-        if (p0 >= end) continue;  // uniform
+        if (single ? s + kBlk * b >= a.L.S : p0 >= end) continue;  // uniform
         if (wr == (b >> 1)) {
             const int rb = b & 1;
 #pragma unroll
@@ -498,7 +310,7 @@ __global__ __launch_bounds__(256 * WR) void qkv_gemm128_kernel(QkvArgs a) {
         __syncthreads();
         if (tid < 256) {
             RowTile t;
-            t.s = s;
+            t.s = single ? s + kBlk * b : s;
             t.start = start;
             t.blk = blk0 + b;
             t.lo = max(p0, start);
@@ -510,14 +322,10 @@ __global__ __launch_bounds__(256 * WR) void qkv_gemm128_kernel(QkvArgs a) {
     }
 }
 
-// One split of the reduction for small grids (decode): the slice of dim, in batches of 4
-// chunks (256), is loaded in one go -- x for all 4 chunks into LDS as hi/lo (shared by the 4
-// waves), the weights straight into B operands (128 VGPRs) -- so a batch costs one memory
-// round trip, then 64 MFMAs per wave; the f32 partial tile goes to the scratch buffer.
+// One split of the reduction for small grids (decode) through gemm_split_core; the f32
+// partial tile goes to the scratch buffer.
 __global__ __launch_bounds__(256) void qkv_split_kernel(QkvArgs a) {
-    constexpr int NB = 4;  // chunks per batch
-    __shared__ __align__(16) _Float16 ahi[NB][kMT][kAStr];
-    __shared__ __align__(16) _Float16 alo[NB][kMT][kAStr];
+    __shared__ __align__(16) SplitTiles sm;
 
     int rt, ct, sp;
     tile_of(a, blockIdx.x, rt, ct, sp);
@@ -525,61 +333,14 @@ __global__ __launch_bounds__(256) void qkv_split_kernel(QkvArgs a) {
     const RowTile t = row_tile(a, rt);
     if (!t.live) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-    const int si = tid >> 3, sc = tid & 7;
-    const int xr = x_row(a, t, si);
+    const int xr = x_row(a, t, tid >> 3);
     const int kb = sp * a.kps;
-    const int nbat = (min(kb + a.kps, a.dim) - kb) / (NB * kKC);
-    const float *xs = a.x + (size_t)max(xr, 0) * a.dim + kb + 8 * sc;
-    const _Float16 *wp[2];
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++) wp[cb] = w_row(a, ct, 64 * wave + 32 * cb + j) + kb + 32 * hf;
-
+    const int nbat = (min(kb + a.kps, a.dim) - kb) / (4 * kKC);
+    const float *xs = xr >= 0 ? a.x + (size_t)xr * a.dim + kb + 8 * (tid & 7) : nullptr;
+    const _Float16 *const wp[2] = {w_row(a, ct, 64 * wave + j) + kb + 32 * hf,
+                                   w_row(a, ct, 64 * wave + 32 + j) + kb + 32 * hf};
     floatx16 acc[2];
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[cb][e] = 0.0f;
-
-    for (int b = 0; b < nbat; b++) {
-        const int ko = b * NB * kKC;
-        float4 xu[NB], xv[NB];
-        half8 wb[NB][2][4];
-#pragma unroll
-        for (int c = 0; c < NB; c++) {
-            xu[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-            xv[c] = xu[c];
-            if (xr >= 0) {
-                xu[c] = *reinterpret_cast<const float4 *>(xs + ko + c * kKC);
-                xv[c] = *reinterpret_cast<const float4 *>(xs + ko + c * kKC + 4);
-            }
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-                    wb[c][cb][q] = *reinterpret_cast<const half8 *>(wp[cb] + ko + c * kKC + 8 * q);
-        }
-        if (b > 0) __syncthreads();  // the previous batch's x tiles are no longer read
-#pragma unroll
-        for (int c = 0; c < NB; c++) {
-            half8 h, l;
-            split8(xu[c], xv[c], h, l);
-            *reinterpret_cast<half8 *>(&ahi[c][si][8 * sc]) = h;
-            *reinterpret_cast<half8 *>(&alo[c][si][8 * sc]) = l;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int c = 0; c < NB; c++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const half8 ah = *reinterpret_cast<const half8 *>(&ahi[c][j][32 * hf + 8 * q]);
-                const half8 al = *reinterpret_cast<const half8 *>(&alo[c][j][32 * hf + 8 * q]);
-#pragma unroll
-                for (int cb = 0; cb < 2; cb++) {
-                    acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wb[c][cb][q], acc[cb], 0, 0, 0);
-                    acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, wb[c][cb][q], acc[cb], 0, 0, 0);
-                }
-            }
-    }
+    gemm_split_core(sm, xs, wp, nbat, tid, acc);
     // D layout: register 4q + r of column block cb is row 8q + 4hf + r, column 64 wave + 32 cb + j
     float *dst = a.part + (((size_t)sp * a.RT + rt) * a.CT + ct) * (kMT * kNT);
 #pragma unroll
@@ -605,31 +366,7 @@ __global__ __launch_bounds__(256) void qkv_reduce_kernel(QkvArgs a) {
     const size_t stride = (size_t)a.RT * a.CT * (kMT * kNT) / 4;
     const float4 *src = reinterpret_cast<const float4 *>(a.part) + ((size_t)rt * a.CT + ct) * (kMT * kNT / 4) +
                         r0 * (kNT / 4);
-    constexpr int PER = NR / 4;            // float4 of the rows per thread
-    constexpr int U = PER < 2 ? PER : 2;   // float4 per pass
-#pragma unroll
-    for (int pass = 0; pass < PER / U; pass++) {
-        float4 v[U][kMaxSplit];
-#pragma unroll
-        for (int u = 0; u < U; u++)
-#pragma unroll
-            for (int sp = 0; sp < kMaxSplit; sp++)
-                if (sp < a.n_split) v[u][sp] = src[sp * stride + (U * pass + u) * 256 + tid];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            float4 acc = v[u][0];
-#pragma unroll
-            for (int sp = 1; sp < kMaxSplit; sp++)
-                if (sp < a.n_split) {
-                    acc.x = acc.x + v[u][sp].x;
-                    acc.y = acc.y + v[u][sp].y;
-                    acc.z = acc.z + v[u][sp].z;
-                    acc.w = acc.w + v[u][sp].w;
-                }
-            const int e4 = (U * pass + u) * 256 + tid;
-            *reinterpret_cast<float4 *>(&tile[e4 / (kNT / 4)][4 * (e4 % (kNT / 4))]) = acc;
-        }
-    }
+    sum_partials<NR, kMaxSplit>(src, stride, a.n_split, &tile[0][0], kTStr, tid);
     __syncthreads();
     qkv_epilogue(a, t, ct, tile, r0, NR, tid);
 }
@@ -638,30 +375,29 @@ __global__ __launch_bounds__(256) void qkv_reduce_kernel(QkvArgs a) {
 
 QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int dim, int n_tok) {
     QkvPlan p;
-    p.RT = n_tok == 1 ? (n_seq + kMT - 1) / kMT : n_seq * (n_tok / kBlk + 2);
     p.CT = (n_head + 1) / 2 + n_kv;
-    const int tiles = p.RT * p.CT;
     p.kps = dim;
     p.n_split = 1;
-    p.big = false;
-    // Prefill chunks with enough work: 128-row tiles (four V blocks) over all of dim.
-    const int rt_big = n_seq * ((n_tok / kBlk + 2 + kBigBlocks - 1) / kBigBlocks);
-    if (n_tok > 1 && rt_big * p.CT >= 256) {
-        p.big = true;
-        p.RT = rt_big;
-        p.part_bytes = 0;
-        return p;
-    }
-    // Fewer tiles than CUs (decode): dim split into slices of whole 256s (at most kMaxSplit)
-    // so that about 512 workgroups stream the weights.
+    p.part_bytes = 0;
+    // Fewer 32-row tiles than CUs (decode, short chunks): dim split into slices of whole 256s
+    // (at most kMaxSplit) so that about 512 workgroups stream the weights.
+    const int rt32 = n_tok == 1 ? (n_seq + kMT - 1) / kMT : n_seq * (n_tok / kBlk + 2);
+    const int tiles = rt32 * p.CT;
     if (tiles < 256 && dim % 256 == 0 && dim >= 512) {
+        p.big = false;
+        p.RT = rt32;
         const int want = std::min(kMaxSplit, std::max(2, (512 + tiles - 1) / tiles));
         const int nbat = dim / 256;
         const int per = (nbat + want - 1) / want;  // 256s per split
         p.kps = per * 256;
         p.n_split = (nbat + per - 1) / per;
+        p.part_bytes = (uint64_t)p.n_split * tiles * kMT * kNT * sizeof(float);
+        return p;
     }
-    p.part_bytes = p.n_split > 1 ? (uint64_t)p.n_split * tiles * kMT * kNT * sizeof(float) : 0;
+    // Otherwise one workgroup per tile of 32 kBigBlocks rows over all of dim.
+    p.big = true;
+    const int mt = kBlk * kBigBlocks;
+    p.RT = n_tok == 1 ? (n_seq + mt - 1) / mt : n_seq * ((n_tok / kBlk + 2 + kBigBlocks - 1) / kBigBlocks);
     return p;
 }
 
@@ -694,9 +430,7 @@ hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x
     a.n_wg = plan.RT * plan.CT * plan.n_split;
     const int grid = (a.n_wg + 7) / 8 * 8;
     if (plan.big) {
-        qkv_gemm128_kernel<kBigBlocks / 2><<<grid, 128 * kBigBlocks, 0, st>>>(a);
-    } else if (plan.n_split == 1) {
-        qkv_gemm_kernel<<<grid, 256, 0, st>>>(a);
+        qkv_tile_kernel<kBigBlocks / 2><<<grid, 128 * kBigBlocks, 0, st>>>(a);
     } else {
         qkv_split_kernel<<<grid, 256, 0, st>>>(a);
         if (n_tok == 1)

@@ -335,3 +335,36 @@ class KVCache:
 
 # keep the status codes reachable from the package
 TS_ERR_OVERFLOW = _lib.TS_ERR_OVERFLOW
+
+
+_proj_ws: dict = {}
+
+
+def attn_out_proj(attn: torch.Tensor, wo: torch.Tensor, act: torch.Tensor,
+                  stash: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                  stream=None) -> torch.Tensor:
+    """main_attn_proj (sh_layer_v1.wgsl:763-821, F16 weights): act += Wo attn per token, the raw
+    product into `stash` when given.  attn: [n_tok, attn_dim] f32 (any leading shape flattened
+    to tokens), wo: [dim, attn_dim] f16, act (and stash): [n_tok, dim] f32.  Returns act."""
+    attn2 = attn.reshape(-1, attn.shape[-1])
+    n_tok, attn_dim = attn2.shape
+    dim = wo.shape[0]
+    if wo.shape != (dim, attn_dim):
+        raise ValueError("wo must be [dim, attn_dim]")
+    if act.numel() != n_tok * dim or (stash is not None and stash.numel() != n_tok * dim):
+        raise ValueError("act/stash must hold [n_tok, dim]")
+    ws = workspace
+    if ws is None:
+        key = (n_tok, attn_dim, dim)
+        if key not in _proj_ws:
+            b = ctypes.c_uint64()
+            check("ts_attn_out_proj_workspace",
+                  load().ts_attn_out_proj_workspace(n_tok, attn_dim, dim, ctypes.byref(b)))
+            _proj_ws[key] = torch.empty(max(b.value, 16), dtype=torch.uint8, device=attn.device)
+        ws = _proj_ws[key]
+    check("ts_attn_out_proj",
+          load().ts_attn_out_proj(_ptr(attn2, torch.float32, "attn"), n_tok, attn_dim,
+                                  _ptr(wo, torch.float16, "wo"), dim, _ptr(act, torch.float32, "act"),
+                                  _ptr(stash, torch.float32, "stash") if stash is not None else None,
+                                  ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
+    return act

@@ -394,6 +394,38 @@ def run_qkv(args, cfg):
     return ms, byts, 2.0 * M * N * dim, M
 
 
+def run_proj(args, cfg):
+    """The attention output projection with the residual add (ts_attn_out_proj) of one step:
+    one token per sequence for the decode configurations, a 512-token chunk per sequence for
+    config 5; every layer with its own f16 weights.  Returns the mean time of one call, its
+    algorithmic bytes (weights, attention output, the residual read and written) and flops."""
+    import torch
+
+    from airframe_amd.kv_cache import attn_out_proj
+
+    dev = torch.device("cuda:0")
+    L, n_head, hd, B, dim = cfg["layers"], cfg["n_head"], cfg["hd"], cfg["batch"], cfg["dim"]
+    M, K = B * cfg.get("chunk", 1), n_head * hd
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    ws = [(torch.randn((dim, K), generator=gen, device=dev) * 0.02).half() for _ in range(L)]
+    a = torch.randn((M, K), generator=gen, device=dev)
+    act = torch.randn((M, dim), generator=gen, device=dev)
+    for layer in range(L):
+        attn_out_proj(a, ws[layer], act)
+    torch.cuda.synchronize()
+    reps = 5
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for layer in range(L):
+            attn_out_proj(a, ws[layer], act)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * L)
+    return ms, dim * K * 2 + M * K * 4 + M * dim * 8, 2.0 * M * dim * K, M
+
+
 def run_compact(args, cfg):
     """Sliding-window compaction (ts_kv_shift) on a cache of the configuration's shape: every
     sequence of every layer filled to ctx, then each sequence compacted (keep_sink 4, shift
@@ -468,6 +500,8 @@ def main():
                          "the append measurement")
     ap.add_argument("--qkv", action="store_true",
                     help="time the fused QKV projection + append (ts_qkv_append) instead")
+    ap.add_argument("--proj", action="store_true",
+                    help="time the attention output projection + residual (ts_attn_out_proj) instead")
     ap.add_argument("--compact", action="store_true",
                     help="measure sliding-window compaction (ts_kv_shift) on the config's cache "
                          "instead of the decode step")
@@ -506,25 +540,27 @@ def main():
                          "counting": "f32 K and V read, packed K/V rows and two scales written"},
             "data": "synthetic"}), flush=True)
         return
-    if args.qkv:
-        ms, byts, flops, toks = run_qkv(args, cfg)
+    if args.qkv or args.proj:
+        ms, byts, flops, toks = (run_qkv if args.qkv else run_proj)(args, cfg)
+        what = "fused QKV projection + INT4 append" if args.qkv else "attention output projection + residual"
         decode = "ctx" in cfg
         gbs = byts / (ms * 1e-3) / 1e9
         tfs = flops / (ms * 1e-3) / 1e12
         roof = ({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                  "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": byts,
-                 "counting": "f16 weights and f32 x read, f32 q, packed K/V rows and scales written"}
+                 "counting": ("f16 weights and f32 x read, f32 q, packed K/V rows and scales written"
+                              if args.qkv else "f16 weights and f32 attention output read, residual read and written")}
                 if decode else
                 {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                  "unit": "TFLOP/s", "frac": round(tfs / MFMA_F16_PEAK_TFLOPS, 4),
                  "flops_per_call": flops, "counting": "2 M N K of the projection (the hi/lo split "
                  "of x executes twice that on the matrix cores)"})
         print(json.dumps({
-            "metric": "fused QKV projection + INT4 append " + ("HBM GB/s" if decode else "TFLOP/s"),
+            "metric": what + (" HBM GB/s" if decode else " TFLOP/s"),
             "value": round(gbs if decode else tfs, 2), "unit": "GB/s" if decode else "TFLOP/s",
             "n_gpus": 1, "higher_is_better": True, "us_per_call": round(ms * 1e3, 2),
             "tokens_per_s": round(toks / (ms * 1e-3), 1),
-            "config": {"workload": cfg["name"] + "_qkv" + ("_qknorm" if args.qk_norm else ""),
+            "config": {"workload": cfg["name"] + ("_qkv" if args.qkv else "_oproj") + ("_qknorm" if args.qk_norm else ""),
                        "tokens_per_call": toks, "dim": cfg["dim"]},
             "roofline": roof, "data": "synthetic (random f16 weights, N(0,1) x)"}), flush=True)
         return

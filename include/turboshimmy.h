@@ -231,6 +231,23 @@ int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32
                   const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
                   uint64_t workspace_bytes, void *stream);
 
+/* ---- attention output projection ---------------------------------------------------- */
+
+/* Bytes of scratch ts_attn_out_proj needs for this shape (0 when the reduction is not split).
+ * Host only. */
+int ts_attn_out_proj_workspace(int32_t n_tok, int32_t attn_dim, int32_t dim, uint64_t *bytes);
+
+/* main_attn_proj (sh_layer_v1.wgsl:763-821, F16 weights: the formula slot 1 branch at
+ * :777-781) for n_tok tokens: dot = Wo a over attn_dim = n_head * head_dim inputs, then
+ * act = act + dot (:818-820), and dot itself into d_stash when given (the reference's stash
+ * for Gemma-2's post-attention norm, :812-815).  d_attn: [n_tok][attn_dim] f32, the attention
+ * output (ts_attn_decode / ts_attn_prefill); d_wo: [dim][attn_dim] f16 row-major; d_act:
+ * [n_tok][dim] f32, updated in place; d_stash: NULL or [n_tok][dim] f32.  attn_dim a multiple
+ * of 64; pointers 16-byte aligned.  Needs no cache. */
+int ts_attn_out_proj(const float *d_attn, int32_t n_tok, int32_t attn_dim, const uint16_t *d_wo,
+                     int32_t dim, float *d_act, float *d_stash, void *d_workspace,
+                     uint64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,10 @@ def lib():
                                  np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS"),
                                  ctypes.c_int, _f32p]
         L.or_project.restype = None
+        L.or_attn_proj.argtypes = [_f32p, ctypes.c_int, ctypes.c_int,
+                                   np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS"),
+                                   ctypes.c_int, _f32p, ctypes.c_void_p]
+        L.or_attn_proj.restype = None
         _lib = L
     return _lib
 
@@ -89,6 +93,19 @@ def project(x: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
     out = np.zeros((n, n_out), dtype=np.float32)
     lib().or_project(x, n, dim, w_bits, n_out, out)
     return out
+
+
+def attn_proj(attn: np.ndarray, wo_bits: np.ndarray, act: np.ndarray):
+    """main_attn_proj: returns (act + dot, dot) for attn [n, attn_dim] f32, wo [dim, attn_dim]
+    f16 bits, act [n, dim] f32 (not modified)."""
+    attn = np.ascontiguousarray(attn, dtype=np.float32)
+    wo_bits = np.ascontiguousarray(wo_bits, dtype=np.uint16)
+    out = np.ascontiguousarray(act, dtype=np.float32).copy()
+    n, attn_dim = attn.shape
+    dim = wo_bits.shape[0]
+    stash = np.zeros((n, dim), np.float32)
+    lib().or_attn_proj(attn, n, attn_dim, wo_bits, dim, out, stash.ctypes.data)
+    return out, stash
 
 
 def qk_norm_row(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:

@@ -29,6 +29,8 @@
  *                       sh_dequant_any.wgsl:261-265)
  *   or_project          sh_layer_v1_int4.wgsl:454-575 (main_qkv, F16 branch :494-498): one
  *                       f32 dot per output, `dot += x[col] * w[row][col]` in column order
+ *   or_attn_proj        sh_layer_v1.wgsl:763-821 (main_attn_proj, F16 branch :777-781): the same
+ *                       dot over attn_dim, stashed, then act = act + dot
  *   or_attend_head      src/ops/reference/attention.rs:236-313 (per-head QK^T, scale,
  *                       causal softmax, PV), src/ops/reference/matmul.rs:91-104 (f32 products
  *                       accumulated in f64), src/ops/reference/softmax.rs:91-129 (mask to -inf,
@@ -167,6 +169,20 @@ void or_project(const float *x, int n_rows, int dim, const uint16_t *w, int n_ou
         out[(size_t)r * n_out + o] = dot;
     }
     free(wf);
+}
+
+/* main_attn_proj for n_tok tokens: dot[t][o] = or_project(attn[t], wo[o]); stash[t][o] = dot
+ * (stash may be NULL); act[t][o] = act[t][o] + dot (one f32 add, residual first). */
+void or_attn_proj(const float *attn, int n_tok, int attn_dim, const uint16_t *wo, int dim, float *act,
+                  float *stash) {
+    float *dot = (float *)malloc(sizeof(float) * (size_t)n_tok * dim);
+    if (!dot) return;
+    or_project(attn, n_tok, attn_dim, wo, dim, dot);
+    for (size_t i = 0; i < (size_t)n_tok * dim; i++) {
+        if (stash) stash[i] = dot[i];
+        act[i] = act[i] + dot[i];
+    }
+    free(dot);
 }
 
 /* ---- QK norm ------------------------------------------------------------------------- */

@@ -8,7 +8,7 @@ F16 weights, followed by quantize_kv).
   it must write the same bits);
 * a run without the raw K/V outputs writes the same cache and q bits.
 Shapes cover the decode rows (one token per sequence, > 32 sequences), block rows (prefill
-chunks from ragged, unaligned lengths, in 32- and 128-row tiles), the reduction split over dim
+chunks from ragged, unaligned lengths, in 32- and 64-row tiles), the reduction split over dim
 and the unsplit one,
 an odd number of query heads, the QK norm and a compacted sequence."""
 import numpy as np
@@ -60,7 +60,8 @@ def run_case(p: Pair, rng, n_tok, dim, n_head, x_scale=1.0):
     (3, 70, 1024, 8, 2),     # block rows, split
     (3, 70, 256, 8, 2),      # block rows, no split
     (2, 33, 512, 3, 1),      # odd query-head count: the last q tile is half empty
-    (4, 300, 256, 32, 8),    # prefill chunks: 128-row tiles (four V blocks per workgroup)
+    (4, 300, 256, 32, 8),    # prefill chunks: 64-row tiles (two V blocks per workgroup)
+    (70, 1, 320, 8, 2),      # decode rows in 64-row tiles (dim not a multiple of 256: no split)
 ])
 def test_qkv_append(gpu, n_seq, n_tok, dim, n_head, n_kv):
     say(f"qkv n_seq={n_seq} n_tok={n_tok} dim={dim} n_head={n_head} n_kv={n_kv}")

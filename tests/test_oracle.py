@@ -509,3 +509,22 @@ def test_project_sequential_f32_order():
     wc = np.zeros((1, 64), np.float16)
     wc[0, :3] = 1.0
     assert oracle.project(xc, wc.view(np.uint16))[0, 0] == 0.0   # (1 + 2^24) rounds to 2^24
+
+
+def test_attn_proj_adds_the_projection_to_the_residual():
+    """main_attn_proj: stash = the f32 dot, act = act + dot with one rounding (checked on exact
+    integers, where the sum is the integer one, and against the projection itself)."""
+    rng = np.random.default_rng(3)
+    a = rng.integers(-4, 5, size=(3, 128)).astype(np.float32)
+    w = rng.integers(-4, 5, size=(5, 128)).astype(np.float16)
+    act = rng.integers(-100, 100, size=(3, 5)).astype(np.float32)
+    out, stash = oracle.attn_proj(a, w.view(np.uint16), act)
+    dot = a.astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(stash, dot.astype(np.float32))
+    assert np.array_equal(out, (act.astype(np.int64) + dot).astype(np.float32))
+    af = rng.standard_normal((2, 256)).astype(np.float32)
+    wf = (rng.standard_normal((3, 256)) * 0.1).astype(np.float16)
+    actf = rng.standard_normal((2, 3)).astype(np.float32)
+    out, stash = oracle.attn_proj(af, wf.view(np.uint16), actf)
+    assert np.array_equal(stash, oracle.project(af, wf.view(np.uint16)))
+    assert np.array_equal(out, (actf + stash).astype(np.float32))
