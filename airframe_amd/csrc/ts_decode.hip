@@ -963,18 +963,18 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
 
 }  // namespace
 
-// Split plan: aim for ~kTargetWG workgroups in total -- one per CU: measured on the config-3
-// and config-4 shapes, one long split per CU streams faster than two or four shorter ones
-// (2.24 vs 2.26 vs 2.37 ms per config-3 step for 256 / 512 / 1024 workgroups), and a
-// (sequence, kv head) that fits one split needs no combine -- with each split a multiple of
-// 64 positions and at least 256 when the context allows.  n_split is non-decreasing in
-// max_ctx.
+// Split plan: aim for ~kTargetWG workgroups in total -- two per CU: measured on the config-3
+// and config-4 shapes, long splits stream faster than short ones (2.26 vs 2.37 ms per
+// config-3 step for 512 vs 1024 workgroups).  One per CU (256) was faster still on most
+// boxes (2.24 ms) but 10% slower than 1024 on one: with a single workgroup per CU any slow
+// CU sets the kernel's time, two per CU keep some balancing.  Each split is a multiple of 64
+// positions and at least 256 when the context allows.  n_split is non-decreasing in max_ctx.
 DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx) {
     // TS_DECODE_WG overrides the workgroup target (a tuning knob; read once).
     static const int kTargetWG = [] {
         const char *e = getenv("TS_DECODE_WG");
         const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 256;
+        return v > 0 ? v : 512;
     }();
     const int units = n_seq * n_kv;
     int want = (kTargetWG + units - 1) / units;
