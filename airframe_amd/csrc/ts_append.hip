@@ -10,46 +10,29 @@
 // identical to the CPU quantizer.
 //
 // One workgroup (4 waves) owns one 32-position V block of one (sequence, kv head): it
-// quantizes every position of the block that falls in the append range, stages the codes in
-// LDS, and writes whole words with 128-bit stores.  Owning the block means no two workgroups
-// ever write the same V word, although a word interleaves 8 positions.
-#include "ts_store128.h"
+// quantizes every position of the block that falls in the append range from registers and
+// writes the words itself (ts_store.h: each wave assembles the V words of one key group with
+// lane swaps).  Owning the block means no two workgroups ever write the same V word, although
+// a word interleaves 8 positions.
+#include "ts_store.h"
 
 namespace ts {
 namespace {
 
-// Nibble n of the result = byte n of x (every byte < 16).
-__device__ inline uint32_t pack8(uint64_t x) {
-    x = (x | (x >> 4)) & 0x00FF00FF00FF00FFull;
-    x = (x | (x >> 8)) & 0x0000FFFF0000FFFFull;
-    x = (x | (x >> 16)) & 0x00000000FFFFFFFFull;
-    return (uint32_t)x;
-}
-
-// start: first position written for this sequence (d_start[s] if d_start, else fixed_start).
-// Source row of position p: src[((s*ld_tok) + (p - start)) * H + h][hd].
-//
-// Wave w quantizes positions w, w+4, ... of the block.  Every load of the wave is issued
-// before any reduction (positions outside the append range load a valid neighbour's row and
-// are never written), reductions use DPP and permlane swaps, and the quotient takes the
-// reciprocal fast path of encode_fast.  Codes are staged in LDS as K [position][dim] and V
-// [dim][position] bytes, so each output word is one 8-byte (K) or two 4-byte (V) LDS reads.
-template <int HD>
-__global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const float *__restrict__ k,
-                                                             const float *__restrict__ v,
-                                                             const int32_t *__restrict__ d_start,
-                                                             int32_t fixed_start, int32_t count,
-                                                             int32_t ld_tok,
-                                                             const float *__restrict__ rope,
-                                                             int32_t rope_pairs) {
-    constexpr int PAIRS = HD / 2;
-    constexpr int NTD = HD / 16;          // 16-dim tiles of the V block layout
-    constexpr int PPW = kBlk / 4;         // positions per wave
-    constexpr int NJ = (PAIRS + 63) / 64; // pairs per lane
-    constexpr int VROW = kBlk + 4;        // V staging row (bytes): 36 keeps lane writes 2-way
-    __shared__ __align__(16) uint8_t kc[kBlk][HD];
-    __shared__ __align__(16) uint8_t vc[HD][VROW];
-    __shared__ float ksc[kBlk], vsc[kBlk];
+// hd = 64: 8 lanes per position, lane l holding dims 8l..8l+7 -- exactly K word l.  Wave w
+// takes the 8 positions of V key group g = w (lane group r8 = lane / 8 holds position
+// 4w + r8 % 4 + 16 (r8 / 4)), so store_block64 assembles the V words inside the wave.  No LDS.
+// Source row of position p: src[((s*ld_tok) + (p - start)) * H + h][hd]; start is d_start[s]
+// if d_start, else fixed_start.  Positions outside the append range load a valid neighbour's
+// row and are never written.
+__global__ __launch_bounds__(256) void quantize_rows64_kernel(KvLayerView L, const float *__restrict__ k,
+                                                               const float *__restrict__ v,
+                                                               const int32_t *__restrict__ d_start,
+                                                               int32_t fixed_start, int32_t count,
+                                                               int32_t ld_tok,
+                                                               const float *__restrict__ rope,
+                                                               int32_t rope_pairs) {
+    constexpr int HD = 64;
     const int s = blockIdx.z, h = blockIdx.y;
     const int start = d_start ? d_start[s] : fixed_start;
     const int end = start + count;
@@ -57,126 +40,16 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(KvLayerView L, const
     const int p0 = blk * kBlk;
     if (p0 >= end) return;
     const int lo = max(p0, start), hi = min(p0 + kBlk, end);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-
-    float kx[PPW][2 * NJ], vx[PPW][2 * NJ];
-#pragma unroll
-    for (int ii = 0; ii < PPW; ii++) {
-        const int pc = min(max(p0 + wave + 4 * ii, lo), hi - 1);
-        const size_t src = (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD;
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int pi = min(lane + 64 * j, PAIRS - 1);  // lanes past the row repeat its end
-            const float2 kk = *reinterpret_cast<const float2 *>(k + src + 2 * pi);
-            const float2 vv = *reinterpret_cast<const float2 *>(v + src + 2 * pi);
-            kx[ii][2 * j] = kk.x;
-            kx[ii][2 * j + 1] = kk.y;
-            vx[ii][2 * j] = vv.x;
-            vx[ii][2 * j + 1] = vv.y;
-        }
-    }
-    if (L.kn) {
-        // QK norm of every K row before RoPE, the squares summed in order across the lanes
-#pragma unroll
-        for (int ii = 0; ii < PPW; ii++) {
-            static_assert(NJ == 1, "the ordered sum reads one pair per lane");
-            const float ns = qk_norm_scale_from_sum(
-                ordered_sum_pairs(sq_rn(kx[ii][0]), sq_rn(kx[ii][1]), PAIRS), HD, L.norm_eps);
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const int pi = min(lane + 64 * j, PAIRS - 1);
-                kx[ii][2 * j] = qk_norm_apply(kx[ii][2 * j], ns, L.kn[2 * pi]);
-                kx[ii][2 * j + 1] = qk_norm_apply(kx[ii][2 * j + 1], ns, L.kn[2 * pi + 1]);
-            }
-        }
-    }
-    float km[PPW], vm[PPW];
-#pragma unroll
-    for (int ii = 0; ii < PPW; ii++) {
-        const int pc = min(max(p0 + wave + 4 * ii, lo), hi - 1);
-        km[ii] = 0.0f;
-        vm[ii] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int pi = min(lane + 64 * j, PAIRS - 1);
-            if (rope && pi < rope_pairs)
-                rope_rotate(kx[ii][2 * j], kx[ii][2 * j + 1],
-                            *reinterpret_cast<const float2 *>(
-                                rope + ((size_t)rot_of(L, s, pc) * rope_pairs + pi) * 2));
-            km[ii] = fmaxf(km[ii], fmaxf(fabsf(kx[ii][2 * j]), fabsf(kx[ii][2 * j + 1])));
-            vm[ii] = fmaxf(vm[ii], fmaxf(fabsf(vx[ii][2 * j]), fabsf(vx[ii][2 * j + 1])));
-        }
-    }
-#pragma unroll
-    for (int ii = 0; ii < PPW; ii++) {
-        km[ii] = wave_max_nonneg(km[ii]);
-        vm[ii] = wave_max_nonneg(vm[ii]);
-    }
-#pragma unroll
-    for (int ii = 0; ii < PPW; ii++) {
-        const int i = wave + 4 * ii;
-        const float ks = quant_scale(km[ii]);
-        const float vs = quant_scale(vm[ii]);
-        const float kr = __builtin_amdgcn_rcpf(ks), vr = __builtin_amdgcn_rcpf(vs);
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int pi = lane + 64 * j;
-            if (pi < PAIRS) {
-                *reinterpret_cast<uint16_t *>(&kc[i][2 * pi]) =
-                    (uint16_t)(encode_fast(kx[ii][2 * j], ks, kr) | (encode_fast(kx[ii][2 * j + 1], ks, kr) << 8));
-                vc[2 * pi][i] = (uint8_t)encode_fast(vx[ii][2 * j], vs, vr);
-                vc[2 * pi + 1][i] = (uint8_t)encode_fast(vx[ii][2 * j + 1], vs, vr);
-            }
-        }
-        if (lane == 0) {
-            ksc[i] = ks;
-            vsc[i] = vs;
-        }
-    }
-    __syncthreads();
-
-    const size_t row = (size_t)s * L.H + h;
-    // K rows: 16-byte quads, HD/32 per position.
-    {
-        constexpr int QPP = HD / 32;
-        const int i = tid / QPP, quad = tid % QPP;
-        if (tid < kBlk * QPP && p0 + i >= lo && p0 + i < hi) {
-            const uint64_t *src = reinterpret_cast<const uint64_t *>(&kc[i][quad * 32]);
-            const uint4 w = make_uint4(pack8(src[0]), pack8(src[1]), pack8(src[2]), pack8(src[3]));
-            reinterpret_cast<uint4 *>(L.kp + (row * L.P + p0 + i) * (HD / 2))[quad] = w;
-        }
-    }
-    if (tid < kBlk && p0 + tid >= lo && p0 + tid < hi) {
-        L.ks[row * L.P + p0 + tid] = ksc[tid];
-        L.vs[row * L.P + p0 + tid] = vsc[tid];
-    }
-    // V block: HD*4 words, 4 consecutive words per thread.  Word (g, dl, td) holds dim
-    // 16 td + dl at positions 4g..4g+3 (nibbles 0-3) and 16+4g..16+4g+3 (nibbles 4-7).
-    if (tid < HD) {
-        const bool full = (lo == p0 && hi == p0 + kBlk);
-        uint4 *dst = reinterpret_cast<uint4 *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16)) + tid;
-        uint4 old = make_uint4(0, 0, 0, 0);
-        if (!full) old = *dst;
-        uint32_t w[4] = {old.x, old.y, old.z, old.w};
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int widx = tid * 4 + u;
-            const int lanei = widx / NTD, td = widx % NTD;
-            const int g = lanei >> 4, dl = lanei & 15;
-            const int d = 16 * td + dl;
-            const uint64_t x = (uint64_t)*reinterpret_cast<const uint32_t *>(&vc[d][4 * g]) |
-                               ((uint64_t)*reinterpret_cast<const uint32_t *>(&vc[d][16 + 4 * g]) << 32);
-            const uint32_t fresh = pack8(x);
-            uint32_t keep = 0;  // nibbles of positions outside [lo, hi)
-#pragma unroll
-            for (int n = 0; n < 8; n++) {
-                const int i = (n < 4) ? (4 * g + n) : (16 + 4 * g + (n - 4));
-                if (p0 + i < lo || p0 + i >= hi) keep |= 0xFu << (4 * n);
-            }
-            w[u] = (w[u] & keep) | (fresh & ~keep);
-        }
-        *dst = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r8 = lane >> 3, l = lane & 7;
+    const int pc = min(max(p0 + 4 * wave + (r8 & 3) + 16 * (r8 >> 2), lo), hi - 1);
+    float2 cs[4];
+    rope_cs4(L, s, pc, rope, rope_pairs, l, cs);
+    const size_t src = (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD + 8 * l;
+    const float4 a0 = *reinterpret_cast<const float4 *>(k + src), a1 = *reinterpret_cast<const float4 *>(k + src + 4);
+    const float4 b0 = *reinterpret_cast<const float4 *>(v + src), b1 = *reinterpret_cast<const float4 *>(v + src + 4);
+    float kx[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float vx[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    store_block64(L, s, h, blk, lo, hi, kx, vx, cs, rope ? rope_pairs : 0, wave, lane);
 }
 
 // hd = 128: 16 lanes per position, lane l holding dims 8l..8l+7 -- exactly K word l.  Wave w
@@ -321,7 +194,7 @@ hipError_t launch_quantize_rows(const KvLayerView &L, const float *k, const floa
     if (L.hd == 128)
         quantize_rows128_kernel<<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
     else if (L.hd == 64)
-        quantize_rows_kernel<64><<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
+        quantize_rows64_kernel<<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -26,7 +26,7 @@
 //     (gemm_split_core, one memory round trip per slice), f32 partials, and a second kernel
 //     that sums them in split order (deterministic) and runs the epilogue.
 #include "ts_gemm.h"
-#include "ts_store128.h"
+#include "ts_store.h"
 
 namespace ts {
 namespace {

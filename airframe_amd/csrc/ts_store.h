@@ -1,4 +1,4 @@
-// ts_store128.h -- the quantize-and-store step of the INT4 append for head_dim 128, shared
+// ts_store.h -- the quantize-and-store step of the INT4 append (head_dim 128 and 64), shared
 // by the append kernel (rows loaded from f32 K/V) and the fused QKV projection (rows taken
 // from the projection's output tile), so both write bit-identical codes and scales.
 //
@@ -39,6 +39,138 @@ __device__ inline void rope_cs4(const KvLayerView &L, int s, int p, const float 
                     ? *reinterpret_cast<const float2 *>(rope + ((size_t)pr * rope_pairs + pair) * 2)
                     : make_float2(1.0f, 0.0f);
     }
+}
+
+// A head row spread over LPR lanes (16 for hd 128, 8 for hd 64), lane l = lane % LPR holding
+// dims 8l..8l+7.
+
+// Max of v over the row's lanes (values >= 0): DPP inside the 16-lane row.
+template <int LPR>
+__device__ inline float row_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm(1,0,3,2)
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm(2,3,0,1)
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror: 8 lanes
+    if (LPR == 16) v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror: 16 lanes
+    return v;
+}
+
+// Sum of the row's squares in dimension order (lane 0's 8 in order, then lane 1's, ...),
+// from 0, one f32 rounding per add: the running sum walks the lanes with row_shr:1.  Every
+// lane of the row gets the total.
+template <int LPR>
+__device__ inline float row_ordered_sum(const float (&sq)[8], int l) {
+#pragma clang fp contract(off)
+    float run = 0.0f;
+#pragma unroll
+    for (int i = 0; i < LPR; i++) {
+        float t = i == 0 ? 0.0f
+                         : __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(run), 0x111, 0xF, 0xF, true));
+#pragma unroll
+        for (int e = 0; e < 8; e++) t = t + sq[e];
+        run = l == i ? t : run;
+    }
+    return __shfl(run, (__lane_id() & ~(LPR - 1)) | (LPR - 1), 64);
+}
+
+// QK norm of a K row in place (weights kn, the row's lanes as above).
+template <int LPR>
+__device__ inline void row_qk_norm(float (&kx)[8], const float *kn, float eps, int l) {
+    float sq[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) sq[e] = sq_rn(kx[e]);
+    const float ns = qk_norm_scale_from_sum(row_ordered_sum<LPR>(sq, l), 8 * LPR, eps);
+#pragma unroll
+    for (int e = 0; e < 8; e++) kx[e] = qk_norm_apply(kx[e], ns, kn[8 * l + e]);
+}
+
+// Scales and codes of one K row and one V row from their maxima (row_max): the reciprocal
+// fast path of encode_fast, with the exact path for the whole wave when any lane needs it.
+// Every lane of the wave must call it.
+__device__ inline void row_codes(const float (&kx)[8], const float (&vx)[8], float km, float vm, float &ks,
+                                 float &vs, uint32_t (&kc)[8], uint32_t (&vc)[8]) {
+    ks = quant_scale(km);
+    vs = quant_scale(vm);
+    const float kr = __builtin_amdgcn_rcpf(ks), vr = __builtin_amdgcn_rcpf(vs);
+    bool kneed = !(ks >= 1.17549435e-38f && ks <= 4.25352959e37f);
+    bool vneed = !(vs >= 1.17549435e-38f && vs <= 4.25352959e37f);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        kc[e] = code_fast(kx[e] * kr, kneed);
+        vc[e] = code_fast(vx[e] * vr, vneed);
+    }
+    if (__builtin_amdgcn_ballot_w64(kneed) != 0) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) kc[e] = encode(kx[e], ks);
+    }
+    if (__builtin_amdgcn_ballot_w64(vneed) != 0) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) vc[e] = encode(vx[e], vs);
+    }
+}
+
+// hd = 64: quantizes and stores positions [lo, hi) of V block blk of one (sequence s, kv head
+// h).  4 waves, 8 lanes per position (lane l = lane % 8 holds dims 8l..8l+7 of one position in
+// kx / vx, raw, with its pairs' rotation in cs).  Wave w owns the 8 positions of V key group
+// g = w: lane group r8 = lane / 8 holds position 4w + (r8 % 4) + 16 (r8 / 4), which is nibble
+// r8 of the group's V words, so the words are OR-assembled across the wave's 8 lane groups
+// (DPP row_ror:8, then two permlane swaps) and written by the wave.  Rows outside [lo, hi)
+// may hold anything finite; they are never written.  Every lane of the workgroup must call it.
+__device__ inline void store_block64(const KvLayerView &L, int s, int h, int blk, int lo, int hi,
+                                     float (&kx)[8], const float (&vx)[8], const float2 (&cs)[4],
+                                     int rot_pairs, int wave, int lane) {
+    constexpr int HD = 64, NTD = HD / 16;
+    const int r8 = lane >> 3, l = lane & 7;
+    const int p0 = blk * kBlk;
+    const int p = p0 + 4 * wave + (r8 & 3) + 16 * (r8 >> 2);
+    const size_t row = (size_t)s * L.H + h;
+    if (L.kn) row_qk_norm<8>(kx, L.kn, L.norm_eps, l);
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+        if (4 * l + m < rot_pairs) rope_rotate(kx[2 * m], kx[2 * m + 1], cs[m]);
+    float km = 0.0f, vm = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        km = fmaxf(km, fabsf(kx[e]));
+        vm = fmaxf(vm, fabsf(vx[e]));
+    }
+    km = row_max<8>(km);
+    vm = row_max<8>(vm);
+    float ks, vs;
+    uint32_t kc[8], vc[8];
+    row_codes(kx, vx, km, vm, ks, vs, kc, vc);
+    if (p >= lo && p < hi) {
+        uint32_t kw = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) kw |= kc[e] << (4 * e);
+        reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[l] = kw;
+        if (l == 0) {
+            L.ks[row * L.P + p] = ks;
+            L.vs[row * L.P + p] = vs;
+        }
+    }
+    // this lane group's nibble of the words of dims 8l + e, OR-ed over the 8 groups
+    uint32_t vpart[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        uint32_t x = vc[e] << (4 * r8);
+        x |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);  // row_ror:8
+        auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        x = a[0] | a[1];
+        auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        vpart[e] = b[0] | b[1];
+    }
+    uint32_t keep = 0;  // nibbles of positions outside [lo, hi)
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const int pn = p0 + 4 * wave + (n & 3) + 16 * (n >> 2);
+        if (pn < lo || pn >= hi) keep |= 0xFu << (4 * n);
+    }
+    // lane (r8, l) writes the word of dim 8l + r8
+    const uint32_t w = r8 == 0 ? vpart[0] : r8 == 1 ? vpart[1] : r8 == 2 ? vpart[2] : r8 == 3 ? vpart[3]
+                     : r8 == 4 ? vpart[4] : r8 == 5 ? vpart[5] : r8 == 6 ? vpart[6] : vpart[7];
+    const int d = 8 * l + r8, td = d >> 4, dl = d & 15;
+    uint32_t *dst = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16)) + (wave * 16 + dl) * NTD + td;
+    *dst = keep ? (*dst & keep) | (w & ~keep) : w;
 }
 
 // Quantizes and stores positions [lo, hi) of V block blk (positions p0 = 32 blk .. p0 + 31) of
