@@ -130,7 +130,7 @@ struct QkvPlan {
     bool big;             // one workgroup per 64-row tile over all of dim (else split)
     uint64_t part_bytes;  // scratch for the split partials (0 without a split)
 };
-QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int dim, int n_tok);
+QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok);
 hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x, int dim, int n_tok,
                       const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int n_head,
                       float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,

@@ -424,14 +424,14 @@ int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_
 }
 
 static bool qkv_shape_ok(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head) {
-    return kv->d.head_dim == 128 && dim > 0 && dim % 64 == 0 && n_tok >= 0 && heads_ok(kv, n_head);
+    return (kv->d.head_dim == 128 || kv->d.head_dim == 64) && dim > 0 && dim % 64 == 0 && n_tok >= 0 && heads_ok(kv, n_head);
 }
 
 int ts_qkv_workspace(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head, uint64_t *bytes) {
     if (!kv || !bytes) return TS_ERR_INVALID;
-    if (kv->d.head_dim != 128) return TS_ERR_UNSUPPORTED;
+    if (kv->d.head_dim != 128 && kv->d.head_dim != 64) return TS_ERR_UNSUPPORTED;
     if (!qkv_shape_ok(kv, dim, n_tok, n_head)) return TS_ERR_INVALID;
-    *bytes = n_tok == 0 ? 0 : ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, dim, n_tok).part_bytes;
+    *bytes = n_tok == 0 ? 0 : ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, dim, n_tok).part_bytes;
     return TS_OK;
 }
 
@@ -440,7 +440,7 @@ int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32
                   const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
                   uint64_t workspace_bytes, void *stream) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers) return TS_ERR_INVALID;
-    if (kv->d.head_dim != 128) return TS_ERR_UNSUPPORTED;
+    if (kv->d.head_dim != 128 && kv->d.head_dim != 64) return TS_ERR_UNSUPPORTED;
     if (!qkv_shape_ok(kv, dim, n_tok, n_head) || !d_x || !d_wq || !d_wk || !d_wv || !d_q ||
         !aligned16(d_x) || !aligned16(d_wq) || !aligned16(d_wk) || !aligned16(d_wv) ||
         !aligned16(d_q) || (!d_k) != (!d_v) || (d_k && (!aligned16(d_k) || !aligned16(d_v))))
@@ -450,7 +450,7 @@ int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32
     int rc = check_rope(rope, kv->d.head_dim, rot_end(kv, n_tok));
     if (rc) return rc;
     if (n_tok == 0) return TS_OK;
-    const ts::QkvPlan plan = ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, dim, n_tok);
+    const ts::QkvPlan plan = ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, dim, n_tok);
     if (plan.part_bytes > 0 && (!d_workspace || workspace_bytes < plan.part_bytes || !aligned16(d_workspace)))
         return TS_ERR_WORKSPACE;
     return hip_status(ts::launch_qkv(kv->layer(layer), kv->d_len, d_x, dim, n_tok, d_wq, d_wk, d_wv,

@@ -1,5 +1,5 @@
 // ts_qkv.hip -- the QKV projection with the INT4 append as its epilogue, for gfx950 (head_dim
-// 128, f16 weights).
+// 128 or 64, f16 weights).
 //
 // Replaces main_qkv (src/backend/bindless/sh_layer_v1_int4.wgsl:454-575) followed by
 // quantize_kv (dispatched at src/backend/bindless/pipeline/layer.rs:1092-1099): for every
@@ -16,8 +16,8 @@
 // are bounded by 2^-12 * sum|x w|, the same order as the f32 reference's own sequential
 // rounding over dim = 4096 terms (4096 * 2^-24).
 //
-// Column tiles are 256 wide: two q heads, or the K head h next to the V head h, so the
-// epilogue holds whole head rows.  The epilogue works on 32-row units: for n_tok == 1 (decode)
+// Column tiles are 256 wide: 256 / hd q heads, or 128 / hd pairs (K head h, V head h) side by
+// side, so the epilogue holds whole head rows.  The epilogue works on 32-row units: for n_tok == 1 (decode)
 // 32 sequences, one new token each at position len[s]; for n_tok > 1 the 32 positions of one V
 // block of one sequence (the block owns its V words, as in the append kernel).
 //   * Enough tiles (prefill, large batches): one workgroup per 64-row tile over all of dim
@@ -45,14 +45,15 @@ struct QkvArgs {
     KvLayerView L;
     const int32_t *len;    // start position of every sequence
     const float *x;        // [S][n_tok][dim]
-    const _Float16 *wq, *wk, *wv;  // [n_head*128][dim], [H*128][dim], [H*128][dim]
-    float *q_out;          // [S][n_tok][n_head][128]
-    float *k_out, *v_out;  // optional raw projections [S][n_tok][H][128]
+    const _Float16 *wq, *wk, *wv;  // [n_head*hd][dim], [H*hd][dim], [H*hd][dim]
+    float *q_out;          // [S][n_tok][n_head][hd]
+    float *k_out, *v_out;  // optional raw projections [S][n_tok][H][hd]
     const float *rope;
     int rope_pairs;
     float *part;           // split partials [n_split][RT][CT][32][256], or null
     int dim, n_tok, n_head;
-    int n_qt;              // q column tiles (ceil(n_head / 2))
+    int hd, hpt;           // head dim; kv heads per column tile (128 / hd)
+    int n_qt;              // q column tiles (ceil(n_head * hd / 256))
     int RT, CT;            // row and column tiles
     int kps, n_split;      // k per split (multiple of kKC), splits
     int n_wg;              // workgroups of the GEMM launch (before rounding up to 8)
@@ -92,14 +93,17 @@ __device__ inline int x_row(const QkvArgs &a, const RowTile &t, int i) {
     return (p >= t.lo && p < t.hi) ? t.s * a.n_tok + (p - t.start) : -1;
 }
 
-// Weight row of column n (0..255) of column tile ct (clamped to a valid row past n_head).
+// Weight row of column n (0..255) of column tile ct (clamped to a valid row past the last
+// head).  A kv tile holds (K head, V head) pairs: columns 2 hd j .. + hd - 1 are K of head
+// hpt (ct - n_qt) + j, the next hd columns V of the same head.
 __device__ inline const _Float16 *w_row(const QkvArgs &a, int ct, int n) {
     if (ct < a.n_qt) {
-        const int r = min(ct * kNT + n, a.n_head * 128 - 1);
+        const int r = min(ct * kNT + n, a.n_head * a.hd - 1);
         return a.wq + (size_t)r * a.dim;
     }
-    const int h = ct - a.n_qt;
-    return n < 128 ? a.wk + ((size_t)h * 128 + n) * a.dim : a.wv + ((size_t)h * 128 + n - 128) * a.dim;
+    const int j = n / (2 * a.hd), c = n % (2 * a.hd);
+    const int h = min((ct - a.n_qt) * a.hpt + j, a.L.H - 1);
+    return c < a.hd ? a.wk + ((size_t)h * a.hd + c) * a.dim : a.wv + ((size_t)h * a.hd + c - a.hd) * a.dim;
 }
 
 // Workgroup id -> (row tile, column tile, split), ordered so that each XCD (workgroups are
@@ -114,20 +118,23 @@ __device__ inline void tile_of(const QkvArgs &a, int id, int &rt, int &ct, int &
 }
 
 // Quantize-and-store of one new token per row (n_tok == 1): row i = sequence t.s + i at its
-// position len[s], for tile rows r0 .. r0 + nr - 1 (nr a multiple of 4) held in tile[i - r0].
-// 16 lanes per row (lane l = dims 8l..8l+7), rows r0 + 16 m + 4 wave + lane/16.
-// Each row owns its sequence's K row, scales and the nibbles of its position in the V block.
+// position len[s], for tile rows r0 .. r0 + nr - 1 (nr a multiple of 4) held in tile[i - r0],
+// K of kv head h in columns col0 .. col0 + HD - 1 and V in the next HD.  HD / 8 lanes per row
+// (lane l = dims 8l..8l+7), 256 / (HD / 8) rows per pass of the 4 waves.  Each row owns its
+// sequence's K row, scales and the nibbles of its position in the V block.
+template <int HD>
 __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const float (*tile)[kTStr],
-                                  int r0, int nr, int h, int wave, int lane) {
-    constexpr int HD = 128, NTD = HD / 16;
+                                  int r0, int nr, int h, int col0, int wave, int lane) {
+    constexpr int NTD = HD / 16, LPR = HD / 8, RPW = 64 / LPR;  // rows per wave per pass
     const KvLayerView &L = a.L;
-    const int r = lane >> 4, l = lane & 15;
-    for (int base = 0; base < nr; base += 16) {
-        if (base + 4 * wave >= nr) break;  // wave-uniform
-        const int i = r0 + base + 4 * wave + r;
-        const float *trow = tile[i - r0];
+    const int r = lane / LPR, l = lane % LPR;
+    for (int base = 0; base < nr; base += 4 * RPW) {
+        if (base + RPW * wave >= nr) break;  // wave-uniform
+        const int i = r0 + base + RPW * wave + r;
+        const bool in_tile = i < r0 + nr;
+        const float *trow = tile[min(i, r0 + nr - 1) - r0] + col0;
         const int s = min(t.s + i, L.S - 1);
-        const bool live = t.s + i < L.S;
+        const bool live = in_tile && t.s + i < L.S;
         const int p = a.len[s];
         float kx[8], vx[8];
 #pragma unroll
@@ -135,14 +142,7 @@ __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const floa
             kx[e] = trow[8 * l + e];
             vx[e] = trow[HD + 8 * l + e];
         }
-        if (L.kn) {
-            float sq[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) sq[e] = sq_rn(kx[e]);
-            const float ns = qk_norm_scale_from_sum(ordered_sum_row16(sq, l), HD, L.norm_eps);
-#pragma unroll
-            for (int e = 0; e < 8; e++) kx[e] = qk_norm_apply(kx[e], ns, L.kn[8 * l + e]);
-        }
+        if (L.kn) row_qk_norm<LPR>(kx, L.kn, L.norm_eps, l);
         if (a.rope) {
             float2 cs[4];
             rope_cs4(L, s, p, a.rope, a.rope_pairs, l, cs);
@@ -156,32 +156,11 @@ __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const floa
             km = fmaxf(km, fabsf(kx[e]));
             vm = fmaxf(vm, fabsf(vx[e]));
         }
-        km = fmaxf(km, dpp_f<0xB1>(km));
-        vm = fmaxf(vm, dpp_f<0xB1>(vm));
-        km = fmaxf(km, dpp_f<0x4E>(km));
-        vm = fmaxf(vm, dpp_f<0x4E>(vm));
-        km = fmaxf(km, dpp_f<0x141>(km));
-        vm = fmaxf(vm, dpp_f<0x141>(vm));
-        km = fmaxf(km, dpp_f<0x140>(km));
-        vm = fmaxf(vm, dpp_f<0x140>(vm));
-        const float ks = quant_scale(km), vs = quant_scale(vm);
-        const float kr = __builtin_amdgcn_rcpf(ks), vr = __builtin_amdgcn_rcpf(vs);
-        bool kneed = !(ks >= 1.17549435e-38f && ks <= 4.25352959e37f);
-        bool vneed = !(vs >= 1.17549435e-38f && vs <= 4.25352959e37f);
+        km = row_max<LPR>(km);
+        vm = row_max<LPR>(vm);
+        float ks, vs;
         uint32_t kc[8], vc[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            kc[e] = code_fast(kx[e] * kr, kneed);
-            vc[e] = code_fast(vx[e] * vr, vneed);
-        }
-        if (__builtin_amdgcn_ballot_w64(kneed) != 0) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) kc[e] = encode(kx[e], ks);
-        }
-        if (__builtin_amdgcn_ballot_w64(vneed) != 0) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) vc[e] = encode(vx[e], vs);
-        }
+        row_codes(kx, vx, km, vm, ks, vs, kc, vc);
         if (!live) continue;
         const size_t row = (size_t)s * L.H + h;
         uint32_t kw = 0;
@@ -205,55 +184,87 @@ __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const floa
     }
 }
 
+// K/V stores of the (K, V) head pairs of kv column tile ct, for the tile rows in tile[].
+template <int HD>
+__device__ void store_kv_tile(const QkvArgs &a, const RowTile &t, int ct, const float (*tile)[kTStr], int r0,
+                              int nr, int tid) {
+    const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int j = 0; j < 128 / HD; j++) {
+        const int h = (ct - a.n_qt) * (128 / HD) + j;
+        if (h >= a.L.H) break;  // uniform
+        const int col0 = 2 * HD * j;
+        if (a.n_tok == 1) {
+            store_rows_single<HD>(a, t, tile, r0, nr, h, col0, wave, lane);
+            continue;
+        }
+        if constexpr (HD == 128) {
+            const int r = lane >> 4, l = lane & 15;
+            float kx[2][8], vx[2][8];
+            float2 cs[2][4];
+#pragma unroll
+            for (int rd = 0; rd < 2; rd++) {
+                const int i = 16 * rd + 4 * wave + r;
+                const int pc = min(max(t.blk * kBlk + i, t.lo), t.hi - 1);
+                rope_cs4(a.L, t.s, pc, a.rope, a.rope_pairs, l, cs[rd]);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    kx[rd][e] = tile[i][col0 + 8 * l + e];
+                    vx[rd][e] = tile[i][col0 + HD + 8 * l + e];
+                }
+            }
+            store_block128(a.L, t.s, h, t.blk, t.lo, t.hi, kx, vx, cs, a.rope ? a.rope_pairs : 0, wave, lane);
+        } else {
+            const int r8 = lane >> 3, l = lane & 7;
+            const int i = 4 * wave + (r8 & 3) + 16 * (r8 >> 2);
+            const int pc = min(max(t.blk * kBlk + i, t.lo), t.hi - 1);
+            float2 cs[4];
+            rope_cs4(a.L, t.s, pc, a.rope, a.rope_pairs, l, cs);
+            float kx[8], vx[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                kx[e] = tile[i][col0 + 8 * l + e];
+                vx[e] = tile[i][col0 + HD + 8 * l + e];
+            }
+            store_block64(a.L, t.s, h, t.blk, t.lo, t.hi, kx, vx, cs, a.rope ? a.rope_pairs : 0, wave, lane);
+        }
+    }
+}
+
 // The epilogue of tile rows r0 .. r0 + nr - 1 of a finished 32 x 256 tile, held in LDS as
 // tile[i - r0].  Block rows (n_tok > 1) need the whole tile (r0 = 0, nr = 32).  256 threads.
 __device__ void qkv_epilogue(const QkvArgs &a, const RowTile &t, int ct, const float (*tile)[kTStr],
                              int r0, int nr, int tid) {
-    const int wave = tid >> 6, lane = tid & 63;
     if (ct < a.n_qt) {
-        // q: two heads side by side, contiguous in q_out
+        // q: 256 / hd heads side by side, contiguous in q_out
         const int c4 = tid & 63, i0 = tid >> 6;
         const int col = ct * kNT + 4 * c4;
-        if (col >= a.n_head * 128) return;
+        if (col >= a.n_head * a.hd) return;
         for (int i = r0 + i0; i < r0 + nr; i += 4) {
             const int xr = x_row(a, t, i);
             if (xr < 0) continue;
             const float4 v = *reinterpret_cast<const float4 *>(&tile[i - r0][4 * c4]);
-            *reinterpret_cast<float4 *>(a.q_out + (size_t)xr * a.n_head * 128 + col) = v;
+            *reinterpret_cast<float4 *>(a.q_out + (size_t)xr * a.n_head * a.hd + col) = v;
         }
         return;
     }
-    const int h = ct - a.n_qt;
     if (a.k_out) {
         const int c4 = tid & 63, i0 = tid >> 6;
-        float *dst = c4 < 32 ? a.k_out : a.v_out;
-        const int c = 4 * (c4 & 31);
-        for (int i = r0 + i0; i < r0 + nr; i += 4) {
-            const int xr = x_row(a, t, i);
-            if (xr < 0) continue;
-            *reinterpret_cast<float4 *>(dst + ((size_t)xr * a.L.H + h) * 128 + c) =
-                *reinterpret_cast<const float4 *>(&tile[i - r0][4 * c4]);
-        }
+        const int c = 4 * c4, j = c / (2 * a.hd), cc = c % (2 * a.hd);
+        const int h = (ct - a.n_qt) * a.hpt + j;
+        float *dst = cc < a.hd ? a.k_out : a.v_out;
+        if (h < a.L.H)
+            for (int i = r0 + i0; i < r0 + nr; i += 4) {
+                const int xr = x_row(a, t, i);
+                if (xr < 0) continue;
+                *reinterpret_cast<float4 *>(dst + ((size_t)xr * a.L.H + h) * a.hd + cc % a.hd) =
+                    *reinterpret_cast<const float4 *>(&tile[i - r0][c]);
+            }
     }
-    if (a.n_tok == 1) {
-        store_rows_single(a, t, tile, r0, nr, h, wave, lane);
-        return;
-    }
-    const int r = lane >> 4, l = lane & 15;
-    float kx[2][8], vx[2][8];
-    float2 cs[2][4];
-#pragma unroll
-    for (int rd = 0; rd < 2; rd++) {
-        const int i = 16 * rd + 4 * wave + r;
-        const int pc = min(max(t.blk * kBlk + i, t.lo), t.hi - 1);
-        rope_cs4(a.L, t.s, pc, a.rope, a.rope_pairs, l, cs[rd]);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            kx[rd][e] = tile[i][8 * l + e];
-            vx[rd][e] = tile[i][128 + 8 * l + e];
-        }
-    }
-    store_block128(a.L, t.s, h, t.blk, t.lo, t.hi, kx, vx, cs, a.rope ? a.rope_pairs : 0, wave, lane);
+    if (a.hd == 128)
+        store_kv_tile<128>(a, t, ct, tile, r0, nr, tid);
+    else
+        store_kv_tile<64>(a, t, ct, tile, r0, nr, tid);
 }
 
 // One workgroup per tile over all of dim (grids with enough tiles): MT = 64 WR rows -- for
@@ -373,9 +384,10 @@ __global__ __launch_bounds__(256) void qkv_reduce_kernel(QkvArgs a) {
 
 }  // namespace
 
-QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int dim, int n_tok) {
+QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok) {
     QkvPlan p;
-    p.CT = (n_head + 1) / 2 + n_kv;
+    const int hpt = 128 / hd;
+    p.CT = (n_head * hd + kNT - 1) / kNT + (n_kv + hpt - 1) / hpt;
     p.kps = dim;
     p.n_split = 1;
     p.part_bytes = 0;
@@ -405,7 +417,7 @@ hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x
                       const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int n_head,
                       float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,
                       const QkvPlan &plan, float *part, hipStream_t st) {
-    if (L.hd != 128 || dim % kKC != 0) return hipErrorInvalidValue;
+    if ((L.hd != 128 && L.hd != 64) || dim % kKC != 0) return hipErrorInvalidValue;
     QkvArgs a;
     a.L = L;
     a.len = d_len;
@@ -422,7 +434,9 @@ hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x
     a.dim = dim;
     a.n_tok = n_tok;
     a.n_head = n_head;
-    a.n_qt = (n_head + 1) / 2;
+    a.hd = L.hd;
+    a.hpt = 128 / L.hd;
+    a.n_qt = (n_head * L.hd + kNT - 1) / kNT;
     a.RT = plan.RT;
     a.CT = plan.CT;
     a.kps = plan.kps;

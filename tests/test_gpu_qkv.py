@@ -10,7 +10,8 @@ F16 weights, followed by quantize_kv).
 Shapes cover the decode rows (one token per sequence, > 32 sequences), block rows (prefill
 chunks from ragged, unaligned lengths, in 32- and 64-row tiles), the reduction split over dim
 and the unsplit one,
-an odd number of query heads, the QK norm and a compacted sequence."""
+an odd number of query or kv heads, head_dim 128 and 64, the QK norm and a compacted
+sequence."""
 import numpy as np
 import pytest
 import torch
@@ -136,9 +137,19 @@ def test_qkv_append_errors(gpu):
     with pytest.raises(TsError) as e:          # past max_seq
         p.gpu.qkv_append(0, dev(np.zeros((2, 8, 256), np.float32)), dev(wq), dev(wk), dev(wk), p.rope)
     assert e.value.code == -2
-    g64 = KVCache.new_int4(1, 2, 64, 64, 2)
-    with pytest.raises(TsError) as e:          # head_dim 64 is not built for the fused projection
-        g64.qkv_append(0, x, dev(np.zeros((8 * 64, 256), np.float16)),
-                       dev(np.zeros((128, 256), np.float16)), dev(np.zeros((128, 256), np.float16)),
-                       p.rope)
-    assert e.value.code == -3
+
+
+@pytest.mark.parametrize("n_seq,n_tok,dim,n_head,n_kv", [
+    (5, 1, 2048, 32, 8),     # Llama-3.2-1B projection shape, decode rows, split reduction
+    (3, 70, 512, 8, 2),      # block rows, split
+    (4, 300, 256, 32, 8),    # prefill chunks in 64-row tiles
+    (70, 1, 320, 6, 3),      # odd kv-head count: the last (K, V) tile holds one pair
+])
+def test_qkv_append_hd64(gpu, n_seq, n_tok, dim, n_head, n_kv):
+    say(f"qkv hd64 n_seq={n_seq} n_tok={n_tok} dim={dim} n_head={n_head} n_kv={n_kv}")
+    rng = np.random.default_rng(640 + dim + n_tok)
+    p = Pair(n_seq, n_kv, 64, 128 + 2 * n_tok + 16, 5e5)
+    lens = rng.integers(0, 100, size=n_seq).astype(np.int32)
+    p.set_lens(lens)
+    run_case(p, rng, n_tok, dim, n_head)
+    run_case(p, rng, 3, dim, n_head)
