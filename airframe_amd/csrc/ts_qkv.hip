@@ -25,6 +25,8 @@
 //   * Few tiles (decode): 32-row tiles with the reduction over dim split across workgroups
 //     (gemm_split_core, one memory round trip per slice), f32 partials, and a second kernel
 //     that sums them in split order (deterministic) and runs the epilogue.
+#include <type_traits>
+
 #include "ts_gemm.h"
 #include "ts_store.h"
 
@@ -304,33 +306,39 @@ __global__ __launch_bounds__(256 * WR) void qkv_tile_kernel(QkvArgs a) {
     gemm_tile_core<WR>(sm.x, xs, wp, a.dim / kKC, tid, acc);
 
     // Epilogue, one 32-row block at a time: the waves holding it (wr = b / 2, row block b % 2)
-    // write it to the LDS tile, then the first 4 waves run the block's epilogue.
-    // (unrolled, so that acc is indexed with constants and stays in registers)
+    // write it to the LDS tile, then the first 4 waves run the block's epilogue.  The block
+    // index is a template constant so that acc is indexed with constants and stays in
+    // registers.
+    auto block = [&](auto bc) {
+        constexpr int b = decltype(bc)::value;
+        if constexpr (b < NBLK) {
+            const int p0 = (blk0 + b) * kBlk;
+            if (single ? s + kBlk * b >= a.L.S : p0 >= end) return;  // uniform
+            if (wr == (b >> 1)) {
 #pragma unroll
-    for (int b = 0; b < NBLK; b++) {
-        const int p0 = (blk0 + b) * kBlk;
-        if (single ? s + kBlk * b >= a.L.S : p0 >= end) continue;  // uniform
-        if (wr == (b >> 1)) {
-            const int rb = b & 1;
+                for (int cb = 0; cb < 2; cb++)
 #pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                for (int e = 0; e < 16; e++)
-                    sm.tile[8 * (e >> 2) + 4 * hf + (e & 3)][64 * wc + 32 * cb + j] = acc[rb][cb][e];
+                    for (int e = 0; e < 16; e++)
+                        sm.tile[8 * (e >> 2) + 4 * hf + (e & 3)][64 * wc + 32 * cb + j] = acc[b & 1][cb][e];
+            }
+            __syncthreads();
+            if (tid < 256) {
+                RowTile t;
+                t.s = single ? s + kBlk * b : s;
+                t.start = start;
+                t.blk = blk0 + b;
+                t.lo = max(p0, start);
+                t.hi = min(p0 + kBlk, end);
+                t.live = true;
+                qkv_epilogue(a, t, ct, sm.tile, 0, kMT, tid);
+            }
+            __syncthreads();
         }
-        __syncthreads();
-        if (tid < 256) {
-            RowTile t;
-            t.s = single ? s + kBlk * b : s;
-            t.start = start;
-            t.blk = blk0 + b;
-            t.lo = max(p0, start);
-            t.hi = min(p0 + kBlk, end);
-            t.live = true;
-            qkv_epilogue(a, t, ct, sm.tile, 0, kMT, tid);
-        }
-        __syncthreads();
-    }
+    };
+    block(std::integral_constant<int, 0>{});
+    block(std::integral_constant<int, 1>{});
+    block(std::integral_constant<int, 2>{});
+    block(std::integral_constant<int, 3>{});
 }
 
 // One split of the reduction for small grids (decode) through gemm_split_core; the f32
