@@ -91,3 +91,26 @@ def test_create_validates_before_touching_the_device():
     assert L.ts_kv_increment(None, 1, None) == _lib.TS_ERR_INVALID
     assert L.ts_attn_decode(None, 0, None, 32, None, 0.0, None, None, 0, None) == _lib.TS_ERR_INVALID
     assert L.ts_append_quant(None, 0, None, None, 1, None, None) == _lib.TS_ERR_INVALID
+
+
+def test_out_proj_workspace_sizing_and_validation():
+    """ts_attn_out_proj_workspace is host-only: the split partials for decode-sized batches,
+    nothing for prefill tiles or unsplittable reductions, and argument checks."""
+    L = airframe_amd.load()
+    b = ctypes.c_uint64()
+    # decode batch 32 at attn_dim 4096 -> dim 4096: 16 column tiles of 256, one 32-row tile,
+    # the reduction split into slices of 256 (16 splits) -> 16 * 16 * 32 * 256 f32
+    assert L.ts_attn_out_proj_workspace(32, 4096, 4096, ctypes.byref(b)) == _lib.TS_OK
+    assert b.value == 16 * 16 * 32 * 256 * 4
+    assert L.ts_attn_out_proj_workspace(2048, 4096, 2560, ctypes.byref(b)) == _lib.TS_OK
+    assert b.value == 0                       # 64-row tiles over all of attn_dim
+    assert L.ts_attn_out_proj_workspace(4, 320, 200, ctypes.byref(b)) == _lib.TS_OK
+    assert b.value == 0                       # 320 is not a multiple of 256: no split
+    assert L.ts_attn_out_proj_workspace(0, 4096, 4096, ctypes.byref(b)) == _lib.TS_OK
+    assert b.value == 0
+    assert L.ts_attn_out_proj_workspace(4, 100, 64, ctypes.byref(b)) == _lib.TS_ERR_INVALID
+    assert L.ts_attn_out_proj_workspace(4, 128, 64, None) == _lib.TS_ERR_INVALID
+    assert L.ts_attn_out_proj(None, 1, 128, None, 64, None, None, None, 0, None) == _lib.TS_ERR_INVALID
+    assert L.ts_qkv_workspace(None, 4096, 1, 32, ctypes.byref(b)) == _lib.TS_ERR_INVALID
+    assert L.ts_qkv_append(None, 0, None, 4096, 1, None, None, None, 32, None, None, None, None,
+                           None, 0, None) == _lib.TS_ERR_INVALID
