@@ -45,10 +45,18 @@ struct XTiles {
 // 64 wr + 32 rb + .., columns 64 wc + 32 cb + .. in acc[rb][cb].  Staging thread (si = tid / 4,
 // sc = tid % 4) owns 16 floats of x row si per chunk: xs points at them for chunk 0 (null: a
 // zero row).  wp[cb]: the lane's weight row of column block cb at its chunk-0 offset 32 hf.
-// x goes through LDS one chunk ahead, the weights into registers two chunks ahead.
-template <int WR>
-__device__ __forceinline__ void gemm_tile_core(XTiles<64 * WR> &sm, const float *xs, const _Float16 *const (&wp)[2],
-                                               int nch, int tid, floatx16 (&acc)[2][2]) {
+// Both operands run D chunks ahead: x and the weights of chunk c + D are loaded into a ring of
+// D register sets while chunk c is multiplied, and x of chunk c + 1 goes to LDS (hi/lo,
+// double-buffered) after chunk c's matrix work, so each load has D - 1 iterations to arrive.
+// D = 3 keeps two waves per SIMD; measured 10% faster than x one chunk and the weights two
+// chunks ahead, while D = 4 drops to one wave per SIMD and is slower.
+#ifndef TS_GEMM_DEPTH
+#define TS_GEMM_DEPTH 3
+#endif
+template <int WR, int D = TS_GEMM_DEPTH>
+__device__ __forceinline__ void gemm_tile_core(XTiles<64 * WR> &sm, const float *xs,
+                                                    const _Float16 *const (&wp)[2], int nch, int tid,
+                                                    floatx16 (&acc)[2][2]) {
     const int wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5, wr = wave >> 2;
     const int si = tid >> 2, sc = tid & 3;
 #pragma unroll
@@ -56,65 +64,58 @@ __device__ __forceinline__ void gemm_tile_core(XTiles<64 * WR> &sm, const float 
 #pragma unroll
         for (int cb = 0; cb < 2; cb++) zero(acc[rb][cb]);
 
-    float4 xq[4];
-    auto load_x = [&](int c) {
+    float4 xq[D][4];
+    half8 wq[D][2][4];
+    auto load = [&](float4 (&x)[4], half8 (&w)[2][4], int c) {
+        const bool on = c < nch;
 #pragma unroll
         for (int u = 0; u < 4; u++)
-            xq[u] = xs ? *reinterpret_cast<const float4 *>(xs + c * kKC + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
-    };
-    auto store_x = [&](int buf) {
-        half8 h, l;
-        split8(xq[0], xq[1], h, l);
-        *reinterpret_cast<half8 *>(&sm.hi[buf][si][16 * sc]) = h;
-        *reinterpret_cast<half8 *>(&sm.lo[buf][si][16 * sc]) = l;
-        split8(xq[2], xq[3], h, l);
-        *reinterpret_cast<half8 *>(&sm.hi[buf][si][16 * sc + 8]) = h;
-        *reinterpret_cast<half8 *>(&sm.lo[buf][si][16 * sc + 8]) = l;
-    };
-    half8 wb[2][4], wn[2][4];
-    auto load_w = [&](half8 (&w)[2][4], int c) {
+            x[u] = (xs && on) ? *reinterpret_cast<const float4 *>(xs + c * kKC + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int cb = 0; cb < 2; cb++)
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                w[cb][q] = c < nch ? *reinterpret_cast<const half8 *>(wp[cb] + c * kKC + 8 * q)
-                                   : (half8)(_Float16)0.0f;
+                w[cb][q] = on ? *reinterpret_cast<const half8 *>(wp[cb] + c * kKC + 8 * q) : (half8)(_Float16)0.0f;
     };
-    load_x(0);
-    load_w(wb, 0);
-    load_w(wn, 1);
-    store_x(0);
+    auto store_x = [&](int buf, const float4 (&x)[4]) {
+        half8 h, l;
+        split8(x[0], x[1], h, l);
+        *reinterpret_cast<half8 *>(&sm.hi[buf][si][16 * sc]) = h;
+        *reinterpret_cast<half8 *>(&sm.lo[buf][si][16 * sc]) = l;
+        split8(x[2], x[3], h, l);
+        *reinterpret_cast<half8 *>(&sm.hi[buf][si][16 * sc + 8]) = h;
+        *reinterpret_cast<half8 *>(&sm.lo[buf][si][16 * sc + 8]) = l;
+    };
+#pragma unroll
+    for (int u = 0; u < D; u++) load(xq[u], wq[u], u);
+    store_x(0, xq[0]);
     __syncthreads();
 
-    for (int c = 0; c < nch; c++) {
-        const int buf = c & 1;
-        const bool more = c + 1 < nch;
-        half8 wf[2][4];
-        load_w(wf, c + 2);
-        if (more) load_x(c + 1);
+    for (int c0 = 0; c0 < nch; c0 += D) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
+        for (int u = 0; u < D; u++) {
+            const int c = c0 + u;
+            if (c < nch) {  // uniform
+                const int buf = c & 1;
 #pragma unroll
-            for (int rb = 0; rb < 2; rb++) {
-                const int row = 64 * wr + 32 * rb + j;
-                const half8 ah = *reinterpret_cast<const half8 *>(&sm.hi[buf][row][32 * hf + 8 * q]);
-                const half8 al = *reinterpret_cast<const half8 *>(&sm.lo[buf][row][32 * hf + 8 * q]);
+                for (int q = 0; q < 4; q++) {
 #pragma unroll
-                for (int cb = 0; cb < 2; cb++) {
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wb[cb][q], acc[rb][cb], 0, 0, 0);
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, wb[cb][q], acc[rb][cb], 0, 0, 0);
+                    for (int rb = 0; rb < 2; rb++) {
+                        const int row = 64 * wr + 32 * rb + j;
+                        const half8 ah = *reinterpret_cast<const half8 *>(&sm.hi[buf][row][32 * hf + 8 * q]);
+                        const half8 al = *reinterpret_cast<const half8 *>(&sm.lo[buf][row][32 * hf + 8 * q]);
+#pragma unroll
+                        for (int cb = 0; cb < 2; cb++) {
+                            acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wq[u][cb][q], acc[rb][cb], 0, 0, 0);
+                            acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, wq[u][cb][q], acc[rb][cb], 0, 0, 0);
+                        }
+                    }
                 }
+                if (c + 1 < nch) store_x(buf ^ 1, xq[(u + 1) % D]);
+                load(xq[u], wq[u], c + D);
+                __syncthreads();
             }
         }
-        if (more) store_x(buf ^ 1);
-#pragma unroll
-        for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                wb[cb][q] = wn[cb][q];
-                wn[cb][q] = wf[cb][q];
-            }
-        __syncthreads();
     }
 }
 
