@@ -248,11 +248,14 @@ __device__ inline float half_sum(float v) {
 }
 
 // Scores of one 64-key window for this lane's column, in place (sc[kb][4q + r] is key
-// 32kb + qk_row_key(8q + 4h + r)): times s_k, softcap, causal mask, then the online-softmax
-// state update.  Leaves sc - m_run ready for exp2.
+// 32kb + qk_row_key(8q + 4h + r)), left relative to the running reference m_run:
+// sc = x s_k - m_run (one FMA per score; softcap in between when on), causal mask, then the
+// online-softmax state update.  The reference is raised only when the window breaks
+// p <= 2^8 or p*s_v <= 2^15 (f16 range), and the scores move down with it; the first window
+// (first, uniform; m_run = 0 and nothing accumulated yet) sets it from its own max.
 template <int NDB, bool SOFTCAP>
 __device__ inline void window_scores(floatx16 (&sc)[2], const float *sk, float svl, float softcap,
-                                     bool mask, int base, int h, int qpos, float &m_run,
+                                     bool mask, bool first, int base, int h, int qpos, float &m_run,
                                      float &l_run, floatx16 (&o)[NDB]) {
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
@@ -261,8 +264,13 @@ __device__ inline void window_scores(floatx16 (&sc)[2], const float *sk, float s
             const floatx4 sk4 = *reinterpret_cast<const floatx4 *>(sk + 32 * kb + 16 * (q >> 1) + 8 * h + 4 * (q & 1));
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                float x = sc[kb][4 * q + r] * sk4[r];
-                if (SOFTCAP) x = tanhf(x / softcap) * softcap * kLog2e;
+                float x;
+                if constexpr (SOFTCAP) {
+                    x = sc[kb][4 * q + r] * sk4[r];
+                    x = tanhf(x / softcap) * softcap * kLog2e - m_run;
+                } else {
+                    x = __builtin_fmaf(sc[kb][4 * q + r], sk4[r], -m_run);
+                }
                 sc[kb][4 * q + r] = x;
             }
         }
@@ -284,16 +292,20 @@ __device__ inline void window_scores(floatx16 (&sc)[2], const float *sk, float s
 #pragma unroll
         for (int i = 0; i < 16; i++) mloc = fmaxf(mloc, sc[kb][i]);
     mloc = half_max(mloc);
-    // Keep p <= 2^8 and p*s_v <= 2^15 (f16 range); raise the running max only when the window
-    // breaks either bound.
-    const float need = fmaxf(mloc - 8.0f, mloc + svl - 15.0f);
-    if (__builtin_amdgcn_ballot_w64(need > m_run) != 0) {
-        const float m_new = need > m_run ? mloc + fmaxf(0.0f, svl - 15.0f) : m_run;
-        const float alpha = exp2f(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
+    const float need = fmaxf(mloc - 8.0f, mloc + svl - 15.0f);  // relative to m_run
+    if (__builtin_amdgcn_ballot_w64(first || need > 0.0f) != 0) {
+        const float delta = (first || need > 0.0f) ? mloc + fmaxf(0.0f, svl - 15.0f) : 0.0f;
+        if (!first) {
+            const float alpha = exp2f(-delta);
+            l_run *= alpha;
 #pragma unroll
-        for (int db = 0; db < NDB; db++) o[db] *= alpha;
+            for (int db = 0; db < NDB; db++) o[db] *= alpha;
+        }
+        m_run += delta;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) sc[kb][i] = sc[kb][i] - delta;
     }
 }
 
@@ -302,7 +314,7 @@ __device__ inline void window_scores(floatx16 (&sc)[2], const float *sk, float s
 // ~22 bits: one f16 would carry a relative error of 2^-11 into the output whenever a few
 // keys dominate the row.
 __device__ inline void step_probs(const floatx16 (&sc)[2], const float *sv, int st, int h,
-                                  float m_run, float &l_run, half8 &pb, half8 &pl) {
+                                  float &l_run, half8 &pb, half8 &pl) {
     const int kb = st >> 1;
 #pragma unroll
     for (int qq = 0; qq < 2; qq++) {
@@ -310,7 +322,7 @@ __device__ inline void step_probs(const floatx16 (&sc)[2], const float *sv, int 
         const floatx4 sv4 = *reinterpret_cast<const floatx4 *>(sv + 32 * kb + 16 * (q >> 1) + 8 * h + 4 * (q & 1));
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float p = __builtin_amdgcn_exp2f(sc[kb][4 * q + r] - m_run);
+            const float p = __builtin_amdgcn_exp2f(sc[kb][4 * q + r]);  // sc is relative
             l_run += p;
             const float pv = p * sv4[r];
             const float hi = split_hi(pv);
@@ -409,7 +421,8 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     floatx16 o[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; db++) o[db] = (floatx16)0.0f;
-    float m_run = kMinit, l_run = 0.0f;
+    float m_run = 0.0f, l_run = 0.0f;  // m_run: exp2 reference, set by the first window
+    bool first = true;
 
     // Window w+1 is staged into LDS while window w's QK^T runs on the matrix cores (the
     // staging is VALU and LDS-write work); its global loads were issued one iteration earlier.
@@ -452,14 +465,15 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
         if (w + 2 < n_win) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, base + 2 * kWin, tid, wave);
         if (base <= qmax_w) {
             const bool mask = base + kWin - 1 > qmin_w;  // some key of the window is masked
-            window_scores<NDB, SOFTCAP>(sc, sm.sk[buf], sm.svlog[buf], a.softcap, mask, base, hf, qpos,
-                                        m_run, l_run, o);
+            window_scores<NDB, SOFTCAP>(sc, sm.sk[buf], sm.svlog[buf], a.softcap, mask, first,
+                                        base, hf, qpos, m_run, l_run, o);
+            first = false;
             // O^T += V^T P^T one 16-key step at a time: the exps of step st+1 overlap the
             // MFMAs of step st.
 #pragma unroll
             for (int st = 0; st < 4; st++) {
                 half8 pb, pl;  // p*s_v high and low f16 parts
-                step_probs(sc, sm.sv[buf], st, hf, m_run, l_run, pb, pl);
+                step_probs(sc, sm.sv[buf], st, hf, l_run, pb, pl);
                 __builtin_amdgcn_s_setprio(2);
                 half8 va[NDB];
 #pragma unroll
