@@ -556,27 +556,44 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     const float *mm = ml + hidx * a.n_split;
     const float *ll = ml + (size_t)a.L.S * a.n_head * a.n_split + hidx * a.n_split;
 
-    float M = kMinit;
-    for (int i = tid; i < ns; i += 256) M = fmaxf(M, mm[i]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    if ((tid & 63) == 0) wmax[tid >> 6] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-
     const int g = tid / V4, j = tid % V4;
     const float4 *o4 = reinterpret_cast<const float4 *>(a.ws + hidx * a.n_split * HD);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     float lsum = 0.0f;
+    if (ns <= NG) {
+        // One split per row group: every load is issued at once (each thread reads all ns
+        // maxima itself), no reduction round for the maximum.
+        float mv[NG];
+#pragma unroll
+        for (int i = 0; i < NG; i++) mv[i] = i < ns ? mm[i] : kMinit;
+        const bool mine = g < ns;
+        const float4 x = mine ? o4[(size_t)g * V4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float lg = mine ? ll[g] : 0.0f;
+        const float mg = mine ? mm[g] : kMinit;
+        float M = kMinit;
+#pragma unroll
+        for (int i = 0; i < NG; i++) M = fmaxf(M, mv[i]);
+        const float e = mine ? exp2f(mg - M) : 0.0f;
+        acc = make_float4(e * x.x, e * x.y, e * x.z, e * x.w);
+        lsum = e * lg;
+    } else {
+        float M = kMinit;
+        for (int i = tid; i < ns; i += 256) M = fmaxf(M, mm[i]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        if ((tid & 63) == 0) wmax[tid >> 6] = M;
+        __syncthreads();
+        M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
 #pragma unroll 4
-    for (int i = g; i < ns; i += NG) {
-        const float e = exp2f(mm[i] - M);
-        const float4 x = o4[(size_t)i * V4 + j];
-        acc.x += e * x.x;
-        acc.y += e * x.y;
-        acc.z += e * x.z;
-        acc.w += e * x.w;
-        lsum += e * ll[i];
+        for (int i = g; i < ns; i += NG) {
+            const float e = exp2f(mm[i] - M);
+            const float4 x = o4[(size_t)i * V4 + j];
+            acc.x += e * x.x;
+            acc.y += e * x.y;
+            acc.z += e * x.z;
+            acc.w += e * x.w;
+            lsum += e * ll[i];
+        }
     }
     part[g][j] = acc;
     if (j == 0) lpart[g] = lsum;
