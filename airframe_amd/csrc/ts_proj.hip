@@ -105,11 +105,25 @@ __global__ __launch_bounds__(256) void proj_reduce_kernel(ProjArgs p) {
     const size_t stride = (size_t)p.RT * p.CT * (32 * kPT) / 4;
     const float4 *src = reinterpret_cast<const float4 *>(p.part) + ((size_t)rt * p.CT + ct) * (32 * kPT / 4) +
                         r0 * (kPT / 4);
+    // the residual this thread updates (row r0 + i, column tid of the tile), read while the
+    // partials stream in
+    const int col = kPT * ct + tid;
+    float res[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        const int row = 32 * rt + r0 + i;
+        res[i] = (row < p.M && col < p.N) ? p.act[(size_t)row * p.N + col] : 0.0f;
+    }
     sum_partials<NR, kMaxPSplit>(src, stride, p.n_split, &tile[0][0], kPT + 4, tid);
     __syncthreads();
-    for (int e = tid; e < NR * kPT; e += 256) {
-        const int i = e / kPT, c = e % kPT;
-        proj_out(p, 32 * rt + r0 + i, kPT * ct + c, tile[i][c]);
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        const int row = 32 * rt + r0 + i;
+        if (row >= p.M || col >= p.N) continue;
+        const float v = tile[i][tid];
+        const size_t idx = (size_t)row * p.N + col;
+        if (p.stash) p.stash[idx] = v;
+        p.act[idx] = res[i] + v;
     }
 }
 
