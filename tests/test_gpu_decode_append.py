@@ -122,3 +122,25 @@ def test_long_splits(gpu, n_head, softcap):
         out, ref = fused_step(p, rng, n_head, skv[None, None], sq[None], softcap=softcap)
         assert_close(out, ref, "fused long-split out")
     p.check_codes()
+
+
+def test_many_sequences(gpu):
+    """300 sequences (more than one workgroup per CU on the sequence axis alone) with ragged
+    short contexts: fused decode, then a prefill chunk, against the oracle; codes bit-exact."""
+    say("decode/prefill with 300 sequences")
+    rng = np.random.default_rng(300)
+    n_seq, n_kv, n_head, hd = 300, 2, 8, 128
+    p = Pair(n_seq, n_kv, hd, 160, 1e6)
+    p.set_lens(rng.integers(0, 90, size=n_seq).astype(np.int32))
+    for _ in range(2):
+        out, ref = fused_step(p, rng, n_head)
+        assert_close(out, ref, "fused decode, 300 sequences")
+    k = synth.normal(rng, (n_seq, 9, n_kv, hd))
+    v = synth.normal(rng, (n_seq, 9, n_kv, hd))
+    q = synth.normal(rng, (n_seq, 9, n_head, hd))
+    p.append(k, v)
+    out = p.gpu.attn_prefill(0, dev(q), p.rope).cpu().numpy()
+    ref = p.ora.attend(q, 9, threads=8)
+    assert_close(out, ref, "prefill, 300 sequences")
+    p.advance(9)
+    p.check_codes()
