@@ -355,7 +355,7 @@ def attn_out_proj(attn: torch.Tensor, wo: torch.Tensor, act: torch.Tensor,
         raise ValueError("act/stash must hold [n_tok, dim]")
     ws = workspace
     if ws is None:
-        key = (n_tok, attn_dim, dim)
+        key = (attn.device.index, n_tok, attn_dim, dim)
         if key not in _proj_ws:
             b = ctypes.c_uint64()
             check("ts_attn_out_proj_workspace",
