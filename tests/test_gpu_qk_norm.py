@@ -113,3 +113,36 @@ def test_norm_off_again_and_bad_args(gpu):
         p.gpu.set_qk_norm(0, torch.zeros(63, device="cuda"), None)
     with pytest.raises(TsError):
         p.gpu.set_qk_norm(5, None, None)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_norm_softcap_and_compaction_together(gpu, hd):
+    """QK norm, the tanh softcap and a compacted window base at once: codes bit-exact, fused
+    decode and prefill within tolerance."""
+    say(f"qk norm + softcap + compaction hd={hd}")
+    rng = np.random.default_rng(900 + hd)
+    p = Pair(2, 2, hd, 600, 1e6, rope_n_pos=1200)
+    with_norm(p, rng)
+    fill(p, rng, 400, step=150)
+    n = int(p.ora.lens[0])
+    p.gpu.compact(4, 200, 0)
+    p.ora.shift(0, 4, 200)
+    p.ora.advance_window_base(0, 200)
+    p.ora.lens[0] = n - 200
+    fill(p, rng, 50, step=50)
+    p.check_codes()
+    k = synth.normal(rng, (2, 1, 2, hd))
+    v = synth.normal(rng, (2, 1, 2, hd))
+    q = synth.normal(rng, (2, 8, hd))
+    out = p.gpu.attn_decode_append(0, dev(k), dev(v), dev(q), p.rope, softcap=30.0).cpu().numpy()
+    p.ora.append(k, v)
+    assert_close(out, p.ora.attend(q[:, None], 1, softcap=30.0, threads=8)[:, 0], "fused decode")
+    p.advance(1)
+    k = synth.normal(rng, (2, 12, 2, hd))
+    v = synth.normal(rng, (2, 12, 2, hd))
+    q = synth.normal(rng, (2, 12, 8, hd))
+    p.append(k, v)
+    out = p.gpu.attn_prefill(0, dev(q), p.rope, softcap=30.0).cpu().numpy()
+    assert_close(out, p.ora.attend(q, 12, softcap=30.0, threads=8), "prefill")
+    p.advance(12)
+    p.check_codes()
