@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
 template <int HD>
 __global__ void export_kernel(KvLayerView L, int seq, int pos0, int n_pos, uint32_t *kp,
                               uint32_t *vp, float *ks, float *vs) {
-    constexpr int WPR = HD / 8, NTD = HD / 16;
+    constexpr int WPR = HD / 8;
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     const long total = (long)n_pos * L.H * WPR;
     if (idx >= total) return;
@@ -111,13 +111,13 @@ __global__ void export_kernel(KvLayerView L, int seq, int pos0, int n_pos, uint3
     const int pi = idx / (WPR * L.H);
     const int p = pos0 + pi;
     const size_t row = (size_t)seq * L.H + h;
-    kp[idx] = reinterpret_cast<const uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[u];
+    kp[idx] = reinterpret_cast<const uint32_t *>(L.kp + row * L.P * (HD / 2))[k_word_idx<HD>(p, u)];
     const uint32_t *vb = reinterpret_cast<const uint32_t *>(L.vp + (row * (L.P / 32) + p / 32) * (HD * 16));
     const int q = p % 32, tile = q / 16, g = (q % 16) / 4, r = q % 4, n = r + 4 * tile;
     uint32_t word = 0;
     for (int e = 0; e < 8; e++) {
         const int d = 8 * u + e, td = d / 16, dl = d % 16;
-        const uint32_t src = vb[(g * 16 + dl) * NTD + td];
+        const uint32_t src = vb[v_word_idx(g * 16 + dl, td)];
         word |= ((src >> (4 * n)) & 0xFu) << (4 * e);
     }
     vp[idx] = word;
@@ -140,7 +140,7 @@ __global__ void import_k_kernel(KvLayerView L, int seq, int pos0, int n_pos, con
     const int h = (idx / WPR) % L.H;
     const int p = pos0 + (int)(idx / (WPR * L.H));
     const size_t row = (size_t)seq * L.H + h;
-    reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[u] = kp[idx];
+    reinterpret_cast<uint32_t *>(L.kp + row * L.P * (HD / 2))[k_word_idx<HD>(p, u)] = kp[idx];
     if (u == 0) {
         L.ks[row * L.P + p] = ks[idx / WPR];
         L.vs[row * L.P + p] = vs[idx / WPR];
@@ -153,14 +153,16 @@ __global__ void import_k_kernel(KvLayerView L, int seq, int pos0, int n_pos, con
 // (n < 4) and 16 + 4g + n - 4 (n >= 4).
 template <int HD>
 __global__ void import_v_kernel(KvLayerView L, int seq, int pos0, int n_pos, const uint32_t *vp) {
-    constexpr int NTD = HD / 16, WPB = HD * 4;  // words per block
+    constexpr int WPB = HD * 4;  // words per block
     const int b0 = pos0 / 32, nb = (pos0 + n_pos - 1) / 32 - b0 + 1;
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long)L.H * nb * WPB) return;
     const int w = idx % WPB;
     const int b = b0 + (int)((idx / WPB) % nb);
     const int h = (int)(idx / ((long)WPB * nb));
-    const int g = w / (16 * NTD), dl = (w / NTD) % 16, td = w % NTD;
+    // w = v_word_idx(16 g + dl, td)
+    const int c = w >> 2, ln = c & 63, td = ((c >> 6) << 2) | (w & 3);
+    const int g = ln >> 4, dl = ln & 15;
     const int d = 16 * td + dl;
     const size_t row = (size_t)seq * L.H + h;
     uint32_t *dst = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / 32) + b) * (HD * 16)) + w;

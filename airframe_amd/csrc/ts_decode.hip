@@ -9,9 +9,13 @@
 //
 // * grid = (split, kv head, sequence); a split is `chunk` positions (multiple of 64) of one
 //   (sequence, kv head) stream, so every workgroup reads contiguous runs of K rows, V blocks
-//   and scales exactly once for all G = n_head/n_kv query heads that share them.
-// * each of the 4 waves takes 64-position windows round robin: K rows are 16-byte loads per
-//   lane, V blocks 32-byte loads per lane, scales 16-byte loads.
+//   and scales exactly once for all G = n_head/n_kv query heads that share them.  The chunk
+//   is planned from the total context of the batch, so ragged batches get more splits for
+//   their long sequences and the count of busy workgroups stays at the planned one.
+// * each wave takes 64-position windows round robin; in the G <= 4 kernel every 16-byte load
+//   instruction reads one contiguous kilobyte (the cache's chunk order puts each lane's K row
+//   segment and V words there), non-temporally, and each workgroup starts its windows at its
+//   own offset, so the concurrent streams spread over the HBM channels.
 // * QK^T and PV run on the matrix cores (v_mfma_f32_16x16x32_f16).  INT4 codes convert to
 //   exact f16 integers with two bit tricks (0x6400|nibble is 1024+nibble; the second nibble of
 //   a byte is taken as 1024+16*nibble and fixed with one packed f16 FMA), so K and V enter the
@@ -30,21 +34,8 @@
 #include "ts_mfma.h"
 #include "ts_quant.h"
 
-#ifndef TS_DECODE_WAVES
-#define TS_DECODE_WAVES 2
-#endif
-#ifndef TS_DECODE_NW
-#define TS_DECODE_NW 4
-#endif
-#ifndef TS_DECODE4_WAVES
-#define TS_DECODE4_WAVES 2
-#endif
-#ifndef TS_DECODE_FORCE16
-#define TS_DECODE_FORCE16 0
-#endif
-#ifndef TS_DECODE_DEPTH
-#define TS_DECODE_DEPTH 2
-#endif
+// Waves per workgroup of the 16x16 kernel.
+constexpr int kNW16 = 4;
 
 namespace ts {
 namespace {
@@ -58,7 +49,7 @@ struct DecodeArgs {
     int n_head;
     int G;
     int chunk;
-    int n_split;
+    int n_split;  // grid.x: the last split of a sequence runs to its end
     float inv_sqrt_hd;
     float softcap;
     float *out;
@@ -98,29 +89,31 @@ template <int HD>
 __device__ __forceinline__ void load_window(Window<HD> &w, const Streams &st, int base, int n,
                                             int g, int lane) {
     constexpr int WPG = HD / 32, NTD = HD / 16, ROWB = HD / 2;
-    const int koff = n * ROWB + g * (WPG * 4);
+    // lane (n, g) takes words g*WPG.. of row 16 kt + n: segment (g*WPG)/4 of that row (the
+    // chunk order of ts_internal.h), at word (g*WPG)%4 of the chunk
+    const int koff = (((g * WPG) >> 2) * 64 + n) * 16 + ((g * WPG) & 3) * 4;
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
         if constexpr (WPG == 4) {
-            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, koff + kt * 16 * ROWB, base * ROWB, 0);
+            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, koff + kt * 256, base * ROWB, 0);
             w.kw[kt][0] = t4[0]; w.kw[kt][1] = t4[1]; w.kw[kt][2] = t4[2]; w.kw[kt][3] = t4[3];
         } else {
-            const u32x2 t2 = __builtin_amdgcn_raw_buffer_load_b64(st.k, koff + kt * 16 * ROWB, base * ROWB, 0);
+            const u32x2 t2 = __builtin_amdgcn_raw_buffer_load_b64(st.k, koff + kt * 256, base * ROWB, 0);
             w.kw[kt][0] = t2[0]; w.kw[kt][1] = t2[1];
         }
     }
-    const int voff = lane * NTD * 4;
 #pragma unroll
     for (int b = 0; b < 2; b++) {
 #pragma unroll
         for (int q4 = 0; q4 < NTD / 4; q4++) {
-            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.v, voff + 16 * q4 + b * (HD * 16), (base / 32) * (HD * 16), 0);
+            // words 4 q4 .. 4 q4 + 3 of lane group `lane`: chunk q4 * 64 + lane
+            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.v, (q4 * 64 + lane) * 16 + b * (HD * 16), (base / 32) * (HD * 16), 0);
             w.vw[b][4 * q4 + 0] = t4[0]; w.vw[b][4 * q4 + 1] = t4[1];
             w.vw[b][4 * q4 + 2] = t4[2]; w.vw[b][4 * q4 + 3] = t4[3];
         }
     }
-    // Scales: plain loads with the index clamped into the split (4-byte raw buffer loads of
-    // this stream measured ~20% slower); windows past the end re-read valid, unused scales.
+    // Scales: plain loads with the index clamped into the split; windows past the end re-read
+    // valid, unused scales.
     const int sp = min(base + lane, st.last);
     w.sk = st.ksb[sp];
     w.sv = st.vsb[sp];
@@ -264,32 +257,64 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
 // rotation pair (2i, 2i+1).  Writes the K row, both scales and the position's nibble of every
 // V word (read-modify-write: only this workgroup touches the block), and leaves the
 // dequantized row ((code - 8) * scale, the values the cache now holds) in kd / vd.
+//
+// Two phases, so a caller can issue every load of the append together (one memory round trip)
+// before anything else: append_load, then append_store.
+struct AppendIn {
+    float k0, k1, v0, v1;  // raw new K / V, dims 2i, 2i+1
+    float2 cs;             // rotation of pair i at the position's rotation position
+    float kn0, kn1;        // K norm weights of dims 2i, 2i+1 (QK norm)
+    uint32_t vold[2];      // the V words holding dims 2i, 2i+1 at this position
+};
+
 template <int HD, bool NORM>
-__device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, float *kd, float *vd) {
-    constexpr int NTD = HD / 16, ROWB = HD / 2;
+__device__ __forceinline__ void append_load(const DecodeArgs &a, int s, int h, int p, int lane, AppendIn &in) {
+    constexpr int NTD = HD / 16;
     const KvLayerView &L = a.L;
-    const float *const KN = NORM ? L.kn : nullptr;  // QK norm of K (compiled out when off)
     const size_t row = (size_t)s * L.H + h;
     const bool on = lane < HD / 2;
     const int i = on ? lane : 0;
     const size_t src = row * HD + 2 * i;
-    float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+    in.k0 = in.k1 = in.v0 = in.v1 = 0.f;
     if (on) {
         const float2 kk = *reinterpret_cast<const float2 *>(a.k_new + src);
         const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
-        k0 = kk.x; k1 = kk.y; v0 = vv.x; v1 = vv.y;
+        in.k0 = kk.x; in.k1 = kk.y; in.v0 = vv.x; in.v1 = vv.y;
     }
+    const int ir = i < a.rope_pairs ? i : 0;
+    in.cs = *reinterpret_cast<const float2 *>(a.rope + ((size_t)rot_of(L, s, p) * a.rope_pairs + ir) * 2);
+    in.kn0 = NORM && L.kn ? L.kn[2 * i] : 1.0f;
+    in.kn1 = NORM && L.kn ? L.kn[2 * i + 1] : 1.0f;
+    const int q = p & 31, gq = (q & 15) >> 2;
+    const uint32_t *vb = reinterpret_cast<const uint32_t *>(L.vp + (row * (L.P / 32) + (p >> 5)) * (HD * 16));
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int d = 2 * i + j;
+        in.vold[j] = vb[v_word_idx(gq * 16 + (d & 15), d >> 4)];
+    }
+    (void)NTD;
+}
+
+template <int HD, bool NORM>
+__device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane, const AppendIn &in,
+                             float *kd, float *vd) {
+    constexpr int ROWB = HD / 2;
+    const KvLayerView &L = a.L;
+    const bool KN = NORM && L.kn != nullptr;  // QK norm of K
+    const size_t row = (size_t)s * L.H + h;
+    const bool on = lane < HD / 2;
+    const int i = on ? lane : 0;
+    float k0 = in.k0, k1 = in.k1;
+    const float v0 = in.v0, v1 = in.v1;
     // QK norm scale of the new K row: its squares summed in dimension order across the lanes
     float ns = 0.0f;
     if (KN) ns = qk_norm_scale_from_sum(ordered_sum_pairs(sq_rn(k0), sq_rn(k1), HD / 2), HD, L.norm_eps);
     if (on) {
         if (KN) {
-            k0 = qk_norm_apply(k0, ns, KN[2 * i]);
-            k1 = qk_norm_apply(k1, ns, KN[2 * i + 1]);
+            k0 = qk_norm_apply(k0, ns, in.kn0);
+            k1 = qk_norm_apply(k1, ns, in.kn1);
         }
-        if (i < a.rope_pairs)
-            rope_rotate(k0, k1, *reinterpret_cast<const float2 *>(
-                                    a.rope + ((size_t)rot_of(L, s, p) * a.rope_pairs + i) * 2));
+        if (i < a.rope_pairs) rope_rotate(k0, k1, in.cs);
     }
     const float ks = quant_scale(wave_max(fmaxf(fabsf(k0), fabsf(k1))));
     const float vs = quant_scale(wave_max(fmaxf(fabsf(v0), fabsf(v1))));
@@ -300,12 +325,12 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
     kw |= __shfl_xor(kw, 1, 64);
     kw |= __shfl_xor(kw, 2, 64);
     if (on && (i & 3) == 0)
-        reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * ROWB)[i >> 2] = kw;
+        reinterpret_cast<uint32_t *>(L.kp + row * L.P * ROWB)[k_word_idx<HD>(p, i >> 2)] = kw;
     if (lane == 0) {
         L.ks[row * L.P + p] = ks;
         L.vs[row * L.P + p] = vs;
     }
-    // V block p/32: dim d of key group gq sits in word (gq*16 + d%16)*NTD + d/16, position
+    // V block p/32: dim d of key group gq sits in word v_word_idx(gq*16 + d%16, d/16), position
     // 4gq + r of tile t at nibble r + 4t.
     const int q = p & 31, t = q >> 4, gq = (q & 15) >> 2, nib = (q & 3) + 4 * t;
     uint32_t *vb = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / 32) + (p >> 5)) * (HD * 16));
@@ -313,8 +338,7 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int d = 2 * i + j;
-            uint32_t *w = vb + (gq * 16 + (d & 15)) * NTD + (d >> 4);
-            *w = (*w & ~(0xFu << (4 * nib))) | ((j ? e1 : e0) << (4 * nib));
+            vb[v_word_idx(gq * 16 + (d & 15), d >> 4)] = (in.vold[j] & ~(0xFu << (4 * nib))) | ((j ? e1 : e0) << (4 * nib));
         }
         kd[2 * i] = (float)((int)c0 - 8) * ks;
         kd[2 * i + 1] = (float)((int)c1 - 8) * ks;
@@ -323,9 +347,55 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
     }
 }
 
+template <int HD, bool NORM>
+__device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, float *kd, float *vd) {
+    AppendIn in;
+    append_load<HD, NORM>(a, s, h, p, lane, in);
+    append_store<HD, NORM>(a, s, h, p, lane, in, kd, vd);
+}
+
+// Scores of the new position (dequantized row kd, in this wave's LDS) for the G query heads
+// of kv head h, in the exp2 domain, from the rotated f32 q (as load_q8 rotates it); one wave.
+// qp[hh]: dims (2i, 2i+1) of head hh's raw q (lane i < HD/2), cs: the rotation of pair i at
+// the query's rotation position.
+template <int HD, bool SOFTCAP, bool NORM, int GMAX>
+__device__ void new_token_scores(const DecodeArgs &a, int s, int h, int G, int lane, const float2 (&qp)[GMAX],
+                                 float2 cs, const float *kd, float *xnew) {
+    const float *const QN = NORM ? a.L.qn : nullptr;
+    const float *qg = a.q + ((size_t)s * a.n_head + h * G) * HD;
+    const int i = lane < HD / 2 ? lane : 0;
+#pragma unroll
+    for (int hh = 0; hh < GMAX; hh++) {
+        if (hh >= G) break;
+        float q0 = qp[hh].x, q1 = qp[hh].y;
+        if (QN) {
+            const float nh = q_norm_scale_wave<HD>(qg, G, hh, a.L.norm_eps);
+            q0 = qk_norm_apply(q0, nh, QN[2 * i]);
+            q1 = qk_norm_apply(q1, nh, QN[2 * i + 1]);
+        }
+        if (i < a.rope_pairs) rope_rotate(q0, q1, cs);
+        float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+        float x = dot * a.inv_sqrt_hd;
+        if constexpr (SOFTCAP) x = tanhf(x / a.softcap) * a.softcap;
+        if (lane == 0) xnew[hh] = x * kLog2e;
+    }
+}
+
+// The raw q pairs new_token_scores takes: dims (2i, 2i+1) of the G heads of kv head h.
+template <int HD, int GMAX>
+__device__ __forceinline__ void load_q_pairs(const DecodeArgs &a, int s, int h, int G, int lane, float2 (&qp)[GMAX]) {
+    const float *qg = a.q + ((size_t)s * a.n_head + h * G) * HD;
+    const int i = lane < HD / 2 ? lane : 0;
+#pragma unroll
+    for (int hh = 0; hh < GMAX; hh++)
+        qp[hh] = hh < G ? *reinterpret_cast<const float2 *>(qg + (size_t)hh * HD + 2 * i) : make_float2(0.f, 0.f);
+}
+
 template <int HD, bool SOFTCAP, bool NORM>
-__global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_split_kernel(DecodeArgs a) {
-    constexpr int NW = TS_DECODE_NW;  // waves per workgroup
+__global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs a) {
+    constexpr int NW = kNW16;  // waves per workgroup
     constexpr int SPAN = 64 * NW;     // positions one round of windows covers
     constexpr int WPG = HD / 32;   // K words per lane group = MFMA k-steps per 16-row tile
     constexpr int NTD = HD / 16;   // 16-dim output tiles
@@ -339,11 +409,13 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     const int n_ctx = qpos + 1;
     const int start = split * a.chunk;
     if (start >= n_ctx) return;
-    const int n_split_s = (n_ctx + a.chunk - 1) / a.chunk;
+    const int n_split_s = min((n_ctx + a.chunk - 1) / a.chunk, a.n_split);
     // With the fused append, this split's workgroup writes position qpos itself and adds its
     // score from registers; the window loop then stops short of it.
     const bool fused = a.k_new != nullptr && split == n_split_s - 1;
-    const int end = fused ? qpos : min(start + a.chunk, n_ctx);
+    // the last split runs to the end, also past chunk * n_split (a launch captured for shorter
+    // contexts stays correct, only less balanced)
+    const int end = fused ? qpos : (split == n_split_s - 1 ? n_ctx : start + a.chunk);
 
     const int tid = threadIdx.x, lane = tid & 63;
     // wave index in an SGPR: window bases are then provably wave-uniform and feed the scalar
@@ -379,7 +451,8 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     const float *vsb = L.vs + row * L.P;
 
     Streams str;
-    str.k = make_rsrc(kbase, (uint32_t)end * ROWB);
+    // K rows are cut into segments spread over their 64-position window: bound at the window
+    str.k = make_rsrc(kbase, (uint32_t)((end + 63) & ~63) * ROWB);
     str.v = make_rsrc(vbase, (uint32_t)((end + 31) / 32) * (HD * 16));
     str.ksb = ksb;
     str.vsb = vsb;
@@ -387,9 +460,6 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
 
     // First window in flight before anything else.
     Window<HD> w0, w1;
-#if TS_DECODE_DEPTH == 3
-    Window<HD> w2;
-#endif
     int base = start + wave * 64;
     load_window<HD>(w0, str, base, n, g, lane);
 
@@ -414,28 +484,17 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
                 QN, ns);
         sm.run.q.p[t][lane] = !live ? (half8)(_Float16)0.0f : (lo_col ? ql : qh);
     }
-    if (fused && wave == 0) append_one<HD, NORM>(a, s, h, qpos, lane, kd, vd);
-    __syncthreads();
-    if (fused) {
-        // score of the new position for head h*G + hh, from the rotated f32 q (as load_q8)
-        for (int hh = wave; hh < G; hh += NW) {
-            const int i = lane < HD / 2 ? lane : 0;
-            const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
-            float q0 = qq.x, q1 = qq.y;
-            if (QN) {
-                const float nh = q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, hh, L.norm_eps);
-                q0 = qk_norm_apply(q0, nh, QN[2 * i]);
-                q1 = qk_norm_apply(q1, nh, QN[2 * i + 1]);
-            }
-            if (i < a.rope_pairs)
-                rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + i) * 2));
-            float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
-            float x = dot * a.inv_sqrt_hd;
-            if constexpr (SOFTCAP) x = tanhf(x / a.softcap) * a.softcap;
-            if (lane == 0) xnew[hh] = x * kLog2e;
-        }
+    __syncthreads();  // q operands
+    // The appending wave (the last: it has the fewest windows) quantizes the new token and
+    // scores it against every head before its windows; the others start at once.  kd, vd and
+    // xnew are read after the barrier that opens the merge.
+    if (fused && wave == NW - 1) {
+        AppendIn ain;
+        float2 qp[8];
+        append_load<HD, NORM>(a, s, h, qpos, lane, ain);
+        load_q_pairs<HD, 8>(a, s, h, G, lane, qp);
+        append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd);
+        new_token_scores<HD, SOFTCAP, NORM, 8>(a, s, h, G, lane, qp, ain.cs, kd, xnew);
     }
 
     WaveState<HD> st;
@@ -445,29 +504,6 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
     st.l = 0.0f;
     float *stage = sm.run.stage[wave];
 
-#if TS_DECODE_DEPTH == 3
-    // Register triple buffering: windows i+1 and i+2 are in flight while window i is computed.
-    load_window<HD>(w1, str, base + SPAN, n, g, lane);
-#define TS_STEP(CUR, NXT)                                                                       \
-    {                                                                                          \
-        load_window<HD>(NXT, str, base + 2 * SPAN, n, g, lane);                                     \
-        /* keep the prefetch here: the scheduler would otherwise sink it below CUR's use */     \
-        asm volatile("" ::: "memory");                                                         \
-        __builtin_amdgcn_sched_barrier(0);                                                     \
-        if (base + 64 <= end)                                                                  \
-            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
-        else                                                                                   \
-            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
-        base += SPAN;                                                                           \
-        if (base >= end) break;                                                                \
-    }
-    while (base < end) {
-        TS_STEP(w0, w2)
-        TS_STEP(w1, w0)
-        TS_STEP(w2, w1)
-    }
-#undef TS_STEP
-#else
     // Register double buffering: window i+1 is in flight while window i is computed.  Full
     // windows take the unmasked path; only the window that crosses `end` is masked.
 #define TS_STEP(CUR, NXT)                                                                       \
@@ -488,7 +524,6 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE_WAVES) void decode_spl
         TS_STEP(w1, w0)
     }
 #undef TS_STEP
-#endif
 
     // ---- merge the 4 waves through LDS ---------------------------------------------------------
     const float l_run = group_sum(st.l);
@@ -549,7 +584,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     __shared__ float wmax[4];
     const int head = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
     const int n_ctx = a.len[s] + 1;
-    const int ns = (n_ctx + a.chunk - 1) / a.chunk;
+    const int ns = min((n_ctx + a.chunk - 1) / a.chunk, a.n_split);
     if (ns <= 1) return;
     const size_t hidx = (size_t)s * a.n_head + head;
     const float *ml = a.ws + (size_t)a.L.S * a.n_head * a.n_split * HD;
@@ -638,27 +673,39 @@ struct Window4 {
     float sk, sv;         // scales of position base + lane
 };
 
+// Buffer resources of one split for the G <= 4 kernel: K, V and both scale arrays, each
+// bounded to the split's positions (loads past the bound return zeros and touch no memory).
+struct Streams4 {
+    __amdgpu_buffer_rsrc_t k, v, sk, sv;
+};
+
+// Cache policy of the window loads: non-temporal.  Every byte is read exactly once per launch,
+// and each instruction covers whole cache lines.
+constexpr int kNT = 2;
+
+// One window (64 positions from `base`, a multiple of 64): each instruction reads one
+// contiguous kilobyte.  K: chunk j*64 + lane of the window is segment j of the row of position
+// base + lane (words 4j..4j+3).  V: chunk q*64 + lane of each 32-position block holds words
+// 4q..4q+3 of lane group `lane`.  Scales: position base + lane.
 template <int HD>
-__device__ __forceinline__ void load_window4(Window4<HD> &w, const Streams &st, int base, int lane) {
+__device__ __forceinline__ void load_window4(Window4<HD> &w, const Streams4 &st, int base, int lane) {
     constexpr int NKW = HD / 8, NTD = HD / 16, ROWB = HD / 2;
 #pragma unroll
     for (int j = 0; j < NKW / 4; j++) {
-        const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, lane * ROWB + 16 * j, base * ROWB, 0);
+        const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, lane * 16 + j * 1024, base * ROWB, kNT);
         w.kw[4 * j + 0] = t4[0]; w.kw[4 * j + 1] = t4[1]; w.kw[4 * j + 2] = t4[2]; w.kw[4 * j + 3] = t4[3];
     }
-    const int voff = lane * NTD * 4;
 #pragma unroll
     for (int b = 0; b < 2; b++) {
 #pragma unroll
         for (int q4 = 0; q4 < NTD / 4; q4++) {
-            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.v, voff + 16 * q4 + b * (HD * 16), (base / 32) * (HD * 16), 0);
+            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.v, lane * 16 + q4 * 1024 + b * (HD * 16), (base / 32) * (HD * 16), kNT);
             w.vw[b][4 * q4 + 0] = t4[0]; w.vw[b][4 * q4 + 1] = t4[1];
             w.vw[b][4 * q4 + 2] = t4[2]; w.vw[b][4 * q4 + 3] = t4[3];
         }
     }
-    const int sp = min(base + lane, st.last);
-    w.sk = st.ksb[sp];
-    w.sv = st.vsb[sp];
+    w.sk = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(st.sk, lane * 4, base * 4, kNT));
+    w.sv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(st.sv, lane * 4, base * 4, kNT));
 }
 
 // Wave state: O^T accumulators (column n < 4: head n from the high parts of p*s_v, 4 <= n < 8:
@@ -728,7 +775,7 @@ __device__ __forceinline__ void process_window4(const Window4<HD> &w, WaveState4
                                                 const half4_t (&qh)[HD / 64], const half4_t (&ql)[HD / 64],
                                                 _Float16 (*pt)[64], int base, int end, int lane, int G,
                                                 float inv_s, float softcap, const DeqConst &dc) {
-    constexpr int NKW = HD / 8, NTD = HD / 16;
+    constexpr int NTD = HD / 16;
     // ---- S = Q K^T --------------------------------------------------------------------------------
     floatx4 acc[2] = {(floatx4)0.0f, (floatx4)0.0f};  // hi and lo parts of q
     QkWords<HD, 0>::run(w, qh, ql, acc, dc);
@@ -803,10 +850,11 @@ __device__ __forceinline__ void process_window4(const Window4<HD> &w, WaveState4
     }
 }
 
-template <int HD, bool SOFTCAP, bool NORM>
-__global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_split4_kernel(DecodeArgs a) {
-    constexpr int NW = TS_DECODE_NW;
-    constexpr int SPAN = 64 * NW;
+// NW waves per workgroup, D windows in registers per wave (D - 1 in flight while one is
+// computed).  The plan places one workgroup of 4 waves per CU (one wave per SIMD).  Measured
+// on config 3 (ms per step): D = 2 1.915, D = 3 1.951; 8 waves with D = 2 2.05.
+template <int HD, bool SOFTCAP, bool NORM, int NW, int D>
+__global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeArgs a) {
     constexpr int NTD = HD / 16;
     constexpr int NQ = HD / 64;  // q register pairs (16 k-steps each)
     constexpr int OST = HD + 1;
@@ -818,9 +866,11 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     const int n_ctx = qpos + 1;
     const int start = split * a.chunk;
     if (start >= n_ctx) return;
-    const int n_split_s = (n_ctx + a.chunk - 1) / a.chunk;
+    const int n_split_s = min((n_ctx + a.chunk - 1) / a.chunk, a.n_split);
     const bool fused = a.k_new != nullptr && split == n_split_s - 1;
-    const int end = fused ? qpos : min(start + a.chunk, n_ctx);
+    // the last split runs to the end, also past chunk * n_split (a launch captured for shorter
+    // contexts stays correct, only less balanced)
+    const int end = fused ? qpos : (split == n_split_s - 1 ? n_ctx : start + a.chunk);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.G;
@@ -838,37 +888,84 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
 
     const size_t row = (size_t)s * L.H + h;
     constexpr int ROWB = HD / 2;
-    Streams str;
-    str.k = make_rsrc(L.kp + row * L.P * ROWB, (uint32_t)end * ROWB);
+    Streams4 str;
+    // K rows are cut into segments spread over their 64-position window: bound at the window
+    str.k = make_rsrc(L.kp + row * L.P * ROWB, (uint32_t)((end + 63) & ~63) * ROWB);
     str.v = make_rsrc(L.vp + row * (L.P / 32) * (HD * 16), (uint32_t)((end + 31) / 32) * (HD * 16));
-    str.ksb = L.ks + row * L.P;
-    str.vsb = L.vs + row * L.P;
-    str.last = max(end - 1, 0);
+    str.sk = make_rsrc(L.ks + row * L.P, (uint32_t)end * 4);
+    str.sv = make_rsrc(L.vs + row * L.P, (uint32_t)end * 4);
 
-    Window4<HD> w0, w1;
-    int base = start + wave * 64;
-    load_window4<HD>(w0, str, base, lane);
+    // This wave's windows: w = wave, wave + NW, ... below nwin, taken in rotated order starting
+    // at a per-workgroup offset, so that the workgroups streaming at the same time read
+    // different regions of their streams (spread over the HBM channels).  Window indices past
+    // cnt load from past the bound (zeros, no memory traffic).
+    const int nwin = (end - start + 63) >> 6;
+    const int cnt = wave < nwin ? (nwin - wave + NW - 1) / NW : 0;
+    const int rot = cnt ? (int)((unsigned)(row * 37 + split * 11) % (unsigned)cnt) : 0;
+    const int oob = start + 64 * nwin;
+    auto win_base = [&](int i) {
+        if (i >= cnt) return oob;
+        int r = i + rot;
+        r = r >= cnt ? r - cnt : r;
+        return start + 64 * (wave + NW * r);
+    };
+    Window4<HD> w[D];
 
     // q operands: lane 4 blk + i holds head i (zero past G) for k-step 16 c + blk of pair c; a
-    // k-step is half of a dequantized word's slots: word t/2, slots 4 (t%2) .. +3.
+    // k-step is half of a dequantized word's slots: word t/2, slots 4 (t%2) .. +3.  The raw q
+    // loads go out before the windows' prefetch: loads complete in order, so consuming q then
+    // does not wait for the windows.
     half4_t qh[NQ], ql[NQ];
     float q_s, inv_s;
+    const bool appender = fused && wave == NW - 1;
+    AppendIn ain;
+    float2 qp[4];
     {
         const int blk = lane >> 2, i = lane & 3;
         const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (i < G ? i : 0)) * HD;
+        float qx[NQ][8], nwv[NQ][8];
+        float2 qcs[NQ][4];
+#pragma unroll
+        for (int c = 0; c < NQ; c++) {
+            const int u = (16 * c + blk) >> 1;
+            q_read8(qrow, u, nullptr, 1.0f, qx[c]);
+            load_rot8(a.rope, a.rope_pairs, u, qrot, qcs[c]);
+            if (QN) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) nwv[c][e] = QN[8 * u + e];
+            }
+        }
         const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, i < G ? i : 0,
                                                     L.norm_eps)
                             : 1.0f;
+        // The appending wave (the last: it has the fewest windows) quantizes the new token and
+        // scores it against every head before its windows; the others start at once.  Its
+        // loads go out with q's.  kd, vd and xnew are read after the barrier that opens the
+        // merge.
+        if (appender) {
+            append_load<HD, NORM>(a, s, h, qpos, lane, ain);
+            load_q_pairs<HD, 4>(a, s, h, G, lane, qp);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < D - 1; d++) load_window4<HD>(w[d], str, win_base(d), lane);
+        __builtin_amdgcn_sched_barrier(0);
         float qb = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NQ; c++) qb = fmaxf(qb, q_bound8(qrow, (16 * c + blk) >> 1, QN, ns));
+        for (int c = 0; c < NQ; c++) {
+            if (QN) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) qx[c][e] = qk_norm_apply(qx[c][e], ns, nwv[c][e]);
+            }
+            qb = fmaxf(qb, fmaxf(fmaxf(fabsf(qx[c][0]) + fabsf(qx[c][1]), fabsf(qx[c][2]) + fabsf(qx[c][3])),
+                                 fmaxf(fabsf(qx[c][4]) + fabsf(qx[c][5]), fabsf(qx[c][6]) + fabsf(qx[c][7]))));
+        }
         q_scale(wave_max_all(qb) * (a.inv_sqrt_hd * kLog2e), q_s, inv_s);
 #pragma unroll
         for (int c = 0; c < NQ; c++) {
             const int t = 16 * c + blk;
             half8 hh8, ll8;
-            load_q8(a.rope, a.rope_pairs, qrow, t >> 1, qrot, a.inv_sqrt_hd * kLog2e * q_s, hh8, ll8,
-                    QN, ns);
+            split_q8(qx[c], qcs[c], t >> 1, a.rope_pairs, a.inv_sqrt_hd * kLog2e * q_s, hh8, ll8);
             const int o4 = 4 * (t & 1);
             half4_t hv = {hh8[o4], hh8[o4 + 1], hh8[o4 + 2], hh8[o4 + 3]};
             half4_t lv = {ll8[o4], ll8[o4 + 1], ll8[o4 + 2], ll8[o4 + 3]};
@@ -876,28 +973,13 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
             ql[c] = i < G ? lv : (half4_t)(_Float16)0.0f;
         }
     }
-    if (fused && wave == 0) append_one<HD, NORM>(a, s, h, qpos, lane, kd, vd);
-    __syncthreads();
-    if (fused) {
-        for (int hh = wave; hh < G; hh += NW) {
-            const int i = lane < HD / 2 ? lane : 0;
-            const float2 qq = *reinterpret_cast<const float2 *>(a.q + ((size_t)s * a.n_head + h * G + hh) * HD + 2 * i);
-            float q0 = qq.x, q1 = qq.y;
-            if (QN) {
-                const float nh = q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, hh, L.norm_eps);
-                q0 = qk_norm_apply(q0, nh, QN[2 * i]);
-                q1 = qk_norm_apply(q1, nh, QN[2 * i + 1]);
-            }
-            if (i < a.rope_pairs)
-                rope_rotate(q0, q1, *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + i) * 2));
-            float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
-            float x = dot * a.inv_sqrt_hd;
-            if constexpr (SOFTCAP) x = tanhf(x / a.softcap) * a.softcap;
-            if (lane == 0) xnew[hh] = x * kLog2e;
-        }
+    if (appender) {
+        append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd);
+        new_token_scores<HD, SOFTCAP, NORM, 4>(a, s, h, G, lane, qp, ain.cs, kd, xnew);
     }
+    // The appending wave (the last: it has the fewest windows) quantizes the new token and
+    // scores it against every head before its windows; the others start at once.  kd, vd and
+    // xnew are read after the barrier that opens the merge.
 
     WaveState4<HD> st;
 #pragma unroll
@@ -909,23 +991,25 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     }
     _Float16 (*pt)[64] = sm.pt[wave];
 
-#define TS_STEP4(CUR, NXT)                                                                      \
-    {                                                                                          \
-        load_window4<HD>(NXT, str, base + SPAN, lane);                                          \
-        asm volatile("" ::: "memory");                                                         \
-        __builtin_amdgcn_sched_barrier(0);                                                     \
-        if (base + 64 <= end)                                                                  \
-            process_window4<HD, SOFTCAP, false>(CUR, st, qh, ql, pt, base, end, lane, G, inv_s, a.softcap, dc); \
-        else                                                                                   \
-            process_window4<HD, SOFTCAP, true>(CUR, st, qh, ql, pt, base, end, lane, G, inv_s, a.softcap, dc); \
-        base += SPAN;                                                                          \
-        if (base >= end) break;                                                                \
+    int it = 0;
+    if (cnt > 0) {
+        while (true) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                load_window4<HD>(w[(d + D - 1) % D], str, win_base(it + D - 1), lane);
+                // keep the prefetch here: the scheduler would otherwise sink it below the use
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+                const int base = win_base(it);
+                if (base + 64 <= end)
+                    process_window4<HD, SOFTCAP, false>(w[d], st, qh, ql, pt, base, end, lane, G, inv_s, a.softcap, dc);
+                else
+                    process_window4<HD, SOFTCAP, true>(w[d], st, qh, ql, pt, base, end, lane, G, inv_s, a.softcap, dc);
+                if (++it >= cnt) goto windows_done;
+            }
+        }
     }
-    while (base < end) {
-        TS_STEP4(w0, w1)
-        TS_STEP4(w1, w0)
-    }
-#undef TS_STEP4
+windows_done:
 
     // ---- merge the waves through LDS ------------------------------------------------------------
     float l_run[4];
@@ -946,7 +1030,7 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
     }
     __syncthreads();
 
-    for (int idx = tid; idx < G * HD; idx += SPAN) {
+    for (int idx = tid; idx < G * HD; idx += 64 * NW) {
         const int hh = idx / HD, d = idx % HD;
         float M = kMinit;
 #pragma unroll
@@ -980,33 +1064,70 @@ __global__ __launch_bounds__(64 * TS_DECODE_NW, TS_DECODE4_WAVES) void decode_sp
 
 }  // namespace
 
-// Split plan: aim for ~kTargetWG workgroups in total -- two per CU: measured on the config-3
-// and config-4 shapes, long splits stream faster than short ones (2.26 vs 2.37 ms per
-// config-3 step for 512 vs 1024 workgroups).  One per CU (256) was faster still on most
-// boxes (2.24 ms) but 10% slower than 1024 on one: with a single workgroup per CU any slow
-// CU sets the kernel's time, two per CU keep some balancing.  Each split is a multiple of 64
-// positions and at least 256 when the context allows.  n_split is non-decreasing in max_ctx.
-DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx) {
-    // TS_DECODE_WG overrides the workgroup target (a tuning knob; read once).
-    static const int kTargetWG = [] {
-        const char *e = getenv("TS_DECODE_WG");
-        const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 512;
-    }();
-    const int units = n_seq * n_kv;
-    int want = (kTargetWG + units - 1) / units;
-    if (want < 1) want = 1;
-    // Every wave of a workgroup takes 64-position windows round robin: a split shorter than
-    // 4 windows leaves waves idle, so short contexts get fewer, fuller splits.
-    const int max_split = (max_ctx + 64 * TS_DECODE_NW - 1) / (64 * TS_DECODE_NW);
-    if (want > max_split) want = max_split;
-    int chunk = (max_ctx + want - 1) / want;
-    chunk = (chunk + 63) / 64 * 64;
+// Split plan.  The G <= 4 kernel runs one workgroup of 4 waves per CU, the 16x16 kernel two
+// per CU.  The chunk (positions per split, a multiple of 64) is the smallest one for which
+// the busy workgroups of the whole batch, n_kv * sum_s ceil(n_ctx[s] / chunk), fit in that
+// target: the batch's total context spread evenly, so ragged batches give their long
+// sequences more splits and no CU gets a second workgroup.  (Measured on the config-3 shape
+// with a loads-only probe of the same access pattern: one workgroup per stream and CU 43.2 us,
+// two 44.7 us, three 45.6 us.)  Splits shorter than kMinChunk leave waves without a window.
+namespace {
+constexpr int kMinChunk = 256;
+constexpr int kG4MinChunk = 1024;  // the 4x4x4 kernel needs >= 4 windows per wave to pay off
+
+int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    const int v = e ? atoi(e) : 0;
+    return v > 0 ? v : dflt;
+}
+
+int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
+    int64_t total = 0;
+    int max_ctx = 1;
+    for (int s = 0; s < n_seq; s++) {
+        total += n_ctx[s];
+        max_ctx = std::max(max_ctx, (int)n_ctx[s]);
+    }
+    auto busy = [&](int chunk) {
+        int64_t n = 0;
+        for (int s = 0; s < n_seq; s++) n += (n_ctx[s] + chunk - 1) / chunk;
+        return n * n_kv;
+    };
+    const int hi_c = std::max(kMinChunk, (max_ctx + 63) / 64 * 64);
+    int lo_c = (int)std::min<int64_t>(hi_c, std::max<int64_t>(kMinChunk, (total * n_kv + target - 1) / target));
+    lo_c = (lo_c + 63) / 64 * 64;
+    // smallest multiple of 64 in [lo_c, hi_c] with busy <= target (busy is non-increasing)
+    int lo = lo_c / 64, hi = hi_c / 64;
+    while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        if (busy(64 * mid) <= target) hi = mid; else lo = mid + 1;
+    }
+    return 64 * lo;
+}
+}  // namespace
+
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu) {
+    // TS_DECODE_WG overrides the workgroup target of the G <= 4 kernel (a tuning knob).
+    static const int kTarget4 = env_int("TS_DECODE_WG", 0);
     DecodePlan p;
-    p.chunk = chunk;
-    p.n_split = (max_ctx + chunk - 1) / chunk;  // <= want
-    p.cap = want;
+    int max_ctx = 1;
+    for (int s = 0; s < n_seq; s++) max_ctx = std::max(max_ctx, (int)n_ctx[s]);
+    p.g4 = false;
+    if (G <= 4) {
+        p.chunk = plan_chunk(n_ctx, n_seq, n_kv, kTarget4 ? kTarget4 : n_cu);
+        p.g4 = p.chunk >= kG4MinChunk;
+    }
+    if (!p.g4) p.chunk = plan_chunk(n_ctx, n_seq, n_kv, 2 * n_cu);
+    p.n_split = (max_ctx + p.chunk - 1) / p.chunk;
     return p;
+}
+
+int decode_cap(int n_kv, int max_seq, int n_cu) {
+    // One sequence alone can take at most target / n_kv splits (plus one for rounding); the
+    // 16x16 kernel's target, 2 n_cu, is the larger.
+    static const int kTarget4 = env_int("TS_DECODE_WG", 0);
+    const int target = std::max(2 * n_cu, kTarget4);
+    return std::min((max_seq + 63) / 64, target / n_kv + 2);
 }
 
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
@@ -1031,13 +1152,20 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.v_new = v_new;
     dim3 grid(plan.n_split, L.H, L.S);
     // The 4x4x4 QK kernel does less VALU work per window but has the longer per-window
-    // dependency chain (QK chains of 32 MFMAs, P through LDS): measured faster once every wave
-    // streams at least 4 windows per split, slower for short splits (batch-1 shapes).
-    const bool g4 = a.G <= 4 && plan.chunk >= 4 * 64 * TS_DECODE_NW && !TS_DECODE_FORCE16;
+    // dependency chain (QK chains of 32 MFMAs, P through LDS); it runs when every wave streams
+    // at least 4 windows of its split (plan.g4).  TS_DECODE_SHAPE=2 selects its 8-wave,
+    // double-buffered form (a tuning knob).
+    static const int kShape = env_int("TS_DECODE_SHAPE", 1);
+    // The G <= 4 kernel fits two workgroups per CU by registers, but the plan wants one per
+    // CU: the unused dynamic LDS reservation (with the kernel's own ~17 KB, more than half of
+    // the CU's 160 KB) makes the dispatcher place busy workgroups on distinct CUs, also when
+    // the grid holds idle ones (splits past a short sequence's end) that exit at once.
+    constexpr size_t kOnePerCuLds = 64 * 1024;
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
-#define TS_SPLIT(HDV, SC, NM)                                                                 \
-    (g4 ? (decode_split4_kernel<HDV, SC, NM><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a), 0)       \
-        : (decode_split_kernel<HDV, SC, NM><<<grid, 64 * TS_DECODE_NW, 0, st>>>(a), 0))
+#define TS_SPLIT(HDV, SC, NM)                                                                  \
+    (plan.g4 ? (kShape == 2 ? (decode_split4_kernel<HDV, SC, NM, 8, 2><<<grid, 512, kOnePerCuLds, st>>>(a), 0)    \
+                            : (decode_split4_kernel<HDV, SC, NM, 4, 2><<<grid, 256, kOnePerCuLds, st>>>(a), 0))   \
+             : (decode_split_kernel<HDV, SC, NM><<<grid, 64 * kNW16, 0, st>>>(a), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \
     (cap ? (norm ? TS_SPLIT(HDV, true, true) : TS_SPLIT(HDV, true, false))                    \
          : (norm ? TS_SPLIT(HDV, false, true) : TS_SPLIT(HDV, false, false)))

@@ -2,19 +2,26 @@
 //
 // HBM layout of one layer (S sequences, H kv heads, P = max_seq rounded up to 64, hd dims):
 //
-//   K packed  [S][H][P][hd/2 bytes]            row p = the reference's per-(pos, head) row:
-//                                              word u holds dims 8u..8u+7, dim 8u+n in bits 4n..
+//   K packed  [S][H][P/64][hd*32 bytes]        64-position windows.  Position p's row is the
+//                                              reference's per-(pos, head) row (word u holds
+//                                              dims 8u..8u+7, dim 8u+n in bits 4n..4n+3), cut
+//                                              into 16-byte segments j = u/4; segment j of
+//                                              window row r = p % 64 sits at 16-byte chunk
+//                                              j*64 + r of the window (k_word_idx)
 //   V packed  [S][H][P/32][hd*16 bytes]        32-position blocks, "position-packed": word
-//                                              (g, dl, td) of a block sits at index
-//                                              (g*16 + dl)*(hd/16) + td and holds dim 16*td+dl
-//                                              at 8 positions: nibble n<4 -> position 4g+n,
-//                                              nibble n>=4 -> position 16+4g+(n-4)
+//                                              (g, dl, td) of a block holds dim 16*td+dl at 8
+//                                              positions (nibble n<4 -> position 4g+n, nibble
+//                                              n>=4 -> position 16+4g+(n-4)); lane group
+//                                              ln = g*16+dl owns words td = 0..hd/16-1, held in
+//                                              16-byte chunks (td/4)*64 + ln (v_word_idx)
 //   K scale   [S][H][P] f32
 //   V scale   [S][H][P] f32
 //
-// Each (sequence, kv head) is one contiguous stream per buffer, so a decode workgroup reads
-// whole 1-2 KB runs.  The V block layout is what the PV matrix-core step consumes directly:
-// every 32-bit word is the 8 positions one lane feeds to one v_mfma_f32_16x16x32_f16.
+// Each (sequence, kv head) is one contiguous stream per buffer.  The chunk orders make every
+// 16-byte load instruction of a decode wave read one contiguous kilobyte while lane r still
+// receives exactly the data it feeds to the matrix cores: segment j of its own K row, and the
+// words of its own V lane group.  Every V word is the 8 positions one lane feeds to one
+// v_mfma_f32_16x16x32_f16.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -27,6 +34,16 @@
 namespace ts {
 
 constexpr int kPosAlign = 64;  // P is a multiple of this (one decode window)
+
+// Word index of K word u of position p, counted from the start of its (sequence, kv head)
+// stream (the layout above).
+template <int HD>
+__host__ __device__ inline size_t k_word_idx(int p, int u) {
+    return (size_t)(p >> 6) * (HD * 8) + (size_t)((((u >> 2) << 6) + (p & 63)) << 2) + (u & 3);
+}
+
+// Word index of V word (lane group ln = 16 g + dl, tile td) inside its 32-position block.
+__host__ __device__ inline int v_word_idx(int ln, int td) { return ((((td >> 2) << 6) + ln) << 2) + (td & 3); }
 
 struct KvLayerView {
     uint8_t *kp;  // K packed
@@ -65,7 +82,9 @@ struct ts_kv {
     std::vector<int32_t> h_len, h_rot, h_sink;
     std::vector<const float *> q_norm, k_norm;  // per layer, device pointers or null
     std::vector<float> norm_eps;
+    std::vector<int32_t> h_ctx;  // scratch for the decode plan: len + 1 per sequence
     int device;
+    int n_cu;                    // compute units of the device (the decode plan's target)
 
     ts::KvLayerView layer(int l) const {
         ts::KvLayerView v;
@@ -111,10 +130,13 @@ hipError_t launch_len_update(int32_t *d_len, int n, int32_t seq, int32_t value, 
 
 struct DecodePlan {
     int chunk;    // positions per split (multiple of 64)
-    int n_split;  // splits for the longest sequence
-    int cap;      // upper bound of n_split for any context <= the one planned for
+    int n_split;  // splits of the longest sequence (grid.x)
+    bool g4;      // the G <= 4 (4x4x4 QK) kernel
 };
-DecodePlan decode_plan(int n_seq, int n_kv, int max_ctx);
+// n_ctx: keys per sequence (len + 1), on the host; n_cu: compute units of the device.
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu);
+// Upper bound of plan.n_split for any lengths up to max_seq (sizes the workspace).
+int decode_cap(int n_kv, int max_seq, int n_cu);
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,

@@ -152,10 +152,13 @@ int ts_kv_create(const ts_kv_desc *desc, ts_kv **out) {
     kv->q_norm.assign(desc->n_layers, nullptr);
     kv->k_norm.assign(desc->n_layers, nullptr);
     kv->norm_eps.assign(desc->n_layers, 1e-6f);
-    if (hipGetDevice(&kv->device) != hipSuccess) {
+    if (hipGetDevice(&kv->device) != hipSuccess ||
+        hipDeviceGetAttribute(&kv->n_cu, hipDeviceAttributeMultiprocessorCount, kv->device) != hipSuccess ||
+        kv->n_cu <= 0) {
         delete kv;
         return TS_ERR_HIP;
     }
+    kv->h_ctx.assign(desc->n_seq, 0);
     uint64_t total = kv->layer_bytes * (uint64_t)desc->n_layers;
     if (hipMalloc(&kv->base, total) != hipSuccess) {
         delete kv;
@@ -364,8 +367,8 @@ static bool heads_ok(const ts_kv *kv, int32_t n_head) {
 
 int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes) {
     if (!kv || !bytes || !heads_ok(kv, n_head)) return TS_ERR_INVALID;
-    ts::DecodePlan plan = ts::decode_plan(kv->d.n_seq, kv->d.n_head_kv, kv->d.max_seq);
-    *bytes = (uint64_t)kv->d.n_seq * n_head * plan.cap * (kv->d.head_dim + 2) * sizeof(float);
+    const int cap = ts::decode_cap(kv->d.n_head_kv, kv->d.max_seq, kv->n_cu);
+    *bytes = (uint64_t)kv->d.n_seq * n_head * cap * (kv->d.head_dim + 2) * sizeof(float);
     return TS_OK;
 }
 
@@ -383,10 +386,13 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
     if (rc) return rc;
     uint64_t need = 0;
     ts_attn_decode_workspace(kv, n_head, &need);
-    ts::DecodePlan plan = ts::decode_plan(kv->d.n_seq, kv->d.n_head_kv, max_len + 1);
+    std::vector<int32_t> &ctx = const_cast<ts_kv *>(kv)->h_ctx;
+    for (int s = 0; s < kv->d.n_seq; s++) ctx[s] = kv->h_len[s] + 1;
+    ts::DecodePlan plan = ts::decode_plan(ctx.data(), kv->d.n_seq, kv->d.n_head_kv, n_head / kv->d.n_head_kv,
+                                          kv->n_cu);
     if (plan.n_split > 1 && (!d_workspace || workspace_bytes < need)) return TS_ERR_WORKSPACE;
     if (plan.n_split > 1 && !aligned16(d_workspace)) return TS_ERR_INVALID;
-    // plan.n_split <= cap(max_seq), the count the workspace was sized for.
+    // plan.n_split <= decode_cap(max_seq), the count the workspace was sized for.
     return hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
                                         rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
                                         plan, k_new, v_new, as_stream(stream)));

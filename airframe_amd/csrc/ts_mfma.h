@@ -156,23 +156,15 @@ __device__ inline void q_scale(float m, float &s, float &inv_s) {
     inv_s = ldexpf(1.0f, e - 13);
 }
 
-// Rotated q for the 8 dims 8u..8u+7 of one head (rope.rs:186-196, table row qpos), after the
-// optional QK norm, times `mul`, split x = hi + lo into f16 and arranged in the slot order of
-// dequant8.
-__device__ inline void load_q8(const float *rope, int rope_pairs, const float *qrow, int u,
-                               int qpos, float mul, half8 &hi, half8 &lo,
-                               const float *nw = nullptr, float ns = 1.0f) {
+// Rotated q for the 8 dims 8u..8u+7 of one head from its (normalized) values x and the
+// rotation cs[i] of pair 4u + i (pairs at or past rope_pairs are not rotated), times `mul`,
+// split x = hi + lo into f16 and arranged in the slot order of dequant8.
+__device__ inline void split_q8(float (&x)[8], const float2 (&cs)[4], int u, int rope_pairs, float mul,
+                                half8 &hi, half8 &lo) {
 #pragma clang fp contract(off)
-    float x[8];
-    q_read8(qrow, u, nw, ns, x);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int pair = 4 * u + i;
-        if (pair < rope_pairs) {
-            const float2 cs = *reinterpret_cast<const float2 *>(rope + ((size_t)qpos * rope_pairs + pair) * 2);
-            rope_rotate(x[2 * i], x[2 * i + 1], cs);
-        }
-    }
+    for (int i = 0; i < 4; i++)
+        if (4 * u + i < rope_pairs) rope_rotate(x[2 * i], x[2 * i + 1], cs[i]);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const float v = opaque(x[kPerm[j]] * mul);
@@ -180,6 +172,29 @@ __device__ inline void load_q8(const float *rope, int rope_pairs, const float *q
         hi[j] = h;
         lo[j] = (_Float16)(v - (float)h);
     }
+}
+
+// The rotations split_q8 needs for dims 8u..8u+7 at table row qpos.
+__device__ inline void load_rot8(const float *rope, int rope_pairs, int u, int qpos, float2 (&cs)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int pair = 4 * u + i;
+        cs[i] = pair < rope_pairs ? *reinterpret_cast<const float2 *>(rope + ((size_t)qpos * rope_pairs + pair) * 2)
+                                  : make_float2(1.0f, 0.0f);
+    }
+}
+
+// Rotated q for the 8 dims 8u..8u+7 of one head (rope.rs:186-196, table row qpos), after the
+// optional QK norm, times `mul`, split x = hi + lo into f16 and arranged in the slot order of
+// dequant8.
+__device__ inline void load_q8(const float *rope, int rope_pairs, const float *qrow, int u,
+                               int qpos, float mul, half8 &hi, half8 &lo,
+                               const float *nw = nullptr, float ns = 1.0f) {
+    float x[8];
+    q_read8(qrow, u, nw, ns, x);
+    float2 cs[4];
+    load_rot8(rope, rope_pairs, u, qpos, cs);
+    split_q8(x, cs, u, rope_pairs, mul, hi, lo);
 }
 
 }  // namespace

@@ -115,12 +115,16 @@ __device__ inline void fetch_window(Pending<HD, NW> &pd, const uint8_t *kbase, c
     auto load_k = [&](int c) {
         int key, part;
         k_piece<HD>(c, key, part);
-        return *reinterpret_cast<const uint4 *>(kbase + (size_t)(base + key) * ROWB + part * 16);
+        // segment `part` of row `key` of the 64-position window at base (k_word_idx)
+        return *reinterpret_cast<const uint4 *>(kbase + (size_t)base * ROWB + (part * 64 + key) * 16);
     };
     auto load_v = [&](int c) {
         int b, piece;
         v_piece<HD>(c, b, piece);
-        return *reinterpret_cast<const uint4 *>(vbase + (size_t)(base / 32 + b) * (HD * 16) + piece * 16);
+        // piece = (HD/64) * ln + t: the t-th 16-byte chunk of lane group ln (v_word_idx)
+        constexpr int PPL = HD / 64;
+        const int chunk = (piece % PPL) * 64 + piece / PPL;
+        return *reinterpret_cast<const uint4 *>(vbase + (size_t)(base / 32 + b) * (HD * 16) + chunk * 16);
     };
     if constexpr (P::SPLIT) {
         // wave-uniform: the first KCH/64 waves take K pieces, the rest V pieces

@@ -127,7 +127,7 @@ __device__ inline void tile_of(const QkvArgs &a, int id, int &rt, int &ct, int &
 template <int HD>
 __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const float (*tile)[kTStr],
                                   int r0, int nr, int h, int col0, int wave, int lane) {
-    constexpr int NTD = HD / 16, LPR = HD / 8, RPW = 64 / LPR;  // rows per wave per pass
+    constexpr int LPR = HD / 8, RPW = 64 / LPR;  // rows per wave per pass
     const KvLayerView &L = a.L;
     const int r = lane / LPR, l = lane % LPR;
     for (int base = 0; base < nr; base += 4 * RPW) {
@@ -168,19 +168,19 @@ __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const floa
         uint32_t kw = 0;
 #pragma unroll
         for (int e = 0; e < 8; e++) kw |= kc[e] << (4 * e);
-        reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[l] = kw;
+        reinterpret_cast<uint32_t *>(L.kp + row * L.P * (HD / 2))[k_word_idx<HD>(p, l)] = kw;
         if (l == 0) {
             L.ks[row * L.P + p] = ks;
             L.vs[row * L.P + p] = vs;
         }
-        // V: dims 8l + e live in words (g*16 + dl)*NTD + td with d = 16 td + dl; position
+        // V: dims 8l + e live in words v_word_idx(g*16 + dl, td) with d = 16 td + dl; position
         // q = p % 32 is nibble (q % 4) + 4 (q / 16) of group g = (q % 16) / 4.
         const int q = p & 31, g = (q & 15) >> 2, n = (q & 3) + 4 * (q >> 4);
         uint32_t *vb = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / kBlk) + p / kBlk) * (HD * 16));
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int d = 8 * l + e, td = d >> 4, dl = d & 15;
-            uint32_t *dst = vb + (g * 16 + dl) * NTD + td;
+            uint32_t *dst = vb + v_word_idx(g * 16 + dl, td);
             *dst = (*dst & ~(0xFu << (4 * n))) | (vc[e] << (4 * n));
         }
     }

@@ -118,7 +118,7 @@ __device__ inline void row_codes(const float (&kx)[8], const float (&vx)[8], flo
 __device__ inline void store_block64(const KvLayerView &L, int s, int h, int blk, int lo, int hi,
                                      float (&kx)[8], const float (&vx)[8], const float2 (&cs)[4],
                                      int rot_pairs, int wave, int lane) {
-    constexpr int HD = 64, NTD = HD / 16;
+    constexpr int HD = 64;
     const int r8 = lane >> 3, l = lane & 7;
     const int p0 = blk * kBlk;
     const int p = p0 + 4 * wave + (r8 & 3) + 16 * (r8 >> 2);
@@ -142,7 +142,7 @@ __device__ inline void store_block64(const KvLayerView &L, int s, int h, int blk
         uint32_t kw = 0;
 #pragma unroll
         for (int e = 0; e < 8; e++) kw |= kc[e] << (4 * e);
-        reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[l] = kw;
+        reinterpret_cast<uint32_t *>(L.kp + row * L.P * (HD / 2))[k_word_idx<HD>(p, l)] = kw;
         if (l == 0) {
             L.ks[row * L.P + p] = ks;
             L.vs[row * L.P + p] = vs;
@@ -169,7 +169,7 @@ __device__ inline void store_block64(const KvLayerView &L, int s, int h, int blk
     const uint32_t w = r8 == 0 ? vpart[0] : r8 == 1 ? vpart[1] : r8 == 2 ? vpart[2] : r8 == 3 ? vpart[3]
                      : r8 == 4 ? vpart[4] : r8 == 5 ? vpart[5] : r8 == 6 ? vpart[6] : vpart[7];
     const int d = 8 * l + r8, td = d >> 4, dl = d & 15;
-    uint32_t *dst = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16)) + (wave * 16 + dl) * NTD + td;
+    uint32_t *dst = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16)) + v_word_idx(wave * 16 + dl, td);
     *dst = keep ? (*dst & keep) | (w & ~keep) : w;
 }
 
@@ -273,7 +273,7 @@ __device__ inline void store_block128(const KvLayerView &L, int s, int h, int bl
             vpart[e] |= vc[e] << (4 * r + 16 * rd);
         }
         if (in) {
-            reinterpret_cast<uint32_t *>(L.kp + (row * L.P + p) * (HD / 2))[l] = kw;
+            reinterpret_cast<uint32_t *>(L.kp + row * L.P * (HD / 2))[k_word_idx<HD>(p, l)] = kw;
             if (l == 0) {
                 L.ks[row * L.P + p] = ks;
                 L.vs[row * L.P + p] = vs;
@@ -304,7 +304,7 @@ __device__ inline void store_block128(const KvLayerView &L, int s, int h, int bl
                          : r == 2 ? (q ? vpart[5] : vpart[4])
                                   : (q ? vpart[7] : vpart[6]);
         const int d = 8 * l + e, td = d >> 4, dl = d & 15;
-        uint32_t *dst = vb + (wave * 16 + dl) * (HD / 16) + td;
+        uint32_t *dst = vb + v_word_idx(wave * 16 + dl, td);
         *dst = keep ? (*dst & keep) | (w & ~keep) : w;
     }
 }
