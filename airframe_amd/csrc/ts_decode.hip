@@ -85,20 +85,31 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t by
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// K word that lane group g feeds to the 16x16 QK instruction at k-step t (of the WPG words of
+// its row): the words the cache keeps together in one chunk for that row and group (the
+// chunk order of k_word_idx), so one load per row brings them all.
+template <int HD>
+__device__ inline int k16_word(int g, int t) {
+    if constexpr (HD == 128) return 8 * (t >> 1) + 2 * g + (t & 1);
+    else return 2 * g + t;
+}
+
 template <int HD>
 __device__ __forceinline__ void load_window(Window<HD> &w, const Streams &st, int base, int n,
                                             int g, int lane) {
     constexpr int WPG = HD / 32, NTD = HD / 16, ROWB = HD / 2;
-    // lane (n, g) takes words g*WPG.. of row 16 kt + n: segment (g*WPG)/4 of that row (the
-    // chunk order of ts_internal.h), at word (g*WPG)%4 of the chunk
-    const int koff = (((g * WPG) >> 2) * 64 + n) * 16 + ((g * WPG) & 3) * 4;
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
+        // row r = 16 kt + n of the window: words k16_word(g, 0..WPG-1) sit in chunk
+        // ((r % 4) / (128 / HD)) * 64 + 16 g + r / 4, at word (r % 2) * 2 for hd 64
+        const int r = 16 * kt + n;
         if constexpr (WPG == 4) {
-            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, koff + kt * 256, base * ROWB, 0);
+            const int koff = ((r & 3) * 64 + 16 * g + (r >> 2)) * 16;
+            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, koff, base * ROWB, 0);
             w.kw[kt][0] = t4[0]; w.kw[kt][1] = t4[1]; w.kw[kt][2] = t4[2]; w.kw[kt][3] = t4[3];
         } else {
-            const u32x2 t2 = __builtin_amdgcn_raw_buffer_load_b64(st.k, koff + kt * 256, base * ROWB, 0);
+            const int koff = (((r & 3) >> 1) * 64 + 16 * g + (r >> 2)) * 16 + 8 * (r & 1);
+            const u32x2 t2 = __builtin_amdgcn_raw_buffer_load_b64(st.k, koff, base * ROWB, 0);
             w.kw[kt][0] = t2[0]; w.kw[kt][1] = t2[1];
         }
     }
@@ -475,12 +486,12 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     {
         float qb = 0.0f;
 #pragma unroll
-        for (int t = 0; t < WPG; t++) qb = fmaxf(qb, q_bound8(qrow, WPG * g + t, QN, ns));
+        for (int t = 0; t < WPG; t++) qb = fmaxf(qb, q_bound8(qrow, k16_word<HD>(g, t), QN, ns));
         q_scale(wave_max(qb) * (a.inv_sqrt_hd * kLog2e), q_s, inv_s);
     }
     for (int t = wave; t < WPG; t += NW) {
         half8 qh, ql;
-        load_q8(a.rope, a.rope_pairs, qrow, WPG * g + t, qrot, a.inv_sqrt_hd * kLog2e * q_s, qh, ql,
+        load_q8(a.rope, a.rope_pairs, qrow, k16_word<HD>(g, t), qrot, a.inv_sqrt_hd * kLog2e * q_s, qh, ql,
                 QN, ns);
         sm.run.q.p[t][lane] = !live ? (half8)(_Float16)0.0f : (lo_col ? ql : qh);
     }
@@ -655,26 +666,30 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
 }
 
 
-// ---- G <= 4: QK^T on v_mfma_f32_4x4x4_16b_f16 -------------------------------------------------
+// ---- G <= 4: QK^T on v_mfma_i32_16x16x64_i8 ---------------------------------------------------
 //
-// The 16x16 tiles above leave 8 of 16 columns empty for G <= 4 and give each lane 16 scores,
-// most of them copies.  Here QK^T runs on the 16-block 4x4x4 matrix instruction: block b takes
-// positions 4b..4b+3 of the window (B operand: lane = position, its own K row), the A operand
-// (4 heads x 4 dims of q) is broadcast to all 16 blocks from block `abid`, so one q register
-// pair holds 16 k-steps.  The result leaves lane L with the scores of position base + L for
-// heads 0..3: softmax is 4 values per lane, with the lane's own scales.  p * s_v goes through
-// a per-wave LDS tile into the PV operand layout of the 16x16x32 instruction (as above).
+// QK^T runs in exact integer arithmetic.  The B operand is K^T: column n of tile t is position
+// 4n + t of the window, and lane 16 g + n supplies 16 dims of it as unsigned bytes -- the
+// nibbles of two K words, even dims from (w & 0x0F0F0F0F), odd dims from (w >> 4) & 0x0F0F0F0F,
+// 3 VALU ops per word.  The A operand holds q: row 4 h + c is base-128 digit c (c = 0 most
+// significant) of head h's q, rotated and scaled to an integer of at most 2^27, so the 16 rows
+// carry all 4 digits of all 4 heads.  The accumulators start at -8 * (sum of the row's digits),
+// which takes the nibble bias out exactly, and the products are summed exactly in i32.  Output
+// lane 16 h + n then holds the 4 digit sums of head h at position 4n + t; one f32 Horner step
+// per digit gives the score (one rounding).  Each lane runs the softmax of its head at its 4
+// positions; p * s_v goes through a per-wave LDS tile into the PV operand layout of the
+// 16x16x32 f16 instruction (as above).
 
 template <int HD>
-struct Window4 {
+struct Window8 {
     static constexpr int NKW = HD / 8, NTD = HD / 16;
-    uint32_t kw[NKW];     // K row of position base + lane
+    uint32_t kw[NKW];     // lane order q of k_word_idx: tile t, half m, word i at 2 (t HD/64 + m) + i
     uint32_t vw[2][NTD];  // V words, as Window
-    float sk, sv;         // scales of position base + lane
+    floatx4 sk, sv;       // scales of positions base + 4n .. base + 4n + 3 (n = lane % 16)
 };
 
-// Buffer resources of one split for the G <= 4 kernel: K, V and both scale arrays, each
-// bounded to the split's positions (loads past the bound return zeros and touch no memory).
+// Buffer resources of one split for the G <= 4 kernel: K, V and both scale arrays (loads past
+// the bound return zeros and touch no memory).
 struct Streams4 {
     __amdgpu_buffer_rsrc_t k, v, sk, sv;
 };
@@ -683,12 +698,12 @@ struct Streams4 {
 // and each instruction covers whole cache lines.
 constexpr int kNT = 2;
 
-// One window (64 positions from `base`, a multiple of 64): each instruction reads one
-// contiguous kilobyte.  K: chunk j*64 + lane of the window is segment j of the row of position
-// base + lane (words 4j..4j+3).  V: chunk q*64 + lane of each 32-position block holds words
-// 4q..4q+3 of lane group `lane`.  Scales: position base + lane.
+// One window (64 positions from `base`, a multiple of 64): each K and V instruction reads one
+// contiguous kilobyte (the cache's chunk order puts exactly this lane's operand words there);
+// the scale instructions read the window's 256 bytes, every 16 bytes by the 4 lanes of a
+// column.
 template <int HD>
-__device__ __forceinline__ void load_window4(Window4<HD> &w, const Streams4 &st, int base, int lane) {
+__device__ __forceinline__ void load_window8(Window8<HD> &w, const Streams4 &st, int base, int lane) {
     constexpr int NKW = HD / 8, NTD = HD / 16, ROWB = HD / 2;
 #pragma unroll
     for (int j = 0; j < NKW / 4; j++) {
@@ -704,39 +719,41 @@ __device__ __forceinline__ void load_window4(Window4<HD> &w, const Streams4 &st,
             w.vw[b][4 * q4 + 2] = t4[2]; w.vw[b][4 * q4 + 3] = t4[3];
         }
     }
-    w.sk = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(st.sk, lane * 4, base * 4, kNT));
-    w.sv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(st.sv, lane * 4, base * 4, kNT));
+    const int so = (lane & 15) * 16;
+    w.sk = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(st.sk, so, base * 4, kNT));
+    w.sv = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(st.sv, so, base * 4, kNT));
 }
-
-// Wave state: O^T accumulators (column n < 4: head n from the high parts of p*s_v, 4 <= n < 8:
-// head n - 4 from the low parts), per-head exponent reference (wave-uniform) and this lane's
-// share of the per-head softmax sums.
-template <int HD>
-struct WaveState4 {
-    floatx4 o[HD / 16];
-    float m[4], l[4];
-};
 
 template <int CTRL>
 __device__ inline float dpp_any(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-__device__ inline float wave_max_all(float v) {
-    v = fmaxf(v, dpp_any<0xB1>(v));
-    v = fmaxf(v, dpp_any<0x4E>(v));
-    v = fmaxf(v, dpp_any<0x141>(v));
-    v = fmaxf(v, dpp_any<0x140>(v));
-    return group_max(v);
+// Max / sum over the 16 lanes of a DPP row (every lane gets the result).
+__device__ inline float row_max16(float v) {
+    v = fmaxf(v, dpp_any<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_any<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_any<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_any<0x140>(v));  // row_mirror
+    return v;
 }
-__device__ inline float wave_sum_all(float v) {
+__device__ inline float row_sum16(float v) {
     v += dpp_any<0xB1>(v);
     v += dpp_any<0x4E>(v);
     v += dpp_any<0x141>(v);
     v += dpp_any<0x140>(v);
-    return group_sum(v);
+    return v;
 }
 
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Running state of one wave: O^T accumulators (column n < 4: head n from the high parts of
+// p*s_v, 4 <= n < 8: head n - 4 from the low parts), and for this lane's head (lane / 16) the
+// exponent reference (uniform over the lane's row) and its share of the softmax sum.
+template <int HD>
+struct WaveState8 {
+    floatx4 o[HD / 16];
+    float m, l;
+};
 
 // LDS slot of position `key` (0..63) of a window in the PV operand order: lane (n, g) of the
 // 16x16x32 B operand reads slots 32b + 8g .. +7 = positions 32b + 16t + 4g + r at 2r + t.
@@ -744,119 +761,114 @@ __device__ inline int p_slot(int key) {
     return 32 * (key >> 5) + 8 * ((key >> 2) & 3) + 2 * (key & 3) + ((key >> 4) & 1);
 }
 
-// The QK^T matrix instructions of one window: word U of the lane's K row gives k-steps 2U and
-// 2U + 1, broadcast operand block (k-step % 16) of q pair (k-step / 16).  The broadcast block
-// is an immediate, hence the compile-time recursion over words.
-template <int HD, int U>
-struct QkWords {
-    static __device__ __forceinline__ void run(const Window4<HD> &w, const half4_t (&qh)[HD / 64],
-                                               const half4_t (&ql)[HD / 64], floatx4 (&acc)[2],
-                                               const DeqConst &dc) {
-        const half8 kd = dequant8(w.kw[U], dc);
-        const half4_t k0 = {kd[0], kd[1], kd[2], kd[3]};
-        const half4_t k1 = {kd[4], kd[5], kd[6], kd[7]};
-        constexpr int T0 = 2 * U, T1 = 2 * U + 1;
-        acc[0] = __builtin_amdgcn_mfma_f32_4x4x4f16(qh[T0 / 16], k0, acc[0], 4, T0 % 16, 0);
-        acc[1] = __builtin_amdgcn_mfma_f32_4x4x4f16(ql[T0 / 16], k0, acc[1], 4, T0 % 16, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_4x4x4f16(qh[T1 / 16], k1, acc[0], 4, T1 % 16, 0);
-        acc[1] = __builtin_amdgcn_mfma_f32_4x4x4f16(ql[T1 / 16], k1, acc[1], 4, T1 % 16, 0);
-        QkWords<HD, U + 1>::run(w, qh, ql, acc, dc);
-    }
-};
-template <int HD>
-struct QkWords<HD, HD / 8> {
-    static __device__ __forceinline__ void run(const Window4<HD> &, const half4_t (&)[HD / 64],
-                                               const half4_t (&)[HD / 64], floatx4 (&)[2],
-                                               const DeqConst &) {}
-};
-
 template <int HD, bool SOFTCAP, bool TAIL>
-__device__ __forceinline__ void process_window4(const Window4<HD> &w, WaveState4<HD> &st,
-                                                const half4_t (&qh)[HD / 64], const half4_t (&ql)[HD / 64],
-                                                _Float16 (*pt)[64], int base, int end, int lane, int G,
-                                                float inv_s, float softcap, const DeqConst &dc) {
-    constexpr int NTD = HD / 16;
-    // ---- S = Q K^T --------------------------------------------------------------------------------
-    floatx4 acc[2] = {(floatx4)0.0f, (floatx4)0.0f};  // hi and lo parts of q
-    QkWords<HD, 0>::run(w, qh, ql, acc, dc);
-    const floatx4 sc = acc[0] + acc[1];
-    // ---- softmax on this lane's position for heads 0..3 ---------------------------------------
-    const float sk = w.sk * inv_s;  // undo the q operand scale (a power of two: exact)
-    float sv = w.sv;
-    float x[4];
+__device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8<HD> &st,
+                                                const i32x4 (&qa)[HD / 64], const i32x4 &bias,
+                                                float qinv, _Float16 (*pt)[64], int base, int end,
+                                                int lane, bool live, float softcap, const DeqConst &dc) {
+    constexpr int NTD = HD / 16, NM = HD / 64;
+    const int n = lane & 15, hg = lane >> 4;
+    // ---- S = Q K^T, exact -----------------------------------------------------------------
+    i32x4 acc[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float v = sc[i] * sk;
+    for (int t = 0; t < 4; t++) {
+        acc[t] = bias;
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const uint32_t w0 = w.kw[2 * (t * NM + m)], w1 = w.kw[2 * (t * NM + m) + 1];
+            const i32x4 kb = {(int)(w0 & 0x0F0F0F0Fu), (int)((w0 >> 4) & 0x0F0F0F0Fu),
+                              (int)(w1 & 0x0F0F0F0Fu), (int)((w1 >> 4) & 0x0F0F0F0Fu)};
+            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[m], kb, acc[t], 0, 0, 0);
+        }
+    }
+    // ---- softmax of head hg at positions base + 4n + t ------------------------------------
+    float x[4], sv[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        // digits 0..3 carry weights 2^21, 2^14, 2^7, 1; each digit sum is an exact integer
+        // below 2^18, so the first step is exact and the whole score rounds ~once.
+        float v = fmaf(fmaf(fmaf((float)acc[t][0], 128.0f, (float)acc[t][1]), 128.0f, (float)acc[t][2]), 128.0f,
+                       (float)acc[t][3]);
+        v *= qinv * w.sk[t];
         if constexpr (SOFTCAP) v = tanhf(v * (1.0f / kLog2e) / softcap) * softcap * kLog2e;
-        x[i] = v;
+        x[t] = v;
+        sv[t] = w.sv[t];
     }
     if constexpr (TAIL) {
-        if (base + lane >= end) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) x[i] = -INFINITY;
-            sv = 0.0f;
+        for (int t = 0; t < 4; t++) {
+            if (base + 4 * n + t >= end) {
+                x[t] = -INFINITY;
+                sv[t] = 0.0f;
+            }
         }
     }
     // P = 2^(x - m) * s_v must stay <= 2^8 (f16 range for its two parts, with room).  The
-    // per-head reference m moves only when some position of the window breaks that: a ballot
-    // in the common case, wave reductions only then (to m = max(x) + log2(max s_v), P <= 1).
+    // reference m of a head moves only when some position of the window breaks that: a ballot
+    // in the common case, row reductions only then (to m = max(x) + log2(max s_v), P <= 1).
     float p[4], pv[4];
     bool need = false;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        p[i] = i < G ? fast_exp2(x[i] - st.m[i]) : 0.0f;
-        pv[i] = p[i] * sv;
-        need |= !(pv[i] <= 256.0f);
+    for (int t = 0; t < 4; t++) {
+        p[t] = live ? fast_exp2(x[t] - st.m) : 0.0f;
+        pv[t] = p[t] * sv[t];
+        need |= !(pv[t] <= 256.0f);
     }
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
         asm volatile("" ::: "memory");  // keep this a branch: the rescale is the rare case
-        const float svl = __builtin_amdgcn_logf(wave_max_all(sv));
-        float al[4];
+        const float svl = __builtin_amdgcn_logf(row_max16(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))));
+        const float xm = row_max16(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+        const float mw = fminf(fmaxf(xm + svl, xm - 64.0f), xm + 64.0f);
+        const float m_new = fmaxf(st.m, mw);
+        const float al = fast_exp2(st.m - m_new);
+        st.l *= al;
+        st.m = m_new;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float xm = wave_max_all(x[i]);
-            const float mw = fminf(fmaxf(xm + svl, xm - 64.0f), xm + 64.0f);
-            const float m_new = fmaxf(st.m[i], mw);
-            al[i] = fast_exp2(st.m[i] - m_new);
-            st.l[i] *= al[i];
-            st.m[i] = m_new;
-            p[i] = i < G ? fast_exp2(x[i] - st.m[i]) : 0.0f;
-            pv[i] = p[i] * sv;
+        for (int t = 0; t < 4; t++) {
+            p[t] = live ? fast_exp2(x[t] - st.m) : 0.0f;
+            pv[t] = p[t] * sv[t];
         }
-        const int n = lane & 3;
-        const float a = n == 0 ? al[0] : n == 1 ? al[1] : n == 2 ? al[2] : al[3];
+        // the O^T column of head c (c and c + 4) takes the factor of row c
+        const float f0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 0));
+        const float f1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 16));
+        const float f2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 32));
+        const float f3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 48));
+        const int c = lane & 3;
+        const float f = c == 0 ? f0 : c == 1 ? f1 : c == 2 ? f2 : f3;
 #pragma unroll
-        for (int td = 0; td < NTD; td++) st.o[td] *= a;
+        for (int td = 0; td < NTD; td++) st.o[td] *= f;
     }
-    const int slot = p_slot(lane);
+    st.l += (p[0] + p[1]) + (p[2] + p[3]);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        st.l[i] += p[i];
-        const float hi = split_hi(pv[i]);
-        pt[i][slot] = (_Float16)hi;
-        pt[4 + i][slot] = (_Float16)(pv[i] - hi);
+    for (int t = 0; t < 4; t++) {
+        const int slot = p_slot(4 * n + t);
+        const float hi = split_hi(pv[t]);
+        pt[hg][slot] = (_Float16)hi;
+        pt[4 + hg][slot] = (_Float16)(pv[t] - hi);
     }
     // ---- O^T += V^T P^T (the wave's own LDS writes are ordered before its reads) -------------
-    const int n = lane & 15, g = lane >> 4;
+    const int g = lane >> 4;
 #pragma unroll
     for (int b = 0; b < 2; b++) {
         // columns 8..15 read real p values: their outputs are never used
         const half8 pb = *reinterpret_cast<const half8 *>(&pt[n & 7][32 * b + 8 * g]);
+        // every word of the block dequantized into its own registers first, so the conversions
+        // of later words overlap the matrix instructions of earlier ones
+        half8 va[NTD];
 #pragma unroll
-        for (int td = 0; td < NTD; td++) {
-            const half8 va = dequant8(w.vw[b][td], dc);
-            st.o[td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, st.o[td], 0, 0, 0);
-        }
+        for (int td = 0; td < NTD; td++) va[td] = dequant8(w.vw[b][td], dc);
+#pragma unroll
+        for (int td = 0; td < NTD; td++)
+            st.o[td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[td], pb, st.o[td], 0, 0, 0);
     }
 }
 
 // NW waves per workgroup, D windows in registers per wave (D - 1 in flight while one is
-// computed).  The plan places one workgroup of 4 waves per CU (one wave per SIMD).  Measured
-// on config 3 (ms per step): D = 2 1.915, D = 3 1.951; 8 waves with D = 2 2.05.
+// computed).  The plan places one workgroup of 4 waves per CU (one wave per SIMD).
 template <int HD, bool SOFTCAP, bool NORM, int NW, int D>
 __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeArgs a) {
     constexpr int NTD = HD / 16;
-    constexpr int NQ = HD / 64;  // q register pairs (16 k-steps each)
+    constexpr int NM = HD / 64;  // i8 instructions per 16-position tile
     constexpr int OST = HD + 1;
     const KvLayerView &L = a.L;
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
@@ -885,15 +897,19 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     };
     __shared__ Smem sm;
     __shared__ float kd[HD], vd[HD], xnew[8];
+    __shared__ int32_t qsum[NW][16];  // per wave: digit sums of the 16 q rows
+    __shared__ float qinv_s[NW][4];   // per wave: 2^-e of each head's q integer scale
 
     const size_t row = (size_t)s * L.H + h;
     constexpr int ROWB = HD / 2;
     Streams4 str;
-    // K rows are cut into segments spread over their 64-position window: bound at the window
-    str.k = make_rsrc(L.kp + row * L.P * ROWB, (uint32_t)((end + 63) & ~63) * ROWB);
+    // K and the scales are bounded at the window: a window's K chunks mix its rows, and a
+    // scale load covers 4 positions
+    const uint32_t wend = (uint32_t)((end + 63) & ~63);
+    str.k = make_rsrc(L.kp + row * L.P * ROWB, wend * ROWB);
     str.v = make_rsrc(L.vp + row * (L.P / 32) * (HD * 16), (uint32_t)((end + 31) / 32) * (HD * 16));
-    str.sk = make_rsrc(L.ks + row * L.P, (uint32_t)end * 4);
-    str.sv = make_rsrc(L.vs + row * L.P, (uint32_t)end * 4);
+    str.sk = make_rsrc(L.ks + row * L.P, wend * 4);
+    str.sv = make_rsrc(L.vs + row * L.P, wend * 4);
 
     // This wave's windows: w = wave, wave + NW, ... below nwin, taken in rotated order starting
     // at a per-workgroup offset, so that the workgroups streaming at the same time read
@@ -909,33 +925,45 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         r = r >= cnt ? r - cnt : r;
         return start + 64 * (wave + NW * r);
     };
-    Window4<HD> w[D];
+    Window8<HD> w[D];
 
-    // q operands: lane 4 blk + i holds head i (zero past G) for k-step 16 c + blk of pair c; a
-    // k-step is half of a dequantized word's slots: word t/2, slots 4 (t%2) .. +3.  The raw q
-    // loads go out before the windows' prefetch: loads complete in order, so consuming q then
-    // does not wait for the windows.
-    half4_t qh[NQ], ql[NQ];
-    float q_s, inv_s;
+    // q operand: lane 16 g + n holds row n = 4 hh + c (digit c of head hh) for k-group g, i.e.
+    // dims 64 m + 16 g .. + 15 of instruction m, bytes [even dims of word 8m + 2g, its odd
+    // dims, even dims of word 8m + 2g + 1, its odd dims] like the K operand.  The raw q loads
+    // go out before the windows' prefetch: loads complete in order, so consuming q then does
+    // not wait for the windows.
+    i32x4 qa[NM], bias;
+    float qinv;
     const bool appender = fused && wave == NW - 1;
     AppendIn ain;
     float2 qp[4];
     {
-        const int blk = lane >> 2, i = lane & 3;
-        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (i < G ? i : 0)) * HD;
-        float qx[NQ][8], nwv[NQ][8];
-        float2 qcs[NQ][4];
+        const int n = lane & 15, g = lane >> 4, hh = n >> 2, dg = n & 3;
+        const bool hl = hh < G;
+        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (hl ? hh : 0)) * HD;
+        float qx[NM][16], nwv[NM][16];
+        float2 qcs[NM][8];
 #pragma unroll
-        for (int c = 0; c < NQ; c++) {
-            const int u = (16 * c + blk) >> 1;
-            q_read8(qrow, u, nullptr, 1.0f, qx[c]);
-            load_rot8(a.rope, a.rope_pairs, u, qrot, qcs[c]);
-            if (QN) {
+        for (int m = 0; m < NM; m++) {
+            const int d0 = 64 * m + 16 * g;
 #pragma unroll
-                for (int e = 0; e < 8; e++) nwv[c][e] = QN[8 * u + e];
+            for (int e4 = 0; e4 < 4; e4++) {
+                const float4 v4 = *reinterpret_cast<const float4 *>(qrow + d0 + 4 * e4);
+                qx[m][4 * e4] = v4.x; qx[m][4 * e4 + 1] = v4.y; qx[m][4 * e4 + 2] = v4.z; qx[m][4 * e4 + 3] = v4.w;
+                if (QN) {
+                    const float4 n4 = *reinterpret_cast<const float4 *>(QN + d0 + 4 * e4);
+                    nwv[m][4 * e4] = n4.x; nwv[m][4 * e4 + 1] = n4.y; nwv[m][4 * e4 + 2] = n4.z; nwv[m][4 * e4 + 3] = n4.w;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int pair = d0 / 2 + i;
+                qcs[m][i] = pair < a.rope_pairs
+                                ? *reinterpret_cast<const float2 *>(a.rope + ((size_t)qrot * a.rope_pairs + pair) * 2)
+                                : make_float2(1.0f, 0.0f);
             }
         }
-        const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, i < G ? i : 0,
+        const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, hl ? hh : 0,
                                                     L.norm_eps)
                             : 1.0f;
         // The appending wave (the last: it has the fewest windows) quantizes the new token and
@@ -948,47 +976,77 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int d = 0; d < D - 1; d++) load_window4<HD>(w[d], str, win_base(d), lane);
+        for (int d = 0; d < D - 1; d++) load_window8<HD>(w[d], str, win_base(d), lane);
         __builtin_amdgcn_sched_barrier(0);
-        float qb = 0.0f;
+        // rotated q times log2(e)/sqrt(hd) (rope.rs:186-196 after the optional QK norm)
+        float qm = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NQ; c++) {
-            if (QN) {
+        for (int m = 0; m < NM; m++) {
+#pragma clang fp contract(off)
 #pragma unroll
-                for (int e = 0; e < 8; e++) qx[c][e] = qk_norm_apply(qx[c][e], ns, nwv[c][e]);
+            for (int i = 0; i < 8; i++) {
+                float x0 = qx[m][2 * i], x1 = qx[m][2 * i + 1];
+                if (QN) {
+                    x0 = qk_norm_apply(x0, ns, nwv[m][2 * i]);
+                    x1 = qk_norm_apply(x1, ns, nwv[m][2 * i + 1]);
+                }
+                if ((64 * m + 16 * g) / 2 + i < a.rope_pairs) rope_rotate(x0, x1, qcs[m][i]);
+                qx[m][2 * i] = x0 * (a.inv_sqrt_hd * kLog2e);
+                qx[m][2 * i + 1] = x1 * (a.inv_sqrt_hd * kLog2e);
+                qm = fmaxf(qm, fmaxf(fabsf(qx[m][2 * i]), fabsf(qx[m][2 * i + 1])));
             }
-            qb = fmaxf(qb, fmaxf(fmaxf(fabsf(qx[c][0]) + fabsf(qx[c][1]), fabsf(qx[c][2]) + fabsf(qx[c][3])),
-                                 fmaxf(fabsf(qx[c][4]) + fabsf(qx[c][5]), fabsf(qx[c][6]) + fabsf(qx[c][7]))));
         }
-        q_scale(wave_max_all(qb) * (a.inv_sqrt_hd * kLog2e), q_s, inv_s);
+        // head hh's integer scale 2^e: max |q| 2^e in [2^26, 2^27), so every digit fits int8
+        qm = group_max(qm);
+        int e = 0;
+        if (qm > 0.0f && qm < 3.0e38f) e = 26 - min(max(ilogbf(qm), -100), 100);
+        const float sc = ldexpf(1.0f, e);
+        // digits: Q = d0 2^21 + d1 2^14 + d2 2^7 + d3, d1..d3 in [-64, 63], |d0| <= 64
+        int dsum = 0;
 #pragma unroll
-        for (int c = 0; c < NQ; c++) {
-            const int t = 16 * c + blk;
-            half8 hh8, ll8;
-            split_q8(qx[c], qcs[c], t >> 1, a.rope_pairs, a.inv_sqrt_hd * kLog2e * q_s, hh8, ll8);
-            const int o4 = 4 * (t & 1);
-            half4_t hv = {hh8[o4], hh8[o4 + 1], hh8[o4 + 2], hh8[o4 + 3]};
-            half4_t lv = {ll8[o4], ll8[o4 + 1], ll8[o4 + 2], ll8[o4 + 3]};
-            qh[c] = i < G ? hv : (half4_t)(_Float16)0.0f;
-            ql[c] = i < G ? lv : (half4_t)(_Float16)0.0f;
+        for (int m = 0; m < NM; m++) {
+            uint32_t reg[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int el = 0; el < 16; el++) {
+                int Q = hl ? (int)rintf(qx[m][el] * sc) : 0;
+                int dig = 0;
+#pragma unroll
+                for (int k = 3; k >= 0; k--) {
+                    const int d = k == 0 ? Q : ((Q + 64) & 127) - 64;
+                    if (k == dg) dig = d;
+                    Q = (Q - d) >> 7;
+                }
+                dsum += dig;
+                // element el = dim 64 m + 16 g + el: word 8m + 2g + el / 8, parity el % 2 selects
+                // the even (reg 0 / 2) or odd (reg 1 / 3) register, byte (el % 8) / 2
+                const int rr = 2 * (el >> 3) + (el & 1), by = (el & 7) >> 1;
+                reg[rr] |= (uint32_t)(dig & 0xFF) << (8 * by);
+            }
+            qa[m] = (i32x4){(int)reg[0], (int)reg[1], (int)reg[2], (int)reg[3]};
         }
+        // bias of accumulator (head hg, digit r): -8 * (digit sum of row 4 hg + r)
+        dsum += __shfl_xor(dsum, 16, 64);
+        dsum += __shfl_xor(dsum, 32, 64);
+        if (g == 0) qsum[wave][n] = dsum;
+        if (g == 0 && dg == 0) qinv_s[wave][hh] = ldexpf(1.0f, -e);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+        const int hg = lane >> 4;
+        bias = (i32x4){-8 * qsum[wave][4 * hg], -8 * qsum[wave][4 * hg + 1], -8 * qsum[wave][4 * hg + 2],
+                       -8 * qsum[wave][4 * hg + 3]};
+        qinv = qinv_s[wave][hg];
     }
     if (appender) {
         append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd);
         new_token_scores<HD, SOFTCAP, NORM, 4>(a, s, h, G, lane, qp, ain.cs, kd, xnew);
     }
-    // The appending wave (the last: it has the fewest windows) quantizes the new token and
-    // scores it against every head before its windows; the others start at once.  kd, vd and
-    // xnew are read after the barrier that opens the merge.
 
-    WaveState4<HD> st;
+    WaveState8<HD> st;
 #pragma unroll
     for (int td = 0; td < NTD; td++) st.o[td] = (floatx4)0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        st.m[i] = kMinit;
-        st.l[i] = 0.0f;
-    }
+    st.m = kMinit;
+    st.l = 0.0f;
+    const bool live = (lane >> 4) < G;
     _Float16 (*pt)[64] = sm.pt[wave];
 
     int it = 0;
@@ -996,15 +1054,15 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         while (true) {
 #pragma unroll
             for (int d = 0; d < D; d++) {
-                load_window4<HD>(w[(d + D - 1) % D], str, win_base(it + D - 1), lane);
+                load_window8<HD>(w[(d + D - 1) % D], str, win_base(it + D - 1), lane);
                 // keep the prefetch here: the scheduler would otherwise sink it below the use
                 asm volatile("" ::: "memory");
                 __builtin_amdgcn_sched_barrier(0);
                 const int base = win_base(it);
                 if (base + 64 <= end)
-                    process_window4<HD, SOFTCAP, false>(w[d], st, qh, ql, pt, base, end, lane, G, inv_s, a.softcap, dc);
+                    process_window8<HD, SOFTCAP, false>(w[d], st, qa, bias, qinv, pt, base, end, lane, live, a.softcap, dc);
                 else
-                    process_window4<HD, SOFTCAP, true>(w[d], st, qh, ql, pt, base, end, lane, G, inv_s, a.softcap, dc);
+                    process_window8<HD, SOFTCAP, true>(w[d], st, qa, bias, qinv, pt, base, end, lane, live, a.softcap, dc);
                 if (++it >= cnt) goto windows_done;
             }
         }
@@ -1012,15 +1070,12 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
 windows_done:
 
     // ---- merge the waves through LDS ------------------------------------------------------------
-    float l_run[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) l_run[i] = wave_sum_all(st.l[i]);
+    const float l_run = row_sum16(st.l);
     __syncthreads();  // all waves are done with their P tiles
     const int n = lane & 15, g = lane >> 4;
-    if (lane < 4) {
-        const int i = lane;
-        sm.merge.m[wave][i] = i == 0 ? st.m[0] : i == 1 ? st.m[1] : i == 2 ? st.m[2] : st.m[3];
-        sm.merge.l[wave][i] = i == 0 ? l_run[0] : i == 1 ? l_run[1] : i == 2 ? l_run[2] : l_run[3];
+    if (n == 0 && g < 4) {
+        sm.merge.m[wave][g] = st.m;
+        sm.merge.l[wave][g] = l_run;
     }
     if (n < 8) {
 #pragma unroll

@@ -4,10 +4,13 @@
 //
 //   K packed  [S][H][P/64][hd*32 bytes]        64-position windows.  Position p's row is the
 //                                              reference's per-(pos, head) row (word u holds
-//                                              dims 8u..8u+7, dim 8u+n in bits 4n..4n+3), cut
-//                                              into 16-byte segments j = u/4; segment j of
-//                                              window row r = p % 64 sits at 16-byte chunk
-//                                              j*64 + r of the window (k_word_idx)
+//                                              dims 8u..8u+7, dim 8u+n in bits 4n..4n+3).  In
+//                                              a window, row r = 4n + t (n < 16, t < 4) gives
+//                                              lane L = 16 g + n the words 8m + 2g + i
+//                                              (m < hd/64, i < 2) in lane order
+//                                              q = (t*(hd/64) + m)*2 + i, and lane L's word q
+//                                              sits at word 4 (64 (q/4) + L) + q%4 of the
+//                                              window (k_word_idx)
 //   V packed  [S][H][P/32][hd*16 bytes]        32-position blocks, "position-packed": word
 //                                              (g, dl, td) of a block holds dim 16*td+dl at 8
 //                                              positions (nibble n<4 -> position 4g+n, nibble
@@ -18,10 +21,11 @@
 //   V scale   [S][H][P] f32
 //
 // Each (sequence, kv head) is one contiguous stream per buffer.  The chunk orders make every
-// 16-byte load instruction of a decode wave read one contiguous kilobyte while lane r still
-// receives exactly the data it feeds to the matrix cores: segment j of its own K row, and the
-// words of its own V lane group.  Every V word is the 8 positions one lane feeds to one
-// v_mfma_f32_16x16x32_f16.
+// 16-byte load instruction of a decode wave read one contiguous kilobyte while each lane still
+// receives exactly the data it feeds to the matrix cores: in K, the 16-dim slices (two words)
+// that lane 16 g + n supplies to v_mfma_i32_16x16x64_i8 as column n (positions 4n + t) and
+// k-group g; in V, the words of its own lane group.  Every V word is the 8 positions one lane
+// feeds to one v_mfma_f32_16x16x32_f16.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -39,7 +43,10 @@ constexpr int kPosAlign = 64;  // P is a multiple of this (one decode window)
 // stream (the layout above).
 template <int HD>
 __host__ __device__ inline size_t k_word_idx(int p, int u) {
-    return (size_t)(p >> 6) * (HD * 8) + (size_t)((((u >> 2) << 6) + (p & 63)) << 2) + (u & 3);
+    const int r = p & 63, n = r >> 2, t = r & 3;
+    const int g = (u & 7) >> 1, m = u >> 3, i = u & 1;
+    const int q = ((t * (HD / 64) + m) << 1) + i;
+    return (size_t)(p >> 6) * (HD * 8) + (size_t)((((q >> 2) << 6) + 16 * g + n) << 2) + (q & 3);
 }
 
 // Word index of V word (lane group ln = 16 g + dl, tile td) inside its 32-position block.

@@ -91,14 +91,32 @@ __device__ inline int qk_row_key(int R) {
 
 // Which 16-byte piece of the window a staging thread owns.  The maps are chosen so that 16
 // consecutive lanes write 16 different LDS bank groups:
-//  K piece c: key (c & 15) + 16 * (c / (16 * PPR)), part (c >> 4) % PPR of the key's row;
+//  K piece c: chunk k_chunk(c) of the window (the cache's K chunk order, k_word_idx), whose
+//  word j is word u of key `key` (k_piece_word); 16 consecutive pieces hold 16 consecutive
+//  keys;
 //  V piece c: block c / HD, and within it lane group L = c % 64 of the packed layout, its
 //  (HD/64)-th piece (c % HD) / 64.
 template <int HD>
-__device__ inline void k_piece(int c, int &key, int &part) {
-    constexpr int PPR = HD / 32;  // 16-byte pieces per K row
-    key = (c & 15) + 16 * (c / (16 * PPR));
-    part = (c >> 4) % PPR;
+__device__ inline int k_chunk(int c) {
+    if constexpr (HD == 128) {
+        const int t = c & 3, n = ((c >> 2) & 3) + 4 * ((c >> 4) & 3), g = (c >> 6) & 3;
+        return t * 64 + 16 * g + n;
+    } else {
+        const int qc = c & 1, n = (c >> 1) & 15, g = (c >> 5) & 3;
+        return qc * 64 + 16 * g + n;
+    }
+}
+template <int HD>
+__device__ inline void k_piece_word(int c, int j, int &key, int &u) {
+    if constexpr (HD == 128) {
+        const int t = c & 3, n = ((c >> 2) & 3) + 4 * ((c >> 4) & 3), g = (c >> 6) & 3;
+        key = 4 * n + t;
+        u = 8 * (j >> 1) + 2 * g + (j & 1);
+    } else {
+        const int qc = c & 1, n = (c >> 1) & 15, g = (c >> 5) & 3;
+        key = 4 * n + 2 * qc + (j >> 1);
+        u = 2 * g + (j & 1);
+    }
 }
 template <int HD>
 __device__ inline void v_piece(int cv, int &b, int &piece) {
@@ -113,10 +131,7 @@ __device__ inline void fetch_window(Pending<HD, NW> &pd, const uint8_t *kbase, c
     using P = Pending<HD, NW>;
     constexpr int ROWB = HD / 2;
     auto load_k = [&](int c) {
-        int key, part;
-        k_piece<HD>(c, key, part);
-        // segment `part` of row `key` of the 64-position window at base (k_word_idx)
-        return *reinterpret_cast<const uint4 *>(kbase + (size_t)base * ROWB + (part * 64 + key) * 16);
+        return *reinterpret_cast<const uint4 *>(kbase + (size_t)base * ROWB + k_chunk<HD>(c) * 16);
     };
     auto load_v = [&](int c) {
         int b, piece;
@@ -157,9 +172,9 @@ __device__ inline void stage_part(PrefillLds<HD> &sm, int buf, const Pending<HD,
     if (part < 4 * P::NK) {
         const uint4 &x = pd.k[i];
         const uint32_t wj = j == 0 ? x.x : j == 1 ? x.y : j == 2 ? x.z : x.w;
-        int key, kpart;
-        k_piece<HD>(c, key, kpart);
-        sm.k[buf][key][k_slot<HD>(key, 4 * kpart + j)] = dequant8_c(wj);
+        int key, u;
+        k_piece_word<HD>(c, j, key, u);
+        sm.k[buf][key][k_slot<HD>(key, u)] = dequant8_c(wj);
     } else {
         // V: lane L holds 4 words of packed lane group ln = L (key group g = ln/16, dim row dl
         // = ln%16); lane L^16 holds the same words of key group g^1.  Words of groups 2p and
@@ -192,10 +207,12 @@ __device__ inline void stage_codes(PrefillLds<HD> &sm, int buf, const Pending<HD
         // V staging as in stage_part, for a thread that holds one V piece
         auto put_k = [&](int c, const uint4 &x) {
             const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-            int key, part;
-            k_piece<HD>(c, key, part);
 #pragma unroll
-            for (int j = 0; j < 4; j++) sm.k[buf][key][k_slot<HD>(key, 4 * part + j)] = dequant8_c(w[j]);
+            for (int j = 0; j < 4; j++) {
+                int key, u;
+                k_piece_word<HD>(c, j, key, u);
+                sm.k[buf][key][k_slot<HD>(key, u)] = dequant8_c(w[j]);
+            }
         };
         auto put_v = [&](int c, const uint4 &x) {
             const uint32_t w[4] = {x.x, x.y, x.z, x.w};
