@@ -46,6 +46,7 @@ SIGNATURES = {
     "ts_kv_increment": (ctypes.c_int, [_vp, _i32, _vp]),
     "ts_kv_set_seq_len": (ctypes.c_int, [_vp, _i32, _i32, _vp]),
     "ts_kv_reset": (ctypes.c_int, [_vp, _vp]),
+    "ts_kv_reset_seq": (ctypes.c_int, [_vp, _i32, _vp]),
     "ts_kv_export": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "ts_kv_set_qk_norm": (ctypes.c_int, [_vp, _i32, _vp, _vp, _f]),
     "ts_kv_window_base": (ctypes.c_int, [_vp, _i32, _i32p]),

@@ -241,6 +241,19 @@ int ts_kv_reset(ts_kv *kv, void *stream) {
     return TS_OK;
 }
 
+int ts_kv_reset_seq(ts_kv *kv, int32_t seq, void *stream) {
+    if (!kv || seq < 0 || seq >= kv->d.n_seq) return TS_ERR_INVALID;
+    hipStream_t st = as_stream(stream);
+    hipError_t e = ts::launch_len_update(kv->d_len, kv->d.n_seq, seq, 0, 1, st);
+    if (e == hipSuccess) e = ts::launch_len_update(kv->d_rot, kv->d.n_seq, seq, 0, 1, st);
+    if (e == hipSuccess) e = ts::launch_len_update(kv->d_sink, kv->d.n_seq, seq, 0, 1, st);
+    if (e != hipSuccess) return TS_ERR_HIP;
+    kv->h_len[seq] = 0;
+    kv->h_rot[seq] = 0;
+    kv->h_sink[seq] = 0;
+    return TS_OK;
+}
+
 int ts_kv_set_qk_norm(ts_kv *kv, int32_t layer, const float *d_q_norm, const float *d_k_norm,
                       float eps) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers || !(eps >= 0.0f) || !(eps < 1e30f) ||
@@ -284,6 +297,15 @@ int ts_kv_shift(ts_kv *kv, int32_t layer, int32_t seq, int32_t keep_sink, int32_
     // rotation of its own position
     if ((kv->h_sink[seq] != 0 || kv->h_rot[seq] != 0) && kv->h_sink[seq] != keep_sink)
         return TS_ERR_INVALID;
+    hipStream_t st = as_stream(stream);
+    // The first call records the sink count, also when nothing moves, so that a caller who
+    // advances the window base after every shift (as the reference's caller does) keeps the
+    // sinks at their own rotation.
+    if (kv->h_sink[seq] != keep_sink) {
+        hipError_t e = ts::launch_len_update(kv->d_sink, kv->d.n_seq, seq, keep_sink, 1, st);
+        if (e != hipSuccess) return TS_ERR_HIP;
+        kv->h_sink[seq] = keep_sink;
+    }
     const int64_t n_move = (int64_t)kv->h_len[seq] - keep_sink - shift_amt;
     if (n_move <= 0 || shift_amt == 0) return TS_OK;  // elements_to_shift == 0: nothing moves
     const uint64_t wpp = (uint64_t)kv->d.n_head_kv * (kv->d.head_dim / 8);  // words per position
@@ -292,14 +314,9 @@ int ts_kv_shift(ts_kv *kv, int32_t layer, int32_t seq, int32_t keep_sink, int32_
     if (!aligned16(d_workspace)) return TS_ERR_INVALID;
     uint32_t *kp = (uint32_t *)d_workspace, *vp = kp + n_move * wpp;
     float *ks = (float *)(vp + n_move * wpp), *vs = ks + n_move * kv->d.n_head_kv;
-    hipStream_t st = as_stream(stream);
     const ts::KvLayerView L = kv->layer(layer);
     hipError_t e = ts::launch_export(L, seq, keep_sink + shift_amt, (int)n_move, kp, vp, ks, vs, st);
     if (e == hipSuccess) e = ts::launch_import(L, seq, keep_sink, (int)n_move, kp, vp, ks, vs, st);
-    if (e == hipSuccess && kv->h_sink[seq] != keep_sink) {
-        e = ts::launch_len_update(kv->d_sink, kv->d.n_seq, seq, keep_sink, 1, st);
-        if (e == hipSuccess) kv->h_sink[seq] = keep_sink;
-    }
     return hip_status(e);
 }
 
@@ -355,7 +372,11 @@ int ts_requant_all(ts_kv *kv, int32_t layer, const float *d_k_cache, const float
     }
     if (seq_len == 0) return TS_OK;
     int32_t blocks = (seq_len + 31) / 32;
-    return hip_status(ts::launch_quantize_rows(kv->layer(layer), d_k_cache, d_v_cache, nullptr, 0,
+    // K is taken as given: the reference normalizes its f32 cache before requantizing, so the
+    // layer's QK norm is not applied again
+    ts::KvLayerView L = kv->layer(layer);
+    L.qn = L.kn = nullptr;
+    return hip_status(ts::launch_quantize_rows(L, d_k_cache, d_v_cache, nullptr, 0,
                                                seq_len, ld_pos, rope ? rope->d_table : nullptr,
                                                rope ? rope->rope_dim / 2 : 0, blocks,
                                                as_stream(stream)));

@@ -116,8 +116,13 @@ class KVCache:
     def set_seq_len(self, new_len: int, seq: int = 0, stream=None):
         check("ts_kv_set_seq_len", load().ts_kv_set_seq_len(self._h, seq, new_len, _stream(stream)))
 
-    def reset(self, stream=None):
-        check("ts_kv_reset", load().ts_kv_reset(self._h, _stream(stream)))
+    def reset(self, seq: int | None = None, stream=None):
+        """KVCache::reset (kv_cache.rs:256-259): length, window base and sink count to 0, for
+        every sequence or only `seq`."""
+        if seq is None:
+            check("ts_kv_reset", load().ts_kv_reset(self._h, _stream(stream)))
+        else:
+            check("ts_kv_reset_seq", load().ts_kv_reset_seq(self._h, seq, _stream(stream)))
 
     # ---- QK norm (Qwen3: attention.rs:92-108 before RoPE, :186-189) ----------------------
 
@@ -216,8 +221,7 @@ class KVCache:
         n_head = q.shape[1]
         if q.dim() != 3 or q.shape[0] != self.n_seq or q.shape[2] != self.head_dim:
             raise ValueError("q must be [n_seq, n_head, head_dim]")
-        if out is None:
-            out = torch.empty_like(q)
+        out = self._out_like(q, out)
         ws = workspace if workspace is not None else self.workspace(n_head)
         check("ts_attn_decode",
               load().ts_attn_decode(self._h, layer, _ptr(q, torch.float32, "q"), n_head,
@@ -236,8 +240,7 @@ class KVCache:
             raise ValueError("q must be [n_seq, n_head, head_dim]")
         self._check_kv(k.reshape(self.n_seq, 1, self.n_head_kv, self.head_dim),
                        v.reshape(self.n_seq, 1, self.n_head_kv, self.head_dim), 1)
-        if out is None:
-            out = torch.empty_like(q)
+        out = self._out_like(q, out)
         ws = workspace if workspace is not None else self.workspace(n_head)
         check("ts_attn_decode_append",
               load().ts_attn_decode_append(self._h, layer, _ptr(k, torch.float32, "k"),
@@ -253,8 +256,7 @@ class KVCache:
         """Chunked-prefill causal attention.  q: [n_seq, n_tok, n_head, head_dim]."""
         if q.dim() != 4 or q.shape[0] != self.n_seq or q.shape[3] != self.head_dim:
             raise ValueError("q must be [n_seq, n_tok, n_head, head_dim]")
-        if out is None:
-            out = torch.empty_like(q)
+        out = self._out_like(q, out)
         check("ts_attn_prefill",
               load().ts_attn_prefill(self._h, layer, _ptr(q, torch.float32, "q"), q.shape[2],
                                      q.shape[1], rope.handle, softcap,
@@ -299,9 +301,11 @@ class KVCache:
         if (wq.shape != (n_head * self.head_dim, dim) or wk.shape != (kv_rows, dim)
                 or wv.shape != (kv_rows, dim)):
             raise ValueError("wq must be [n_head*head_dim, dim], wk/wv [n_head_kv*head_dim, dim]")
+        want = (self.n_seq, n_tok, n_head, self.head_dim)
         if q_out is None:
-            q_out = torch.empty((self.n_seq, n_tok, n_head, self.head_dim), dtype=torch.float32,
-                                device=x.device)
+            q_out = torch.empty(want, dtype=torch.float32, device=x.device)
+        elif tuple(q_out.shape) != want:
+            raise ValueError(f"q_out must be {want}")
         kp = vp = None
         if kv_out is not None:
             k_out, v_out = kv_out
@@ -315,6 +319,15 @@ class KVCache:
                                    _ptr(q_out, torch.float32, "q_out"), kp, vp,
                                    ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
         return q_out
+
+    @staticmethod
+    def _out_like(q, out):
+        """A caller's output tensor must have q's shape (the kernels write that many floats)."""
+        if out is None:
+            return torch.empty_like(q)
+        if tuple(out.shape) != tuple(q.shape):
+            raise ValueError(f"out must have q's shape {tuple(q.shape)}, got {tuple(out.shape)}")
+        return out
 
     def _check_kv(self, k, v, n_tok):
         want = (self.n_seq, n_tok, self.n_head_kv, self.head_dim)

@@ -105,6 +105,10 @@ int ts_kv_set_seq_len(ts_kv *kv, int32_t seq, int32_t len, void *stream);
  * buffers stay allocated. */
 int ts_kv_reset(ts_kv *kv, void *stream);
 
+/* KVCache::reset (kv_cache.rs:256-259) for one sequence: its length, window base and sink
+ * count to 0, so a reused slot starts like a fresh reference cache; the others keep theirs. */
+int ts_kv_reset_seq(ts_kv *kv, int32_t seq, void *stream);
+
 /* Copy positions [pos0, pos0+n_pos) of one sequence and layer out of the cache into the
  * reference's layout (kv_cache.rs:26-37): packed [n_pos][n_head_kv][head_dim/8] u32, scales
  * [n_pos][n_head_kv] f32.  All four outputs are device pointers.  Stands in for the
@@ -146,9 +150,9 @@ int ts_kv_shift_workspace(const ts_kv *kv, uint64_t *bytes);
  * for one layer of one sequence: slots keep_sink + shift_amt .. len-1 move down by shift_amt
  * (packed K and V and both scales, copied unchanged through a snapshot in d_workspace); the
  * keep_sink sinks stay.  Nothing moves when len <= keep_sink + shift_amt.  The first call on a
- * sequence records keep_sink as its sink count; a different keep_sink later is TS_ERR_INVALID
- * (slots below the sink count keep the rotation of their own position).  Lengths and the
- * window base do not change. */
+ * sequence records keep_sink as its sink count, also when nothing moves; a different keep_sink
+ * later is TS_ERR_INVALID (slots below the sink count keep the rotation of their own position)
+ * until ts_kv_reset / ts_kv_reset_seq.  Lengths and the window base do not change. */
 int ts_kv_shift(ts_kv *kv, int32_t layer, int32_t seq, int32_t keep_sink, int32_t shift_amt,
                 void *d_workspace, uint64_t workspace_bytes, void *stream);
 

@@ -138,9 +138,11 @@ def test_golden_fixture_through_gpu(gpu):
         assert np.array_equal(vs.cpu().numpy(), g["v_scale"][s])
 
 
-def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, sample, outliers):
+def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, sample, outliers, fused=False):
     """One layer at the full BASELINE shape: the GPU runs every sequence; the oracle checks a
-    sample of (sequence, head) pairs on identical inputs (copied back from the device)."""
+    sample of (sequence, head) pairs on identical inputs (copied back from the device).  With
+    `fused`, the new token goes through ts_attn_decode_append (the launch bench.py times), and
+    its appended K/V row is checked bit-exact for every sequence and kv head."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     dims = synth.outlier_dims(n_kv, hd, seed) if outliers else None
@@ -165,9 +167,25 @@ def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, sample, outliers):
     k1 = torch.randn((n_seq, 1, n_kv, hd), generator=gen, device="cuda") * skv
     v1 = torch.randn((n_seq, 1, n_kv, hd), generator=gen, device="cuda") * skv
     q = torch.randn((n_seq, n_head, hd), generator=gen, device="cuda") * sq
-    p.gpu.append_quant(0, k1, v1, p.rope)
-    out = p.gpu.attn_decode(0, q, p.rope).cpu().numpy()
+    if fused:
+        out = p.gpu.attn_decode_append(0, k1, v1, q, p.rope).cpu().numpy()
+    else:
+        p.gpu.append_quant(0, k1, v1, p.rope)
+        out = p.gpu.attn_decode(0, q, p.rope).cpu().numpy()
     qh, k1h, v1h = q.cpu().numpy(), k1.cpu().numpy(), v1.cpu().numpy()
+    if fused:
+        # the appended row of every sequence: K rotated at its position, V raw
+        for s in range(n_seq):
+            kp, vp, ks, vs = p.gpu.export(0, s, lens[s], 1)
+            kp, vp = kp.cpu().numpy().view(np.uint32)[0], vp.cpu().numpy().view(np.uint32)[0]
+            ks, vs = ks.cpu().numpy()[0], vs.cpu().numpy()[0]
+            for h in range(n_kv):
+                sk, wk = oracle.quantize_row(oracle.rope_rotate(k1h[s, 0, h], p.ora.table[lens[s]]))
+                sv, wv = oracle.quantize_row(v1h[s, 0, h])
+                assert np.array_equal(kp[h], wk), f"seq {s} head {h}: appended K row differs"
+                assert np.array_equal(vp[h], wv), f"seq {s} head {h}: appended V row differs"
+                assert ks[h].view(np.uint32) == sk.view(np.uint32) and vs[h].view(np.uint32) == sv.view(np.uint32), \
+                    f"seq {s} head {h}: appended scales differ"
     for s in seqs:
         kk = np.concatenate(host_k[s])[:lens[s]]
         vv = np.concatenate(host_v[s])[:lens[s]]
@@ -188,6 +206,23 @@ def test_full_size_config3_one_layer(gpu):
     say("decode full cfg3")
     sample = [(0, 0), (0, 31), (17, 5), (31, 12), (31, 30)]
     _full_size(32, 8, 32, 128, [8192] * 32, 1e6, 33, sample, True)
+
+
+def test_full_size_config3_fused(gpu):
+    """Config 3 at full size through the fused append + decode launch that bench.py times:
+    sampled heads against the oracle, the appended row of every sequence bit-exact."""
+    say("decode full cfg3 fused")
+    sample = [(0, 3), (5, 0), (17, 22), (31, 31)]
+    _full_size(32, 8, 32, 128, [8192] * 32, 1e6, 34, sample, True, fused=True)
+
+
+def test_full_size_config4_ragged_fused(gpu):
+    """Config 4 (ragged 16K-32K, batch 8) through the fused launch."""
+    say("decode full cfg4 fused")
+    rng = np.random.default_rng(45)
+    lens = [int(x) for x in rng.integers(16384, 32768, size=8)]
+    sample = [(1, 4), (6, 30)]
+    _full_size(8, 8, 32, 128, lens, 500000.0, 45, sample, False, fused=True)
 
 
 def test_full_size_config4_ragged_one_layer(gpu):
