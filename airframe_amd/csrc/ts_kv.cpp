@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <new>
 
 #include "ts_internal.h"
@@ -393,11 +394,14 @@ int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes) {
     return TS_OK;
 }
 
-// Shared by ts_attn_decode and ts_attn_decode_append (k_new/v_new null for the former).
+// Shared by ts_attn_decode, ts_attn_decode_append and ts_attn_decode_append_noalloc
+// (k_new/v_new null for the first).  d_workspace: the caller's workspace of workspace_bytes,
+// checked against the worst case the workspace query promises; or, with noalloc, the
+// library's scratch array, checked against what this call's plan needs.
 static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
                        const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
                        uint64_t workspace_bytes, const float *k_new, const float *v_new,
-                       void *stream) {
+                       void *stream, bool noalloc = false) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_q || !d_out || !heads_ok(kv, n_head) ||
         !(softcap >= 0.0f) || !aligned16(d_q) || !aligned16(d_out))
         return TS_ERR_INVALID;
@@ -405,15 +409,19 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
     if (max_len + 1 > kv->d.max_seq) return TS_ERR_OVERFLOW;
     int rc = check_rope(rope, kv->d.head_dim, rot_end(kv, 1));
     if (rc) return rc;
-    uint64_t need = 0;
-    ts_attn_decode_workspace(kv, n_head, &need);
     std::vector<int32_t> &ctx = const_cast<ts_kv *>(kv)->h_ctx;
     for (int s = 0; s < kv->d.n_seq; s++) ctx[s] = kv->h_len[s] + 1;
     ts::DecodePlan plan = ts::decode_plan(ctx.data(), kv->d.n_seq, kv->d.n_head_kv, n_head / kv->d.n_head_kv,
                                           kv->n_cu);
-    if (plan.n_split > 1 && (!d_workspace || workspace_bytes < need)) return TS_ERR_WORKSPACE;
-    if (plan.n_split > 1 && !aligned16(d_workspace)) return TS_ERR_INVALID;
-    // plan.n_split <= decode_cap(max_seq), the count the workspace was sized for.
+    if (plan.n_split > 1) {
+        uint64_t need = 0;
+        if (noalloc)  // partials [S][n_head][n_split][hd], then m and l [S][n_head][n_split]
+            need = (uint64_t)kv->d.n_seq * n_head * plan.n_split * (kv->d.head_dim + 2) * sizeof(float);
+        else  // plan.n_split <= decode_cap(max_seq), the count the workspace was sized for
+            ts_attn_decode_workspace(kv, n_head, &need);
+        if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
+        if (!aligned16(d_workspace)) return TS_ERR_INVALID;
+    }
     return hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
                                         rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
                                         plan, k_new, v_new, as_stream(stream)));
@@ -432,6 +440,48 @@ int ts_attn_decode_append(ts_kv *kv, int32_t layer, const float *d_k, const floa
     if (!d_k || !d_v || !aligned16(d_k) || !aligned16(d_v)) return TS_ERR_INVALID;
     return attn_decode(kv, layer, d_q, n_head, rope, softcap, d_out, d_workspace, workspace_bytes,
                        d_k, d_v, stream);
+}
+
+// ---- allocation-free decode ----------------------------------------------------------------
+//
+// The split partials of ts_attn_decode_append_noalloc live in `scratch`, a file-scope device
+// array: every GPU the library runs on holds one copy until the process ends, and every call
+// on that GPU shares it (calls that overlap on one GPU race).  Nothing in it has to start at
+// zero: each call writes every partial it reads.  Host code never uses the array's name as an
+// address; the address comes from hipGetSymbolAddress, once per device.
+
+namespace {
+constexpr uint64_t kScratchBytes = 8ull << 20;
+__device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// This device's copy of `scratch` (the current device's; looked up on its first use).
+int scratch_ptr(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TS_ERR_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TS_ERR_HIP;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TS_OK;
+}
+}  // namespace
+
+int ts_attn_decode_append_noalloc(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
+                                  const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
+                                  float *d_out, void *stream) {
+    if (!d_k || !d_v || !aligned16(d_k) || !aligned16(d_v)) return TS_ERR_INVALID;
+    void *ws = nullptr;
+    int rc = scratch_ptr(&ws);
+    if (rc) return rc;
+    return attn_decode(kv, layer, d_q, n_head, rope, softcap, d_out, ws, kScratchBytes, d_k, d_v, stream,
+                       true);
 }
 
 int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,

@@ -204,6 +204,17 @@ int ts_attn_decode_append(ts_kv *kv, int32_t layer, const float *d_k, const floa
                           const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
                           float *d_out, void *d_workspace, uint64_t workspace_bytes, void *stream);
 
+/* ts_attn_decode_append without a workspace argument and without allocating anything: the
+ * split partials go to a scratch array the library keeps on every GPU it runs on (8 MiB each,
+ * until the process ends).  No counterpart in the reference: for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Returns TS_ERR_WORKSPACE when this call's partials, n_seq * n_head * splits * (head_dim + 2)
+ * floats, would exceed 8 MiB (a call that needs no split needs none).  All calls on one GPU
+ * share the array: calls that overlap on one GPU (other streams, other threads) race. */
+int ts_attn_decode_append_noalloc(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
+                                  const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
+                                  float *d_out, void *stream);
+
 /* Chunked-prefill attention over the INT4 cache.  Stands in for the f32 main_attn_out of
  * batched prefill (sh_layer_v1.wgsl:662-762, inference.rs:1160-1166) with the INT4 cache as
  * its source.  d_q: [n_seq][n_tok][n_head][head_dim] raw f32 for the n_tok tokens just
