@@ -1,0 +1,125 @@
+// ts_probe.hip -- HBM streaming ceilings for the decode's access pattern (a measurement tool,
+// not part of the C ABI in include/turboshimmy.h; bench.py --stream-ceiling loads it).
+//
+// probe_decode_loads_kernel reads exactly what one ts_attn_decode launch of the G <= 4 kernel
+// reads, in the same way: one workgroup of 4 waves per (sequence, kv head) stream, 64-position
+// windows round robin over the waves starting at a per-workgroup offset, every K/V instruction
+// one contiguous kilobyte, non-temporal, scales 16 bytes per 4 lanes, one window in flight
+// while the previous one is consumed.  Consuming is an XOR into a register, so the launch time
+// is the memory system's time for this pattern.  probe_flat_read_kernel reads one flat buffer
+// grid-strided (every workgroup a different 4 KB piece at a time), the pattern HBM likes best.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+constexpr int kNT = 2;  // non-temporal
+
+struct ProbeArgs {
+    const uint8_t *kp, *vp;  // [rows][P/64][64 * HD / 2] and [rows][P/32][HD * 16] bytes
+    const float *ks, *vs;    // [rows][P]
+    int P, n_ctx;
+    uint32_t *sink;
+};
+
+template <int HD>
+__global__ __launch_bounds__(256, 1) void probe_decode_loads_kernel(ProbeArgs a) {
+    constexpr int NW = 4, ROWB = HD / 2, NKW = HD / 8, NTD = HD / 16;
+    const int row = blockIdx.y * gridDim.x + blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int end = a.n_ctx;
+    const uint32_t wend = (uint32_t)((end + 63) & ~63);
+    const auto rk = rsrc(a.kp + (size_t)row * a.P * ROWB, wend * ROWB);
+    const auto rv = rsrc(a.vp + (size_t)row * (a.P / 32) * (HD * 16), (uint32_t)((end + 31) / 32) * (HD * 16));
+    const auto rs = rsrc(a.ks + (size_t)row * a.P, wend * 4);
+    const auto rt = rsrc(a.vs + (size_t)row * a.P, wend * 4);
+    const int nwin = (end + 63) >> 6;
+    const int cnt = wave < nwin ? (nwin - wave + NW - 1) / NW : 0;
+    const int rot = cnt ? (int)((unsigned)(row * 37) % (unsigned)cnt) : 0;
+    auto win_base = [&](int i) {
+        if (i >= cnt) return 64 * nwin;
+        int r = i + rot;
+        r = r >= cnt ? r - cnt : r;
+        return 64 * (wave + NW * r);
+    };
+    u32x4 buf[2][NKW / 4 + NTD / 2 + 2];
+    auto load = [&](u32x4 *w, int base) {
+#pragma unroll
+        for (int j = 0; j < NKW / 4; j++) w[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16 + j * 1024, base * ROWB, kNT);
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int q = 0; q < NTD / 4; q++)
+                w[NKW / 4 + b * (NTD / 4) + q] =
+                    __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16 + q * 1024 + b * (HD * 16), (base / 32) * (HD * 16), kNT);
+        w[NKW / 4 + NTD / 2] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane & 15) * 16, base * 4, kNT);
+        w[NKW / 4 + NTD / 2 + 1] = __builtin_amdgcn_raw_buffer_load_b128(rt, (lane & 15) * 16, base * 4, kNT);
+    };
+    uint32_t acc = 0;
+    load(buf[0], win_base(0));
+    for (int it = 0; it < cnt; it += 2) {
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            load(buf[d ^ 1], win_base(it + d + 1));
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            if (it + d < cnt) {
+#pragma unroll
+                for (int j = 0; j < NKW / 4 + NTD / 2 + 2; j++) acc ^= buf[d][j].x ^ buf[d][j].y ^ buf[d][j].z ^ buf[d][j].w;
+            }
+        }
+    }
+    if (acc == 0x9E3779B9u) a.sink[0] = acc;  // keeps the loads; practically never taken
+}
+
+template <int UN>
+__global__ __launch_bounds__(256) void probe_flat_read_kernel(const u32x4 *__restrict__ p, size_t n, uint32_t *sink) {
+    uint32_t acc = 0;
+    const size_t stride = (size_t)gridDim.x * 256 * UN;
+    for (size_t i = (size_t)blockIdx.x * 256 * UN + threadIdx.x; i < n; i += stride) {
+        u32x4 t[UN];
+#pragma unroll
+        for (int u = 0; u < UN; u++) t[u] = i + u * 256 < n ? __builtin_nontemporal_load(p + i + u * 256) : (u32x4)0u;
+#pragma unroll
+        for (int u = 0; u < UN; u++) acc ^= t[u].x ^ t[u].y ^ t[u].z ^ t[u].w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+}  // namespace
+
+// One loads-only pass of the decode pattern over rows = n_seq * n_kv streams of n_ctx
+// positions (P = padded positions per stream, a multiple of 64).  Returns a hipError_t.
+extern "C" int ts_probe_decode_loads(const void *kp, const void *vp, const void *ks, const void *vs,
+                                     int n_seq, int n_kv, int hd, int P, int n_ctx, void *sink,
+                                     void *stream) {
+    if (P % 64 || n_ctx > P || n_ctx <= 0 || n_seq <= 0 || n_kv <= 0) return (int)hipErrorInvalidValue;
+    ProbeArgs a{(const uint8_t *)kp, (const uint8_t *)vp, (const float *)ks, (const float *)vs, P, n_ctx,
+                (uint32_t *)sink};
+    const dim3 grid(n_kv, n_seq);
+    // one workgroup per CU, as the decode's plan places them: an unused LDS reservation of
+    // more than half the CU's 160 KB keeps a second one off
+    const size_t lds = 96 * 1024;
+    if (hd == 128) {
+        hipFuncSetAttribute((const void *)probe_decode_loads_kernel<128>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        probe_decode_loads_kernel<128><<<grid, 256, lds, (hipStream_t)stream>>>(a);
+    } else if (hd == 64) {
+        hipFuncSetAttribute((const void *)probe_decode_loads_kernel<64>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        probe_decode_loads_kernel<64><<<grid, 256, lds, (hipStream_t)stream>>>(a);
+    } else {
+        return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+// One grid-strided read of n16 16-byte elements.
+extern "C" int ts_probe_flat_read(const void *p, size_t n16, int grid, void *sink, void *stream) {
+    probe_flat_read_kernel<4><<<grid, 256, 0, (hipStream_t)stream>>>((const u32x4 *)p, n16, (uint32_t *)sink);
+    return (int)hipGetLastError();
+}

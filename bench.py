@@ -59,6 +59,18 @@ def append_bytes(batch, n_kv, hd):
     return batch * n_kv * (2 * hd * 4 + hd + 8)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the baseline's record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(kv, cfg, qs, ks, vs, lens, max_seq, table, layers_mt=2, seqs_st=2, norms=None):
     """Time the C oracle (oracle/ts_oracle.c) on a bounded sample of the same step: append the
     step's token and attend, for every sequence of `layers_mt` layers (OpenMP over
@@ -306,7 +318,37 @@ def run_prefill(args, cfg):
     n_tot = C * NC
     flops_layer = 4 * hd * n_head * B * (n_tot * (n_tot + 1) // 2)
     kernel_ms_layer = float(np.sum(kt)) / reps / L
-    return dict(total_ms=total_ms, kernel_ms_layer=kernel_ms_layer, flops_layer=flops_layer)
+    res = dict(total_ms=total_ms, kernel_ms_layer=kernel_ms_layer, flops_layer=flops_layer)
+    if not args.no_cpu:
+        res["cpu"] = cpu_baseline_prefill(cfg, qs, ks, vs)
+    return res
+
+
+def cpu_baseline_prefill(cfg, qs, ks, vs):
+    """The C oracle on a bounded sample of config 5's layer: sequence 0 of layer 0, all chunks
+    (append + causal attention), OpenMP over heads; and its first chunk single-threaded.  The
+    rates are flops of the sample / its time (the same causal-exact counting as the GPU)."""
+    from oracle import oracle
+    n_head, n_kv, hd, C, NC = cfg["n_head"], cfg["n_kv"], cfg["hd"], cfg["chunk"], cfg["n_chunks"]
+    threads = min(16, os.cpu_count() or 1)
+    table = oracle.rope_table(C * NC, hd, cfg["theta"])
+
+    def run(n_chunks, thr):
+        ora = oracle.OracleKV(1, C * NC, n_kv, hd, table)
+        t = 0.0
+        for c in range(n_chunks):
+            k = ks[c][0][:1].cpu().numpy()
+            v = vs[c][0][:1].cpu().numpy()
+            q = qs[c][0][:1].cpu().numpy()
+            t0 = time.perf_counter()
+            ora.append(k, v)
+            ora.attend(q, C, threads=thr)
+            t += time.perf_counter() - t0
+            ora.advance(C)
+        n = n_chunks * C
+        return 4 * hd * n_head * (n * (n + 1) // 2) / t / 1e12
+
+    return dict(tflops_mt=run(NC, threads), cores=threads, tflops_st=run(1, 1))
 
 
 def run_append(args, cfg):
@@ -467,15 +509,82 @@ def run_compact(args, cfg):
     return ms, 4 * per * B * L, B * L
 
 
-def _split_kernel_name(cfg):
+def run_stream_ceiling(args, cfg):
+    """HBM ceilings for the decode step's reads (airframe_amd/csrc/ts_probe.hip): the decode
+    kernel's exact access pattern with no math (one launch reads what one layer's decode
+    reads), and a flat grid-strided read of the same byte count.  Four distinct buffer sets,
+    used round robin, so the 256 MB Infinity Cache cannot serve repeats."""
+    import ctypes
+    import torch
+    from airframe_amd.build import PROBE_PATH
+    if not os.path.exists(PROBE_PATH):
+        sys.exit(f"{PROBE_PATH} is missing: run python -m airframe_amd.build")
+    lib = ctypes.CDLL(PROBE_PATH)
+    lib.ts_probe_flat_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    B, H, hd, ctx = cfg["batch"], cfg["n_kv"], cfg["hd"], cfg["ctx"] + 1
+    P = (ctx + 63) // 64 * 64
+    rows = B * H
+    n_sets = 4
+    sets = [(torch.empty(rows * P * hd // 2, dtype=torch.uint8, device="cuda"),
+             torch.empty(rows * P * hd // 2, dtype=torch.uint8, device="cuda"),
+             torch.empty(rows * P, dtype=torch.float32, device="cuda"),
+             torch.empty(rows * P, dtype=torch.float32, device="cuda")) for _ in range(n_sets)]
+    nbytes = rows * ctx * (hd + 8)
+    flat = [torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda") for _ in range(n_sets)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def timed(f, n):
+        for i in range(3):
+            f(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            f(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    def dec(i):
+        kp, vp, ks, vs = sets[i % n_sets]
+        rc = lib.ts_probe_decode_loads(ctypes.c_void_p(kp.data_ptr()), ctypes.c_void_p(vp.data_ptr()),
+                                       ctypes.c_void_p(ks.data_ptr()), ctypes.c_void_p(vs.data_ptr()),
+                                       B, H, hd, P, ctx, ctypes.c_void_p(sink.data_ptr()), st)
+        assert rc == 0, rc
+
+    def flat_read(i):
+        rc = lib.ts_probe_flat_read(ctypes.c_void_p(flat[i % n_sets].data_ptr()), nbytes // 16, 2048,
+                                    ctypes.c_void_p(sink.data_ptr()), st)
+        assert rc == 0, rc
+
+    n = max(args.steps, 20)
+    us_dec = timed(dec, n)
+    us_flat = timed(flat_read, n)
+    return dict(bytes=nbytes, us_decode_pattern=us_dec, us_flat=us_flat, launches=n)
+
+
+def _split_kernel_name(cfg, n_cu=256):
     """Which split kernel the library launches for this shape: decode_plan and the dispatch
-    rule of launch_decode (ts_decode.hip), restated for the bench label."""
-    max_ctx = cfg["ctx"] + 1  # upper bound of the step's longest context
-    units = cfg["batch"] * cfg["n_kv"]
-    want = max(1, -(-1024 // units))
-    want = min(want, -(-max_ctx // 256))
-    chunk = -(-(-(-max_ctx // want)) // 64) * 64
-    g4 = cfg["n_head"] // cfg["n_kv"] <= 4 and chunk >= 1024
+    rule of launch_decode (ts_decode.hip), restated for the bench label (the step's starting
+    lengths; MI355X has 256 CUs)."""
+    if "ragged" in cfg:
+        rng = np.random.default_rng(2024)
+        ctx = [int(x) + 1 for x in rng.integers(cfg["ragged"][0], cfg["ragged"][1], size=cfg["batch"])]
+    else:
+        ctx = [cfg["ctx"] + 1] * cfg["batch"]
+
+    def chunk_for(target):
+        busy = lambda c: sum(-(-x // c) for x in ctx) * cfg["n_kv"]
+        hi = max(256, -(-max(ctx) // 64) * 64)
+        c = min(hi, max(256, -(-sum(ctx) * cfg["n_kv"] // target)))
+        c = -(-c // 64) * 64
+        while c < hi and busy(c) > target:
+            c += 64
+        return c
+
+    g4 = cfg["n_head"] // cfg["n_kv"] <= 4 and chunk_for(n_cu) >= 1024
     return "decode_split4_kernel" if g4 else "decode_split_kernel"
 
 
@@ -505,6 +614,9 @@ def main():
     ap.add_argument("--compact", action="store_true",
                     help="measure sliding-window compaction (ts_kv_shift) on the config's cache "
                          "instead of the decode step")
+    ap.add_argument("--stream-ceiling", action="store_true",
+                    help="measure the HBM ceiling of the decode's access pattern with no math "
+                         "(loads-only probe at the config's shape) and of a flat read of the same size")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="launch every kernel eagerly instead of replaying captured HIP graphs")
     args = ap.parse_args()
@@ -564,6 +676,22 @@ def main():
                        "tokens_per_call": toks, "dim": cfg["dim"]},
             "roofline": roof, "data": "synthetic (random f16 weights, N(0,1) x)"}), flush=True)
         return
+    if args.stream_ceiling:
+        if "ctx" not in cfg or "ragged" in cfg:
+            sys.exit("--stream-ceiling needs a uniform decode configuration (1-3)")
+        r = run_stream_ceiling(args, cfg)
+        g_dec = r["bytes"] / (r["us_decode_pattern"] * 1e-6) / 1e9
+        g_flat = r["bytes"] / (r["us_flat"] * 1e-6) / 1e9
+        print(json.dumps({
+            "metric": "HBM streaming ceiling of the decode access pattern (loads only) GB/s",
+            "value": round(g_dec, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+            "us_per_launch": round(r["us_decode_pattern"], 2), "frac": round(g_dec / HBM_PEAK_GBS, 4),
+            "flat_read": {"GBps": round(g_flat, 1), "us_per_launch": round(r["us_flat"], 2),
+                          "frac": round(g_flat / HBM_PEAK_GBS, 4)},
+            "bytes_per_launch": r["bytes"], "launches": r["launches"],
+            "config": {"workload": cfg["name"] + "_loads_only"}, "data": "uninitialised device buffers"}),
+            flush=True)
+        return
     if args.compact:
         if "ctx" not in cfg:
             sys.exit("--compact needs a decode configuration (1-4)")
@@ -583,13 +711,15 @@ def main():
         return
     # HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated) for
     # this configuration, as recorded in its profile summary; null when none was taken.
-    traffic = None
+    traffic = traffic_commit = None
     tpath = os.path.join(ROOT, "profiles", f"decode_cfg{args.config}.md")
     if os.path.exists(tpath):
         with open(tpath) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     traffic = int(float(line.split(":")[1]))
+                elif line.startswith("traffic_measured_at_commit:"):
+                    traffic_commit = line.split(":", 1)[1].strip()
 
     if args.copy_calib:
         x = torch.empty(2**28, dtype=torch.float32, device="cuda")
@@ -613,7 +743,13 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
-            "cpu_baseline": None,
+            "cpu_baseline": None if "cpu" not in r else {
+                "value": round(r["cpu"]["tflops_mt"], 6), "unit": "TFLOP/s", "cores": r["cpu"]["cores"],
+                "kind": "port", "cpu_model": cpu_model(),
+                "single_thread_value": round(r["cpu"]["tflops_st"], 6),
+                "sample": "C oracle: sequence 0 of layer 0, 4 chunks x 512 (append + causal "
+                          f"attention, OpenMP over heads, {r['cpu']['cores']} threads); its first "
+                          "chunk single-threaded; rates in the same causal-exact flops"},
         }
         print(json.dumps(line), flush=True)
         return
@@ -628,9 +764,11 @@ def main():
         split_name = _split_kernel_name(cfg)
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "traffic_source": f"profiles/decode_cfg{args.config}.md" if traffic else None,
-                "kernel": (f"{split_name}<{cfg['hd']}>+decode_combine_kernel (ts_attn_decode)" if args.separate
-                           else f"{split_name}<{cfg['hd']}> with fused append + decode_combine_kernel (ts_attn_decode_append)"),
+                "traffic_source": (f"profiles/decode_cfg{args.config}.md (rocprofv3 --pmc FETCH_SIZE / "
+                                   f"WRITE_SIZE at commit {traffic_commit})") if traffic else None,
+                "kernel": (f"{split_name}<{cfg['hd']}> (+ decode_combine_kernel when the plan splits; ts_attn_decode)"
+                           if args.separate else
+                           f"{split_name}<{cfg['hd']}> with fused append (+ decode_combine_kernel when the plan splits; ts_attn_decode_append)"),
                 "bytes_per_launch": int(r["kernel_bytes"]),
                 "avg_launch_us": round(r["kernel_ms"] * 1e3, 2),
                 "timing": "HIP events around each decode launch, eager pass of 16 steps"}
@@ -638,7 +776,7 @@ def main():
     if cpu:
         cpu_gbs = r["step_bytes"] / cpu["step_s_mt"] / 1e9
         cpu_line = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": cpu["cores"],
-                    "kind": "port",
+                    "kind": "port", "cpu_model": cpu_model(),
                     "tokens_per_s": round(B / cpu["step_s_mt"], 4),
                     "single_thread_tokens_per_s": round(B / cpu["step_s_st"], 5),
                     "sample": f"C oracle: append + attention of step 0 for all {B} sequences of "
