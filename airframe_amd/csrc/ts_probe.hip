@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256, 1) void probe_decode_loads_kernel(ProbeArgs a)
     const auto rt = rsrc(a.vs + (size_t)row * a.P, wend * 4);
     const int nwin = (end + 63) >> 6;
     const int cnt = wave < nwin ? (nwin - wave + NW - 1) / NW : 0;
-    const int rot = cnt ? (int)((unsigned)(row * 37) % (unsigned)cnt) : 0;
+    const int rot = cnt ? (int)((unsigned)(blockIdx.y * 13 + blockIdx.x * 5) % (unsigned)cnt) : 0;
     auto win_base = [&](int i) {
         if (i >= cnt) return 64 * nwin;
         int r = i + rot;
