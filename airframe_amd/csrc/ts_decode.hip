@@ -54,6 +54,7 @@ struct DecodeArgs {
     float softcap;
     float *out;
     float *ws;  // partial o [S][n_head][n_split][hd], then m [..][n_split], l [..][n_split]
+
     // Fused append (ts_attn_decode_append): the new token's raw K and V, [S][H][hd], or null.
     const float *k_new, *v_new;
 };
@@ -404,6 +405,18 @@ __device__ __forceinline__ void load_q_pairs(const DecodeArgs &a, int s, int h, 
         qp[hh] = hh < G ? *reinterpret_cast<const float2 *>(qg + (size_t)hh * HD + 2 * i) : make_float2(0.f, 0.f);
 }
 
+// Split partial of one head: unnormalized o (dim d), and with d == 0 the reference exponent m
+// and the sum l, for decode_combine_kernel.
+__device__ inline void store_partial(const DecodeArgs &a, size_t head, int split, int HD, int d, float acc,
+                                     float M, float lsum) {
+    const size_t rows = (size_t)a.L.S * a.n_head * a.n_split, r = head * a.n_split + split;
+    a.ws[r * HD + d] = acc;
+    if (d == 0) {
+        a.ws[rows * HD + r] = M;
+        a.ws[rows * (HD + 1) + r] = lsum;
+    }
+}
+
 template <int HD, bool SOFTCAP, bool NORM>
 __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs a) {
     constexpr int NW = kNW16;  // waves per workgroup
@@ -415,10 +428,44 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     const KvLayerView &L = a.L;
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+    const int start = split * a.chunk;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave index in an SGPR: window bases are then provably wave-uniform and feed the scalar
+    // offset of the buffer loads directly
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int G = a.G;
+    const size_t row = (size_t)s * L.H + h;
+    const uint8_t *kbase = L.kp + row * L.P * ROWB;
+    const uint8_t *vbase = L.vp + row * (L.P / 32) * (HD * 16);
+    const float *ksb = L.ks + row * L.P;
+    const float *vsb = L.vs + row * L.P;
+
+    // The first window and the raw q go out before the sequence's length is known (a memory
+    // round trip of its own): the first window is bounded by the stream's capacity, and the
+    // positions of it past the split's end are masked like any tail.
+    Streams str;
+    str.k = make_rsrc(kbase, (uint32_t)L.P * ROWB);
+    str.v = make_rsrc(vbase, (uint32_t)(L.P / 32) * (HD * 16));
+    str.ksb = ksb;
+    str.vsb = vsb;
+    str.last = L.P - 1;
+    Window<HD> w0, w1;
+    int base = start + wave * 64;
+    load_window<HD>(w0, str, base, n, g, lane);
+    // accumulator column n: high parts of head h*G + n (n < G), low parts of head
+    // h*G + n - G (G <= n < 2G), unused beyond
+    const bool live = n < 2 * G, lo_col = n >= G;
+    const int qhead = n < G ? n : (live ? n - G : 0);
+    const float *qrow = a.q + ((size_t)s * a.n_head + h * G + qhead) * HD;
+    float qraw[WPG][8];
+#pragma unroll
+    for (int t = 0; t < WPG; t++) q_read8(qrow, k16_word<HD>(g, t), nullptr, 1.0f, qraw[t]);
+    asm volatile("" ::: "memory");
+
     const int qpos = a.len[s];
     const int qrot = rot_of(a.L, s, qpos);  // rotation position of the query
     const int n_ctx = qpos + 1;
-    const int start = split * a.chunk;
     if (start >= n_ctx) return;
     const int n_split_s = min((n_ctx + a.chunk - 1) / a.chunk, a.n_split);
     // With the fused append, this split's workgroup writes position qpos itself and adds its
@@ -427,16 +474,6 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     // the last split runs to the end, also past chunk * n_split (a launch captured for shorter
     // contexts stays correct, only less balanced)
     const int end = fused ? qpos : (split == n_split_s - 1 ? n_ctx : start + a.chunk);
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    // wave index in an SGPR: window bases are then provably wave-uniform and feed the scalar
-    // offset of the buffer loads directly
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n = lane & 15, g = lane >> 4;
-    const int G = a.G;
-    // accumulator column n: high parts of head h*G + n (n < G), low parts of head
-    // h*G + n - G (G <= n < 2G), unused beyond
-    const bool live = n < 2 * G, lo_col = n >= G;
     const int partner4 = 4 * (n < G ? lane + G : (live ? lane - G : lane));
     const DeqConst dc;
 
@@ -455,44 +492,40 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     // fused append: the new position's dequantized K and V rows and its score per head
     __shared__ float kd[HD], vd[HD], xnew[8];
 
-    const size_t row = (size_t)s * L.H + h;
-    const uint8_t *kbase = L.kp + row * L.P * ROWB;
-    const uint8_t *vbase = L.vp + row * (L.P / 32) * (HD * 16);
-    const float *ksb = L.ks + row * L.P;
-    const float *vsb = L.vs + row * L.P;
-
-    Streams str;
-    // K rows are cut into segments spread over their 64-position window: bound at the window
+    // Later windows: bounded to the split (K rows are cut into segments spread over their
+    // 64-position window: bound at the window)
     str.k = make_rsrc(kbase, (uint32_t)((end + 63) & ~63) * ROWB);
     str.v = make_rsrc(vbase, (uint32_t)((end + 31) / 32) * (HD * 16));
-    str.ksb = ksb;
-    str.vsb = vsb;
     str.last = max(end - 1, 0);
-
-    // First window in flight before anything else.
-    Window<HD> w0, w1;
-    int base = start + wave * 64;
-    load_window<HD>(w0, str, base, n, g, lane);
 
     // q operands: wave w builds k-step t = w (rotated, scaled by log2(e)/sqrt(hd), split hi/lo)
     // for all 64 lanes; zero in the columns past G.
     // One power-of-two scale for the G heads: every wave reads the bound of all of them.
-    const int qhead = n < G ? n : (live ? n - G : 0);
-    const float *qrow = a.q + ((size_t)s * a.n_head + h * G + qhead) * HD;
     // QK norm scale of this lane's query head (each wave computes it for itself)
     const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, qhead, L.norm_eps)
                         : 1.0f;
+    if (QN) {
+#pragma unroll
+        for (int t = 0; t < WPG; t++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) qraw[t][e] = qk_norm_apply(qraw[t][e], ns, QN[8 * k16_word<HD>(g, t) + e]);
+    }
     float q_s, inv_s;
     {
         float qb = 0.0f;
 #pragma unroll
-        for (int t = 0; t < WPG; t++) qb = fmaxf(qb, q_bound8(qrow, k16_word<HD>(g, t), QN, ns));
+        for (int t = 0; t < WPG; t++)
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) qb = fmaxf(qb, fabsf(qraw[t][e]) + fabsf(qraw[t][e + 1]));
         q_scale(wave_max(qb) * (a.inv_sqrt_hd * kLog2e), q_s, inv_s);
     }
-    for (int t = wave; t < WPG; t += NW) {
+#pragma unroll
+    for (int t = 0; t < WPG; t++) {
+        if (t % NW != wave) continue;
         half8 qh, ql;
-        load_q8(a.rope, a.rope_pairs, qrow, k16_word<HD>(g, t), qrot, a.inv_sqrt_hd * kLog2e * q_s, qh, ql,
-                QN, ns);
+        float2 cs[4];
+        load_rot8(a.rope, a.rope_pairs, k16_word<HD>(g, t), qrot, cs);
+        split_q8(qraw[t], cs, k16_word<HD>(g, t), a.rope_pairs, a.inv_sqrt_hd * kLog2e * q_s, qh, ql);
         sm.run.q.p[t][lane] = !live ? (half8)(_Float16)0.0f : (lo_col ? ql : qh);
     }
     __syncthreads();  // q operands
@@ -571,16 +604,10 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
             lsum += e;
         }
         const size_t head = (size_t)s * a.n_head + h * G + hh;
-        if (n_split_s == 1) {
+        if (n_split_s == 1)
             a.out[head * HD + d] = lsum > 0.0f ? acc / lsum : 0.0f;
-        } else {
-            a.ws[(head * a.n_split + split) * HD + d] = acc;
-            if (d == 0) {
-                float *ml = a.ws + (size_t)L.S * a.n_head * a.n_split * HD;
-                ml[head * a.n_split + split] = M;
-                ml[(size_t)L.S * a.n_head * a.n_split + head * a.n_split + split] = lsum;
-            }
-        }
+        else
+            store_partial(a, head, split, HD, d, acc, M, lsum);
     }
 }
 
@@ -1109,16 +1136,10 @@ windows_done:
             lsum += e;
         }
         const size_t head = (size_t)s * a.n_head + h * G + hh;
-        if (n_split_s == 1) {
+        if (n_split_s == 1)
             a.out[head * HD + d] = lsum > 0.0f ? acc / lsum : 0.0f;
-        } else {
-            a.ws[(head * a.n_split + split) * HD + d] = acc;
-            if (d == 0) {
-                float *ml = a.ws + (size_t)L.S * a.n_head * a.n_split * HD;
-                ml[head * a.n_split + split] = M;
-                ml[(size_t)L.S * a.n_head * a.n_split + head * a.n_split + split] = lsum;
-            }
-        }
+        else
+            store_partial(a, head, split, HD, d, acc, M, lsum);
     }
 }
 
@@ -1133,13 +1154,7 @@ windows_done:
 // two 44.7 us, three 45.6 us.)  Splits shorter than kMinChunk leave waves without a window.
 namespace {
 constexpr int kMinChunk = 256;
-constexpr int kG4MinChunk = 1024;  // the 4x4x4 kernel needs >= 4 windows per wave to pay off
-
-int env_int(const char *name, int dflt) {
-    const char *e = getenv(name);
-    const int v = e ? atoi(e) : 0;
-    return v > 0 ? v : dflt;
-}
+constexpr int kG4MinChunk = 1024;  // the G <= 4 kernel needs >= 4 windows per wave to pay off
 
 int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
     int64_t total = 0;
@@ -1167,14 +1182,12 @@ int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
 }  // namespace
 
 DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu) {
-    // TS_DECODE_WG overrides the workgroup target of the G <= 4 kernel (a tuning knob).
-    static const int kTarget4 = env_int("TS_DECODE_WG", 0);
     DecodePlan p;
     int max_ctx = 1;
     for (int s = 0; s < n_seq; s++) max_ctx = std::max(max_ctx, (int)n_ctx[s]);
     p.g4 = false;
     if (G <= 4) {
-        p.chunk = plan_chunk(n_ctx, n_seq, n_kv, kTarget4 ? kTarget4 : n_cu);
+        p.chunk = plan_chunk(n_ctx, n_seq, n_kv, n_cu);
         p.g4 = p.chunk >= kG4MinChunk;
     }
     if (!p.g4) p.chunk = plan_chunk(n_ctx, n_seq, n_kv, 2 * n_cu);
@@ -1185,9 +1198,7 @@ DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_c
 int decode_cap(int n_kv, int max_seq, int n_cu) {
     // One sequence alone can take at most target / n_kv splits (plus one for rounding); the
     // 16x16 kernel's target, 2 n_cu, is the larger.
-    static const int kTarget4 = env_int("TS_DECODE_WG", 0);
-    const int target = std::max(2 * n_cu, kTarget4);
-    return std::min((max_seq + 63) / 64, target / n_kv + 2);
+    return std::min((max_seq + 63) / 64, 2 * n_cu / n_kv + 2);
 }
 
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
@@ -1211,20 +1222,16 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.k_new = k_new;
     a.v_new = v_new;
     dim3 grid(plan.n_split, L.H, L.S);
-    // The 4x4x4 QK kernel does less VALU work per window but has the longer per-window
-    // dependency chain (QK chains of 32 MFMAs, P through LDS); it runs when every wave streams
-    // at least 4 windows of its split (plan.g4).  TS_DECODE_SHAPE=2 selects its 8-wave,
-    // double-buffered form (a tuning knob).
-    static const int kShape = env_int("TS_DECODE_SHAPE", 1);
-    // The G <= 4 kernel fits two workgroups per CU by registers, but the plan wants one per
+    // The G <= 4 kernel does less VALU work per window than the 16x16 one but has the longer
+    // per-window dependency chain; it runs when every wave streams at least 4 windows of its
+    // split (plan.g4).  It fits two workgroups per CU by registers, but the plan wants one per
     // CU: the unused dynamic LDS reservation (with the kernel's own ~17 KB, more than half of
     // the CU's 160 KB) makes the dispatcher place busy workgroups on distinct CUs, also when
     // the grid holds idle ones (splits past a short sequence's end) that exit at once.
     constexpr size_t kOnePerCuLds = 64 * 1024;
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
 #define TS_SPLIT(HDV, SC, NM)                                                                  \
-    (plan.g4 ? (kShape == 2 ? (decode_split4_kernel<HDV, SC, NM, 8, 2><<<grid, 512, kOnePerCuLds, st>>>(a), 0)    \
-                            : (decode_split4_kernel<HDV, SC, NM, 4, 2><<<grid, 256, kOnePerCuLds, st>>>(a), 0))   \
+    (plan.g4 ? (decode_split4_kernel<HDV, SC, NM, 4, 2><<<grid, 256, kOnePerCuLds, st>>>(a), 0)        \
              : (decode_split_kernel<HDV, SC, NM><<<grid, 64 * kNW16, 0, st>>>(a), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \
     (cap ? (norm ? TS_SPLIT(HDV, true, true) : TS_SPLIT(HDV, true, false))                    \
