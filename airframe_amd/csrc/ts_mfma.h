@@ -35,6 +35,15 @@ struct DeqConst {
     uint32_t lo, hi, magic;
     __device__ DeqConst() : lo(0x000F000Fu), hi(0x00F000F0u), magic(0x64006400u) {}
 };
+// The same, hidden from constant folding (an empty asm per value), so that plain C code
+// using them keeps them in registers.
+struct DeqConstV : DeqConst {
+    __device__ DeqConstV() {
+        asm volatile("" : "+v"(lo));
+        asm volatile("" : "+v"(hi));
+        asm volatile("" : "+v"(magic));
+    }
+};
 
 // 8 nibbles of w -> half8 holding (code - 8) in slot order [e0,e4,e1,e5,e2,e6,e3,e7].
 // 0x6400 | n is the f16 1024 + n; 0x6400 | (n << 4) is 1024 + 16 n, brought back with
@@ -79,12 +88,14 @@ __device__ inline float group_sum(float v) {
 
 // dequant8 written in plain C: the same instructions, but visible to the scheduler, so it can
 // be interleaved with matrix-core work (prefill staging).
-__device__ inline half8 dequant8_c(uint32_t w) {
+// k: the masks and the magic in VGPRs (see DeqConstV), so that each mask-and-or is one
+// v_and_or_b32 (two literal operands cannot be encoded in one instruction).
+__device__ inline half8 dequant8_c(uint32_t w, const DeqConst &k) {
     const uint32_t w8 = w >> 8;
-    const uint32_t a = (w & 0x000F000Fu) | 0x64006400u;
-    const uint32_t b = (w & 0x00F000F0u) | 0x64006400u;
-    const uint32_t c = (w8 & 0x000F000Fu) | 0x64006400u;
-    const uint32_t d = (w8 & 0x00F000F0u) | 0x64006400u;
+    const uint32_t a = (w & k.lo) | k.magic;
+    const uint32_t b = (w & k.hi) | k.magic;
+    const uint32_t c = (w8 & k.lo) | k.magic;
+    const uint32_t d = (w8 & k.hi) | k.magic;
     half2_t ha = __builtin_bit_cast(half2_t, a), hb = __builtin_bit_cast(half2_t, b);
     half2_t hc = __builtin_bit_cast(half2_t, c), hd = __builtin_bit_cast(half2_t, d);
     const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};

@@ -42,9 +42,7 @@ struct PrefillArgs {
     float *out;
 };
 
-#ifndef TS_PREFILL_NW
-#define TS_PREFILL_NW 4
-#endif
+constexpr int kPrefillNW = 4;  // waves per workgroup
 
 constexpr int kColsPerWave = 32;
 constexpr int kWin = 64;  // keys per window
@@ -162,9 +160,9 @@ __device__ inline void fetch_window(Pending<HD, NW> &pd, const uint8_t *kbase, c
 // Staging of one window's codes, as 8 * NK parts of one 32-bit word each per thread (parts
 // [0, 4 NK): K words, [4 NK, 8 NK): V words), so the caller can spread them over other work.
 // Only for the layout where every thread holds NK K pieces and NK V pieces (!SPLIT).
-template <int HD, int NW>
-__device__ inline void stage_part(PrefillLds<HD> &sm, int buf, const Pending<HD, NW> &pd, int tid,
-                                  int part) {
+template <int HD, int NW, class SM>
+__device__ inline void stage_part(SM &sm, int buf, const Pending<HD, NW> &pd, int tid,
+                                  int part, const DeqConst &dk) {
     using P = Pending<HD, NW>;
     static_assert(!P::SPLIT, "per-part staging needs whole K and V pieces per thread");
     const int i = (part % (4 * P::NK)) / 4, j = part % 4;
@@ -174,7 +172,7 @@ __device__ inline void stage_part(PrefillLds<HD> &sm, int buf, const Pending<HD,
         const uint32_t wj = j == 0 ? x.x : j == 1 ? x.y : j == 2 ? x.z : x.w;
         int key, u;
         k_piece_word<HD>(c, j, key, u);
-        sm.k[buf][key][k_slot<HD>(key, u)] = dequant8_c(wj);
+        sm.k[buf][key][k_slot<HD>(key, u)] = dequant8_c(wj, dk);
     } else {
         // V: lane L holds 4 words of packed lane group ln = L (key group g = ln/16, dim row dl
         // = ln%16); lane L^16 holds the same words of key group g^1.  Words of groups 2p and
@@ -194,14 +192,14 @@ __device__ inline void stage_part(PrefillLds<HD> &sm, int buf, const Pending<HD,
         const uint32_t pw = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (threadIdx.x ^ 16), (int)wj);
         const uint32_t d = __builtin_amdgcn_perm(pw, wj, sel);
         const int row = 16 * (td0 + j) + dl;
-        sm.v[buf][row][v_slot(row, sl)] = dequant8_c(d);
+        sm.v[buf][row][v_slot(row, sl)] = dequant8_c(d, dk);
     }
 }
 
 // All of one window's codes into LDS.
-template <int HD, int NW>
-__device__ inline void stage_codes(PrefillLds<HD> &sm, int buf, const Pending<HD, NW> &pd, int tid,
-                                   int wave) {
+template <int HD, int NW, class SM>
+__device__ inline void stage_codes(SM &sm, int buf, const Pending<HD, NW> &pd, int tid,
+                                   int wave, const DeqConst &dk) {
     using P = Pending<HD, NW>;
     if constexpr (P::SPLIT) {
         // V staging as in stage_part, for a thread that holds one V piece
@@ -211,7 +209,7 @@ __device__ inline void stage_codes(PrefillLds<HD> &sm, int buf, const Pending<HD
             for (int j = 0; j < 4; j++) {
                 int key, u;
                 k_piece_word<HD>(c, j, key, u);
-                sm.k[buf][key][k_slot<HD>(key, u)] = dequant8_c(w[j]);
+                sm.k[buf][key][k_slot<HD>(key, u)] = dequant8_c(w[j], dk);
             }
         };
         auto put_v = [&](int c, const uint4 &x) {
@@ -227,7 +225,7 @@ __device__ inline void stage_codes(PrefillLds<HD> &sm, int buf, const Pending<HD
                 const uint32_t pw = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (threadIdx.x ^ 16), (int)w[j]);
                 const uint32_t d = __builtin_amdgcn_perm(pw, w[j], sel);
                 const int row = 16 * (td0 + j) + dl;
-                sm.v[buf][row][v_slot(row, sl)] = dequant8_c(d);
+                sm.v[buf][row][v_slot(row, sl)] = dequant8_c(d, dk);
             }
         };
         if (wave < P::KCH / 64)
@@ -236,14 +234,14 @@ __device__ inline void stage_codes(PrefillLds<HD> &sm, int buf, const Pending<HD
             put_v(tid - P::KCH, pd.k[0]);
     } else {
 #pragma unroll
-        for (int part = 0; part < 8 * P::NK; part++) stage_part<HD, NW>(sm, buf, pd, tid, part);
+        for (int part = 0; part < 8 * P::NK; part++) stage_part<HD, NW, SM>(sm, buf, pd, tid, part, dk);
     }
 }
 
 // The window's scales into LDS (kept apart from the code staging, which is branch-free so it
 // can be scheduled in between the QK matrix-core instructions).
-template <int HD, int NW>
-__device__ inline void stage_scales(PrefillLds<HD> &sm, int buf, const Pending<HD, NW> &pd, int tid,
+template <int HD, int NW, class SM>
+__device__ inline void stage_scales(SM &sm, int buf, const Pending<HD, NW> &pd, int tid,
                                     float inv_s) {
     if (tid < kWin) {
         sm.sk[buf][tid] = pd.scale * inv_s;  // undo the q operand scale (a power of two: exact)
@@ -345,18 +343,19 @@ __device__ inline void step_probs(const floatx16 (&sc)[2], const float *sv, int 
         for (int r = 0; r < 4; r++) {
             const float p = __builtin_amdgcn_exp2f(sc[kb][4 * q + r]);  // sc is relative
             l_run += p;
-            const float pv = p * sv4[r];
-            const float hi = split_hi(pv);
+            // hi: the exact product p s_v rounded once to f16; lo: the exact remainder
+            // p s_v - hi rounded once (both one fused multiply-add with an f16 result)
+            const _Float16 hi = (_Float16)__builtin_fmaf(p, sv4[r], 0.0f);
             // key 16st + 8h + 4(q&1) + r: slot 2r + (q&1)
-            pb[2 * r + (q & 1)] = (_Float16)hi;
-            pl[2 * r + (q & 1)] = (_Float16)(pv - hi);
+            pb[2 * r + (q & 1)] = hi;
+            pl[2 * r + (q & 1)] = (_Float16)__builtin_fmaf(p, sv4[r], -(float)hi);
         }
     }
 }
 
 template <int HD, bool SOFTCAP, bool NORM>
-__global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillArgs a) {
-    constexpr int NW = TS_PREFILL_NW;
+__global__ __launch_bounds__(64 * kPrefillNW, 2) void prefill_kernel(PrefillArgs a) {
+    constexpr int NW = kPrefillNW;
     constexpr int NKS = HD / 16;   // MFMA k-steps over the head dim
     constexpr int NDB = HD / 32;   // 32-dim output tiles
     constexpr int ROWB = HD / 2;
@@ -448,8 +447,9 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
     // Window w+1 is staged into LDS while window w's QK^T runs on the matrix cores (the
     // staging is VALU and LDS-write work); its global loads were issued one iteration earlier.
     Pending<HD, NW> pd;
+    const DeqConstV dk;
     fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, 0, tid, wave);
-    stage_codes<HD, NW>(sm, 0, pd, tid, wave);
+    stage_codes<HD, NW>(sm, 0, pd, tid, wave, dk);
     stage_scales<HD, NW>(sm, 0, pd, tid, inv_s);
     if (n_win > 1) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, kWin, tid, wave);
     __syncthreads();
@@ -477,10 +477,10 @@ __global__ __launch_bounds__(64 * TS_PREFILL_NW, 2) void prefill_kernel(PrefillA
             if constexpr (NPART > 0) {
 #pragma unroll
                 for (int part = t * NPART / NKS; part < (t + 1) * NPART / NKS; part++)
-                    stage_part<HD, NW>(sm, buf ^ 1, pd, tid, part);
+                    stage_part<HD, NW>(sm, buf ^ 1, pd, tid, part, dk);
             }
         }
-        if constexpr (NPART == 0) stage_codes<HD, NW>(sm, buf ^ 1, pd, tid, wave);
+        if constexpr (NPART == 0) stage_codes<HD, NW>(sm, buf ^ 1, pd, tid, wave, dk);
         __builtin_amdgcn_s_setprio(0);
         if (more) stage_scales<HD, NW>(sm, buf ^ 1, pd, tid, inv_s);
         if (w + 2 < n_win) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, base + 2 * kWin, tid, wave);
@@ -545,15 +545,15 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
     a.softcap = softcap;
     a.out = out;
     const int n_cols = n_tok * a.G;
-    const int cols = TS_PREFILL_NW * kColsPerWave;
+    const int cols = kPrefillNW * kColsPerWave;
     const int n_blk = (n_cols + cols - 1) / cols;
     dim3 grid(n_blk, L.H, L.S);
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr;
 #define TS_PF(HDV)                                                                                      \
-    (cap ? (norm ? (prefill_kernel<HDV, true, true><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a), 0)         \
-                 : (prefill_kernel<HDV, true, false><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a), 0))       \
-         : (norm ? (prefill_kernel<HDV, false, true><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a), 0)        \
-                 : (prefill_kernel<HDV, false, false><<<grid, 64 * TS_PREFILL_NW, 0, st>>>(a), 0)))
+    (cap ? (norm ? (prefill_kernel<HDV, true, true><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)         \
+                 : (prefill_kernel<HDV, true, false><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0))       \
+         : (norm ? (prefill_kernel<HDV, false, true><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)        \
+                 : (prefill_kernel<HDV, false, false><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)))
     if (L.hd == 128)
         TS_PF(128);
     else if (L.hd == 64)
