@@ -67,9 +67,6 @@ SIGNATURES = {
     "ts_attn_out_proj_workspace": (ctypes.c_int, [_i32, _i32, _i32, _u64p]),
     "ts_attn_out_proj": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, ctypes.c_uint64,
                                         _vp]),
-    "ts_attn_decode_append_proj_workspace": (ctypes.c_int, [_vp, _i32, _i32, _u64p]),
-    "ts_attn_decode_append_proj": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i32, _vp, _f, _vp, _i32,
-                                                  _vp, _vp, _vp, _vp, ctypes.c_uint64, _vp]),
 }
 
 _lib = None

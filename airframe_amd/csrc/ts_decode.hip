@@ -1204,7 +1204,7 @@ int decode_cap(int n_kv, int max_seq, int n_cu) {
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,
-                         const float *v_new, hipStream_t st, bool combine) {
+                         const float *v_new, hipStream_t st) {
     DecodeArgs a;
     a.L = L;
     a.len = d_len;
@@ -1238,10 +1238,10 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
          : (norm ? TS_SPLIT(HDV, false, true) : TS_SPLIT(HDV, false, false)))
     if (L.hd == 128) {
         TS_SPLIT_HD(128);
-        if (plan.n_split > 1 && combine) decode_combine_kernel<128><<<dim3(n_head, L.S), 256, 0, st>>>(a);
+        if (plan.n_split > 1) decode_combine_kernel<128><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else if (L.hd == 64) {
         TS_SPLIT_HD(64);
-        if (plan.n_split > 1 && combine) decode_combine_kernel<64><<<dim3(n_head, L.S), 256, 0, st>>>(a);
+        if (plan.n_split > 1) decode_combine_kernel<64><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else {
         return hipErrorInvalidValue;
     }

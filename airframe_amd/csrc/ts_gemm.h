@@ -131,31 +131,8 @@ struct SplitTiles {
 // accumulates columns 64 w + 32 cb + .. in acc[cb].  Staging thread (si = tid / 8, sc = tid % 8)
 // owns 8 floats of x row si per chunk (xs at chunk 0 of the slice, null: a zero row); wp[cb]:
 // the lane's weight row of column block cb at the slice's chunk 0, offset 32 hf.
-//
-// gemm_split_core_x takes the x values from a loader instead: xload(k, u, v) gives the
-// thread's 8 floats of its row at chunk offset k of the slice (k = 64 c + 256 b).
-template <class XLoad>
-__device__ __forceinline__ void gemm_split_core_x(SplitTiles &sm, XLoad xload, const _Float16 *const (&wp)[2],
-                                                  int nbat, int tid, floatx16 (&acc)[2]);
-
 __device__ __forceinline__ void gemm_split_core(SplitTiles &sm, const float *xs, const _Float16 *const (&wp)[2],
                                                 int nbat, int tid, floatx16 (&acc)[2]) {
-    gemm_split_core_x(
-        sm,
-        [&](int k, float4 &u, float4 &v) {
-            u = make_float4(0.f, 0.f, 0.f, 0.f);
-            v = u;
-            if (xs) {
-                u = *reinterpret_cast<const float4 *>(xs + k);
-                v = *reinterpret_cast<const float4 *>(xs + k + 4);
-            }
-        },
-        wp, nbat, tid, acc);
-}
-
-template <class XLoad>
-__device__ __forceinline__ void gemm_split_core_x(SplitTiles &sm, XLoad xload, const _Float16 *const (&wp)[2],
-                                                  int nbat, int tid, floatx16 (&acc)[2]) {
     constexpr int NB = 4;
     const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int si = tid >> 3, sc = tid & 7;
@@ -167,7 +144,12 @@ __device__ __forceinline__ void gemm_split_core_x(SplitTiles &sm, XLoad xload, c
         half8 wb[NB][2][4];
 #pragma unroll
         for (int c = 0; c < NB; c++) {
-            xload(ko + c * kKC, xu[c], xv[c]);
+            xu[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[c] = xu[c];
+            if (xs) {
+                xu[c] = *reinterpret_cast<const float4 *>(xs + ko + c * kKC);
+                xv[c] = *reinterpret_cast<const float4 *>(xs + ko + c * kKC + 4);
+            }
 #pragma unroll
             for (int cb = 0; cb < 2; cb++)
 #pragma unroll

@@ -147,7 +147,7 @@ int decode_cap(int n_kv, int max_seq, int n_cu);
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,
-                         const float *v_new, hipStream_t st, bool combine = true);
+                         const float *v_new, hipStream_t st);
 hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const float *q,
                           int n_head, int n_tok, const float *rope, int rope_pairs,
                           float softcap, float *out, hipStream_t st);
@@ -171,19 +171,7 @@ struct ProjPlan {
     uint64_t part_bytes;
 };
 ProjPlan proj_plan(int M, int K, int N);
-// The split-K decode's output as the projection's input: partials ws, the decode output out
-// (complete for sequences with one split), the lengths and the decode plan.
-struct CombineSrc {
-    const float *ws;
-    float *out;
-    const int32_t *len;
-    int chunk, n_split, hd, n_head, S;
-};
 hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, float *act, float *stash,
                        const ProjPlan &plan, float *part, hipStream_t st);
-// ts_attn_decode_append_proj's projection: the decode's split partials merged on the fly
-// (plan.n_split >= 2), the merged values also written to cs.out.
-hipError_t launch_proj_combine(const CombineSrc &cs, int M, int K, const uint16_t *w, int N, float *act,
-                               float *stash, const ProjPlan &plan, float *part, hipStream_t st);
 
 }  // namespace ts

@@ -401,7 +401,7 @@ int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes) {
 static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
                        const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
                        uint64_t workspace_bytes, const float *k_new, const float *v_new,
-                       void *stream, bool noalloc = false, ts::DecodePlan *plan_out = nullptr) {
+                       void *stream, bool noalloc = false) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_q || !d_out || !heads_ok(kv, n_head) ||
         !(softcap >= 0.0f) || !aligned16(d_q) || !aligned16(d_out))
         return TS_ERR_INVALID;
@@ -422,11 +422,9 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
         if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
         if (!aligned16(d_workspace)) return TS_ERR_INVALID;
     }
-    // with plan_out the caller merges the splits itself (ts_attn_decode_append_proj)
-    if (plan_out) *plan_out = plan;
     return hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
                                         rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
-                                        plan, k_new, v_new, as_stream(stream), plan_out == nullptr));
+                                        plan, k_new, v_new, as_stream(stream)));
 }
 
 int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
@@ -555,59 +553,6 @@ int ts_attn_out_proj(const float *d_attn, int32_t n_tok, int32_t attn_dim, const
         return TS_ERR_WORKSPACE;
     return hip_status(ts::launch_proj(d_attn, n_tok, attn_dim, d_wo, dim, d_act, d_stash, plan,
                                       static_cast<float *>(d_workspace), as_stream(stream)));
-}
-
-// Workspace of ts_attn_decode_append_proj: the decode's (its split partials) at the front,
-// then, 256-byte aligned, the projection's.
-static uint64_t align256(uint64_t x) { return (x + 255) & ~255ull; }
-
-int ts_attn_decode_append_proj_workspace(const ts_kv *kv, int32_t n_head, int32_t dim, uint64_t *bytes) {
-    if (!kv || !bytes || !heads_ok(kv, n_head) || dim <= 0) return TS_ERR_INVALID;
-    uint64_t dec = 0;
-    int rc = ts_attn_decode_workspace(kv, n_head, &dec);
-    if (rc) return rc;
-    const int K = n_head * kv->d.head_dim;
-    *bytes = align256(dec) + ts::proj_plan(kv->d.n_seq, K, dim).part_bytes;
-    return TS_OK;
-}
-
-int ts_attn_decode_append_proj(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
-                               const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
-                               const uint16_t *d_wo, int32_t dim, float *d_attn, float *d_act,
-                               float *d_stash, void *d_workspace, uint64_t workspace_bytes, void *stream) {
-    if (!kv || !d_k || !d_v || !d_wo || !d_act || !d_attn || dim <= 0 || !aligned16(d_wo) ||
-        !aligned16(d_act) || !aligned16(d_stash) || !aligned16(d_attn) || !heads_ok(kv, n_head))
-        return TS_ERR_INVALID;
-    uint64_t need = 0;
-    int rc = ts_attn_decode_append_proj_workspace(kv, n_head, dim, &need);
-    if (rc) return rc;
-    if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
-    if (!aligned16(d_workspace)) return TS_ERR_INVALID;
-    uint64_t dec = 0;
-    ts_attn_decode_workspace(kv, n_head, &dec);
-    float *dws = static_cast<float *>(d_workspace);
-    float *pws = reinterpret_cast<float *>(static_cast<uint8_t *>(d_workspace) + align256(dec));
-    const int S = kv->d.n_seq, K = n_head * kv->d.head_dim;
-    const ts::ProjPlan pplan = ts::proj_plan(S, K, dim);
-    ts::DecodePlan plan;
-    // the decode without its combine launch when the projection can merge the splits
-    rc = attn_decode(kv, layer, d_q, n_head, rope, softcap, d_attn, dws, dec, d_k, d_v, stream, false,
-                     pplan.n_split > 1 ? &plan : nullptr);
-    if (rc) return rc;
-    if (pplan.n_split > 1 && plan.n_split > 1) {
-        ts::CombineSrc cs;
-        cs.ws = dws;
-        cs.out = d_attn;
-        cs.len = kv->d_len;
-        cs.chunk = plan.chunk;
-        cs.n_split = plan.n_split;
-        cs.hd = kv->d.head_dim;
-        cs.n_head = n_head;
-        cs.S = S;
-        return hip_status(ts::launch_proj_combine(cs, S, K, d_wo, dim, d_act, d_stash, pplan, pws,
-                                                  as_stream(stream)));
-    }
-    return hip_status(ts::launch_proj(d_attn, S, K, d_wo, dim, d_act, d_stash, pplan, pws, as_stream(stream)));
 }
 
 }  // extern "C"

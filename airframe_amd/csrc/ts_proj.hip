@@ -127,103 +127,6 @@ __global__ __launch_bounds__(256) void proj_reduce_kernel(ProjArgs p) {
     }
 }
 
-// ---- the split-K combine folded into the projection (ts_attn_decode_append_proj) ---------------
-//
-// One decode token per sequence (row = sequence).  The x values of a staging thread -- 8 dims
-// of one head -- come straight from the split-K decode's partials: the log-sum-exp merge of
-// that head's splits (the decode_combine_kernel arithmetic), or the decode output itself for
-// a sequence that had one split.  Every column tile recombines what it needs (the partials
-// are small and stay in L2); the tiles of column block 0 also write the merged values to the
-// attention output, so it is complete afterwards.
-__device__ inline float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
-
-__device__ inline void combined8(const CombineSrc &c, int row, int k0, bool write, float4 &u, float4 &v) {
-    const int head = k0 / c.hd, d0 = k0 - head * c.hd;
-    const int n_ctx = c.len[row] + 1;
-    const int ns = min((n_ctx + c.chunk - 1) / c.chunk, c.n_split);
-    float *orow = c.out + ((size_t)row * c.n_head + head) * c.hd + d0;
-    if (ns <= 1) {
-        u = ld4(orow);
-        v = ld4(orow + 4);
-        return;
-    }
-    const size_t rows = (size_t)c.S * c.n_head * c.n_split;
-    const size_t hidx = (size_t)row * c.n_head + head;
-    const float *mm = c.ws + rows * c.hd + hidx * c.n_split, *ll = mm + rows;
-    const float *ob = c.ws + hidx * c.n_split * c.hd + d0;
-    constexpr int B = 8;
-    float M = kMinit, L = 0.0f;
-    u = make_float4(0.f, 0.f, 0.f, 0.f);
-    v = u;
-    for (int p0 = 0; p0 < ns; p0 += B) {
-        float mv[B], lv[B];
-        float4 xu[B], xv[B];
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            const int p = p0 + i;
-            const bool in = p < ns;
-            mv[i] = in ? mm[p] : kMinit;
-            lv[i] = in ? ll[p] : 0.0f;
-            xu[i] = in ? ld4(ob + (size_t)p * c.hd) : make_float4(0.f, 0.f, 0.f, 0.f);
-            xv[i] = in ? ld4(ob + (size_t)p * c.hd + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        float Mb = M;
-#pragma unroll
-        for (int i = 0; i < B; i++) Mb = fmaxf(Mb, mv[i]);
-        const float r = exp2f(M - Mb);  // 0 while nothing is accumulated
-        L *= r;
-        u.x *= r; u.y *= r; u.z *= r; u.w *= r;
-        v.x *= r; v.y *= r; v.z *= r; v.w *= r;
-        M = Mb;
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            const float e = p0 + i < ns ? exp2f(mv[i] - M) : 0.0f;
-            L += e * lv[i];
-            u.x += e * xu[i].x; u.y += e * xu[i].y; u.z += e * xu[i].z; u.w += e * xu[i].w;
-            v.x += e * xv[i].x; v.y += e * xv[i].y; v.z += e * xv[i].z; v.w += e * xv[i].w;
-        }
-    }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    u.x *= inv; u.y *= inv; u.z *= inv; u.w *= inv;
-    v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
-    if (write) {
-        *reinterpret_cast<float4 *>(orow) = u;
-        *reinterpret_cast<float4 *>(orow + 4) = v;
-    }
-}
-
-// proj_split_kernel with the x values merged from the decode partials.
-__global__ __launch_bounds__(256) void proj_combine_split_kernel(ProjArgs p, CombineSrc cs) {
-    __shared__ __align__(16) SplitTiles sm;
-    int rt, ct, sp;
-    proj_tile_of(p, blockIdx.x, rt, ct, sp);
-    if (sp >= p.n_split) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-    const int row0 = 32 * rt, col0 = kPT * ct + 64 * wave;
-    const int kb = sp * p.kps;
-    const int nbat = (min(kb + p.kps, p.K) - kb) / (4 * kKC);
-    const int si = tid >> 3, sc = tid & 7;
-    const int row = row0 + si;
-    const bool has = row < p.M;
-    const _Float16 *const wp[2] = {p.w + (size_t)min(col0 + j, p.N - 1) * p.K + kb + 32 * hf,
-                                   p.w + (size_t)min(col0 + 32 + j, p.N - 1) * p.K + kb + 32 * hf};
-    floatx16 acc[2];
-    gemm_split_core_x(
-        sm,
-        [&](int k, float4 &u, float4 &v) {
-            u = make_float4(0.f, 0.f, 0.f, 0.f);
-            v = u;
-            if (has) combined8(cs, row, kb + k + 8 * sc, ct == 0, u, v);
-        },
-        wp, nbat, tid, acc);
-    float *dst = p.part + (((size_t)sp * p.RT + rt) * p.CT + ct) * (32 * kPT);
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-        for (int e = 0; e < 16; e++)
-            dst[(8 * (e >> 2) + 4 * hf + (e & 3)) * kPT + 64 * wave + 32 * cb + j] = acc[cb][e];
-}
-
 }  // namespace
 
 ProjPlan proj_plan(int M, int K, int N) {
@@ -272,29 +175,6 @@ hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, f
         proj_split_kernel<<<grid, 256, 0, st>>>(p);
         proj_reduce_kernel<<<plan.RT * plan.CT * 4, 256, 0, st>>>(p);
     }
-    return hipGetLastError();
-}
-
-hipError_t launch_proj_combine(const CombineSrc &cs, int M, int K, const uint16_t *w, int N, float *act,
-                               float *stash, const ProjPlan &plan, float *part, hipStream_t st) {
-    if (K % kKC != 0 || M <= 0 || N <= 0 || plan.n_split < 2) return hipErrorInvalidValue;
-    ProjArgs p;
-    p.a = nullptr;
-    p.w = reinterpret_cast<const _Float16 *>(w);
-    p.act = act;
-    p.stash = stash;
-    p.part = part;
-    p.M = M;
-    p.N = N;
-    p.K = K;
-    p.RT = plan.RT;
-    p.CT = plan.CT;
-    p.kps = plan.kps;
-    p.n_split = plan.n_split;
-    p.n_wg = plan.RT * plan.CT * plan.n_split;
-    const int grid = (p.n_wg + 7) / 8 * 8;
-    proj_combine_split_kernel<<<grid, 256, 0, st>>>(p, cs);
-    proj_reduce_kernel<<<plan.RT * plan.CT * 4, 256, 0, st>>>(p);
     return hipGetLastError();
 }
 

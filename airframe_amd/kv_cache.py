@@ -251,49 +251,6 @@ class KVCache:
                                            _stream(stream)))
         return out
 
-    def attn_decode_append_proj(self, layer: int, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
-                                rope: RopeTable, wo: torch.Tensor, act: torch.Tensor,
-                                stash: torch.Tensor | None = None, out: torch.Tensor = None,
-                                softcap: float = 0.0, workspace: torch.Tensor = None, stream=None):
-        """attn_decode_append followed by attn_out_proj on its output in one call (the
-        main_attn_out_int4 + main_attn_proj pair of one decode layer), the split-K combine
-        merged into the projection.  wo: [dim, n_head * head_dim] f16; act (and stash):
-        [n_seq, dim] f32, act updated in place.  Returns the attention output
-        [n_seq, n_head, head_dim]."""
-        n_head = q.shape[1]
-        if q.dim() != 3 or q.shape[0] != self.n_seq or q.shape[2] != self.head_dim:
-            raise ValueError("q must be [n_seq, n_head, head_dim]")
-        self._check_kv(k.reshape(self.n_seq, 1, self.n_head_kv, self.head_dim),
-                       v.reshape(self.n_seq, 1, self.n_head_kv, self.head_dim), 1)
-        dim = wo.shape[0]
-        if wo.shape != (dim, n_head * self.head_dim):
-            raise ValueError("wo must be [dim, n_head * head_dim]")
-        if act.numel() != self.n_seq * dim or (stash is not None and stash.numel() != self.n_seq * dim):
-            raise ValueError("act/stash must hold [n_seq, dim]")
-        out = self._out_like(q, out)
-        ws = workspace
-        if ws is None:
-            b = ctypes.c_uint64()
-            check("ts_attn_decode_append_proj_workspace",
-                  load().ts_attn_decode_append_proj_workspace(self._h, n_head, dim, ctypes.byref(b)))
-            ws = torch.empty(max(b.value, 16), dtype=torch.uint8, device=q.device)
-        check("ts_attn_decode_append_proj",
-              load().ts_attn_decode_append_proj(
-                  self._h, layer, _ptr(k, torch.float32, "k"), _ptr(v, torch.float32, "v"),
-                  _ptr(q, torch.float32, "q"), n_head, rope.handle, softcap,
-                  _ptr(wo, torch.float16, "wo"), dim, _ptr(out, torch.float32, "out"),
-                  _ptr(act, torch.float32, "act"),
-                  _ptr(stash, torch.float32, "stash") if stash is not None else None,
-                  ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
-        return out
-
-    def proj_workspace(self, n_head: int, dim: int) -> torch.Tensor:
-        """A workspace for attn_decode_append_proj with n_head query heads and this dim."""
-        b = ctypes.c_uint64()
-        check("ts_attn_decode_append_proj_workspace",
-              load().ts_attn_decode_append_proj_workspace(self._h, n_head, dim, ctypes.byref(b)))
-        return torch.empty(max(b.value, 16), dtype=torch.uint8, device=torch.device("cuda"))
-
     def attn_prefill(self, layer: int, q: torch.Tensor, rope: RopeTable, out: torch.Tensor = None,
                      softcap: float = 0.0, stream=None):
         """Chunked-prefill causal attention.  q: [n_seq, n_tok, n_head, head_dim]."""

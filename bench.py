@@ -19,7 +19,6 @@ Other configs (--config 1,2,4 decode; 5 chunked prefill) print their own line.
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import math
 import os
@@ -469,77 +468,6 @@ def run_proj(args, cfg):
     return ms, dim * K * 2 + M * K * 4 + M * dim * 8, 2.0 * M * dim * K, M
 
 
-def run_decode_proj(args, cfg):
-    """A/B of the split-K combine folded into the output projection: per layer, the fused
-    append + decode (ts_attn_decode_append, its combine launch included) followed by
-    ts_attn_out_proj, against ts_attn_decode_append_proj (the combine merged inside the
-    projection).  The config's cache shape and starting lengths (contents zero: the timing does
-    not depend on them), up to 8 layers with their own f16 weights, each variant captured as one
-    HIP graph of all layers and replayed.  Returns (us per layer unfused, fused, n_split)."""
-    import torch
-
-    from airframe_amd.kv_cache import KVCache, RopeTable, attn_out_proj
-    from airframe_amd import _lib
-
-    dev = torch.device("cuda:0")
-    L = min(cfg["layers"], 8)
-    n_head, n_kv, hd, B, dim = cfg["n_head"], cfg["n_kv"], cfg["hd"], cfg["batch"], cfg["dim"]
-    if "ragged" in cfg:
-        rng = np.random.default_rng(args.seed)
-        lens0 = [int(x) for x in rng.integers(cfg["ragged"][0], cfg["ragged"][1], size=B)]
-    else:
-        lens0 = [cfg["ctx"]] * B
-    kv = KVCache.new_int4(L, n_kv, hd, max(lens0) + 8, B)
-    rope = RopeTable(max(lens0) + 8, hd, cfg["theta"])
-    for s_, l in enumerate(lens0):
-        kv.set_seq_len(l, seq=s_)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
-    K = n_head * hd
-    wos = [(torch.randn((dim, K), generator=gen, device=dev) * 0.02).half() for _ in range(L)]
-    q = torch.randn((B, n_head, hd), generator=gen, device=dev)
-    k = torch.randn((B, 1, n_kv, hd), generator=gen, device=dev)
-    v = torch.randn((B, 1, n_kv, hd), generator=gen, device=dev)
-    act = torch.randn((B, dim), generator=gen, device=dev)
-    out = torch.empty((B, n_head, hd), device=dev)
-    ws_dec = kv.workspace(n_head)
-    b = ctypes.c_uint64()
-    _lib.check("ts_attn_out_proj_workspace", _lib.load().ts_attn_out_proj_workspace(B, K, dim, ctypes.byref(b)))
-    ws_proj = torch.empty(max(b.value, 16), dtype=torch.uint8, device=dev)
-    ws_f = kv.proj_workspace(n_head, dim)
-
-    def unfused():
-        for layer in range(L):
-            kv.attn_decode_append(layer, k, v, q, rope, out=out, workspace=ws_dec)
-            attn_out_proj(out.view(B, K), wos[layer], act, workspace=ws_proj)
-
-    def fused():
-        for layer in range(L):
-            kv.attn_decode_append_proj(layer, k, v, q, rope, wos[layer], act, out=out, workspace=ws_f)
-
-    res = []
-    for fn in (unfused, fused):
-        fn()
-        torch.cuda.synchronize()
-        cap = torch.cuda.Stream()
-        cap.wait_stream(torch.cuda.current_stream())
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr, stream=cap):
-            fn()
-        for _ in range(3):
-            gr.replay()
-        torch.cuda.synchronize()
-        reps = 20
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            gr.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        res.append(e0.elapsed_time(e1) * 1e3 / (reps * L))
-    return res[0], res[1], lens0
-
-
 def run_compact(args, cfg):
     """Sliding-window compaction (ts_kv_shift) on a cache of the configuration's shape: every
     sequence of every layer filled to ctx, then each sequence compacted (keep_sink 4, shift
@@ -683,9 +611,6 @@ def main():
                     help="time the fused QKV projection + append (ts_qkv_append) instead")
     ap.add_argument("--proj", action="store_true",
                     help="time the attention output projection + residual (ts_attn_out_proj) instead")
-    ap.add_argument("--decode-proj", action="store_true",
-                    help="A/B of the decode + output projection per layer: combine launch + "
-                         "ts_attn_out_proj against ts_attn_decode_append_proj")
     ap.add_argument("--compact", action="store_true",
                     help="measure sliding-window compaction (ts_kv_shift) on the config's cache "
                          "instead of the decode step")
@@ -750,19 +675,6 @@ def main():
             "config": {"workload": cfg["name"] + ("_qkv" if args.qkv else "_oproj") + ("_qknorm" if args.qk_norm else ""),
                        "tokens_per_call": toks, "dim": cfg["dim"]},
             "roofline": roof, "data": "synthetic (random f16 weights, N(0,1) x)"}), flush=True)
-        return
-    if args.decode_proj:
-        if "ctx" not in cfg:
-            sys.exit("--decode-proj needs a decode configuration (1-4)")
-        us_u, us_f, lens0 = run_decode_proj(args, cfg)
-        print(json.dumps({
-            "metric": "decode attention + output projection, us per layer (combine launch vs merged into the projection)",
-            "value": round(us_f, 2), "unit": "us", "n_gpus": 1, "higher_is_better": False,
-            "unfused_us_per_layer": round(us_u, 2), "fused_us_per_layer": round(us_f, 2),
-            "speedup": round(us_u / us_f, 4),
-            "config": {"workload": cfg["name"] + "_decode_oproj", "dim": cfg["dim"],
-                       "lens": lens0[:8]},
-            "data": "synthetic (zero cache contents, random q/k/v and f16 weights)"}), flush=True)
         return
     if args.stream_ceiling:
         if "ctx" not in cfg or "ragged" in cfg:

@@ -263,23 +263,6 @@ int ts_attn_out_proj(const float *d_attn, int32_t n_tok, int32_t attn_dim, const
                      int32_t dim, float *d_act, float *d_stash, void *d_workspace,
                      uint64_t workspace_bytes, void *stream);
 
-/* Bytes of workspace ts_attn_decode_append_proj needs for n_head query heads and this dim.
- * Host only. */
-int ts_attn_decode_append_proj_workspace(const ts_kv *kv, int32_t n_head, int32_t dim, uint64_t *bytes);
-
-/* One decode token per sequence through main_attn_out_int4 and main_attn_proj in one call, as
- * the reference's layer encodes them back to back (pipeline/layer.rs:1100-1115): the append of
- * d_k/d_v and the attention of ts_attn_decode_append, then ts_attn_out_proj on its output,
- * with the split-K combine folded into the projection (each of its column tiles merges the
- * attention splits it reads; no separate combine launch).  d_attn: [n_seq][n_head][head_dim]
- * f32, receives the attention output; d_wo, d_act, d_stash as ts_attn_out_proj with
- * attn_dim = n_head * head_dim and n_tok = n_seq.  Lengths do not change. */
-int ts_attn_decode_append_proj(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
-                               const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
-                               const uint16_t *d_wo, int32_t dim, float *d_attn, float *d_act,
-                               float *d_stash, void *d_workspace, uint64_t workspace_bytes,
-                               void *stream);
-
 #ifdef __cplusplus
 }
 #endif
