@@ -47,7 +47,9 @@ struct DecodeArgs {
     const float *rope;
     int rope_pairs;
     int n_head;
-    int G;
+    int G;   // query heads per workgroup: n_head / n_kv, at most 8 per group (16x16 kernel)
+    int Gt;  // query heads per kv head (n_head / n_kv)
+    int NG;  // head groups per kv head: grid.y = n_kv * NG (G4 kernel: 1)
     int chunk;
     int n_split;  // grid.x: the last split of a sequence runs to its end
     float inv_sqrt_hd;
@@ -307,9 +309,11 @@ __device__ __forceinline__ void append_load(const DecodeArgs &a, int s, int h, i
     (void)NTD;
 }
 
+// write = false: only the dequantized rows (a head group other than the first, whose
+// workgroup quantizes the same row for its own heads' scores).
 template <int HD, bool NORM>
 __device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane, const AppendIn &in,
-                             float *kd, float *vd) {
+                             float *kd, float *vd, bool write = true) {
     constexpr int ROWB = HD / 2;
     const KvLayerView &L = a.L;
     const bool KN = NORM && L.kn != nullptr;  // QK norm of K
@@ -336,9 +340,9 @@ __device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane,
     uint32_t kw = on ? (c0 | (c1 << 4)) << (8 * (i & 3)) : 0u;
     kw |= __shfl_xor(kw, 1, 64);
     kw |= __shfl_xor(kw, 2, 64);
-    if (on && (i & 3) == 0)
+    if (write && on && (i & 3) == 0)
         reinterpret_cast<uint32_t *>(L.kp + row * L.P * ROWB)[k_word_idx<HD>(p, i >> 2)] = kw;
-    if (lane == 0) {
+    if (write && lane == 0) {
         L.ks[row * L.P + p] = ks;
         L.vs[row * L.P + p] = vs;
     }
@@ -347,10 +351,12 @@ __device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane,
     const int q = p & 31, t = q >> 4, gq = (q & 15) >> 2, nib = (q & 3) + 4 * t;
     uint32_t *vb = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / 32) + (p >> 5)) * (HD * 16));
     if (on) {
+        if (write) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int d = 2 * i + j;
-            vb[v_word_idx(gq * 16 + (d & 15), d >> 4)] = (in.vold[j] & ~(0xFu << (4 * nib))) | ((j ? e1 : e0) << (4 * nib));
+            for (int j = 0; j < 2; j++) {
+                const int d = 2 * i + j;
+                vb[v_word_idx(gq * 16 + (d & 15), d >> 4)] = (in.vold[j] & ~(0xFu << (4 * nib))) | ((j ? e1 : e0) << (4 * nib));
+            }
         }
         kd[2 * i] = (float)((int)c0 - 8) * ks;
         kd[2 * i + 1] = (float)((int)c1 - 8) * ks;
@@ -367,14 +373,15 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
 }
 
 // Scores of the new position (dequantized row kd, in this wave's LDS) for the G query heads
-// of kv head h, in the exp2 domain, from the rotated f32 q (as load_q8 rotates it); one wave.
+// hb .. hb + G - 1 of sequence s, in the exp2 domain, from the rotated f32 q (as load_q8
+// rotates it); one wave.
 // qp[hh]: dims (2i, 2i+1) of head hh's raw q (lane i < HD/2), cs: the rotation of pair i at
 // the query's rotation position.
 template <int HD, bool SOFTCAP, bool NORM, int GMAX>
-__device__ void new_token_scores(const DecodeArgs &a, int s, int h, int G, int lane, const float2 (&qp)[GMAX],
+__device__ void new_token_scores(const DecodeArgs &a, int s, int hb, int G, int lane, const float2 (&qp)[GMAX],
                                  float2 cs, const float *kd, float *xnew) {
     const float *const QN = NORM ? a.L.qn : nullptr;
-    const float *qg = a.q + ((size_t)s * a.n_head + h * G) * HD;
+    const float *qg = a.q + ((size_t)s * a.n_head + hb) * HD;
     const int i = lane < HD / 2 ? lane : 0;
 #pragma unroll
     for (int hh = 0; hh < GMAX; hh++) {
@@ -395,10 +402,10 @@ __device__ void new_token_scores(const DecodeArgs &a, int s, int h, int G, int l
     }
 }
 
-// The raw q pairs new_token_scores takes: dims (2i, 2i+1) of the G heads of kv head h.
+// The raw q pairs new_token_scores takes: dims (2i, 2i+1) of query heads hb .. hb + G - 1.
 template <int HD, int GMAX>
-__device__ __forceinline__ void load_q_pairs(const DecodeArgs &a, int s, int h, int G, int lane, float2 (&qp)[GMAX]) {
-    const float *qg = a.q + ((size_t)s * a.n_head + h * G) * HD;
+__device__ __forceinline__ void load_q_pairs(const DecodeArgs &a, int s, int hb, int G, int lane, float2 (&qp)[GMAX]) {
+    const float *qg = a.q + ((size_t)s * a.n_head + hb) * HD;
     const int i = lane < HD / 2 ? lane : 0;
 #pragma unroll
     for (int hh = 0; hh < GMAX; hh++)
@@ -427,14 +434,17 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     constexpr int OST = HD + 1;
     const KvLayerView &L = a.L;
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
-    const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+    const int split = blockIdx.x, s = blockIdx.z;
+    // kv head h, and head group gi of its a.Gt query heads (groups of 8)
+    const int h = blockIdx.y / a.NG, gi = blockIdx.y - h * a.NG;
     const int start = split * a.chunk;
     const int tid = threadIdx.x, lane = tid & 63;
     // wave index in an SGPR: window bases are then provably wave-uniform and feed the scalar
     // offset of the buffer loads directly
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
-    const int G = a.G;
+    const int G = min(a.G, a.Gt - 8 * gi);  // query heads of this workgroup
+    const int hb = h * a.Gt + 8 * gi;       // the first of them within the sequence
     const size_t row = (size_t)s * L.H + h;
     const uint8_t *kbase = L.kp + row * L.P * ROWB;
     const uint8_t *vbase = L.vp + row * (L.P / 32) * (HD * 16);
@@ -457,7 +467,7 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     // h*G + n - G (G <= n < 2G), unused beyond
     const bool live = n < 2 * G, lo_col = n >= G;
     const int qhead = n < G ? n : (live ? n - G : 0);
-    const float *qrow = a.q + ((size_t)s * a.n_head + h * G + qhead) * HD;
+    const float *qrow = a.q + ((size_t)s * a.n_head + hb + qhead) * HD;
     float qraw[WPG][8];
 #pragma unroll
     for (int t = 0; t < WPG; t++) q_read8(qrow, k16_word<HD>(g, t), nullptr, 1.0f, qraw[t]);
@@ -502,7 +512,7 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     // for all 64 lanes; zero in the columns past G.
     // One power-of-two scale for the G heads: every wave reads the bound of all of them.
     // QK norm scale of this lane's query head (each wave computes it for itself)
-    const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, qhead, L.norm_eps)
+    const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + hb) * HD, G, qhead, L.norm_eps)
                         : 1.0f;
     if (QN) {
 #pragma unroll
@@ -536,9 +546,9 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
         AppendIn ain;
         float2 qp[8];
         append_load<HD, NORM>(a, s, h, qpos, lane, ain);
-        load_q_pairs<HD, 8>(a, s, h, G, lane, qp);
-        append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd);
-        new_token_scores<HD, SOFTCAP, NORM, 8>(a, s, h, G, lane, qp, ain.cs, kd, xnew);
+        load_q_pairs<HD, 8>(a, s, hb, G, lane, qp);
+        append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd, gi == 0);
+        new_token_scores<HD, SOFTCAP, NORM, 8>(a, s, hb, G, lane, qp, ain.cs, kd, xnew);
     }
 
     WaveState<HD> st;
@@ -603,7 +613,7 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
             acc += e * vd[d];
             lsum += e;
         }
-        const size_t head = (size_t)s * a.n_head + h * G + hh;
+        const size_t head = (size_t)s * a.n_head + hb + hh;
         if (n_split_s == 1)
             a.out[head * HD + d] = lsum > 0.0f ? acc / lsum : 0.0f;
         else
@@ -1003,7 +1013,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         // merge.
         if (appender) {
             append_load<HD, NORM>(a, s, h, qpos, lane, ain);
-            load_q_pairs<HD, 4>(a, s, h, G, lane, qp);
+            load_q_pairs<HD, 4>(a, s, h * G, G, lane, qp);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1068,7 +1078,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     }
     if (appender) {
         append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd);
-        new_token_scores<HD, SOFTCAP, NORM, 4>(a, s, h, G, lane, qp, ain.cs, kd, xnew);
+        new_token_scores<HD, SOFTCAP, NORM, 4>(a, s, h * G, G, lane, qp, ain.cs, kd, xnew);
     }
 
     WaveState8<HD> st;
@@ -1190,7 +1200,8 @@ DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_c
         p.chunk = plan_chunk(n_ctx, n_seq, n_kv, n_cu);
         p.g4 = p.chunk >= kG4MinChunk;
     }
-    if (!p.g4) p.chunk = plan_chunk(n_ctx, n_seq, n_kv, 2 * n_cu);
+    // the 16x16 kernel takes up to 8 query heads per workgroup: more as several head groups
+    if (!p.g4) p.chunk = plan_chunk(n_ctx, n_seq, n_kv * ((G + 7) / 8), 2 * n_cu);
     p.n_split = (max_ctx + p.chunk - 1) / p.chunk;
     return p;
 }
@@ -1212,7 +1223,9 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.rope = rope;
     a.rope_pairs = rope_pairs;
     a.n_head = n_head;
-    a.G = n_head / L.H;
+    a.Gt = n_head / L.H;
+    a.NG = plan.g4 ? 1 : (a.Gt + 7) / 8;
+    a.G = std::min(a.Gt, 8);
     a.chunk = plan.chunk;
     a.n_split = plan.n_split;
     a.inv_sqrt_hd = 1.0f / sqrtf((float)L.hd);
@@ -1221,7 +1234,7 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.ws = ws;
     a.k_new = k_new;
     a.v_new = v_new;
-    dim3 grid(plan.n_split, L.H, L.S);
+    dim3 grid(plan.n_split, L.H * a.NG, L.S);
     // The G <= 4 kernel does less VALU work per window than the 16x16 one but has the longer
     // per-window dependency chain; it runs when every wave streams at least 4 windows of its
     // split (plan.g4).  It fits two workgroups per CU by registers, but the plan wants one per

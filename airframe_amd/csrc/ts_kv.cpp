@@ -383,8 +383,10 @@ int ts_requant_all(ts_kv *kv, int32_t layer, const float *d_k_cache, const float
                                                as_stream(stream)));
 }
 
+// Any GQA group size: the decode takes more than 8 query heads per kv head as several head
+// groups (each reads the kv head's stream).
 static bool heads_ok(const ts_kv *kv, int32_t n_head) {
-    return n_head > 0 && n_head % kv->d.n_head_kv == 0 && n_head / kv->d.n_head_kv <= 8;
+    return n_head > 0 && n_head % kv->d.n_head_kv == 0;
 }
 
 int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes) {

@@ -187,8 +187,8 @@ int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes);
  * d_q: [n_seq][n_head][head_dim] raw f32 for the token just appended; it is rotated at
  * position len[s] and attends to positions 0..len[s] (len[s]+1 keys, the state between
  * ts_append_quant and ts_kv_increment, like CacheParams{current_pos, seq_len+1}).
- * d_out: [n_seq][n_head][head_dim] f32.  n_head must be a multiple of n_head_kv with
- * n_head/n_head_kv <= 8.  softcap > 0 applies tanh(s/softcap)*softcap to the scaled scores
+ * d_out: [n_seq][n_head][head_dim] f32.  n_head must be a multiple of n_head_kv (any group
+ * size; more than 8 query heads per kv head run as groups of 8).  softcap > 0 applies tanh(s/softcap)*softcap to the scaled scores
  * (sh_layer_v1_int4.wgsl:1116-1118).  d_workspace: ts_attn_decode_workspace bytes. */
 int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
                    const ts_rope *rope, float softcap, float *d_out, void *d_workspace,

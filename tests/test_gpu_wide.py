@@ -1,0 +1,58 @@
+"""GPU parity beyond the configurations' shapes: GQA groups of more than 8 query heads per kv
+head (the decode runs them as groups of 8, each reading the kv head's stream; the reference
+accepts any n_head that n_head_kv divides, kv_cache.rs / attention.rs).  Decode (fused with
+the append, and separate, with splits) and prefill against the oracle, |err| <= 2e-3 +
+1e-3*|ref|; appended codes bit-exact."""
+import numpy as np
+import pytest
+
+from airframe_amd import synth
+from tests.gpu_util import Pair, assert_close, dev, say
+from tests.test_gpu_decode_append import fill, fused_step
+from tests.test_gpu_prefill import run_chunks
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("n_kv,n_head,hd,softcap", [
+    (2, 24, 128, 0.0),   # G = 12: a group of 8 and one of 4
+    (1, 16, 64, 0.0),    # G = 16, one kv head
+    (1, 32, 128, 30.0),  # G = 32 (multi-query), softcap
+])
+def test_fused_decode_large_groups(gpu, n_kv, n_head, hd, softcap):
+    say(f"fused decode G={n_head // n_kv} n_kv={n_kv} hd={hd} softcap={softcap}")
+    rng = np.random.default_rng(300 + n_head + hd)
+    lens = [1500, 3, 640, 2047]
+    p = Pair(len(lens), n_kv, hd, 2100, 500000.0)
+    fill(p, rng, max(lens))
+    p.set_lens(lens)
+    for _ in range(2):
+        out, ref = fused_step(p, rng, n_head, softcap=softcap)
+        assert_close(out, ref, "fused out")
+    p.check_codes()
+
+
+def test_separate_decode_large_group(gpu):
+    say("separate decode G=12")
+    rng = np.random.default_rng(310)
+    n_kv, n_head, hd = 2, 24, 128
+    p = Pair(3, n_kv, hd, 1300, 500000.0)
+    fill(p, rng, 1200)
+    p.set_lens([1200, 17, 800])
+    k = synth.normal(rng, (3, 1, n_kv, hd))
+    v = synth.normal(rng, (3, 1, n_kv, hd))
+    q = synth.normal(rng, (3, n_head, hd))
+    p.append(k, v)
+    out = p.gpu.attn_decode(0, dev(q), p.rope).cpu().numpy()
+    ref = p.ora.attend(q[:, None], 1, threads=8)[:, 0]
+    assert_close(out, ref, "decode out")
+
+
+@pytest.mark.parametrize("n_kv,n_head,hd", [(2, 24, 128), (1, 16, 64)])
+def test_prefill_large_groups(gpu, n_kv, n_head, hd):
+    say(f"prefill G={n_head // n_kv} hd={hd}")
+    rng = np.random.default_rng(320 + n_head)
+    p = Pair(2, n_kv, hd, 300, 500000.0)
+    p.set_lens([0, 37])
+    run_chunks(p, rng, n_head, [50, 90])
+    p.check_codes()
