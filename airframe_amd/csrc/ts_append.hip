@@ -44,9 +44,14 @@ __global__ __launch_bounds__(256) void quantize_rows64_kernel(KvLayerView L, con
     const int pc = min(max(p0 + 4 * wave + (r8 & 3) + 16 * (r8 >> 2), lo), hi - 1);
     float2 cs[4];
     rope_cs4(L, s, pc, rope, rope_pairs, l, cs);
-    const size_t src = (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD + 8 * l;
-    const float4 a0 = *reinterpret_cast<const float4 *>(k + src), a1 = *reinterpret_cast<const float4 *>(k + src + 4);
-    const float4 b0 = *reinterpret_cast<const float4 *>(v + src), b1 = *reinterpret_cast<const float4 *>(v + src + 4);
+    // rows of hdr floats; the stored dims past hdr quantize zeros (code 8)
+    // (lanes past the row load its first dims, unconditionally, and drop them)
+    const bool in = 8 * l < L.hdr;
+    const size_t src = (((size_t)s * ld_tok + (pc - start)) * L.H + h) * L.hdr + 8 * (in ? l : 0);
+    const float4 a0 = keep4(in, *reinterpret_cast<const float4 *>(k + src));
+    const float4 a1 = keep4(in, *reinterpret_cast<const float4 *>(k + src + 4));
+    const float4 b0 = keep4(in, *reinterpret_cast<const float4 *>(v + src));
+    const float4 b1 = keep4(in, *reinterpret_cast<const float4 *>(v + src + 4));
     float kx[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
     const float vx[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
     store_block64(L, s, h, blk, lo, hi, kx, vx, cs, rope ? rope_pairs : 0, wave, lane);
@@ -87,9 +92,13 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
                             ? *reinterpret_cast<const float2 *>(rope + ((size_t)pr * rope_pairs + pair) * 2)
                             : make_float2(1.0f, 0.0f);
         }
-        const float4 *ks4 = reinterpret_cast<const float4 *>(k + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD + 8 * l);
-        const float4 *vs4 = reinterpret_cast<const float4 *>(v + (((size_t)s * ld_tok + (pc - start)) * L.H + h) * HD + 8 * l);
-        const float4 a = ks4[0], b = ks4[1], c = vs4[0], d = vs4[1];
+        // rows of hdr floats; the stored dims past hdr quantize zeros (code 8)
+        // (lanes past the row load its first dims, unconditionally, and drop them)
+        const bool in = 8 * l < L.hdr;
+        const size_t src = (((size_t)s * ld_tok + (pc - start)) * L.H + h) * L.hdr + 8 * (in ? l : 0);
+        const float4 *ks4 = reinterpret_cast<const float4 *>(k + src);
+        const float4 *vs4 = reinterpret_cast<const float4 *>(v + src);
+        const float4 a = keep4(in, ks4[0]), b = keep4(in, ks4[1]), c = keep4(in, vs4[0]), d = keep4(in, vs4[1]);
         kx[rd][0] = a.x; kx[rd][1] = a.y; kx[rd][2] = a.z; kx[rd][3] = a.w;
         kx[rd][4] = b.x; kx[rd][5] = b.y; kx[rd][6] = b.z; kx[rd][7] = b.w;
         vx[rd][0] = c.x; vx[rd][1] = c.y; vx[rd][2] = c.z; vx[rd][3] = c.w;
@@ -102,7 +111,7 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
 template <int HD>
 __global__ void export_kernel(KvLayerView L, int seq, int pos0, int n_pos, uint32_t *kp,
                               uint32_t *vp, float *ks, float *vs) {
-    constexpr int WPR = HD / 8;
+    const int WPR = L.hdr / 8;  // the reference row: hdr dims
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     const long total = (long)n_pos * L.H * WPR;
     if (idx >= total) return;
@@ -132,7 +141,7 @@ __global__ void export_kernel(KvLayerView L, int seq, int pos0, int n_pos, uint3
 template <int HD>
 __global__ void import_k_kernel(KvLayerView L, int seq, int pos0, int n_pos, const uint32_t *kp,
                                 const float *ks, const float *vs) {
-    constexpr int WPR = HD / 8;
+    const int WPR = L.hdr / 8;  // the reference row: hdr dims (stored words past it keep code 8)
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     const long total = (long)n_pos * L.H * WPR;
     if (idx >= total) return;
@@ -164,6 +173,7 @@ __global__ void import_v_kernel(KvLayerView L, int seq, int pos0, int n_pos, con
     const int c = w >> 2, ln = c & 63, td = ((c >> 6) << 2) | (w & 3);
     const int g = ln >> 4, dl = ln & 15;
     const int d = 16 * td + dl;
+    if (d >= L.hdr) return;  // a stored dim past the reference row: keeps code 8
     const size_t row = (size_t)seq * L.H + h;
     uint32_t *dst = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / 32) + b) * (HD * 16)) + w;
     uint32_t word = *dst;
@@ -171,7 +181,7 @@ __global__ void import_v_kernel(KvLayerView L, int seq, int pos0, int n_pos, con
     for (int n = 0; n < 8; n++) {
         const int p = 32 * b + (n < 4 ? 4 * g + n : 16 + 4 * g + n - 4);
         if (p >= pos0 && p < pos0 + n_pos) {
-            const uint32_t src = vp[((size_t)(p - pos0) * L.H + h) * (HD / 8) + d / 8];
+            const uint32_t src = vp[((size_t)(p - pos0) * L.H + h) * (L.hdr / 8) + d / 8];
             word = (word & ~(0xFu << (4 * n))) | (((src >> (4 * (d % 8))) & 0xFu) << (4 * n));
         }
     }
@@ -204,7 +214,7 @@ hipError_t launch_quantize_rows(const KvLayerView &L, const float *k, const floa
 
 hipError_t launch_export(const KvLayerView &L, int seq, int pos0, int n_pos, uint32_t *kp,
                          uint32_t *vp, float *ks, float *vs, hipStream_t st) {
-    const long total = (long)n_pos * L.H * (L.hd / 8);
+    const long total = (long)n_pos * L.H * (L.hdr / 8);
     const int blocks = (int)((total + 255) / 256);
     if (L.hd == 128)
         export_kernel<128><<<blocks, 256, 0, st>>>(L, seq, pos0, n_pos, kp, vp, ks, vs);
@@ -217,7 +227,7 @@ hipError_t launch_export(const KvLayerView &L, int seq, int pos0, int n_pos, uin
 
 hipError_t launch_import(const KvLayerView &L, int seq, int pos0, int n_pos, const uint32_t *kp,
                          const uint32_t *vp, const float *ks, const float *vs, hipStream_t st) {
-    const long nk = (long)n_pos * L.H * (L.hd / 8);
+    const long nk = (long)n_pos * L.H * (L.hdr / 8);
     const int nb = (pos0 + n_pos - 1) / 32 - pos0 / 32 + 1;
     const long nv = (long)L.H * nb * L.hd * 4;
     if (L.hd == 128) {

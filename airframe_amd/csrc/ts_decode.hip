@@ -282,23 +282,25 @@ struct AppendIn {
 };
 
 template <int HD, bool NORM>
-__device__ __forceinline__ void append_load(const DecodeArgs &a, int s, int h, int p, int lane, AppendIn &in) {
+__device__ __forceinline__ void append_load(const DecodeArgs &a, int s, int h, int p, int lane, AppendIn &in,
+                                            int hdr) {
     constexpr int NTD = HD / 16;
     const KvLayerView &L = a.L;
     const size_t row = (size_t)s * L.H + h;
     const bool on = lane < HD / 2;
     const int i = on ? lane : 0;
-    const size_t src = row * HD + 2 * i;
-    in.k0 = in.k1 = in.v0 = in.v1 = 0.f;
-    if (on) {
-        const float2 kk = *reinterpret_cast<const float2 *>(a.k_new + src);
-        const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
-        in.k0 = kk.x; in.k1 = kk.y; in.v0 = vv.x; in.v1 = vv.y;
-    }
+    // rows of hdr floats; the stored dims past them are 0 (their lanes load the row's first
+    // pair, unconditionally, and drop it)
+    const bool dim_in = on && 2 * i < hdr;
+    const size_t src = row * hdr + 2 * (dim_in ? i : 0);
+    const float2 kk = *reinterpret_cast<const float2 *>(a.k_new + src);
+    const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
+    in.k0 = dim_in ? kk.x : 0.f; in.k1 = dim_in ? kk.y : 0.f;
+    in.v0 = dim_in ? vv.x : 0.f; in.v1 = dim_in ? vv.y : 0.f;
     const int ir = i < a.rope_pairs ? i : 0;
     in.cs = *reinterpret_cast<const float2 *>(a.rope + ((size_t)rot_of(L, s, p) * a.rope_pairs + ir) * 2);
-    in.kn0 = NORM && L.kn ? L.kn[2 * i] : 1.0f;
-    in.kn1 = NORM && L.kn ? L.kn[2 * i + 1] : 1.0f;
+    in.kn0 = NORM && L.kn && 2 * i < hdr ? L.kn[2 * i] : 1.0f;
+    in.kn1 = NORM && L.kn && 2 * i < hdr ? L.kn[2 * i + 1] : 1.0f;
     const int q = p & 31, gq = (q & 15) >> 2;
     const uint32_t *vb = reinterpret_cast<const uint32_t *>(L.vp + (row * (L.P / 32) + (p >> 5)) * (HD * 16));
 #pragma unroll
@@ -313,7 +315,7 @@ __device__ __forceinline__ void append_load(const DecodeArgs &a, int s, int h, i
 // workgroup quantizes the same row for its own heads' scores).
 template <int HD, bool NORM>
 __device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane, const AppendIn &in,
-                             float *kd, float *vd, bool write = true) {
+                             float *kd, float *vd, int hdr, bool write = true) {
     constexpr int ROWB = HD / 2;
     const KvLayerView &L = a.L;
     const bool KN = NORM && L.kn != nullptr;  // QK norm of K
@@ -324,7 +326,7 @@ __device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane,
     const float v0 = in.v0, v1 = in.v1;
     // QK norm scale of the new K row: its squares summed in dimension order across the lanes
     float ns = 0.0f;
-    if (KN) ns = qk_norm_scale_from_sum(ordered_sum_pairs(sq_rn(k0), sq_rn(k1), HD / 2), HD, L.norm_eps);
+    if (KN) ns = qk_norm_scale_from_sum(ordered_sum_pairs(sq_rn(k0), sq_rn(k1), HD / 2), hdr, L.norm_eps);
     if (on) {
         if (KN) {
             k0 = qk_norm_apply(k0, ns, in.kn0);
@@ -368,8 +370,8 @@ __device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane,
 template <int HD, bool NORM>
 __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, float *kd, float *vd) {
     AppendIn in;
-    append_load<HD, NORM>(a, s, h, p, lane, in);
-    append_store<HD, NORM>(a, s, h, p, lane, in, kd, vd);
+    append_load<HD, NORM>(a, s, h, p, lane, in, a.L.hdr);
+    append_store<HD, NORM>(a, s, h, p, lane, in, kd, vd, a.L.hdr);
 }
 
 // Scores of the new position (dequantized row kd, in this wave's LDS) for the G query heads
@@ -379,18 +381,20 @@ __device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, f
 // the query's rotation position.
 template <int HD, bool SOFTCAP, bool NORM, int GMAX>
 __device__ void new_token_scores(const DecodeArgs &a, int s, int hb, int G, int lane, const float2 (&qp)[GMAX],
-                                 float2 cs, const float *kd, float *xnew) {
+                                 float2 cs, const float *kd, float *xnew, int hdr) {
     const float *const QN = NORM ? a.L.qn : nullptr;
-    const float *qg = a.q + ((size_t)s * a.n_head + hb) * HD;
+    const float *qg = a.q + ((size_t)s * a.n_head + hb) * hdr;
     const int i = lane < HD / 2 ? lane : 0;
 #pragma unroll
     for (int hh = 0; hh < GMAX; hh++) {
         if (hh >= G) break;
         float q0 = qp[hh].x, q1 = qp[hh].y;
         if (QN) {
-            const float nh = q_norm_scale_wave<HD>(qg, G, hh, a.L.norm_eps);
-            q0 = qk_norm_apply(q0, nh, QN[2 * i]);
-            q1 = qk_norm_apply(q1, nh, QN[2 * i + 1]);
+            const float nh = q_norm_scale_wave<HD>(qg, G, hh, a.L.norm_eps, hdr);
+            if (2 * i < hdr) {
+                q0 = qk_norm_apply(q0, nh, QN[2 * i]);
+                q1 = qk_norm_apply(q1, nh, QN[2 * i + 1]);
+            }
         }
         if (i < a.rope_pairs) rope_rotate(q0, q1, cs);
         float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
@@ -404,12 +408,16 @@ __device__ void new_token_scores(const DecodeArgs &a, int s, int hb, int G, int 
 
 // The raw q pairs new_token_scores takes: dims (2i, 2i+1) of query heads hb .. hb + G - 1.
 template <int HD, int GMAX>
-__device__ __forceinline__ void load_q_pairs(const DecodeArgs &a, int s, int hb, int G, int lane, float2 (&qp)[GMAX]) {
-    const float *qg = a.q + ((size_t)s * a.n_head + hb) * HD;
+__device__ __forceinline__ void load_q_pairs(const DecodeArgs &a, int s, int hb, int G, int lane, float2 (&qp)[GMAX],
+                                             int hdr) {
+    const float *qg = a.q + ((size_t)s * a.n_head + hb) * hdr;
     const int i = lane < HD / 2 ? lane : 0;
 #pragma unroll
-    for (int hh = 0; hh < GMAX; hh++)
-        qp[hh] = hh < G ? *reinterpret_cast<const float2 *>(qg + (size_t)hh * HD + 2 * i) : make_float2(0.f, 0.f);
+    for (int hh = 0; hh < GMAX; hh++) {
+        const float2 t = *reinterpret_cast<const float2 *>(qg + (size_t)(hh < G ? hh : 0) * hdr + 2 * (2 * i < hdr ? i : 0));
+        const bool use = hh < G && 2 * i < hdr;
+        qp[hh] = make_float2(use ? t.x : 0.f, use ? t.y : 0.f);
+    }
 }
 
 // Split partial of one head: unnormalized o (dim d), and with d == 0 the reference exponent m
@@ -424,7 +432,9 @@ __device__ inline void store_partial(const DecodeArgs &a, size_t head, int split
     }
 }
 
-template <int HD, bool SOFTCAP, bool NORM>
+// PAD: the caller's head dim hdr is below the stored HD (rows of q, new K/V and the output are
+// hdr floats; the stored dims past them hold zeros).
+template <int HD, bool SOFTCAP, bool NORM, bool PAD>
 __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs a) {
     constexpr int NW = kNW16;  // waves per workgroup
     constexpr int SPAN = 64 * NW;     // positions one round of windows covers
@@ -433,6 +443,7 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     constexpr int ROWB = HD / 2;   // bytes per K row
     constexpr int OST = HD + 1;
     const KvLayerView &L = a.L;
+    const int hdr = PAD ? L.hdr : HD;
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     const int split = blockIdx.x, s = blockIdx.z;
     // kv head h, and head group gi of its a.Gt query heads (groups of 8)
@@ -467,10 +478,10 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     // h*G + n - G (G <= n < 2G), unused beyond
     const bool live = n < 2 * G, lo_col = n >= G;
     const int qhead = n < G ? n : (live ? n - G : 0);
-    const float *qrow = a.q + ((size_t)s * a.n_head + hb + qhead) * HD;
+    const float *qrow = a.q + ((size_t)s * a.n_head + hb + qhead) * hdr;
     float qraw[WPG][8];
 #pragma unroll
-    for (int t = 0; t < WPG; t++) q_read8(qrow, k16_word<HD>(g, t), nullptr, 1.0f, qraw[t]);
+    for (int t = 0; t < WPG; t++) q_read8(qrow, k16_word<HD>(g, t), nullptr, 1.0f, qraw[t], hdr);
     asm volatile("" ::: "memory");
 
     const int qpos = a.len[s];
@@ -512,13 +523,15 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     // for all 64 lanes; zero in the columns past G.
     // One power-of-two scale for the G heads: every wave reads the bound of all of them.
     // QK norm scale of this lane's query head (each wave computes it for itself)
-    const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + hb) * HD, G, qhead, L.norm_eps)
+    const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + hb) * hdr, G, qhead, L.norm_eps, hdr)
                         : 1.0f;
     if (QN) {
 #pragma unroll
         for (int t = 0; t < WPG; t++)
+            if (8 * k16_word<HD>(g, t) < hdr) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) qraw[t][e] = qk_norm_apply(qraw[t][e], ns, QN[8 * k16_word<HD>(g, t) + e]);
+                for (int e = 0; e < 8; e++) qraw[t][e] = qk_norm_apply(qraw[t][e], ns, QN[8 * k16_word<HD>(g, t) + e]);
+            }
     }
     float q_s, inv_s;
     {
@@ -545,10 +558,10 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     if (fused && wave == NW - 1) {
         AppendIn ain;
         float2 qp[8];
-        append_load<HD, NORM>(a, s, h, qpos, lane, ain);
-        load_q_pairs<HD, 8>(a, s, hb, G, lane, qp);
-        append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd, gi == 0);
-        new_token_scores<HD, SOFTCAP, NORM, 8>(a, s, hb, G, lane, qp, ain.cs, kd, xnew);
+        append_load<HD, NORM>(a, s, h, qpos, lane, ain, hdr);
+        load_q_pairs<HD, 8>(a, s, hb, G, lane, qp, hdr);
+        append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd, hdr, gi == 0);
+        new_token_scores<HD, SOFTCAP, NORM, 8>(a, s, hb, G, lane, qp, ain.cs, kd, xnew, hdr);
     }
 
     WaveState<HD> st;
@@ -614,10 +627,11 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
             lsum += e;
         }
         const size_t head = (size_t)s * a.n_head + hb + hh;
-        if (n_split_s == 1)
-            a.out[head * HD + d] = lsum > 0.0f ? acc / lsum : 0.0f;
-        else
+        if (n_split_s == 1) {
+            if (d < hdr) a.out[head * hdr + d] = lsum > 0.0f ? acc / lsum : 0.0f;
+        } else {
             store_partial(a, head, split, HD, d, acc, M, lsum);
+        }
     }
 }
 
@@ -681,7 +695,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     part[g][j] = acc;
     if (j == 0) lpart[g] = lsum;
     __syncthreads();
-    if (tid < V4) {
+    if (tid < V4 && 4 * tid < a.L.hdr) {
         float4 r = part[0][tid];
         float l = lpart[0];
 #pragma unroll
@@ -694,7 +708,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
             l += lpart[k];
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        float *o = a.out + hidx * HD + 4 * tid;  // d_out is only 4-byte aligned
+        float *o = a.out + hidx * a.L.hdr + 4 * tid;  // d_out rows of hdr floats
         o[0] = r.x * inv;
         o[1] = r.y * inv;
         o[2] = r.z * inv;
@@ -909,6 +923,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     constexpr int NM = HD / 64;  // i8 instructions per 16-position tile
     constexpr int OST = HD + 1;
     const KvLayerView &L = a.L;
+    constexpr int hdr = HD;  // (padded head dims take the 16x16 kernel)
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
     const int qpos = a.len[s];
@@ -981,7 +996,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     {
         const int n = lane & 15, g = lane >> 4, hh = n >> 2, dg = n & 3;
         const bool hl = hh < G;
-        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (hl ? hh : 0)) * HD;
+        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (hl ? hh : 0)) * hdr;
         float qx[NM][16], nwv[NM][16];
         float2 qcs[NM][8];
 #pragma unroll
@@ -989,10 +1004,12 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
             const int d0 = 64 * m + 16 * g;
 #pragma unroll
             for (int e4 = 0; e4 < 4; e4++) {
-                const float4 v4 = *reinterpret_cast<const float4 *>(qrow + d0 + 4 * e4);
+                const bool in = d0 + 4 * e4 < hdr;  // stored dims past the row are 0
+                const float4 v4 = keep4(in, *reinterpret_cast<const float4 *>(qrow + (in ? d0 + 4 * e4 : 0)));
                 qx[m][4 * e4] = v4.x; qx[m][4 * e4 + 1] = v4.y; qx[m][4 * e4 + 2] = v4.z; qx[m][4 * e4 + 3] = v4.w;
                 if (QN) {
-                    const float4 n4 = *reinterpret_cast<const float4 *>(QN + d0 + 4 * e4);
+                    const float4 n4 = *reinterpret_cast<const float4 *>(QN + (in ? d0 + 4 * e4 : 0));  // (only
+                    // multiplies dims that are zero past the row)
                     nwv[m][4 * e4] = n4.x; nwv[m][4 * e4 + 1] = n4.y; nwv[m][4 * e4 + 2] = n4.z; nwv[m][4 * e4 + 3] = n4.w;
                 }
             }
@@ -1004,16 +1021,16 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
                                 : make_float2(1.0f, 0.0f);
             }
         }
-        const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * HD, G, hl ? hh : 0,
-                                                    L.norm_eps)
+        const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * hdr, G, hl ? hh : 0,
+                                                    L.norm_eps, hdr)
                             : 1.0f;
         // The appending wave (the last: it has the fewest windows) quantizes the new token and
         // scores it against every head before its windows; the others start at once.  Its
         // loads go out with q's.  kd, vd and xnew are read after the barrier that opens the
         // merge.
         if (appender) {
-            append_load<HD, NORM>(a, s, h, qpos, lane, ain);
-            load_q_pairs<HD, 4>(a, s, h * G, G, lane, qp);
+            append_load<HD, NORM>(a, s, h, qpos, lane, ain, hdr);
+            load_q_pairs<HD, 4>(a, s, h * G, G, lane, qp, hdr);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1077,8 +1094,8 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         qinv = qinv_s[wave][hg];
     }
     if (appender) {
-        append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd);
-        new_token_scores<HD, SOFTCAP, NORM, 4>(a, s, h * G, G, lane, qp, ain.cs, kd, xnew);
+        append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd, hdr);
+        new_token_scores<HD, SOFTCAP, NORM, 4>(a, s, h * G, G, lane, qp, ain.cs, kd, xnew, hdr);
     }
 
     WaveState8<HD> st;
@@ -1146,10 +1163,11 @@ windows_done:
             lsum += e;
         }
         const size_t head = (size_t)s * a.n_head + h * G + hh;
-        if (n_split_s == 1)
-            a.out[head * HD + d] = lsum > 0.0f ? acc / lsum : 0.0f;
-        else
+        if (n_split_s == 1) {
+            if (d < hdr) a.out[head * hdr + d] = lsum > 0.0f ? acc / lsum : 0.0f;
+        } else {
             store_partial(a, head, split, HD, d, acc, M, lsum);
+        }
     }
 }
 
@@ -1191,12 +1209,12 @@ int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
 }
 }  // namespace
 
-DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu) {
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, bool padded) {
     DecodePlan p;
     int max_ctx = 1;
     for (int s = 0; s < n_seq; s++) max_ctx = std::max(max_ctx, (int)n_ctx[s]);
     p.g4 = false;
-    if (G <= 4) {
+    if (G <= 4 && !padded) {
         p.chunk = plan_chunk(n_ctx, n_seq, n_kv, n_cu);
         p.g4 = p.chunk >= kG4MinChunk;
     }
@@ -1228,7 +1246,7 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.G = std::min(a.Gt, 8);
     a.chunk = plan.chunk;
     a.n_split = plan.n_split;
-    a.inv_sqrt_hd = 1.0f / sqrtf((float)L.hd);
+    a.inv_sqrt_hd = 1.0f / sqrtf((float)L.hdr);
     a.softcap = softcap;
     a.out = out;
     a.ws = ws;
@@ -1243,9 +1261,12 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     // the grid holds idle ones (splits past a short sequence's end) that exit at once.
     constexpr size_t kOnePerCuLds = 64 * 1024;
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
+    const bool pad = L.hdr != L.hd;
+    if (pad && plan.g4) return hipErrorInvalidValue;  // decode_plan keeps padded heads off it
 #define TS_SPLIT(HDV, SC, NM)                                                                  \
     (plan.g4 ? (decode_split4_kernel<HDV, SC, NM, 4, 2><<<grid, 256, kOnePerCuLds, st>>>(a), 0)        \
-             : (decode_split_kernel<HDV, SC, NM><<<grid, 64 * kNW16, 0, st>>>(a), 0))
+             : pad ? (decode_split_kernel<HDV, SC, NM, true><<<grid, 64 * kNW16, 0, st>>>(a), 0)         \
+                   : (decode_split_kernel<HDV, SC, NM, false><<<grid, 64 * kNW16, 0, st>>>(a), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \
     (cap ? (norm ? TS_SPLIT(HDV, true, true) : TS_SPLIT(HDV, true, false))                    \
          : (norm ? TS_SPLIT(HDV, false, true) : TS_SPLIT(HDV, false, false)))

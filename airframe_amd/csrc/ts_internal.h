@@ -65,7 +65,10 @@ struct KvLayerView {
     // QK norm of this layer (Qwen3): per-dim weights for q and K, or null (no norm), and eps
     const float *qn, *kn;
     float norm_eps;
-    int S, H, P, hd;
+    // hd: the stored head dim (64, 128 or 256: the kernels' template); hdr: the caller's head
+    // dim (a multiple of 8, at most hd), the row length of q, K, V and outputs.  Stored dims
+    // from hdr on hold code 8 (value 0).
+    int S, H, P, hd, hdr;
 };
 
 __device__ __host__ inline int rot_pos(int p, int rot, int sink) { return p < sink ? p : p + rot; }
@@ -92,14 +95,15 @@ struct ts_kv {
     std::vector<int32_t> h_ctx;  // scratch for the decode plan: len + 1 per sequence
     int device;
     int n_cu;                    // compute units of the device (the decode plan's target)
+    int hdp;                     // stored head dim (KvLayerView::hd)
 
     ts::KvLayerView layer(int l) const {
         ts::KvLayerView v;
         uint64_t nrow = (uint64_t)d.n_seq * d.n_head_kv * P;
         uint8_t *b = base + (uint64_t)l * layer_bytes;
         v.kp = b;
-        v.vp = b + nrow * (d.head_dim / 2);
-        v.ks = (float *)(b + nrow * d.head_dim);
+        v.vp = b + nrow * (hdp / 2);
+        v.ks = (float *)(b + nrow * hdp);
         v.vs = v.ks + nrow;
         const bool compacted = std::any_of(h_rot.begin(), h_rot.end(), [](int32_t r) { return r != 0; });
         v.rot = compacted ? d_rot : nullptr;
@@ -110,7 +114,8 @@ struct ts_kv {
         v.S = d.n_seq;
         v.H = d.n_head_kv;
         v.P = P;
-        v.hd = d.head_dim;
+        v.hd = hdp;
+        v.hdr = d.head_dim;
         return v;
     }
 };
@@ -141,7 +146,8 @@ struct DecodePlan {
     bool g4;      // the G <= 4 (4x4x4 QK) kernel
 };
 // n_ctx: keys per sequence (len + 1), on the host; n_cu: compute units of the device.
-DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu);
+// padded: the head dim is stored padded (the G <= 4 kernel takes only unpadded rows).
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, bool padded = false);
 // Upper bound of plan.n_split for any lengths up to max_seq (sizes the workspace).
 int decode_cap(int n_kv, int max_seq, int n_cu);
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,

@@ -22,13 +22,15 @@ bool desc_valid(const ts_kv_desc *d) {
            d->max_seq > 0 && d->head_dim % 8 == 0;
 }
 
-// head_dim values with a built kernel (the reference accepts any multiple of 8).
-bool head_dim_built(int hd) { return hd == 64 || hd == 128; }
+// head_dim values the kernels take: any multiple of 8 up to 128, stored padded to 64 or 128
+// dims (the reference accepts any multiple of 8: kv_cache.rs:150-156).
+bool head_dim_built(int hd) { return hd % 8 == 0 && hd >= 8 && hd <= 128; }
+int stored_head_dim(int hd) { return hd <= 64 ? 64 : 128; }
 
 int padded_positions(int max_seq) { return (max_seq + ts::kPosAlign - 1) / ts::kPosAlign * ts::kPosAlign; }
 
 uint64_t layer_bytes_of(const ts_kv_desc *d) {
-    return (uint64_t)d->n_seq * d->n_head_kv * padded_positions(d->max_seq) * (d->head_dim + 8);
+    return (uint64_t)d->n_seq * d->n_head_kv * padded_positions(d->max_seq) * (stored_head_dim(d->head_dim) + 8);
 }
 
 }  // namespace
@@ -133,6 +135,7 @@ static int64_t rot_end(const ts_kv *kv, int32_t n_tok) {
 
 int ts_kv_bytes(const ts_kv_desc *desc, uint64_t *bytes) {
     if (!desc_valid(desc) || !bytes) return TS_ERR_INVALID;
+    if (!head_dim_built(desc->head_dim)) return TS_ERR_UNSUPPORTED;
     *bytes = layer_bytes_of(desc) * (uint64_t)desc->n_layers;
     return TS_OK;
 }
@@ -147,6 +150,7 @@ int ts_kv_create(const ts_kv_desc *desc, ts_kv **out) {
     kv->d = *desc;
     kv->P = padded_positions(desc->max_seq);
     kv->layer_bytes = layer_bytes_of(desc);
+    kv->hdp = stored_head_dim(desc->head_dim);
     kv->h_len.assign(desc->n_seq, 0);
     kv->h_rot.assign(desc->n_seq, 0);
     kv->h_sink.assign(desc->n_seq, 0);
@@ -392,7 +396,7 @@ static bool heads_ok(const ts_kv *kv, int32_t n_head) {
 int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes) {
     if (!kv || !bytes || !heads_ok(kv, n_head)) return TS_ERR_INVALID;
     const int cap = ts::decode_cap(kv->d.n_head_kv, kv->d.max_seq, kv->n_cu);
-    *bytes = (uint64_t)kv->d.n_seq * n_head * cap * (kv->d.head_dim + 2) * sizeof(float);
+    *bytes = (uint64_t)kv->d.n_seq * n_head * cap * (kv->hdp + 2) * sizeof(float);
     return TS_OK;
 }
 
@@ -414,11 +418,11 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
     std::vector<int32_t> &ctx = const_cast<ts_kv *>(kv)->h_ctx;
     for (int s = 0; s < kv->d.n_seq; s++) ctx[s] = kv->h_len[s] + 1;
     ts::DecodePlan plan = ts::decode_plan(ctx.data(), kv->d.n_seq, kv->d.n_head_kv, n_head / kv->d.n_head_kv,
-                                          kv->n_cu);
+                                          kv->n_cu, kv->hdp != kv->d.head_dim);
     if (plan.n_split > 1) {
         uint64_t need = 0;
         if (noalloc)  // partials [S][n_head][n_split][hd], then m and l [S][n_head][n_split]
-            need = (uint64_t)kv->d.n_seq * n_head * plan.n_split * (kv->d.head_dim + 2) * sizeof(float);
+            need = (uint64_t)kv->d.n_seq * n_head * plan.n_split * (kv->hdp + 2) * sizeof(float);
         else  // plan.n_split <= decode_cap(max_seq), the count the workspace was sized for
             ts_attn_decode_workspace(kv, n_head, &need);
         if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;

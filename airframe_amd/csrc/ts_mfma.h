@@ -133,22 +133,29 @@ __device__ inline float opaque(float x) {
 __device__ inline float split_hi(float v) { return __uint_as_float(__float_as_uint(v) & 0xFFFFE000u); }
 
 // The 8 dims 8u..8u+7 of one head's q, normalized when nw is set (QK norm weights nw, the
-// row's scale ns: attention.rs:186-189 normalizes before RoPE).
-__device__ inline void q_read8(const float *qrow, int u, const float *nw, float ns, float (&x)[8]) {
-    const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * u);
-    const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * u + 4);
+// row's scale ns: attention.rs:186-189 normalizes before RoPE); zeros for the stored dims at
+// or past the row length hdr (a multiple of 8).
+__device__ inline void q_read8(const float *qrow, int u, const float *nw, float ns, float (&x)[8], int hdr = 1 << 30) {
+    // (dims past the row: the row's first dims are loaded, unconditionally, and dropped)
+    const bool in = 8 * u < hdr;
+    const int uc = in ? u : 0;
+    const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * uc);
+    const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * uc + 4);
     x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
     x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
     if (nw) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) x[e] = qk_norm_apply(x[e], ns, nw[8 * u + e]);
+        for (int e = 0; e < 8; e++) x[e] = qk_norm_apply(x[e], ns, nw[8 * uc + e]);
     }
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = in ? x[e] : 0.0f;
 }
 
 // Bound on |rotated q| over the 8 dims 8u..8u+7 of one head: |a cos - b sin| <= |a| + |b|.
-__device__ inline float q_bound8(const float *qrow, int u, const float *nw = nullptr, float ns = 1.0f) {
+__device__ inline float q_bound8(const float *qrow, int u, const float *nw = nullptr, float ns = 1.0f,
+                                int hdr = 1 << 30) {
     float x[8];
-    q_read8(qrow, u, nw, ns, x);
+    q_read8(qrow, u, nw, ns, x, hdr);
     return fmaxf(fmaxf(fabsf(x[0]) + fabsf(x[1]), fabsf(x[2]) + fabsf(x[3])),
                  fmaxf(fabsf(x[4]) + fabsf(x[5]), fabsf(x[6]) + fabsf(x[7])));
 }
@@ -200,9 +207,9 @@ __device__ inline void load_rot8(const float *rope, int rope_pairs, int u, int q
 // dequant8.
 __device__ inline void load_q8(const float *rope, int rope_pairs, const float *qrow, int u,
                                int qpos, float mul, half8 &hi, half8 &lo,
-                               const float *nw = nullptr, float ns = 1.0f) {
+                               const float *nw = nullptr, float ns = 1.0f, int hdr = 1 << 30) {
     float x[8];
-    q_read8(qrow, u, nw, ns, x);
+    q_read8(qrow, u, nw, ns, x, hdr);
     float2 cs[4];
     load_rot8(rope, rope_pairs, u, qpos, cs);
     split_q8(x, cs, u, rope_pairs, mul, hi, lo);

@@ -353,7 +353,8 @@ __device__ inline void step_probs(const floatx16 (&sc)[2], const float *sv, int 
     }
 }
 
-template <int HD, bool SOFTCAP, bool NORM>
+// PAD: the caller's head dim L.hdr is below the stored HD (q and output rows of hdr floats).
+template <int HD, bool SOFTCAP, bool NORM, bool PAD>
 __global__ __launch_bounds__(64 * kPrefillNW, 2) void prefill_kernel(PrefillArgs a) {
     constexpr int NW = kPrefillNW;
     constexpr int NKS = HD / 16;   // MFMA k-steps over the head dim
@@ -403,17 +404,18 @@ __global__ __launch_bounds__(64 * kPrefillNW, 2) void prefill_kernel(PrefillArgs
     const bool live = c < n_cols;
     const int cc = live ? c : n_cols - 1;
     const int tok = cc / G;
-    const float *qrow = a.q + (((size_t)s * a.n_tok + tok) * a.n_head + h * G + cc % G) * HD;
+    const int hdr = PAD ? L.hdr : HD;  // row length of q and the output (stored dims past it are 0)
+    const float *qrow = a.q + (((size_t)s * a.n_tok + tok) * a.n_head + h * G + cc % G) * hdr;
     const int qpos = live ? len0 + tok : -1;
 
     // QK norm scale of this lane's column (its q row walked in order), then one power-of-two
     // q scale per workgroup, from a bound over all its columns.
-    const float ns = QN ? qk_norm_scale(qrow, HD, L.norm_eps) : 1.0f;
+    const float ns = QN ? qk_norm_scale(qrow, hdr, L.norm_eps) : 1.0f;
     float q_s, inv_s;
     {
         float qb = 0.0f;
 #pragma unroll
-        for (int t = 0; t < NKS; t++) qb = fmaxf(qb, q_bound8(qrow, 2 * t + hf, QN, ns));
+        for (int t = 0; t < NKS; t++) qb = fmaxf(qb, q_bound8(qrow, 2 * t + hf, QN, ns, hdr));
         qb = wave_max(qb);
         if (lane == 0) sm_qb[wave] = qb;
         __syncthreads();
@@ -426,7 +428,7 @@ __global__ __launch_bounds__(64 * kPrefillNW, 2) void prefill_kernel(PrefillArgs
 #pragma unroll
     for (int t = 0; t < NKS; t++) {
         load_q8(a.rope, a.rope_pairs, qrow, 2 * t + hf, rot_of(L, s, len0 + tok), qmul * q_s,
-                qh[t], ql[t], QN, ns);
+                qh[t], ql[t], QN, ns, hdr);
         if (!live) {
             qh[t] = (half8)(_Float16)0.0f;
             ql[t] = (half8)(_Float16)0.0f;
@@ -514,7 +516,7 @@ __global__ __launch_bounds__(64 * kPrefillNW, 2) void prefill_kernel(PrefillArgs
 
     const float l = half_sum(l_run);
     if (live) {
-        float *orow = a.out + (((size_t)s * a.n_tok + tok) * a.n_head + h * G + c % G) * HD;
+        float *orow = a.out + (((size_t)s * a.n_tok + tok) * a.n_head + h * G + c % G) * hdr;
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
         for (int db = 0; db < NDB; db++)
@@ -522,7 +524,7 @@ __global__ __launch_bounds__(64 * kPrefillNW, 2) void prefill_kernel(PrefillArgs
             for (int q = 0; q < 4; q++) {
                 float4 v4 = make_float4(o[db][4 * q] * inv, o[db][4 * q + 1] * inv,
                                         o[db][4 * q + 2] * inv, o[db][4 * q + 3] * inv);
-                *reinterpret_cast<float4 *>(orow + 32 * db + 8 * q + 4 * hf) = v4;
+                if (32 * db + 8 * q + 4 * hf < hdr) *reinterpret_cast<float4 *>(orow + 32 * db + 8 * q + 4 * hf) = v4;
             }
     }
 }
@@ -541,7 +543,7 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
     a.n_head = n_head;
     a.G = n_head / L.H;
     a.n_tok = n_tok;
-    a.inv_sqrt_hd = 1.0f / sqrtf((float)L.hd);
+    a.inv_sqrt_hd = 1.0f / sqrtf((float)L.hdr);
     a.softcap = softcap;
     a.out = out;
     const int n_cols = n_tok * a.G;
@@ -549,11 +551,12 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
     const int n_blk = (n_cols + cols - 1) / cols;
     dim3 grid(n_blk, L.H, L.S);
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr;
-#define TS_PF(HDV)                                                                                      \
-    (cap ? (norm ? (prefill_kernel<HDV, true, true><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)         \
-                 : (prefill_kernel<HDV, true, false><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0))       \
-         : (norm ? (prefill_kernel<HDV, false, true><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)        \
-                 : (prefill_kernel<HDV, false, false><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)))
+#define TS_PF2(HDV, PD)                                                                                      \
+    (cap ? (norm ? (prefill_kernel<HDV, true, true, PD><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)         \
+                 : (prefill_kernel<HDV, true, false, PD><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0))       \
+         : (norm ? (prefill_kernel<HDV, false, true, PD><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)        \
+                 : (prefill_kernel<HDV, false, false, PD><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)))
+#define TS_PF(HDV) (L.hdr != L.hd ? TS_PF2(HDV, true) : TS_PF2(HDV, false))
     if (L.hd == 128)
         TS_PF(128);
     else if (L.hd == 64)
@@ -561,6 +564,7 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
     else
         return hipErrorInvalidValue;
 #undef TS_PF
+#undef TS_PF2
     return hipGetLastError();
 }
 

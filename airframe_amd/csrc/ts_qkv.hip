@@ -144,7 +144,7 @@ __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const floa
             kx[e] = trow[8 * l + e];
             vx[e] = trow[HD + 8 * l + e];
         }
-        if (L.kn) row_qk_norm<LPR>(kx, L.kn, L.norm_eps, l);
+        if (L.kn) row_qk_norm<LPR>(kx, L.kn, L.norm_eps, l, L.hdr);
         if (a.rope) {
             float2 cs[4];
             rope_cs4(L, s, p, a.rope, a.rope_pairs, l, cs);

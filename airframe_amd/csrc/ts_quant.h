@@ -12,6 +12,12 @@
 namespace ts {
 namespace {
 
+// v where keep, else zeros, component by component (a conditional on the float4 objects
+// themselves would select between their addresses and put both in scratch memory).
+__device__ inline float4 keep4(bool keep, float4 v) {
+    return make_float4(keep ? v.x : 0.f, keep ? v.y : 0.f, keep ? v.z : 0.f, keep ? v.w : 0.f);
+}
+
 __device__ inline float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -42,9 +48,11 @@ __device__ inline float qk_norm_scale(const float *row, int hd, float eps) {
     for (int d0 = 0; d0 < hd; d0 += 32) {
         float4 x[8];
 #pragma unroll
-        for (int b = 0; b < 8; b++) x[b] = *reinterpret_cast<const float4 *>(row + d0 + 4 * b);
+        for (int b = 0; b < 8; b++)
+            x[b] = d0 + 4 * b < hd ? *reinterpret_cast<const float4 *>(row + d0 + 4 * b) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int b = 0; b < 8; b++) {
+            if (d0 + 4 * b >= hd) break;  // (hd is a multiple of 8: whole float4s)
             sum = sum + x[b].x * x[b].x;
             sum = sum + x[b].y * x[b].y;
             sum = sum + x[b].z * x[b].z;
@@ -152,8 +160,9 @@ __device__ inline float wave_sum(float v) {
 // by the whole wave: every row's squares are summed as a tree across the lanes (the query side
 // only feeds the softmax, compared within tolerance, so the order of the sum is free) and no
 // LDS or barrier is involved.  All lanes must call it.
+// Rows of hdr floats (stride hdr), hdr <= HD.
 template <int HD>
-__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps) {
+__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps, int hdr = HD) {
     static_assert(HD % 64 == 0, "whole float lanes per row");
     constexpr int PER = HD / 64;
     const int lane = __lane_id();
@@ -161,7 +170,8 @@ __device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float
 #pragma unroll
     for (int g = 0; g < 8; g++)
 #pragma unroll
-        for (int e = 0; e < PER; e++) x[g][e] = g < G ? q[(size_t)g * HD + PER * lane + e] : 0.0f;
+        for (int e = 0; e < PER; e++)
+            x[g][e] = g < G && PER * lane + e < hdr ? q[(size_t)g * hdr + PER * lane + e] : 0.0f;
     float out = 1.0f;
 #pragma unroll
     for (int g = 0; g < 8; g++) {
@@ -169,7 +179,7 @@ __device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float
             float ss = 0.0f;
 #pragma unroll
             for (int e = 0; e < PER; e++) ss += x[g][e] * x[g][e];
-            const float sc = qk_norm_scale_from_sum(wave_sum(ss), HD, eps);
+            const float sc = qk_norm_scale_from_sum(wave_sum(ss), hdr, eps);
             out = g == mine ? sc : out;
         }
     }

@@ -73,14 +73,16 @@ __device__ inline float row_ordered_sum(const float (&sq)[8], int l) {
 }
 
 // QK norm of a K row in place (weights kn, the row's lanes as above).
+// Rows of hdr real dims (the stored dims past them are 0 and stay 0).
 template <int LPR>
-__device__ inline void row_qk_norm(float (&kx)[8], const float *kn, float eps, int l) {
+__device__ inline void row_qk_norm(float (&kx)[8], const float *kn, float eps, int l, int hdr) {
     float sq[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) sq[e] = sq_rn(kx[e]);
-    const float ns = qk_norm_scale_from_sum(row_ordered_sum<LPR>(sq, l), 8 * LPR, eps);
+    const float ns = qk_norm_scale_from_sum(row_ordered_sum<LPR>(sq, l), hdr, eps);
+    const int lc = 8 * l < hdr ? l : 0;  // (a lane past the row keeps its zeros: 0 * w = 0)
 #pragma unroll
-    for (int e = 0; e < 8; e++) kx[e] = qk_norm_apply(kx[e], ns, kn[8 * l + e]);
+    for (int e = 0; e < 8; e++) kx[e] = qk_norm_apply(kx[e], ns, kn[8 * lc + e]);
 }
 
 // Scales and codes of one K row and one V row from their maxima (row_max): the reciprocal
@@ -123,7 +125,7 @@ __device__ inline void store_block64(const KvLayerView &L, int s, int h, int blk
     const int p0 = blk * kBlk;
     const int p = p0 + 4 * wave + (r8 & 3) + 16 * (r8 >> 2);
     const size_t row = (size_t)s * L.H + h;
-    if (L.kn) row_qk_norm<8>(kx, L.kn, L.norm_eps, l);
+    if (L.kn) row_qk_norm<8>(kx, L.kn, L.norm_eps, l, L.hdr);
 #pragma unroll
     for (int m = 0; m < 4; m++)
         if (4 * l + m < rot_pairs) rope_rotate(kx[2 * m], kx[2 * m + 1], cs[m]);
@@ -198,9 +200,10 @@ __device__ inline void store_block128(const KvLayerView &L, int s, int h, int bl
             float sq[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) sq[e] = sq_rn(kx[rd][e]);
-            const float ns = qk_norm_scale_from_sum(ordered_sum_row16(sq, l), HD, L.norm_eps);
+            const float ns = qk_norm_scale_from_sum(ordered_sum_row16(sq, l), L.hdr, L.norm_eps);
+            const int lc = 8 * l < L.hdr ? l : 0;  // (a lane past the row keeps its zeros)
 #pragma unroll
-            for (int e = 0; e < 8; e++) kx[rd][e] = qk_norm_apply(kx[rd][e], ns, L.kn[8 * l + e]);
+            for (int e = 0; e < 8; e++) kx[rd][e] = qk_norm_apply(kx[rd][e], ns, L.kn[8 * lc + e]);
         }
     }
     float km[2], vm[2];

@@ -56,3 +56,59 @@ def test_prefill_large_groups(gpu, n_kv, n_head, hd):
     p.set_lens([0, 37])
     run_chunks(p, rng, n_head, [50, 90])
     p.check_codes()
+
+
+# ---- head dims other than 64 and 128 (stored padded to 64 / 128 dims) --------------------------
+
+from tests import test_gpu_compaction as comp  # noqa: E402
+from tests.test_gpu_qk_norm import with_norm  # noqa: E402
+
+
+@pytest.mark.parametrize("hd,n_kv,n_head,rope_dim", [
+    (96, 2, 8, None),    # Phi-3 style, stored as 128
+    (80, 4, 16, 64),     # partial rotation, stored as 128
+    (40, 2, 4, None),    # stored as 64, G <= 4
+    (8, 1, 3, None),     # the smallest head dim the reference accepts
+    (120, 1, 12, None),  # G = 12 with a padded head
+])
+def test_head_dims_append_decode_prefill(gpu, hd, n_kv, n_head, rope_dim):
+    say(f"head_dim {hd} n_kv={n_kv} n_head={n_head} rope_dim={rope_dim}")
+    rng = np.random.default_rng(500 + hd)
+    p = Pair(3, n_kv, hd, 1400, 10000.0, rope_dim=rope_dim)
+    fill(p, rng, 1100, step=300)  # ragged chunks through the append kernel
+    p.set_lens([1100, 5, 700])
+    p.check_codes()
+    for _ in range(2):
+        out, ref = fused_step(p, rng, n_head)
+        assert_close(out, ref, f"hd {hd} fused decode")
+    k = synth.normal(rng, (3, 1, n_kv, hd))
+    v = synth.normal(rng, (3, 1, n_kv, hd))
+    q = synth.normal(rng, (3, n_head, hd))
+    p.append(k, v)
+    out = p.gpu.attn_decode(0, dev(q), p.rope).cpu().numpy()
+    ref = p.ora.attend(q[:, None], 1, threads=8)[:, 0]
+    assert_close(out, ref, f"hd {hd} decode")
+    p.advance(1)
+    run_chunks(p, rng, n_head, [33])
+    p.check_codes()
+
+
+@pytest.mark.parametrize("hd", [96, 48])
+def test_head_dims_qk_norm_and_compaction(gpu, hd):
+    say(f"head_dim {hd}: qk norm, compaction")
+    rng = np.random.default_rng(600 + hd)
+    n_head = 8
+    p = Pair(2, 2, hd, 400, 10000.0, rope_n_pos=1400)
+    with_norm(p, rng)
+    comp.fill(p, rng, 300)
+    p.set_lens([300, 250])
+    p.check_codes()
+    comp.compact(p, 0, 4, 100)
+    comp.compact(p, 1, 4, 37)
+    p.check_codes()
+    for _ in range(2):
+        out, ref = comp.fused_step(p, rng, n_head)
+        assert_close(out, ref, f"hd {hd} fused decode after compaction, qk norm")
+    out, ref = comp.prefill_chunk(p, rng, n_head, 17)
+    assert_close(out, ref, f"hd {hd} prefill after compaction, qk norm")
+    p.check_codes()
