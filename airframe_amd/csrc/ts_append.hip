@@ -107,6 +107,51 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
     store_block128(L, s, h, blk, lo, hi, kx, vx, cs, rope ? rope_pairs : 0, wave, lane);
 }
 
+// hd = 256: 32 lanes per position, lane l holding dims 8l..8l+7 -- K word l; two rows per wave
+// and four rounds (store_block256).  No LDS.
+__global__ __launch_bounds__(256) void quantize_rows256_kernel(KvLayerView L, const float *__restrict__ k,
+                                                                const float *__restrict__ v,
+                                                                const int32_t *__restrict__ d_start,
+                                                                int32_t fixed_start, int32_t count,
+                                                                int32_t ld_tok,
+                                                                const float *__restrict__ rope,
+                                                                int32_t rope_pairs) {
+    const int s = blockIdx.z, h = blockIdx.y;
+    const int start = d_start ? d_start[s] : fixed_start;
+    const int end = start + count;
+    const int blk = start / kBlk + blockIdx.x;
+    const int p0 = blk * kBlk;
+    if (p0 >= end) return;
+    const int lo = max(p0, start), hi = min(p0 + kBlk, end);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane >> 5, l = lane & 31;
+
+    float kx[4][8], vx[4][8];
+    float2 cs[4][4];
+#pragma unroll
+    for (int rd = 0; rd < 4; rd++) {
+        const int pc = min(max(p0 + 4 * wave + 2 * (rd & 1) + r + 16 * (rd >> 1), lo), hi - 1);
+        const int pr = rot_of(L, s, pc);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int pair = 4 * l + m;
+            cs[rd][m] = (rope && pair < rope_pairs)
+                            ? *reinterpret_cast<const float2 *>(rope + ((size_t)pr * rope_pairs + pair) * 2)
+                            : make_float2(1.0f, 0.0f);
+        }
+        // rows of hdr floats; the stored dims past hdr quantize zeros (code 8)
+        const bool in = 8 * l < L.hdr;
+        const size_t src = (((size_t)s * ld_tok + (pc - start)) * L.H + h) * L.hdr + 8 * (in ? l : 0);
+        const float4 *ks4 = reinterpret_cast<const float4 *>(k + src);
+        const float4 *vs4 = reinterpret_cast<const float4 *>(v + src);
+        const float4 a = keep4(in, ks4[0]), b = keep4(in, ks4[1]), c = keep4(in, vs4[0]), d = keep4(in, vs4[1]);
+        kx[rd][0] = a.x; kx[rd][1] = a.y; kx[rd][2] = a.z; kx[rd][3] = a.w;
+        kx[rd][4] = b.x; kx[rd][5] = b.y; kx[rd][6] = b.z; kx[rd][7] = b.w;
+        vx[rd][0] = c.x; vx[rd][1] = c.y; vx[rd][2] = c.z; vx[rd][3] = c.w;
+        vx[rd][4] = d.x; vx[rd][5] = d.y; vx[rd][6] = d.z; vx[rd][7] = d.w;
+    }
+    store_block256(L, s, h, blk, lo, hi, kx, vx, cs, rope ? rope_pairs : 0, wave, lane);
+}
+
 // One thread per (position, kv head, word): reference layout [pos][H][HD/8].
 template <int HD>
 __global__ void export_kernel(KvLayerView L, int seq, int pos0, int n_pos, uint32_t *kp,
@@ -203,7 +248,9 @@ hipError_t launch_quantize_rows(const KvLayerView &L, const float *k, const floa
                                 int32_t ld_tok, const float *rope, int32_t rope_pairs,
                                 int32_t max_blocks, hipStream_t st) {
     dim3 grid(max_blocks, L.H, L.S);
-    if (L.hd == 128)
+    if (L.hd == 256)
+        quantize_rows256_kernel<<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
+    else if (L.hd == 128)
         quantize_rows128_kernel<<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
     else if (L.hd == 64)
         quantize_rows64_kernel<<<grid, 256, 0, st>>>(L, k, v, d_start, fixed_start, count, ld_tok, rope, rope_pairs);
@@ -216,7 +263,9 @@ hipError_t launch_export(const KvLayerView &L, int seq, int pos0, int n_pos, uin
                          uint32_t *vp, float *ks, float *vs, hipStream_t st) {
     const long total = (long)n_pos * L.H * (L.hdr / 8);
     const int blocks = (int)((total + 255) / 256);
-    if (L.hd == 128)
+    if (L.hd == 256)
+        export_kernel<256><<<blocks, 256, 0, st>>>(L, seq, pos0, n_pos, kp, vp, ks, vs);
+    else if (L.hd == 128)
         export_kernel<128><<<blocks, 256, 0, st>>>(L, seq, pos0, n_pos, kp, vp, ks, vs);
     else if (L.hd == 64)
         export_kernel<64><<<blocks, 256, 0, st>>>(L, seq, pos0, n_pos, kp, vp, ks, vs);
@@ -230,7 +279,10 @@ hipError_t launch_import(const KvLayerView &L, int seq, int pos0, int n_pos, con
     const long nk = (long)n_pos * L.H * (L.hdr / 8);
     const int nb = (pos0 + n_pos - 1) / 32 - pos0 / 32 + 1;
     const long nv = (long)L.H * nb * L.hd * 4;
-    if (L.hd == 128) {
+    if (L.hd == 256) {
+        import_k_kernel<256><<<(int)((nk + 255) / 256), 256, 0, st>>>(L, seq, pos0, n_pos, kp, ks, vs);
+        import_v_kernel<256><<<(int)((nv + 255) / 256), 256, 0, st>>>(L, seq, pos0, n_pos, vp);
+    } else if (L.hd == 128) {
         import_k_kernel<128><<<(int)((nk + 255) / 256), 256, 0, st>>>(L, seq, pos0, n_pos, kp, ks, vs);
         import_v_kernel<128><<<(int)((nv + 255) / 256), 256, 0, st>>>(L, seq, pos0, n_pos, vp);
     } else if (L.hd == 64) {

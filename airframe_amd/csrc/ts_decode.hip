@@ -93,7 +93,7 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t by
 // chunk order of k_word_idx), so one load per row brings them all.
 template <int HD>
 __device__ inline int k16_word(int g, int t) {
-    if constexpr (HD == 128) return 8 * (t >> 1) + 2 * g + (t & 1);
+    if constexpr (HD >= 128) return 8 * (t >> 1) + 2 * g + (t & 1);
     else return 2 * g + t;
 }
 
@@ -106,7 +106,15 @@ __device__ __forceinline__ void load_window(Window<HD> &w, const Streams &st, in
         // row r = 16 kt + n of the window: words k16_word(g, 0..WPG-1) sit in chunk
         // ((r % 4) / (128 / HD)) * 64 + 16 g + r / 4, at word (r % 2) * 2 for hd 64
         const int r = 16 * kt + n;
-        if constexpr (WPG == 4) {
+        if constexpr (WPG == 8) {
+            // hd 256: the 8 words sit in chunks (2 (r % 4) + c) * 64 + 16 g + r / 4, c = 0, 1
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int koff = ((2 * (r & 3) + c) * 64 + 16 * g + (r >> 2)) * 16;
+                const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, koff, base * ROWB, 0);
+                w.kw[kt][4 * c] = t4[0]; w.kw[kt][4 * c + 1] = t4[1]; w.kw[kt][4 * c + 2] = t4[2]; w.kw[kt][4 * c + 3] = t4[3];
+            }
+        } else if constexpr (WPG == 4) {
             const int koff = ((r & 3) * 64 + 16 * g + (r >> 2)) * 16;
             const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, koff, base * ROWB, 0);
             w.kw[kt][0] = t4[0]; w.kw[kt][1] = t4[1]; w.kw[kt][2] = t4[2]; w.kw[kt][3] = t4[3];
@@ -268,82 +276,97 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
 // Fused append, run by one wave of the workgroup whose split holds position p = len[s]: the
 // quantize-on-append of ts_append.hip for one (sequence, kv head) and one position, with the
 // same arithmetic (ts_quant.h), so codes and scales are bit-identical.  Lane i owns the
-// rotation pair (2i, 2i+1).  Writes the K row, both scales and the position's nibble of every
-// V word (read-modify-write: only this workgroup touches the block), and leaves the
-// dequantized row ((code - 8) * scale, the values the cache now holds) in kd / vd.
+// rotation pairs i + 64 j (j < PPL: one pair per lane up to head dim 128, two at 256), i.e.
+// dims 2(i + 64j) and +1.  Writes the K row, both scales and the position's nibble of every V
+// word (read-modify-write: only this workgroup touches the block), and leaves the dequantized
+// row ((code - 8) * scale, the values the cache now holds) in kd / vd.
 //
 // Two phases, so a caller can issue every load of the append together (one memory round trip)
 // before anything else: append_load, then append_store.
+template <int HD>
 struct AppendIn {
-    float k0, k1, v0, v1;  // raw new K / V, dims 2i, 2i+1
-    float2 cs;             // rotation of pair i at the position's rotation position
-    float kn0, kn1;        // K norm weights of dims 2i, 2i+1 (QK norm)
-    uint32_t vold[2];      // the V words holding dims 2i, 2i+1 at this position
+    static constexpr int PPL = HD > 128 ? 2 : 1;
+    float k[PPL][2], v[PPL][2];  // raw new K / V of the lane's pairs
+    float2 cs[PPL];              // rotation of each pair at the position's rotation position
+    float kn[PPL][2];            // K norm weights of the pairs' dims (QK norm)
+    uint32_t vold[PPL][2];       // the V words holding the pairs' dims at this position
 };
 
 template <int HD, bool NORM>
-__device__ __forceinline__ void append_load(const DecodeArgs &a, int s, int h, int p, int lane, AppendIn &in,
+__device__ __forceinline__ void append_load(const DecodeArgs &a, int s, int h, int p, int lane, AppendIn<HD> &in,
                                             int hdr) {
-    constexpr int NTD = HD / 16;
+    constexpr int PPL = AppendIn<HD>::PPL;
     const KvLayerView &L = a.L;
     const size_t row = (size_t)s * L.H + h;
-    const bool on = lane < HD / 2;
-    const int i = on ? lane : 0;
-    // rows of hdr floats; the stored dims past them are 0 (their lanes load the row's first
-    // pair, unconditionally, and drop it)
-    const bool dim_in = on && 2 * i < hdr;
-    const size_t src = row * hdr + 2 * (dim_in ? i : 0);
-    const float2 kk = *reinterpret_cast<const float2 *>(a.k_new + src);
-    const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
-    in.k0 = dim_in ? kk.x : 0.f; in.k1 = dim_in ? kk.y : 0.f;
-    in.v0 = dim_in ? vv.x : 0.f; in.v1 = dim_in ? vv.y : 0.f;
-    const int ir = i < a.rope_pairs ? i : 0;
-    in.cs = *reinterpret_cast<const float2 *>(a.rope + ((size_t)rot_of(L, s, p) * a.rope_pairs + ir) * 2);
-    in.kn0 = NORM && L.kn && 2 * i < hdr ? L.kn[2 * i] : 1.0f;
-    in.kn1 = NORM && L.kn && 2 * i < hdr ? L.kn[2 * i + 1] : 1.0f;
+    const int pr = rot_of(L, s, p);
     const int q = p & 31, gq = (q & 15) >> 2;
     const uint32_t *vb = reinterpret_cast<const uint32_t *>(L.vp + (row * (L.P / 32) + (p >> 5)) * (HD * 16));
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int d = 2 * i + j;
-        in.vold[j] = vb[v_word_idx(gq * 16 + (d & 15), d >> 4)];
+    for (int j = 0; j < PPL; j++) {
+        const int i = lane + 64 * j;
+        const bool on = i < HD / 2;
+        // rows of hdr floats; the stored dims past them are 0 (their lanes load the row's
+        // first pair, unconditionally, and drop it)
+        const bool dim_in = on && 2 * i < hdr;
+        const size_t src = row * hdr + 2 * (dim_in ? i : 0);
+        const float2 kk = *reinterpret_cast<const float2 *>(a.k_new + src);
+        const float2 vv = *reinterpret_cast<const float2 *>(a.v_new + src);
+        in.k[j][0] = dim_in ? kk.x : 0.f; in.k[j][1] = dim_in ? kk.y : 0.f;
+        in.v[j][0] = dim_in ? vv.x : 0.f; in.v[j][1] = dim_in ? vv.y : 0.f;
+        const int ir = i < a.rope_pairs ? i : 0;
+        in.cs[j] = *reinterpret_cast<const float2 *>(a.rope + ((size_t)pr * a.rope_pairs + ir) * 2);
+        in.kn[j][0] = NORM && L.kn && dim_in ? L.kn[2 * i] : 1.0f;
+        in.kn[j][1] = NORM && L.kn && dim_in ? L.kn[2 * i + 1] : 1.0f;
+        const int ic = on ? i : 0;
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int d = 2 * ic + e;
+            in.vold[j][e] = vb[v_word_idx(gq * 16 + (d & 15), d >> 4)];
+        }
     }
-    (void)NTD;
 }
 
 // write = false: only the dequantized rows (a head group other than the first, whose
 // workgroup quantizes the same row for its own heads' scores).
 template <int HD, bool NORM>
-__device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane, const AppendIn &in,
+__device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane, const AppendIn<HD> &in,
                              float *kd, float *vd, int hdr, bool write = true) {
-    constexpr int ROWB = HD / 2;
+    constexpr int ROWB = HD / 2, PPL = AppendIn<HD>::PPL;
     const KvLayerView &L = a.L;
     const bool KN = NORM && L.kn != nullptr;  // QK norm of K
     const size_t row = (size_t)s * L.H + h;
-    const bool on = lane < HD / 2;
-    const int i = on ? lane : 0;
-    float k0 = in.k0, k1 = in.k1;
-    const float v0 = in.v0, v1 = in.v1;
-    // QK norm scale of the new K row: its squares summed in dimension order across the lanes
-    float ns = 0.0f;
-    if (KN) ns = qk_norm_scale_from_sum(ordered_sum_pairs(sq_rn(k0), sq_rn(k1), HD / 2), hdr, L.norm_eps);
-    if (on) {
-        if (KN) {
-            k0 = qk_norm_apply(k0, ns, in.kn0);
-            k1 = qk_norm_apply(k1, ns, in.kn1);
-        }
-        if (i < a.rope_pairs) rope_rotate(k0, k1, in.cs);
+    float k[PPL][2], v[PPL][2];
+#pragma unroll
+    for (int j = 0; j < PPL; j++) {
+        k[j][0] = in.k[j][0]; k[j][1] = in.k[j][1];
+        v[j][0] = in.v[j][0]; v[j][1] = in.v[j][1];
     }
-    const float ks = quant_scale(wave_max(fmaxf(fabsf(k0), fabsf(k1))));
-    const float vs = quant_scale(wave_max(fmaxf(fabsf(v0), fabsf(v1))));
-    const uint32_t c0 = encode(k0, ks), c1 = encode(k1, ks);
-    const uint32_t e0 = encode(v0, vs), e1 = encode(v1, vs);
-    // K row: word u holds dims 8u..8u+7 at bits 4*(d - 8u); pairs 4u..4u+3 share word u.
-    uint32_t kw = on ? (c0 | (c1 << 4)) << (8 * (i & 3)) : 0u;
-    kw |= __shfl_xor(kw, 1, 64);
-    kw |= __shfl_xor(kw, 2, 64);
-    if (write && on && (i & 3) == 0)
-        reinterpret_cast<uint32_t *>(L.kp + row * L.P * ROWB)[k_word_idx<HD>(p, i >> 2)] = kw;
+    // QK norm scale of the new K row: its squares summed in dimension order across the lanes
+    // (pairs 0..63, then 64..127)
+    float ns = 0.0f;
+    if (KN) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PPL; j++)
+            sum = ordered_sum_pairs(sq_rn(k[j][0]), sq_rn(k[j][1]), HD / 2 < 64 ? HD / 2 : 64, sum);
+        ns = qk_norm_scale_from_sum(sum, hdr, L.norm_eps);
+    }
+    float km = 0.0f, vm = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PPL; j++) {
+        const int i = lane + 64 * j;
+        if (i < HD / 2) {
+            if (KN) {
+                k[j][0] = qk_norm_apply(k[j][0], ns, in.kn[j][0]);
+                k[j][1] = qk_norm_apply(k[j][1], ns, in.kn[j][1]);
+            }
+            if (i < a.rope_pairs) rope_rotate(k[j][0], k[j][1], in.cs[j]);
+        }
+        km = fmaxf(km, fmaxf(fabsf(k[j][0]), fabsf(k[j][1])));
+        vm = fmaxf(vm, fmaxf(fabsf(v[j][0]), fabsf(v[j][1])));
+    }
+    const float ks = quant_scale(wave_max(km));
+    const float vs = quant_scale(wave_max(vm));
     if (write && lane == 0) {
         L.ks[row * L.P + p] = ks;
         L.vs[row * L.P + p] = vs;
@@ -352,52 +375,62 @@ __device__ void append_store(const DecodeArgs &a, int s, int h, int p, int lane,
     // 4gq + r of tile t at nibble r + 4t.
     const int q = p & 31, t = q >> 4, gq = (q & 15) >> 2, nib = (q & 3) + 4 * t;
     uint32_t *vb = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / 32) + (p >> 5)) * (HD * 16));
-    if (on) {
-        if (write) {
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int d = 2 * i + j;
-                vb[v_word_idx(gq * 16 + (d & 15), d >> 4)] = (in.vold[j] & ~(0xFu << (4 * nib))) | ((j ? e1 : e0) << (4 * nib));
+    for (int j = 0; j < PPL; j++) {
+        const int i = lane + 64 * j;
+        const bool on = i < HD / 2;
+        const uint32_t c0 = encode(k[j][0], ks), c1 = encode(k[j][1], ks);
+        const uint32_t e0 = encode(v[j][0], vs), e1 = encode(v[j][1], vs);
+        // K row: word u holds dims 8u..8u+7 at bits 4*(d - 8u); pairs 4u..4u+3 share word u.
+        uint32_t kw = on ? (c0 | (c1 << 4)) << (8 * (i & 3)) : 0u;
+        kw |= __shfl_xor(kw, 1, 64);
+        kw |= __shfl_xor(kw, 2, 64);
+        if (write && on && (i & 3) == 0)
+            reinterpret_cast<uint32_t *>(L.kp + row * L.P * ROWB)[k_word_idx<HD>(p, i >> 2)] = kw;
+        if (on) {
+            if (write) {
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const int d = 2 * i + e;
+                    vb[v_word_idx(gq * 16 + (d & 15), d >> 4)] =
+                        (in.vold[j][e] & ~(0xFu << (4 * nib))) | ((e ? e1 : e0) << (4 * nib));
+                }
             }
+            kd[2 * i] = (float)((int)c0 - 8) * ks;
+            kd[2 * i + 1] = (float)((int)c1 - 8) * ks;
+            vd[2 * i] = (float)((int)e0 - 8) * vs;
+            vd[2 * i + 1] = (float)((int)e1 - 8) * vs;
         }
-        kd[2 * i] = (float)((int)c0 - 8) * ks;
-        kd[2 * i + 1] = (float)((int)c1 - 8) * ks;
-        vd[2 * i] = (float)((int)e0 - 8) * vs;
-        vd[2 * i + 1] = (float)((int)e1 - 8) * vs;
     }
-}
-
-template <int HD, bool NORM>
-__device__ void append_one(const DecodeArgs &a, int s, int h, int p, int lane, float *kd, float *vd) {
-    AppendIn in;
-    append_load<HD, NORM>(a, s, h, p, lane, in, a.L.hdr);
-    append_store<HD, NORM>(a, s, h, p, lane, in, kd, vd, a.L.hdr);
 }
 
 // Scores of the new position (dequantized row kd, in this wave's LDS) for the G query heads
 // hb .. hb + G - 1 of sequence s, in the exp2 domain, from the rotated f32 q (as load_q8
-// rotates it); one wave.
-// qp[hh]: dims (2i, 2i+1) of head hh's raw q (lane i < HD/2), cs: the rotation of pair i at
-// the query's rotation position.
+// rotates it); one wave.  qp[hh][j]: dims 2(i + 64j), +1 of head hh's raw q, cs[j]: the
+// rotation of that pair at the query's rotation position.
 template <int HD, bool SOFTCAP, bool NORM, int GMAX>
-__device__ void new_token_scores(const DecodeArgs &a, int s, int hb, int G, int lane, const float2 (&qp)[GMAX],
-                                 float2 cs, const float *kd, float *xnew, int hdr) {
+__device__ void new_token_scores(const DecodeArgs &a, int s, int hb, int G, int lane,
+                                 const float2 (&qp)[GMAX][AppendIn<HD>::PPL], const float2 (&cs)[AppendIn<HD>::PPL],
+                                 const float *kd, float *xnew, int hdr) {
+    constexpr int PPL = AppendIn<HD>::PPL;
     const float *const QN = NORM ? a.L.qn : nullptr;
     const float *qg = a.q + ((size_t)s * a.n_head + hb) * hdr;
-    const int i = lane < HD / 2 ? lane : 0;
 #pragma unroll
     for (int hh = 0; hh < GMAX; hh++) {
         if (hh >= G) break;
-        float q0 = qp[hh].x, q1 = qp[hh].y;
-        if (QN) {
-            const float nh = q_norm_scale_wave<HD>(qg, G, hh, a.L.norm_eps, hdr);
-            if (2 * i < hdr) {
+        const float nh = QN ? q_norm_scale_wave<HD>(qg, G, hh, a.L.norm_eps, hdr) : 1.0f;
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PPL; j++) {
+            const int i = lane + 64 * j;
+            float q0 = qp[hh][j].x, q1 = qp[hh][j].y;
+            if (QN && 2 * i < hdr) {
                 q0 = qk_norm_apply(q0, nh, QN[2 * i]);
                 q1 = qk_norm_apply(q1, nh, QN[2 * i + 1]);
             }
+            if (i < a.rope_pairs) rope_rotate(q0, q1, cs[j]);
+            dot += i < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
         }
-        if (i < a.rope_pairs) rope_rotate(q0, q1, cs);
-        float dot = lane < HD / 2 ? q0 * kd[2 * i] + q1 * kd[2 * i + 1] : 0.0f;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
         float x = dot * a.inv_sqrt_hd;
@@ -406,18 +439,20 @@ __device__ void new_token_scores(const DecodeArgs &a, int s, int hb, int G, int 
     }
 }
 
-// The raw q pairs new_token_scores takes: dims (2i, 2i+1) of query heads hb .. hb + G - 1.
+// The raw q pairs new_token_scores takes: dims 2(i + 64j), +1 of query heads hb .. hb + G - 1.
 template <int HD, int GMAX>
-__device__ __forceinline__ void load_q_pairs(const DecodeArgs &a, int s, int hb, int G, int lane, float2 (&qp)[GMAX],
-                                             int hdr) {
+__device__ __forceinline__ void load_q_pairs(const DecodeArgs &a, int s, int hb, int G, int lane,
+                                             float2 (&qp)[GMAX][AppendIn<HD>::PPL], int hdr) {
     const float *qg = a.q + ((size_t)s * a.n_head + hb) * hdr;
-    const int i = lane < HD / 2 ? lane : 0;
 #pragma unroll
-    for (int hh = 0; hh < GMAX; hh++) {
-        const float2 t = *reinterpret_cast<const float2 *>(qg + (size_t)(hh < G ? hh : 0) * hdr + 2 * (2 * i < hdr ? i : 0));
-        const bool use = hh < G && 2 * i < hdr;
-        qp[hh] = make_float2(use ? t.x : 0.f, use ? t.y : 0.f);
-    }
+    for (int hh = 0; hh < GMAX; hh++)
+#pragma unroll
+        for (int j = 0; j < AppendIn<HD>::PPL; j++) {
+            const int i = lane + 64 * j;
+            const bool use = hh < G && i < HD / 2 && 2 * i < hdr;
+            const float2 t = *reinterpret_cast<const float2 *>(qg + (size_t)(hh < G ? hh : 0) * hdr + 2 * (use ? i : 0));
+            qp[hh][j] = make_float2(use ? t.x : 0.f, use ? t.y : 0.f);
+        }
 }
 
 // Split partial of one head: unnormalized o (dim d), and with d == 0 the reference exponent m
@@ -435,7 +470,7 @@ __device__ inline void store_partial(const DecodeArgs &a, size_t head, int split
 // PAD: the caller's head dim hdr is below the stored HD (rows of q, new K/V and the output are
 // hdr floats; the stored dims past them hold zeros).
 template <int HD, bool SOFTCAP, bool NORM, bool PAD>
-__global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_kernel(DecodeArgs a) {
     constexpr int NW = kNW16;  // waves per workgroup
     constexpr int SPAN = 64 * NW;     // positions one round of windows covers
     constexpr int WPG = HD / 32;   // K words per lane group = MFMA k-steps per 16-row tile
@@ -556,8 +591,8 @@ __global__ __launch_bounds__(64 * kNW16, 2) void decode_split_kernel(DecodeArgs 
     // scores it against every head before its windows; the others start at once.  kd, vd and
     // xnew are read after the barrier that opens the merge.
     if (fused && wave == NW - 1) {
-        AppendIn ain;
-        float2 qp[8];
+        AppendIn<HD> ain;
+        float2 qp[8][AppendIn<HD>::PPL];
         append_load<HD, NORM>(a, s, h, qpos, lane, ain, hdr);
         load_q_pairs<HD, 8>(a, s, hb, G, lane, qp, hdr);
         append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd, hdr, gi == 0);
@@ -991,8 +1026,8 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     i32x4 qa[NM], bias;
     float qinv;
     const bool appender = fused && wave == NW - 1;
-    AppendIn ain;
-    float2 qp[4];
+    AppendIn<HD> ain;
+    float2 qp[4][AppendIn<HD>::PPL];
     {
         const int n = lane & 15, g = lane >> 4, hh = n >> 2, dg = n & 3;
         const bool hl = hh < G;
@@ -1270,7 +1305,18 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
 #define TS_SPLIT_HD(HDV)                                                                      \
     (cap ? (norm ? TS_SPLIT(HDV, true, true) : TS_SPLIT(HDV, true, false))                    \
          : (norm ? TS_SPLIT(HDV, false, true) : TS_SPLIT(HDV, false, false)))
-    if (L.hd == 128) {
+    if (L.hd == 256) {
+        // (the G <= 4 kernel is not built for 256-dim rows: decode_plan keeps them off it)
+        if (plan.g4) return hipErrorInvalidValue;
+        if (cap) {
+            if (norm) { if (pad) decode_split_kernel<256, true, true, true><<<grid, 64 * kNW16, 0, st>>>(a); else decode_split_kernel<256, true, true, false><<<grid, 64 * kNW16, 0, st>>>(a); }
+            else { if (pad) decode_split_kernel<256, true, false, true><<<grid, 64 * kNW16, 0, st>>>(a); else decode_split_kernel<256, true, false, false><<<grid, 64 * kNW16, 0, st>>>(a); }
+        } else {
+            if (norm) { if (pad) decode_split_kernel<256, false, true, true><<<grid, 64 * kNW16, 0, st>>>(a); else decode_split_kernel<256, false, true, false><<<grid, 64 * kNW16, 0, st>>>(a); }
+            else { if (pad) decode_split_kernel<256, false, false, true><<<grid, 64 * kNW16, 0, st>>>(a); else decode_split_kernel<256, false, false, false><<<grid, 64 * kNW16, 0, st>>>(a); }
+        }
+        if (plan.n_split > 1) decode_combine_kernel<256><<<dim3(n_head, L.S), 256, 0, st>>>(a);
+    } else if (L.hd == 128) {
         TS_SPLIT_HD(128);
         if (plan.n_split > 1) decode_combine_kernel<128><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else if (L.hd == 64) {

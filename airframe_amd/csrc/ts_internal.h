@@ -146,7 +146,8 @@ struct DecodePlan {
     bool g4;      // the G <= 4 (4x4x4 QK) kernel
 };
 // n_ctx: keys per sequence (len + 1), on the host; n_cu: compute units of the device.
-// padded: the head dim is stored padded (the G <= 4 kernel takes only unpadded rows).
+// padded: the head dim is stored padded, or is 256 (the G <= 4 kernel takes only unpadded
+// rows of 64 or 128 dims).
 DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, bool padded = false);
 // Upper bound of plan.n_split for any lengths up to max_seq (sizes the workspace).
 int decode_cap(int n_kv, int max_seq, int n_cu);

@@ -22,10 +22,10 @@ bool desc_valid(const ts_kv_desc *d) {
            d->max_seq > 0 && d->head_dim % 8 == 0;
 }
 
-// head_dim values the kernels take: any multiple of 8 up to 128, stored padded to 64 or 128
-// dims (the reference accepts any multiple of 8: kv_cache.rs:150-156).
-bool head_dim_built(int hd) { return hd % 8 == 0 && hd >= 8 && hd <= 128; }
-int stored_head_dim(int hd) { return hd <= 64 ? 64 : 128; }
+// head_dim values the kernels take: any multiple of 8 up to 256, stored padded to 64, 128 or
+// 256 dims (the reference accepts any multiple of 8: kv_cache.rs:150-156).
+bool head_dim_built(int hd) { return hd % 8 == 0 && hd >= 8 && hd <= 256; }
+int stored_head_dim(int hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
 
 int padded_positions(int max_seq) { return (max_seq + ts::kPosAlign - 1) / ts::kPosAlign * ts::kPosAlign; }
 
@@ -418,7 +418,7 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
     std::vector<int32_t> &ctx = const_cast<ts_kv *>(kv)->h_ctx;
     for (int s = 0; s < kv->d.n_seq; s++) ctx[s] = kv->h_len[s] + 1;
     ts::DecodePlan plan = ts::decode_plan(ctx.data(), kv->d.n_seq, kv->d.n_head_kv, n_head / kv->d.n_head_kv,
-                                          kv->n_cu, kv->hdp != kv->d.head_dim);
+                                          kv->n_cu, kv->hdp != kv->d.head_dim || kv->hdp > 128);
     if (plan.n_split > 1) {
         uint64_t need = 0;
         if (noalloc)  // partials [S][n_head][n_split][hd], then m and l [S][n_head][n_split]

@@ -96,7 +96,10 @@ __device__ inline int qk_row_key(int R) {
 //  (HD/64)-th piece (c % HD) / 64.
 template <int HD>
 __device__ inline int k_chunk(int c) {
-    if constexpr (HD == 128) {
+    if constexpr (HD == 256) {
+        const int t = c & 3, n = ((c >> 2) & 3) + 4 * ((c >> 4) & 3), g = (c >> 6) & 3, mh = (c >> 8) & 1;
+        return (2 * t + mh) * 64 + 16 * g + n;
+    } else if constexpr (HD == 128) {
         const int t = c & 3, n = ((c >> 2) & 3) + 4 * ((c >> 4) & 3), g = (c >> 6) & 3;
         return t * 64 + 16 * g + n;
     } else {
@@ -106,7 +109,11 @@ __device__ inline int k_chunk(int c) {
 }
 template <int HD>
 __device__ inline void k_piece_word(int c, int j, int &key, int &u) {
-    if constexpr (HD == 128) {
+    if constexpr (HD == 256) {
+        const int t = c & 3, n = ((c >> 2) & 3) + 4 * ((c >> 4) & 3), g = (c >> 6) & 3, mh = (c >> 8) & 1;
+        key = 4 * n + t;
+        u = 16 * mh + 8 * (j >> 1) + 2 * g + (j & 1);
+    } else if constexpr (HD == 128) {
         const int t = c & 3, n = ((c >> 2) & 3) + 4 * ((c >> 4) & 3), g = (c >> 6) & 3;
         key = 4 * n + t;
         u = 8 * (j >> 1) + 2 * g + (j & 1);
@@ -355,7 +362,7 @@ __device__ inline void step_probs(const floatx16 (&sc)[2], const float *sv, int 
 
 // PAD: the caller's head dim L.hdr is below the stored HD (q and output rows of hdr floats).
 template <int HD, bool SOFTCAP, bool NORM, bool PAD>
-__global__ __launch_bounds__(64 * kPrefillNW, 2) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_kernel(PrefillArgs a) {
     constexpr int NW = kPrefillNW;
     constexpr int NKS = HD / 16;   // MFMA k-steps over the head dim
     constexpr int NDB = HD / 32;   // 32-dim output tiles
@@ -385,7 +392,9 @@ __global__ __launch_bounds__(64 * kPrefillNW, 2) void prefill_kernel(PrefillArgs
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, hf = lane >> 5;  // MFMA column / lane half
     const int len0 = a.len[s];
-    __shared__ PrefillLds<HD> sm;
+    // (dynamic: the hd-256 tiles take 128 KB)
+    extern __shared__ __align__(16) unsigned char pf_smem[];
+    PrefillLds<HD> &sm = *reinterpret_cast<PrefillLds<HD> *>(pf_smem);
     __shared__ float sm_qb[NW];
 
     const size_t row = (size_t)s * L.H + h;
@@ -551,20 +560,31 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
     const int n_blk = (n_cols + cols - 1) / cols;
     dim3 grid(n_blk, L.H, L.S);
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr;
-#define TS_PF2(HDV, PD)                                                                                      \
-    (cap ? (norm ? (prefill_kernel<HDV, true, true, PD><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)         \
-                 : (prefill_kernel<HDV, true, false, PD><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0))       \
-         : (norm ? (prefill_kernel<HDV, false, true, PD><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)        \
-                 : (prefill_kernel<HDV, false, false, PD><<<grid, 64 * kPrefillNW, 0, st>>>(a), 0)))
-#define TS_PF(HDV) (L.hdr != L.hd ? TS_PF2(HDV, true) : TS_PF2(HDV, false))
-    if (L.hd == 128)
-        TS_PF(128);
+#define TS_PF3(HDV, SC, NM, PD)                                                                          \
+    {                                                                                                     \
+        constexpr size_t lds = sizeof(PrefillLds<HDV>);                                                   \
+        if (lds > 64 * 1024)                                                                              \
+            (void)hipFuncSetAttribute((const void *)prefill_kernel<HDV, SC, NM, PD>,                      \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);              \
+        prefill_kernel<HDV, SC, NM, PD><<<grid, 64 * kPrefillNW, lds, st>>>(a);                           \
+    }
+#define TS_PF2(HDV, PD)                                                                                    \
+    {                                                                                                     \
+        if (cap) { if (norm) TS_PF3(HDV, true, true, PD) else TS_PF3(HDV, true, false, PD) }              \
+        else { if (norm) TS_PF3(HDV, false, true, PD) else TS_PF3(HDV, false, false, PD) }                \
+    }
+#define TS_PF(HDV) { if (L.hdr != L.hd) TS_PF2(HDV, true) else TS_PF2(HDV, false) }
+    if (L.hd == 256)
+        TS_PF(256)
+    else if (L.hd == 128)
+        TS_PF(128)
     else if (L.hd == 64)
-        TS_PF(64);
+        TS_PF(64)
     else
         return hipErrorInvalidValue;
 #undef TS_PF
 #undef TS_PF2
+#undef TS_PF3
     return hipGetLastError();
 }
 

@@ -70,11 +70,11 @@ __device__ inline float sq_rn(float x) {
 }
 
 // The same sum over a row spread across lanes, without touching memory: lane l holds the
-// squares of dims 2l and 2l + 1 (sq0, sq1); lanes 0..n_lanes-1 are read in order.  Every lane
-// gets the ordered sum (of rounded squares, as qk_norm_scale).
-__device__ inline float ordered_sum_pairs(float sq0, float sq1, int n_lanes) {
+// squares of dims 2l and 2l + 1 (sq0, sq1); lanes 0..n_lanes-1 are read in order and added to
+// sum (a running sum over earlier dims).  Every lane gets the ordered sum (of rounded squares,
+// as qk_norm_scale).
+__device__ inline float ordered_sum_pairs(float sq0, float sq1, int n_lanes, float sum = 0.0f) {
 #pragma clang fp contract(off)
-    float sum = 0.0f;
     for (int l = 0; l < n_lanes; l++) {
         sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sq0), l));
         sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sq1), l));

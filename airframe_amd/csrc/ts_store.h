@@ -312,5 +312,108 @@ __device__ inline void store_block128(const KvLayerView &L, int s, int h, int bl
     }
 }
 
+
+// Ordered sum of a row spread over 32 lanes (lane l holding the 8 squares of dims 8l..8l+7 in
+// order), for hd 256: one lane at a time, in the row's order, the rows of the wave's two lane
+// halves independently.  Every lane gets its half's total.
+__device__ inline float ordered_sum_row32(const float (&sq)[8]) {
+#pragma clang fp contract(off)
+    const int base = __lane_id() & 32;
+    float run = 0.0f;
+    for (int i = 0; i < 32; i++) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) run = run + __shfl(sq[e], base + i, 64);
+    }
+    return run;
+}
+
+// hd = 256: as store_block128 with 32 lanes per position (lane l = lane % 32 holding dims
+// 8l..8l+7, K word l) and two rows per wave (r = lane / 32): wave w takes the 8 positions of
+// V key group g = w, position p0 + 4w + 2 (rd % 2) + r + 16 (rd / 2) in kx[rd] / vx[rd]
+// (rd = 0..3), which is nibble 2 (rd % 2) + r + 4 (rd / 2) of the group's V words.
+__device__ inline void store_block256(const KvLayerView &L, int s, int h, int blk, int lo, int hi,
+                                      float (&kx)[4][8], float (&vx)[4][8], const float2 (&cs)[4][4],
+                                      int rot_pairs, int wave, int lane) {
+    constexpr int HD = 256;
+    const int r = lane >> 5, l = lane & 31;
+    const int p0 = blk * kBlk;
+    const size_t row = (size_t)s * L.H + h;
+    if (L.kn) {
+        const int lc = 8 * l < L.hdr ? l : 0;  // (a lane past the row keeps its zeros)
+#pragma unroll
+        for (int rd = 0; rd < 4; rd++) {
+            float sq[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) sq[e] = sq_rn(kx[rd][e]);
+            const float ns = qk_norm_scale_from_sum(ordered_sum_row32(sq), L.hdr, L.norm_eps);
+#pragma unroll
+            for (int e = 0; e < 8; e++) kx[rd][e] = qk_norm_apply(kx[rd][e], ns, L.kn[8 * lc + e]);
+        }
+    }
+    uint32_t vpart[8];  // this lane's dims 8l + e: the nibbles of the wave's 8 positions
+#pragma unroll
+    for (int e = 0; e < 8; e++) vpart[e] = 0;
+#pragma unroll
+    for (int rd = 0; rd < 4; rd++) {
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            if (4 * l + m < rot_pairs) rope_rotate(kx[rd][2 * m], kx[rd][2 * m + 1], cs[rd][m]);
+        float km = 0.0f, vm = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            km = fmaxf(km, fabsf(kx[rd][e]));
+            vm = fmaxf(vm, fabsf(vx[rd][e]));
+        }
+        // max over the 32 lanes of the row: 16-lane DPP steps, then across the two 16-lane rows
+        km = row_max<16>(km);
+        vm = row_max<16>(vm);
+        {
+            auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(km), __float_as_uint(km), false, false);
+            km = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+            auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(vm), __float_as_uint(vm), false, false);
+            vm = fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+        }
+        float ks, vs;
+        uint32_t kc[8], vc[8];
+        row_codes(kx[rd], vx[rd], km, vm, ks, vs, kc, vc);
+        const int n = 2 * (rd & 1) + r + 4 * (rd >> 1);  // nibble of this position in the words
+        const int p = p0 + 4 * wave + 2 * (rd & 1) + r + 16 * (rd >> 1);
+        if (p >= lo && p < hi) {
+            uint32_t kw = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) kw |= kc[e] << (4 * e);
+            reinterpret_cast<uint32_t *>(L.kp + row * L.P * (HD / 2))[k_word_idx<HD>(p, l)] = kw;
+            if (l == 0) {
+                L.ks[row * L.P + p] = ks;
+                L.vs[row * L.P + p] = vs;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) vpart[e] |= vc[e] << (4 * n);
+    }
+    // OR the two rows' parts: lanes l and l + 32 end up with the same 8 words
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        auto b = __builtin_amdgcn_permlane32_swap(vpart[e], vpart[e], false, false);
+        vpart[e] = b[0] | b[1];
+    }
+    uint32_t keep = 0;  // nibbles of positions outside [lo, hi)
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const int pn = p0 + 4 * wave + (n & 3) + 16 * (n >> 2);
+        if (pn < lo || pn >= hi) keep |= 0xFu << (4 * n);
+    }
+    uint32_t *vb = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / kBlk) + blk) * (HD * 16));
+    // row r writes the words of dims 8l + 4r .. 8l + 4r + 3
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int e = 4 * r + q;
+        const uint32_t w = r == 0 ? (q == 0 ? vpart[0] : q == 1 ? vpart[1] : q == 2 ? vpart[2] : vpart[3])
+                                  : (q == 0 ? vpart[4] : q == 1 ? vpart[5] : q == 2 ? vpart[6] : vpart[7]);
+        const int d = 8 * l + e, td = d >> 4, dl = d & 15;
+        uint32_t *dst = vb + v_word_idx(wave * 16 + dl, td);
+        *dst = keep ? (*dst & keep) | (w & ~keep) : w;
+    }
+}
 }  // namespace
 }  // namespace ts

@@ -71,9 +71,9 @@ typedef struct ts_kv_desc {
     int32_t n_layers;
     int32_t n_seq;     /* independent sequences (batch) */
     int32_t n_head_kv;
-    int32_t head_dim;  /* any multiple of 8 up to 128, as the reference (kv_cache.rs:150-156);
-                        * stored padded to 64 or 128 dims (the padding holds code 8, value 0);
-                        * larger: TS_ERR_UNSUPPORTED */
+    int32_t head_dim;  /* any multiple of 8 up to 256, as the reference (kv_cache.rs:150-156);
+                        * stored padded to 64, 128 or 256 dims (the padding holds code 8,
+                        * value 0); larger: TS_ERR_UNSUPPORTED */
     int32_t max_seq;   /* per-sequence capacity, positions */
 } ts_kv_desc;
 

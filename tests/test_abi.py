@@ -88,11 +88,13 @@ def test_create_validates_before_touching_the_device():
     assert L.ts_kv_create(ctypes.byref(_lib.KvDesc(1, 1, 1, 264, 16)), ctypes.byref(h)) == _lib.TS_ERR_UNSUPPORTED
     b = ctypes.c_uint64()
     assert L.ts_kv_bytes(ctypes.byref(_lib.KvDesc(1, 1, 1, 264, 16)), ctypes.byref(b)) == _lib.TS_ERR_UNSUPPORTED
-    # head dims below 64 and up to 128 are stored padded to 64 / 128 dims
+    # other head dims up to 256 are stored padded to 64 / 128 / 256 dims
     assert L.ts_kv_bytes(ctypes.byref(_lib.KvDesc(2, 3, 4, 96, 100)), ctypes.byref(b)) == _lib.TS_OK
     assert b.value == 2 * 3 * 4 * 128 * (128 + 8)
     assert L.ts_kv_bytes(ctypes.byref(_lib.KvDesc(1, 1, 1, 8, 64)), ctypes.byref(b)) == _lib.TS_OK
     assert b.value == 64 * (64 + 8)
+    assert L.ts_kv_bytes(ctypes.byref(_lib.KvDesc(1, 1, 1, 200, 64)), ctypes.byref(b)) == _lib.TS_OK
+    assert b.value == 64 * (256 + 8)
     assert L.ts_kv_create(None, ctypes.byref(h)) == _lib.TS_ERR_INVALID
     # null handles are rejected everywhere
     assert L.ts_kv_increment(None, 1, None) == _lib.TS_ERR_INVALID

@@ -70,6 +70,9 @@ from tests.test_gpu_qk_norm import with_norm  # noqa: E402
     (40, 2, 4, None),    # stored as 64, G <= 4
     (8, 1, 3, None),     # the smallest head dim the reference accepts
     (120, 1, 12, None),  # G = 12 with a padded head
+    (256, 2, 4, None),   # Gemma-2 / Gemma-3 head dim
+    (192, 1, 4, 128),    # stored as 256, partial rotation
+    (136, 2, 16, None),  # just past 128: stored as 256, G = 8
 ])
 def test_head_dims_append_decode_prefill(gpu, hd, n_kv, n_head, rope_dim):
     say(f"head_dim {hd} n_kv={n_kv} n_head={n_head} rope_dim={rope_dim}")
@@ -93,7 +96,7 @@ def test_head_dims_append_decode_prefill(gpu, hd, n_kv, n_head, rope_dim):
     p.check_codes()
 
 
-@pytest.mark.parametrize("hd", [96, 48])
+@pytest.mark.parametrize("hd", [96, 48, 256])
 def test_head_dims_qk_norm_and_compaction(gpu, hd):
     say(f"head_dim {hd}: qk norm, compaction")
     rng = np.random.default_rng(600 + hd)
@@ -112,3 +115,17 @@ def test_head_dims_qk_norm_and_compaction(gpu, hd):
     out, ref = comp.prefill_chunk(p, rng, n_head, 17)
     assert_close(out, ref, f"hd {hd} prefill after compaction, qk norm")
     p.check_codes()
+
+
+def test_head_dim_256_softcap_long_splits(gpu):
+    """Gemma-2's attention shape (head dim 256, two query heads per kv head, logit softcap 50)
+    with contexts long enough for several splits per sequence."""
+    say("head_dim 256 softcap, splits")
+    rng = np.random.default_rng(700)
+    p = Pair(2, 4, 256, 4200, 10000.0)
+    fill(p, rng, 4000, step=1000)
+    p.set_lens([4000, 2500])
+    for _ in range(2):
+        out, ref = fused_step(p, rng, 8, softcap=50.0)
+        assert_close(out, ref, "hd 256 fused decode, softcap")
+    p.check_codes(upto=[p.ora.lens[0], p.ora.lens[1]])
