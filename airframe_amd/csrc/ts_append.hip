@@ -14,6 +14,8 @@
 // writes the words itself (ts_store.h: each wave assembles the V words of one key group with
 // lane swaps).  Owning the block means no two workgroups ever write the same V word, although
 // a word interleaves 8 positions.
+#include <algorithm>
+
 #include "ts_store.h"
 
 namespace ts {
@@ -233,6 +235,63 @@ __global__ void import_v_kernel(KvLayerView L, int seq, int pos0, int n_pos, con
     *dst = word;
 }
 
+// One round of an in-place compaction move: positions [a, b) of one sequence take the K words,
+// scales and V nibbles of positions [a + S, b + S), with b - a <= S, so no position is both read
+// and written in the round (a V word can hold both: its writer keeps the nibbles outside
+// [a, b) as they are, so a concurrent reader of those sees the same values either way).
+// Work items per kv head (grid.y): the K words of [a, b) (every stored word, the padding's
+// too), then the V words of the blocks [a, b) touches (one thread per word: nibble
+// read-modify-write), then the positions' two scales.
+template <int HD>
+__global__ void shift_move_kernel(KvLayerView L, int seq, int a, int b, int S) {
+    // K: whole 16-byte chunks (4 words of one row) from hd 128 on, single words at hd 64
+    // (where a chunk holds two rows)
+    constexpr int CW = HD >= 128 ? 4 : 1;       // words per K item
+    constexpr int WPR = HD / 8 / CW, WPB = HD * 4;  // K items per row, V words per block
+    const int nk = (b - a) * WPR;
+    const int b0 = a / 32, nb = (b - 1) / 32 - b0 + 1;
+    const int nv = nb * WPB;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)nk + nv + (b - a)) return;
+    const int h = blockIdx.y;
+    const size_t row = (size_t)seq * L.H + h;
+    if (idx < nk) {
+        const int p = a + (int)(idx / WPR), c = (int)(idx % WPR);
+        uint32_t *kw = reinterpret_cast<uint32_t *>(L.kp + row * L.P * (HD / 2));
+        if constexpr (CW == 4) {
+            // chunk c = (g, m / 2): words 8 m + 2 g + i (m even or odd pair, i = 0, 1) of the row
+            const int u = 16 * (c >> 2) + 2 * (c & 3);
+            *reinterpret_cast<uint4 *>(kw + k_word_idx<HD>(p, u)) =
+                *reinterpret_cast<const uint4 *>(kw + k_word_idx<HD>(p + S, u));
+        } else {
+            kw[k_word_idx<HD>(p, c)] = kw[k_word_idx<HD>(p + S, c)];
+        }
+    } else if (idx < (long)nk + nv) {
+        const int i = (int)(idx - nk);
+        const int w = i % WPB, blk = b0 + i / WPB;
+        // w = v_word_idx(16 g + dl, td)
+        const int c = w >> 2, ln = c & 63, td = ((c >> 6) << 2) | (w & 3);
+        const int g = ln >> 4, dl = ln & 15;
+        const uint32_t *vb = reinterpret_cast<const uint32_t *>(L.vp + row * (L.P / 32) * (HD * 16));
+        uint32_t *dst = reinterpret_cast<uint32_t *>(L.vp + (row * (L.P / 32) + blk) * (HD * 16)) + w;
+        uint32_t word = *dst;
+#pragma unroll
+        for (int n = 0; n < 8; n++) {
+            const int p = 32 * blk + (n < 4 ? 4 * g + n : 16 + 4 * g + n - 4);
+            if (p < a || p >= b) continue;
+            const int q = p + S, qq = q & 31;
+            const int gq = (qq & 15) >> 2, nq = (qq & 3) + 4 * (qq >> 4);
+            const uint32_t src = vb[(size_t)(q >> 5) * (HD * 4) + v_word_idx(gq * 16 + dl, td)];
+            word = (word & ~(0xFu << (4 * n))) | (((src >> (4 * nq)) & 0xFu) << (4 * n));
+        }
+        *dst = word;
+    } else {
+        const int p = a + (int)(idx - nk - nv);
+        L.ks[row * L.P + p] = L.ks[row * L.P + p + S];
+        L.vs[row * L.P + p] = L.vs[row * L.P + p + S];
+    }
+}
+
 // mode 0: all lengths += value; mode 1: set (seq < 0: all sequences).
 __global__ void len_update_kernel(int32_t *len, int n, int32_t seq, int32_t value, int mode) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -292,6 +351,26 @@ hipError_t launch_import(const KvLayerView &L, int seq, int pos0, int n_pos, con
         return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_shift_move(const KvLayerView &L, int seq, int keep, int shift, int n_move, hipStream_t st) {
+    for (int a = keep; a < keep + n_move; a += shift) {
+        const int b = std::min(a + shift, keep + n_move);
+        const long items = (long)(b - a) * (L.hd >= 128 ? L.hd / 32 : L.hd / 8) +
+                           (long)((b - 1) / 32 - a / 32 + 1) * L.hd * 4 + (b - a);
+        const dim3 grid((unsigned)((items + 255) / 256), L.H);
+        if (L.hd == 256)
+            shift_move_kernel<256><<<grid, 256, 0, st>>>(L, seq, a, b, shift);
+        else if (L.hd == 128)
+            shift_move_kernel<128><<<grid, 256, 0, st>>>(L, seq, a, b, shift);
+        else if (L.hd == 64)
+            shift_move_kernel<64><<<grid, 256, 0, st>>>(L, seq, a, b, shift);
+        else
+            return hipErrorInvalidValue;
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_len_update(int32_t *d_len, int n, int32_t seq, int32_t value, int mode,

@@ -139,6 +139,10 @@ hipError_t launch_import(const KvLayerView &L, int seq, int pos0, int n_pos, con
                          const uint32_t *vp, const float *ks, const float *vs, hipStream_t st);
 hipError_t launch_len_update(int32_t *d_len, int n, int32_t seq, int32_t value, int mode,
                              hipStream_t st);
+// In-place compaction move of one sequence: slots [keep, keep + n_move) take slots
+// [keep + shift, keep + shift + n_move), in ceil(n_move / shift) launches (rounds of shift slots,
+// each reading only slots that later rounds no longer need).
+hipError_t launch_shift_move(const KvLayerView &L, int seq, int keep, int shift, int n_move, hipStream_t st);
 
 struct DecodePlan {
     int chunk;    // positions per split (multiple of 64)

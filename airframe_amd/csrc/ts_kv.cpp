@@ -317,9 +317,15 @@ int ts_kv_shift(ts_kv *kv, int32_t layer, int32_t seq, int32_t keep_sink, int32_
     const uint64_t need = (uint64_t)n_move * kv->d.n_head_kv * (kv->d.head_dim + 8);
     if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
     if (!aligned16(d_workspace)) return TS_ERR_INVALID;
+    const ts::KvLayerView L = kv->layer(layer);
+    // In place, in rounds of shift_amt slots (each one launch), when there are few of them; a
+    // short shift of a long window goes through the workspace instead (export the moved slots
+    // in the reference layout, import them at their new place).
+    constexpr int64_t kMaxRounds = 8;
+    if ((n_move + shift_amt - 1) / shift_amt <= kMaxRounds)
+        return hip_status(ts::launch_shift_move(L, seq, keep_sink, shift_amt, (int)n_move, st));
     uint32_t *kp = (uint32_t *)d_workspace, *vp = kp + n_move * wpp;
     float *ks = (float *)(vp + n_move * wpp), *vs = ks + n_move * kv->d.n_head_kv;
-    const ts::KvLayerView L = kv->layer(layer);
     hipError_t e = ts::launch_export(L, seq, keep_sink + shift_amt, (int)n_move, kp, vp, ks, vs, st);
     if (e == hipSuccess) e = ts::launch_import(L, seq, keep_sink, (int)n_move, kp, vp, ks, vs, st);
     return hip_status(e);
