@@ -379,7 +379,17 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
         const int n_wg = gridDim.x * gridDim.y * gridDim.z;
         if (n_wg % 8 == 0) {
             const int id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-            const int logical = (id % 8) * (n_wg / 8) + id / 8;
+            // Two workgroups share a CU.  The dispatch order within an XCD is reversed in
+            // every second round of 32 (its CU count), so that a CU's two workgroups tend to
+            // be one heavy (late-token) and one light block (4% faster on a 4 x 512-token
+            // prefill).  The reversal is a permutation of the XCD's range.
+            const int per = n_wg / 8;
+            int k = id / 8;
+            if ((k >> 5) & 1) {
+                const int r0 = k & ~31, rl = min(32, per - r0);
+                k = r0 + rl - 1 - (k - r0);
+            }
+            const int logical = (id % 8) * per + k;
             xb = logical % gridDim.x;
             h = (logical / gridDim.x) % gridDim.y;
             s = logical / (gridDim.x * gridDim.y);
@@ -417,14 +427,26 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
     const float *qrow = a.q + (((size_t)s * a.n_tok + tok) * a.n_head + h * G + cc % G) * hdr;
     const int qpos = live ? len0 + tok : -1;
 
-    // QK norm scale of this lane's column (its q row walked in order), then one power-of-two
-    // q scale per workgroup, from a bound over all its columns.
+    // The first window's K and V loads go out before q is read.
+    Pending<HD, NW> pd;
+    const DeqConstV dk;
+    fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, 0, tid, wave);
+
+    // q of this lane's column, read once: the QK norm scale (its q row walked in order), then
+    // one power-of-two q scale per workgroup from a bound over all its columns, then the
+    // rotation and the hi/lo split from the registers.
     const float ns = QN ? qk_norm_scale(qrow, hdr, L.norm_eps) : 1.0f;
     float q_s, inv_s;
+    float xq[NKS][8];
     {
         float qb = 0.0f;
 #pragma unroll
-        for (int t = 0; t < NKS; t++) qb = fmaxf(qb, q_bound8(qrow, 2 * t + hf, QN, ns, hdr));
+        for (int t = 0; t < NKS; t++) {
+            q_read8(qrow, 2 * t + hf, QN, ns, xq[t], hdr);
+            // |a cos - b sin| <= |a| + |b|
+            qb = fmaxf(qb, fmaxf(fmaxf(fabsf(xq[t][0]) + fabsf(xq[t][1]), fabsf(xq[t][2]) + fabsf(xq[t][3])),
+                                 fmaxf(fabsf(xq[t][4]) + fabsf(xq[t][5]), fabsf(xq[t][6]) + fabsf(xq[t][7]))));
+        }
         qb = wave_max(qb);
         if (lane == 0) sm_qb[wave] = qb;
         __syncthreads();
@@ -434,13 +456,17 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
     }
     // q operands of this lane's column: k-step t holds dims 8(2t + hf) .. +7.
     half8 qh[NKS], ql[NKS];
+    {
+        const int qrot = rot_of(L, s, len0 + tok);
 #pragma unroll
-    for (int t = 0; t < NKS; t++) {
-        load_q8(a.rope, a.rope_pairs, qrow, 2 * t + hf, rot_of(L, s, len0 + tok), qmul * q_s,
-                qh[t], ql[t], QN, ns, hdr);
-        if (!live) {
-            qh[t] = (half8)(_Float16)0.0f;
-            ql[t] = (half8)(_Float16)0.0f;
+        for (int t = 0; t < NKS; t++) {
+            float2 cs[4];
+            load_rot8(a.rope, a.rope_pairs, 2 * t + hf, qrot, cs);
+            split_q8(xq[t], cs, 2 * t + hf, a.rope_pairs, qmul * q_s, qh[t], ql[t]);
+            if (!live) {
+                qh[t] = (half8)(_Float16)0.0f;
+                ql[t] = (half8)(_Float16)0.0f;
+            }
         }
     }
     // Query positions this wave covers (inclusive); qmax < 0 for a wave with no columns.
@@ -457,9 +483,6 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
 
     // Window w+1 is staged into LDS while window w's QK^T runs on the matrix cores (the
     // staging is VALU and LDS-write work); its global loads were issued one iteration earlier.
-    Pending<HD, NW> pd;
-    const DeqConstV dk;
-    fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, 0, tid, wave);
     stage_codes<HD, NW>(sm, 0, pd, tid, wave, dk);
     stage_scales<HD, NW>(sm, 0, pd, tid, inv_s);
     if (n_win > 1) fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, kWin, tid, wave);
