@@ -438,11 +438,14 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
     const float ns = QN ? qk_norm_scale(qrow, hdr, L.norm_eps) : 1.0f;
     float q_s, inv_s;
     float xq[NKS][8];
+    float2 cs[NKS][4];  // the rotation of each q pair, loaded beside q
     {
+        const int qrot = rot_of(L, s, len0 + tok);
         float qb = 0.0f;
 #pragma unroll
         for (int t = 0; t < NKS; t++) {
             q_read8(qrow, 2 * t + hf, QN, ns, xq[t], hdr);
+            load_rot8(a.rope, a.rope_pairs, 2 * t + hf, qrot, cs[t]);
             // |a cos - b sin| <= |a| + |b|
             qb = fmaxf(qb, fmaxf(fmaxf(fabsf(xq[t][0]) + fabsf(xq[t][1]), fabsf(xq[t][2]) + fabsf(xq[t][3])),
                                  fmaxf(fabsf(xq[t][4]) + fabsf(xq[t][5]), fabsf(xq[t][6]) + fabsf(xq[t][7]))));
@@ -457,12 +460,9 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
     // q operands of this lane's column: k-step t holds dims 8(2t + hf) .. +7.
     half8 qh[NKS], ql[NKS];
     {
-        const int qrot = rot_of(L, s, len0 + tok);
 #pragma unroll
         for (int t = 0; t < NKS; t++) {
-            float2 cs[4];
-            load_rot8(a.rope, a.rope_pairs, 2 * t + hf, qrot, cs);
-            split_q8(xq[t], cs, 2 * t + hf, a.rope_pairs, qmul * q_s, qh[t], ql[t]);
+            split_q8(xq[t], cs[t], 2 * t + hf, a.rope_pairs, qmul * q_s, qh[t], ql[t]);
             if (!live) {
                 qh[t] = (half8)(_Float16)0.0f;
                 ql[t] = (half8)(_Float16)0.0f;
