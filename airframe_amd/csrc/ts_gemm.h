@@ -50,10 +50,7 @@ struct XTiles {
 // double-buffered) after chunk c's matrix work, so each load has D - 1 iterations to arrive.
 // D = 3 keeps two waves per SIMD; measured 10% faster than x one chunk and the weights two
 // chunks ahead, while D = 4 drops to one wave per SIMD and is slower.
-#ifndef TS_GEMM_DEPTH
-#define TS_GEMM_DEPTH 3
-#endif
-template <int WR, int D = TS_GEMM_DEPTH>
+template <int WR, int D = 3>
 __device__ __forceinline__ void gemm_tile_core(XTiles<64 * WR> &sm, const float *xs,
                                                     const _Float16 *const (&wp)[2], int nch, int tid,
                                                     floatx16 (&acc)[2][2]) {
