@@ -622,7 +622,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the INT4 KV path shards "
-                          "by sequence or kv head with no exchange (see DESIGN.md), but "
+                          "by sequence or kv head with no exchange, but "
                           "multi-GPU runs are not part of it", "n_gpus": args.gpus}))
         sys.exit(2)
     cfg = CONFIGS[args.config]
