@@ -960,7 +960,10 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     const KvLayerView &L = a.L;
     constexpr int hdr = HD;  // (padded head dims take the 16x16 kernel)
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
-    const int split = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+    // grid (kv head, sequence, split): every sequence's split 0 is dispatched before any
+    // split 1, so the splits that wait for a free CU are the last ones of the longest
+    // sequences (config 4: 1.42 vs 1.45 ms per step against the split-fastest order)
+    const int split = blockIdx.z, h = blockIdx.x, s = blockIdx.y;
     const int qpos = a.len[s];
     const int qrot = rot_of(a.L, s, qpos);  // rotation position of the query
     const int n_ctx = qpos + 1;
@@ -1299,7 +1302,7 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     const bool pad = L.hdr != L.hd;
     if (pad && plan.g4) return hipErrorInvalidValue;  // decode_plan keeps padded heads off it
 #define TS_SPLIT(HDV, SC, NM)                                                                  \
-    (plan.g4 ? (decode_split4_kernel<HDV, SC, NM, 4, 2><<<grid, 256, kOnePerCuLds, st>>>(a), 0)        \
+    (plan.g4 ? (decode_split4_kernel<HDV, SC, NM, 4, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0) \
              : pad ? (decode_split_kernel<HDV, SC, NM, true><<<grid, 64 * kNW16, 0, st>>>(a), 0)         \
                    : (decode_split_kernel<HDV, SC, NM, false><<<grid, 64 * kNW16, 0, st>>>(a), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \
