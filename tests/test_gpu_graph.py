@@ -72,3 +72,64 @@ def test_graph_replays_g4_kernel(gpu):
     fill(p, rng, max(lens), step=1024)
     p.set_lens(lens)
     replay_check(p, rng, 32, 4)
+
+
+def test_graph_replays_noalloc_bit_identical(gpu):
+    """ts_attn_decode_append_noalloc (partials in the library's scratch array) captured with the
+    increment and replayed: on a twin cache driven eagerly through the workspace entry point,
+    every replay's output and appended rows are bit-identical."""
+    import ctypes
+
+    from airframe_amd import _lib
+    from airframe_amd.kv_cache import KVCache, RopeTable, _stream
+
+    say("graph replays noalloc")
+    n_seq, n_kv, hd, n_head = 4, 8, 128, 32
+    max_seq = 8448
+    rope = RopeTable(max_seq, hd, 1e6)
+    rng = np.random.default_rng(320)
+    a = KVCache.new_int4(1, n_kv, hd, max_seq, n_seq)
+    b = KVCache.new_int4(1, n_kv, hd, max_seq, n_seq)
+    for t0 in range(0, 8200, 2050):
+        k = dev(synth.normal(rng, (n_seq, 2050, n_kv, hd)))
+        v = dev(synth.normal(rng, (n_seq, 2050, n_kv, hd)))
+        for c in (a, b):
+            c.append_quant(0, k, v, rope)
+            c.increment(2050)
+    lens = [8191, 5119, 7000, 4095]
+    for c in (a, b):
+        for s, l in enumerate(lens):
+            c.set_seq_len(l, seq=s)
+    k_in = torch.zeros((n_seq, 1, n_kv, hd), device="cuda")
+    v_in = torch.zeros((n_seq, 1, n_kv, hd), device="cuda")
+    q_in = torch.zeros((n_seq, n_head, hd), device="cuda")
+    out = torch.empty((n_seq, n_head, hd), device="cuda")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=cap):
+        rc = _lib.load().ts_attn_decode_append_noalloc(
+            b.handle, 0, ctypes.c_void_p(k_in.data_ptr()), ctypes.c_void_p(v_in.data_ptr()),
+            ctypes.c_void_p(q_in.data_ptr()), n_head, rope.handle, ctypes.c_float(0.0),
+            ctypes.c_void_p(out.data_ptr()), _stream())
+        b.increment(1)
+    assert rc == 0, _lib.load().ts_status_string(rc)
+    torch.cuda.synchronize()
+    for r in range(4):
+        k = dev(synth.normal(rng, (n_seq, 1, n_kv, hd)))
+        v = dev(synth.normal(rng, (n_seq, 1, n_kv, hd)))
+        q = dev(synth.normal(rng, (n_seq, n_head, hd)))
+        k_in.copy_(k)
+        v_in.copy_(v)
+        q_in.copy_(q)
+        graph.replay()
+        ref = a.attn_decode_append(0, k, v, q, rope)
+        a.increment(1)
+        torch.cuda.synchronize()
+        ro, oo = ref.cpu().numpy(), out.cpu().numpy()
+        assert np.array_equal(ro.view(np.uint32), oo.view(np.uint32)), f"replay {r}: max diff {np.abs(ro - oo).max()}"
+        for s, l in enumerate(lens):
+            for x, y in zip(a.export(0, s, l + r, 1), b.export(0, s, l + r, 1)):
+                assert torch.equal(x, y), f"replay {r} sequence {s}: appended row differs"
+    del graph
