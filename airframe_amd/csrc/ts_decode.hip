@@ -160,7 +160,7 @@ struct QLds {
 
 // live: this lane's column carries a head (n < 2G); lo_col: it carries the low parts (G <= n);
 // partner4: byte address (for ds_bpermute) of the lane holding the other part of its scores.
-template <int HD, bool SOFTCAP, bool TAIL>
+template <int HD, bool SOFTCAP>
 __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD> &st,
                                                const QLds<HD> &qs, float *stage, int base, int end,
                                                int lane, int g, bool live, bool lo_col, int partner4,
@@ -206,14 +206,12 @@ __device__ __forceinline__ void process_window(const Window<HD> &w, WaveState<HD
             sv[4 * kt + r] = sv4[r];
         }
     }
-    if constexpr (TAIL) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int pos = base + 16 * (i >> 2) + 4 * g + (i & 3);
-            if (pos >= end) {
-                x[i] = -INFINITY;
-                sv[i] = 0.0f;
-            }
+    for (int i = 0; i < 16; i++) {  // positions past the split's end
+        const int pos = base + 16 * (i >> 2) + 4 * g + (i & 3);
+        if (pos >= end) {
+            x[i] = -INFINITY;
+            sv[i] = 0.0f;
         }
     }
     float xm = x[0], sm = sv[0];
@@ -606,18 +604,16 @@ __global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_ker
     st.l = 0.0f;
     float *stage = sm.run.stage[wave];
 
-    // Register double buffering: window i+1 is in flight while window i is computed.  Full
-    // windows take the unmasked path; only the window that crosses `end` is masked.
+    // Register double buffering: window i+1 is in flight while window i is computed.  One form
+    // for every window, the tail mask included (a masked and an unmasked copy cost 70 VGPRs
+    // in moves at their join).
 #define TS_STEP(CUR, NXT)                                                                       \
     {                                                                                          \
         load_window<HD>(NXT, str, base + SPAN, n, g, lane);                                     \
         /* keep the prefetch here: the scheduler would otherwise sink it below CUR's use */     \
         asm volatile("" ::: "memory");                                                         \
         __builtin_amdgcn_sched_barrier(0);                                                     \
-        if (base + 64 <= end)                                                                  \
-            process_window<HD, SOFTCAP, false>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
-        else                                                                                   \
-            process_window<HD, SOFTCAP, true>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
+        process_window<HD, SOFTCAP>(CUR, st, sm.run.q, stage, base, end, lane, g, live, lo_col, partner4, inv_s, a.softcap, dc); \
         base += SPAN;                                                                           \
         if (base >= end) break;                                                                \
     }
