@@ -584,7 +584,7 @@ def _split_kernel_name(cfg, n_cu=256):
             c += 64
         return c
 
-    g4 = cfg["n_head"] // cfg["n_kv"] <= 4 and chunk_for(n_cu) >= 1024
+    g4 = cfg["n_head"] // cfg["n_kv"] <= 4 and chunk_for(n_cu - n_cu // 8) >= 1024
     return "decode_split4_kernel" if g4 else "decode_split_kernel"
 
 
