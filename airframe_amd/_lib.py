@@ -35,6 +35,8 @@ SIGNATURES = {
     "ts_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ts_rope_table_host": (ctypes.c_int, [_vp, _i32, _i32, _f, _f]),
     "ts_rope_create": (ctypes.c_int, [_i32, _i32, _f, _f, ctypes.POINTER(_vp)]),
+    "ts_rope_table_host_yarn": (ctypes.c_int, [_vp, _i32, _i32, _f, _f, _f, _f]),
+    "ts_rope_create_yarn": (ctypes.c_int, [_i32, _i32, _f, _f, _f, _f, ctypes.POINTER(_vp)]),
     "ts_rope_destroy": (ctypes.c_int, [_vp]),
     "ts_rope_info": (ctypes.c_int, [_vp, ctypes.POINTER(_vp), _i32p, _i32p]),
     "ts_kv_bytes": (ctypes.c_int, [ctypes.POINTER(KvDesc), _u64p]),

@@ -3,6 +3,7 @@
 // (KVCache), pipeline/layer.rs:805-1246 (run_layer_with_cache_int4 / requantize_all_kv_int4),
 // preflight.rs:28-142 (RoPE table).
 #include <math.h>
+#include <cmath>
 #include <string.h>
 
 #include <algorithm>
@@ -52,18 +53,34 @@ const char *ts_status_string(int status) {
 
 // ---- RoPE ----------------------------------------------------------------------------------
 
-// theta_i = scale / base^(2i/rope_dim) in f32; entry = (cos, sin)(pos * theta_i) in f32.
-// preflight.rs:84-90 (non-YaRN branch) and :97-105.
-int ts_rope_table_host(float *table, int32_t n_pos, int32_t rope_dim, float base, float scale) {
-    if (!table || n_pos <= 0 || rope_dim <= 0 || (rope_dim & 1) || !(base > 0.0f))
+// preflight.rs:71-111 (compute_rope_table), n_pos standing for the spec's n_ctx.  Per pair,
+// in f32 with one rounding per operation (volatile keeps the compiler from fusing them):
+// theta_i = 1 / base^(2i/rope_dim); with YaRN (scale < 1, 0 < alpha < beta; :82-84) the factor
+// is (1 - ramp_i) scale + ramp_i, ramp_i = clamp((l_train / (2 pi / theta_i) - alpha) /
+// (beta - alpha), 0, 1) with l_train = round(n_pos scale) (:77-81, :91-97); otherwise it is
+// scale (:88-90).  Entry (pos, i) = (cos, sin)(pos * theta_i * factor_i).
+int ts_rope_table_host_yarn(float *table, int32_t n_pos, int32_t rope_dim, float base, float scale,
+                            float yarn_alpha, float yarn_beta) {
+    if (!table || n_pos <= 0 || rope_dim <= 0 || (rope_dim & 1) || !(base > 0.0f) ||
+        !(scale > 0.0f) || !std::isfinite(scale))
         return TS_ERR_INVALID;
-    if (!(scale >= 1.0f)) return TS_ERR_UNSUPPORTED;
     const int pairs = rope_dim / 2;
+    const bool yarn = scale < 1.0f && yarn_alpha > 0.0f && yarn_beta > yarn_alpha;
+    const float l_train = yarn ? (float)std::lround((float)n_pos * scale) : 0.0f;
     std::vector<float> theta(pairs);
     for (int i = 0; i < pairs; i++) {
         volatile float expo = (2.0f * (float)i) / (float)rope_dim;
         volatile float inv = 1.0f / powf(base, expo);
-        theta[i] = inv * scale;
+        float factor = scale;
+        if (yarn) {
+            volatile float wavelength = 6.2831855f / inv;  // 2 pi in f32
+            volatile float x = l_train / wavelength;
+            volatile float ramp = (x - yarn_alpha) / (yarn_beta - yarn_alpha);
+            const float r = std::min(1.0f, std::max(0.0f, (float)ramp));
+            volatile float unramped = (1.0f - r) * scale;
+            factor = unramped + r;
+        }
+        theta[i] = inv * factor;
     }
     for (int p = 0; p < n_pos; p++) {
         float *row = table + (size_t)p * pairs * 2;
@@ -76,7 +93,16 @@ int ts_rope_table_host(float *table, int32_t n_pos, int32_t rope_dim, float base
     return TS_OK;
 }
 
+int ts_rope_table_host(float *table, int32_t n_pos, int32_t rope_dim, float base, float scale) {
+    return ts_rope_table_host_yarn(table, n_pos, rope_dim, base, scale, 0.0f, 0.0f);
+}
+
 int ts_rope_create(int32_t n_pos, int32_t rope_dim, float base, float scale, ts_rope **out) {
+    return ts_rope_create_yarn(n_pos, rope_dim, base, scale, 0.0f, 0.0f, out);
+}
+
+int ts_rope_create_yarn(int32_t n_pos, int32_t rope_dim, float base, float scale, float yarn_alpha,
+                        float yarn_beta, ts_rope **out) {
     if (!out) return TS_ERR_INVALID;
     *out = nullptr;
     std::vector<float> host;
@@ -85,7 +111,7 @@ int ts_rope_create(int32_t n_pos, int32_t rope_dim, float base, float scale, ts_
     } catch (...) {
         return TS_ERR_NOMEM;
     }
-    int rc = ts_rope_table_host(host.data(), n_pos, rope_dim, base, scale);
+    int rc = ts_rope_table_host_yarn(host.data(), n_pos, rope_dim, base, scale, yarn_alpha, yarn_beta);
     if (rc) return rc;
     ts_rope *r = new (std::nothrow) ts_rope();
     if (!r) return TS_ERR_NOMEM;

@@ -34,19 +34,25 @@ def _ptr(t: torch.Tensor, dtype: torch.dtype, what: str) -> ctypes.c_void_p:
 class RopeTable:
     """PreflightResources' RoPE table (preflight.rs:71-142): host-computed cos/sin, uploaded."""
 
-    def __init__(self, n_pos: int, rope_dim: int, base: float, scale: float = 1.0):
+    def __init__(self, n_pos: int, rope_dim: int, base: float, scale: float = 1.0,
+                 yarn_alpha: float = 0.0, yarn_beta: float = 0.0):
+        """YaRN (preflight.rs:77-97) when scale < 1 and 0 < yarn_alpha < yarn_beta; n_pos is
+        the table length, the spec's n_ctx."""
         L = load()
         h = ctypes.c_void_p()
-        check("ts_rope_create", L.ts_rope_create(n_pos, rope_dim, base, scale, ctypes.byref(h)))
+        check("ts_rope_create_yarn", L.ts_rope_create_yarn(n_pos, rope_dim, base, scale, yarn_alpha, yarn_beta,
+                                                            ctypes.byref(h)))
         self._h = h
         self.n_pos, self.rope_dim, self.base, self.scale = n_pos, rope_dim, base, scale
 
     @staticmethod
-    def host_table(n_pos: int, rope_dim: int, base: float, scale: float = 1.0):
+    def host_table(n_pos: int, rope_dim: int, base: float, scale: float = 1.0,
+                   yarn_alpha: float = 0.0, yarn_beta: float = 0.0):
         import numpy as np
         t = np.zeros((n_pos, rope_dim // 2, 2), np.float32)
-        check("ts_rope_table_host",
-              load().ts_rope_table_host(t.ctypes.data_as(ctypes.c_void_p), n_pos, rope_dim, base, scale))
+        check("ts_rope_table_host_yarn",
+              load().ts_rope_table_host_yarn(t.ctypes.data_as(ctypes.c_void_p), n_pos, rope_dim, base, scale,
+                                             yarn_alpha, yarn_beta))
         return t
 
     @property

@@ -53,13 +53,20 @@ const char *ts_status_string(int status);
 
 typedef struct ts_rope ts_rope;
 
-/* Fill a host table[n_pos][rope_dim/2][2] = (cos, sin)(pos * theta_i),
- * theta_i = scale / base^(2i/rope_dim).  Replaces PreflightResources::compute_rope_table
- * (preflight.rs:71-111) for scale >= 1 (plain and linear); YaRN (scale < 1) returns
- * TS_ERR_UNSUPPORTED.  Host only; needs no GPU. */
+/* Fill a host table[n_pos][rope_dim/2][2] = (cos, sin)(pos * theta_i), n_pos in the place of
+ * the spec's n_ctx.  Replaces PreflightResources::compute_rope_table (preflight.rs:71-111):
+ * theta_i = 1 / base^(2i/rope_dim) times scale, or, with YaRN (scale < 1 and
+ * 0 < yarn_alpha < yarn_beta), times (1 - ramp_i) scale + ramp_i with
+ * ramp_i = clamp((l_train theta_i / (2 pi) - yarn_alpha) / (yarn_beta - yarn_alpha), 0, 1),
+ * l_train = round(n_pos scale).  scale must be positive and finite.  Host only; needs no GPU. */
+int ts_rope_table_host_yarn(float *table, int32_t n_pos, int32_t rope_dim, float base, float scale,
+                            float yarn_alpha, float yarn_beta);
+/* The same without YaRN parameters (a spec whose yarn_alpha = yarn_beta = 0): theta_i * scale. */
 int ts_rope_table_host(float *table, int32_t n_pos, int32_t rope_dim, float base, float scale);
 
 /* Build the table on the host and upload it (preflight.rs:114-142, upload_rope_table). */
+int ts_rope_create_yarn(int32_t n_pos, int32_t rope_dim, float base, float scale, float yarn_alpha,
+                        float yarn_beta, ts_rope **out);
 int ts_rope_create(int32_t n_pos, int32_t rope_dim, float base, float scale, ts_rope **out);
 int ts_rope_destroy(ts_rope *rope);
 /* Device pointer of the uploaded table and its size (n_pos, rope_dim). */

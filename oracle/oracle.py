@@ -37,6 +37,8 @@ def lib():
         L = ctypes.CDLL(_LIB_PATH)
         L.or_rope_table.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float]
         L.or_rope_table.restype = ctypes.c_int
+        L.or_rope_table_yarn.argtypes = [_f32p, ctypes.c_int, ctypes.c_int] + [ctypes.c_float] * 4
+        L.or_rope_table_yarn.restype = ctypes.c_int
         L.or_rope_rotate.argtypes = [_f32p, ctypes.c_int, _f32p]
         L.or_rope_rotate.restype = None
         L.or_quantize_row.argtypes = [_f32p, ctypes.c_int, ctypes.POINTER(ctypes.c_float), _u32p]
@@ -115,10 +117,12 @@ def qk_norm_row(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     return out
 
 
-def rope_table(n_pos: int, rope_dim: int, base: float, scale: float = 1.0) -> np.ndarray:
-    """[n_pos, rope_dim/2, 2] (cos, sin) table, preflight.rs:71-111."""
+def rope_table(n_pos: int, rope_dim: int, base: float, scale: float = 1.0,
+               yarn_alpha: float = 0.0, yarn_beta: float = 0.0) -> np.ndarray:
+    """[n_pos, rope_dim/2, 2] (cos, sin) table, preflight.rs:71-111 (YaRN when scale < 1 and
+    0 < yarn_alpha < yarn_beta, linear otherwise)."""
     t = np.zeros((n_pos, rope_dim // 2, 2), np.float32)
-    rc = lib().or_rope_table(t, n_pos, rope_dim, base, scale)
+    rc = lib().or_rope_table_yarn(t, n_pos, rope_dim, base, scale, yarn_alpha, yarn_beta)
     if rc != 0:
         raise ValueError("unsupported rope parameters")
     return t

@@ -10,8 +10,8 @@
  *
  *   or_qk_norm_row      src/ops/reference/attention.rs:92-108 (apply_qk_norm), applied to q and
  *                       K before RoPE as at :186-199 (Qwen3)
- *   or_rope_table       src/backend/bindless/preflight.rs:71-111  (compute_rope_table,
- *                       plain/linear branch; theta as in src/ops/reference/rope.rs:150-152)
+ *   or_rope_table(_yarn) src/backend/bindless/preflight.rs:71-111  (compute_rope_table,
+ *                       plain, linear and YaRN; theta as in src/ops/reference/rope.rs:150-152)
  *   or_rope_rotate      src/ops/reference/rope.rs:180-197          (adjacent-pair rotation)
  *   or_quantize_row     src/backend/bindless/test_int4_parity.rs:56-75 (cpu_quantize),
  *                       same arithmetic as sh_quantize_kv.wgsl:56-89
@@ -51,18 +51,36 @@
 
 /* ---- RoPE ------------------------------------------------------------------------- */
 
-/* table[pos][pair][0]=cos(pos*theta_pair), [1]=sin(...), theta_i = 1/base^(2i/rope_dim),
- * times `scale` (the non-YaRN branch of preflight.rs:88-90; rope.rs:154-155 is identical for
- * scale == 1).  YaRN (scale < 1) is rejected: no configuration of this path uses it. */
-int or_rope_table(float *table, int n_pos, int rope_dim, float base, float scale) {
-    if (rope_dim <= 0 || (rope_dim & 1) || n_pos <= 0 || scale < 1.0f) return -1;
+/* table[pos][pair][0]=cos(pos*theta_pair), [1]=sin(...), compute_rope_table
+ * (preflight.rs:71-111) with the table length n_pos standing for n_ctx:
+ *   theta_i = 1/base^(2i/rope_dim)                                         (:87)
+ *   YaRN when scale < 1 and 0 < alpha < beta (:82-84):
+ *     l_train = round(n_pos * scale)                                        (:77-81)
+ *     lambda_i = 2 pi / theta_i, ramp_i = clamp((l_train/lambda_i - alpha)/(beta - alpha), 0, 1)
+ *     theta_i *= (1 - ramp_i) * scale + ramp_i                              (:91-97)
+ *   otherwise theta_i *= scale (plain, linear)                              (:88-90)
+ * All in f32, one rounding per operation, as the reference's Rust. */
+int or_rope_table_yarn(float *table, int n_pos, int rope_dim, float base, float scale, float alpha,
+                       float beta) {
+    if (rope_dim <= 0 || (rope_dim & 1) || n_pos <= 0 || !(scale > 0.0f)) return -1;
     int n_pairs = rope_dim / 2;
     float *theta = (float *)malloc(sizeof(float) * n_pairs);
     if (!theta) return -1;
+    int yarn = scale < 1.0f && alpha > 0.0f && beta > alpha;
+    float l_train = yarn ? (float)(long)roundf((float)n_pos * scale) : 0.0f;
     for (int i = 0; i < n_pairs; i++) {
         float e = (2.0f * (float)i) / (float)rope_dim;
         float t = 1.0f / powf(base, e);
-        theta[i] = t * scale;
+        if (!yarn) {
+            theta[i] = t * scale;
+            continue;
+        }
+        float lambda = 6.2831855f / t;
+        float r = (l_train / lambda - alpha) / (beta - alpha);
+        r = r < 0.0f ? 0.0f : (r > 1.0f ? 1.0f : r);
+        float f = (1.0f - r) * scale;
+        f = f + r;
+        theta[i] = t * f;
     }
     for (int p = 0; p < n_pos; p++) {
         for (int i = 0; i < n_pairs; i++) {
@@ -73,6 +91,11 @@ int or_rope_table(float *table, int n_pos, int rope_dim, float base, float scale
     }
     free(theta);
     return 0;
+}
+
+/* compute_rope_table of a spec without YaRN parameters (alpha = beta = 0): theta_i * scale. */
+int or_rope_table(float *table, int n_pos, int rope_dim, float base, float scale) {
+    return or_rope_table_yarn(table, n_pos, rope_dim, base, scale, 0.0f, 0.0f);
 }
 
 /* In-place rotation of one head vector at one position (rope.rs:186-196). */

@@ -35,13 +35,14 @@ def assert_close(gpu: np.ndarray, ref: np.ndarray, what: str = ""):
 class Pair:
     """The GPU cache and the oracle cache, fed identical inputs."""
 
-    def __init__(self, n_seq, n_kv, hd, max_seq, base, n_layers=1, rope_n_pos=None, rope_dim=None):
+    def __init__(self, n_seq, n_kv, hd, max_seq, base, n_layers=1, rope_n_pos=None, rope_dim=None,
+                 rope_scale=1.0, yarn=(0.0, 0.0)):
         self.n_seq, self.n_kv, self.hd = n_seq, n_kv, hd
         n_pos = rope_n_pos or max_seq
         rd = rope_dim or hd
-        self.rope = RopeTable(n_pos, rd, base)
+        self.rope = RopeTable(n_pos, rd, base, rope_scale, *yarn)
         self.gpu = KVCache.new_int4(n_layers, n_kv, hd, max_seq, n_seq)
-        self.ora = oracle.OracleKV(n_seq, max_seq, n_kv, hd, oracle.rope_table(n_pos, rd, base))
+        self.ora = oracle.OracleKV(n_seq, max_seq, n_kv, hd, oracle.rope_table(n_pos, rd, base, rope_scale, *yarn))
 
     def append(self, k, v, layer=0):
         self.gpu.append_quant(layer, dev(k), dev(v), self.rope)

@@ -49,12 +49,17 @@ def test_status_strings():
     assert b"overflow" in L.ts_status_string(_lib.TS_ERR_OVERFLOW)
 
 
-@pytest.mark.parametrize("n_pos,rope_dim,base,scale", [
-    (600, 64, 500000.0, 1.0), (300, 128, 1000000.0, 1.0), (50, 128, 10000.0, 4.0), (9000, 128, 500000.0, 1.0)])
-def test_host_rope_table_bit_exact_with_oracle(n_pos, rope_dim, base, scale):
+@pytest.mark.parametrize("n_pos,rope_dim,base,scale,alpha,beta", [
+    (600, 64, 500000.0, 1.0, 0.0, 0.0), (300, 128, 1000000.0, 1.0, 1.0, 32.0), (50, 128, 10000.0, 4.0, 0.0, 0.0),
+    (9000, 128, 500000.0, 1.0, 0.0, 0.0),
+    (700, 64, 10000.0, 0.5, 0.0, 0.0),           # linear (no YaRN parameters)
+    (8192, 128, 500000.0, 0.25, 1.0, 32.0),      # YaRN, the spec defaults
+    (4000, 4, 1.0001, 0.5, 0.1, 1.0),            # YaRN, preflight.rs:304-331's spec
+    (3001, 96, 1000000.0, 0.3, 2.0, 16.0)])
+def test_host_rope_table_bit_exact_with_oracle(n_pos, rope_dim, base, scale, alpha, beta):
     from airframe_amd.kv_cache import RopeTable
-    t = RopeTable.host_table(n_pos, rope_dim, base, scale)
-    ref = oracle.rope_table(n_pos, rope_dim, base, scale)
+    t = RopeTable.host_table(n_pos, rope_dim, base, scale, alpha, beta)
+    ref = oracle.rope_table(n_pos, rope_dim, base, scale, alpha, beta)
     assert np.array_equal(t.view(np.uint32), ref.view(np.uint32))
 
 
@@ -63,7 +68,10 @@ def test_host_rope_table_rejects_bad_args():
     buf = np.zeros(64, np.float32)
     p = buf.ctypes.data_as(ctypes.c_void_p)
     assert L.ts_rope_table_host(p, 4, 7, 10000.0, 1.0) == _lib.TS_ERR_INVALID
-    assert L.ts_rope_table_host(p, 4, 8, 10000.0, 0.5) == _lib.TS_ERR_UNSUPPORTED
+    assert L.ts_rope_table_host(p, 4, 8, 10000.0, 0.0) == _lib.TS_ERR_INVALID
+    assert L.ts_rope_table_host(p, 4, 8, 10000.0, float("nan")) == _lib.TS_ERR_INVALID
+    assert L.ts_rope_table_host_yarn(p, 4, 8, 10000.0, -0.5, 1.0, 32.0) == _lib.TS_ERR_INVALID
+    assert L.ts_rope_table_host_yarn(p, 4, 8, 10000.0, 0.5, 1.0, 32.0) == 0
     assert L.ts_rope_table_host(None, 4, 8, 10000.0, 1.0) == _lib.TS_ERR_INVALID
 
 

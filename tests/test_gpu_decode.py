@@ -50,6 +50,20 @@ def test_config1_llama32_1b_single_layer(gpu):
     p.check_codes()
 
 
+@pytest.mark.parametrize("scale,yarn", [(0.25, (1.0, 32.0)), (0.5, (0.0, 0.0))])
+def test_scaled_rope_tables(gpu, scale, yarn):
+    """A YaRN (preflight.rs:77-97) and a linear (scale < 1, :88-90) table: the appended codes
+    bit-exact and the decode within tolerance, both against the oracle on the same table."""
+    say(f"decode rope scale={scale} yarn={yarn}")
+    rng = np.random.default_rng(31)
+    p = Pair(2, 4, 128, 1500, 500000.0, rope_n_pos=4096, rope_scale=scale, yarn=yarn)
+    prefill_cache(p, rng, 1200)
+    for _ in range(2):
+        out, ref = decode_step(p, rng, 16)
+        assert_close(out, ref, "scaled-rope out")
+    p.check_codes()
+
+
 def test_gqa3_hd128_llama32_3b_shape(gpu):
     """Config 2's head shape (24 q / 8 kv, group 3) at a shorter context, several steps."""
     say("decode gqa3")

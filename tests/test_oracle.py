@@ -138,7 +138,49 @@ def test_rope_table_closed_forms():
     t2 = oracle.rope_table(8, 8, 10000.0, 2.0)
     assert np.allclose(t2[3, 0], [np.cos(6.0), np.sin(6.0)], atol=1e-6)
     with pytest.raises(ValueError):
-        oracle.rope_table(8, 8, 10000.0, 0.5)  # YaRN branch is not part of this path
+        oracle.rope_table(8, 8, 10000.0, 0.0)
+
+
+def test_rope_table_reference_vectors():
+    """The reference's own table tests (preflight.rs:266-331)."""
+    # distance 0 is (1, 0) whatever the scaling (:266-285)
+    for args in [(4, 4, 10000.0, 1.0), (4, 4, 10000.0, 0.5), (4000, 4, 1.0001, 0.5, 0.1, 1.0)]:
+        t = oracle.rope_table(*args)
+        assert (np.abs(t[0, :, 0] - 1.0) < 1e-6).all() and (np.abs(t[0, :, 1]) < 1e-6).all()
+    # linear scale 0.5, no YaRN parameters: pair 0 at distance 1 is cos(0.5) (:287-302)
+    t = oracle.rope_table(4, 4, 10000.0, 0.5)
+    assert abs(t[1, 0, 0] - np.cos(np.float32(0.5))) < 1e-6
+    # YaRN with a tiny base: pair 0 is a short wavelength, its ramp clamps to 1 and it keeps
+    # theta unscaled, cos(1), unlike the linear table's cos(0.5) (:304-331)
+    ty = oracle.rope_table(4000, 4, 1.0001, 0.5, 0.1, 1.0)
+    tl = oracle.rope_table(4000, 4, 1.0001, 0.5)
+    assert abs(ty[1, 0, 0] - tl[1, 0, 0]) > 1e-3
+    assert abs(ty[1, 0, 0] - np.cos(1.0)) < 1e-4
+
+
+def test_rope_table_yarn_ramp_ends_and_transition():
+    """YaRN's two ends reduce to the plain tables: pairs whose ramp clamps to 1 equal the
+    unscaled table bit for bit (factor (1-1) s + 1 = 1), pairs clamped to 0 equal the linear one
+    (factor s).  Between them the factor falls monotonically, and where each end starts pins
+    l_train = round(n_pos * scale) and the roles of alpha and beta."""
+    n_pos, d, base, s, a, b = 8192, 128, 500000.0, 0.25, 1.0, 32.0
+    ty = oracle.rope_table(n_pos, d, base, s, a, b)
+    t1 = oracle.rope_table(n_pos, d, base, 1.0)
+    ts = oracle.rope_table(n_pos, d, base, s)
+    i = np.arange(d // 2)
+    theta = base ** (-2.0 * i / d)
+    x = round(n_pos * s) * theta / (2 * np.pi)  # l_train / wavelength, float64
+    hi, lo = x >= b * 1.001, x <= a * 0.999
+    assert hi.sum() >= 3 and lo.sum() >= 3 and (~hi & ~lo).sum() >= 3
+    assert np.array_equal(ty[:, hi].view(np.uint32), t1[:, hi].view(np.uint32))
+    assert np.array_equal(ty[:, lo].view(np.uint32), ts[:, lo].view(np.uint32))
+    # effective theta from the table: angle at distance 1
+    eff = np.arctan2(ty[1, :, 1], ty[1, :, 0]).astype(np.float64) / theta
+    mid = ~hi & ~lo
+    assert ((eff[mid] > s) & (eff[mid] < 1.0)).all()
+    assert (np.diff(eff[mid]) < 0).all()  # ramp falls as the wavelength grows
+    # a linear ramp in x between the ends: factor = s + (1 - s) (x - a) / (b - a)
+    assert np.allclose(eff[mid], s + (1 - s) * (x[mid] - a) / (b - a), rtol=2e-5)
 
 
 def test_rope_rotation_is_pairwise_rotation():
