@@ -35,6 +35,8 @@ SIGNATURES = {
     "ts_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ts_rope_table_host": (ctypes.c_int, [_vp, _i32, _i32, _f, _f]),
     "ts_rope_create": (ctypes.c_int, [_i32, _i32, _f, _f, ctypes.POINTER(_vp)]),
+    "ts_weights_src_bytes": (ctypes.c_int, [_i32, ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint64)]),
+    "ts_weights_to_f16": (ctypes.c_int, [_i32, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp]),
     "ts_rope_table_host_yarn": (ctypes.c_int, [_vp, _i32, _i32, _f, _f, _f, _f]),
     "ts_rope_create_yarn": (ctypes.c_int, [_i32, _i32, _f, _f, _f, _f, ctypes.POINTER(_vp)]),
     "ts_rope_destroy": (ctypes.c_int, [_vp]),
@@ -69,6 +71,11 @@ SIGNATURES = {
     "ts_attn_out_proj_workspace": (ctypes.c_int, [_i32, _i32, _i32, _u64p]),
     "ts_attn_out_proj": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, ctypes.c_uint64,
                                         _vp]),
+    "ts_qkv_append_x2": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp,
+                                        _vp, _vp, _vp, ctypes.c_uint64, _vp]),
+    "ts_attn_out_proj_x2": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, ctypes.c_uint64,
+                                           _vp]),
+    "ts_weights_to_f16x2": (ctypes.c_int, [_i32, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp]),
 }
 
 _lib = None

@@ -39,6 +39,7 @@ SOURCES = {
     "ts_prefill.hip": MFMA_VGPR,
     "ts_qkv.hip": EXACT,
     "ts_proj.hip": EXACT,
+    "ts_weights.hip": EXACT,
 }
 HEADERS = ["ts_internal.h", "ts_mfma.h", "ts_quant.h", "ts_store.h", "ts_gemm.h", os.path.join("..", "..", "include", "turboshimmy.h")]
 

@@ -45,6 +45,8 @@ struct XTiles {
 // 64 wr + 32 rb + .., columns 64 wc + 32 cb + .. in acc[rb][cb].  Staging thread (si = tid / 4,
 // sc = tid % 4) owns 16 floats of x row si per chunk: xs points at them for chunk 0 (null: a
 // zero row).  wp[cb]: the lane's weight row of column block cb at its chunk-0 offset 32 hf.
+// xwrap: x has xwrap chunks and weight chunk c multiplies x chunk c mod xwrap (nch = 2 xwrap:
+// rows of two weight planes, hi then lo, against the same x; nch = xwrap: one plane).
 // Both operands run D chunks ahead: x and the weights of chunk c + D are loaded into a ring of
 // D register sets while chunk c is multiplied, and x of chunk c + 1 goes to LDS (hi/lo,
 // double-buffered) after chunk c's matrix work, so each load has D - 1 iterations to arrive.
@@ -52,8 +54,8 @@ struct XTiles {
 // chunks ahead, while D = 4 drops to one wave per SIMD and is slower.
 template <int WR, int D = 3>
 __device__ __forceinline__ void gemm_tile_core(XTiles<64 * WR> &sm, const float *xs,
-                                                    const _Float16 *const (&wp)[2], int nch, int tid,
-                                                    floatx16 (&acc)[2][2]) {
+                                                    const _Float16 *const (&wp)[2], int nch, int xwrap,
+                                                    int tid, floatx16 (&acc)[2][2]) {
     const int wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5, wr = wave >> 2;
     const int si = tid >> 2, sc = tid & 3;
 #pragma unroll
@@ -65,9 +67,10 @@ __device__ __forceinline__ void gemm_tile_core(XTiles<64 * WR> &sm, const float 
     half8 wq[D][2][4];
     auto load = [&](float4 (&x)[4], half8 (&w)[2][4], int c) {
         const bool on = c < nch;
+        const int cx = c >= xwrap ? c - xwrap : c;
 #pragma unroll
         for (int u = 0; u < 4; u++)
-            x[u] = (xs && on) ? *reinterpret_cast<const float4 *>(xs + c * kKC + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+            x[u] = (xs && on) ? *reinterpret_cast<const float4 *>(xs + cx * kKC + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int cb = 0; cb < 2; cb++)
 #pragma unroll
@@ -126,10 +129,12 @@ struct SplitTiles {
 // loaded in one go -- x into LDS as hi/lo (shared by the 4 waves), the weights straight into B
 // operands -- so a batch costs one memory round trip, then 64 MFMAs per wave.  Wave w
 // accumulates columns 64 w + 32 cb + .. in acc[cb].  Staging thread (si = tid / 8, sc = tid % 8)
-// owns 8 floats of x row si per chunk (xs at chunk 0 of the slice, null: a zero row); wp[cb]:
-// the lane's weight row of column block cb at the slice's chunk 0, offset 32 hf.
-__device__ __forceinline__ void gemm_split_core(SplitTiles &sm, const float *xs, const _Float16 *const (&wp)[2],
-                                                int nbat, int tid, floatx16 (&acc)[2]) {
+// owns 8 floats of x row si per chunk (xs at chunk 0 of the row, null: a zero row); the slice
+// starts at weight chunk c0, and weight chunk c multiplies x chunk c mod xwrap (as in
+// gemm_tile_core); wp[cb]: the lane's weight row of column block cb at chunk c0, offset 32 hf.
+__device__ __forceinline__ void gemm_split_core(SplitTiles &sm, const float *xs, int c0, int xwrap,
+                                                const _Float16 *const (&wp)[2], int nbat, int tid,
+                                                floatx16 (&acc)[2]) {
     constexpr int NB = 4;
     const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int si = tid >> 3, sc = tid & 7;
@@ -144,8 +149,10 @@ __device__ __forceinline__ void gemm_split_core(SplitTiles &sm, const float *xs,
             xu[c] = make_float4(0.f, 0.f, 0.f, 0.f);
             xv[c] = xu[c];
             if (xs) {
-                xu[c] = *reinterpret_cast<const float4 *>(xs + ko + c * kKC);
-                xv[c] = *reinterpret_cast<const float4 *>(xs + ko + c * kKC + 4);
+                int cx = c0 + b * NB + c;
+                cx = cx >= xwrap ? cx - xwrap : cx;
+                xu[c] = *reinterpret_cast<const float4 *>(xs + cx * kKC);
+                xv[c] = *reinterpret_cast<const float4 *>(xs + cx * kKC + 4);
             }
 #pragma unroll
             for (int cb = 0; cb < 2; cb++)

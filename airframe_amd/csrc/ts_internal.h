@@ -174,7 +174,7 @@ QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok);
 hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x, int dim, int n_tok,
                       const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int n_head,
                       float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,
-                      const QkvPlan &plan, float *part, hipStream_t st);
+                      const QkvPlan &plan, float *part, int planes, hipStream_t st);
 
 // Attention output projection (ts_proj.hip).
 struct ProjPlan {
@@ -183,6 +183,6 @@ struct ProjPlan {
 };
 ProjPlan proj_plan(int M, int K, int N);
 hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, float *act, float *stash,
-                       const ProjPlan &plan, float *part, hipStream_t st);
+                       const ProjPlan &plan, float *part, int planes, hipStream_t st);
 
 }  // namespace ts

@@ -546,14 +546,18 @@ int ts_qkv_workspace(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head
     if (!kv || !bytes) return TS_ERR_INVALID;
     if (kv->d.head_dim != 128 && kv->d.head_dim != 64) return TS_ERR_UNSUPPORTED;
     if (!qkv_shape_ok(kv, dim, n_tok, n_head)) return TS_ERR_INVALID;
-    *bytes = n_tok == 0 ? 0 : ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, dim, n_tok).part_bytes;
+    // enough for f16 rows and for two-plane rows (ts_qkv_append_x2)
+    *bytes = 0;
+    for (int planes = 1; n_tok > 0 && planes <= 2; planes++)
+        *bytes = std::max(*bytes, ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, planes * dim,
+                                               n_tok).part_bytes);
     return TS_OK;
 }
 
-int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32_t n_tok,
-                  const uint16_t *d_wq, const uint16_t *d_wk, const uint16_t *d_wv, int32_t n_head,
-                  const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
-                  uint64_t workspace_bytes, void *stream) {
+static int qkv_append_planes(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32_t n_tok,
+                             const uint16_t *d_wq, const uint16_t *d_wk, const uint16_t *d_wv, int32_t n_head,
+                             const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
+                             uint64_t workspace_bytes, void *stream, int planes) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers) return TS_ERR_INVALID;
     if (kv->d.head_dim != 128 && kv->d.head_dim != 64) return TS_ERR_UNSUPPORTED;
     if (!qkv_shape_ok(kv, dim, n_tok, n_head) || !d_x || !d_wq || !d_wk || !d_wv || !d_q ||
@@ -565,32 +569,64 @@ int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32
     int rc = check_rope(rope, kv->d.head_dim, rot_end(kv, n_tok));
     if (rc) return rc;
     if (n_tok == 0) return TS_OK;
-    const ts::QkvPlan plan = ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, dim, n_tok);
+    const ts::QkvPlan plan = ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, planes * dim, n_tok);
     if (plan.part_bytes > 0 && (!d_workspace || workspace_bytes < plan.part_bytes || !aligned16(d_workspace)))
         return TS_ERR_WORKSPACE;
     return hip_status(ts::launch_qkv(kv->layer(layer), kv->d_len, d_x, dim, n_tok, d_wq, d_wk, d_wv,
                                      n_head, d_q, d_k, d_v, rope->d_table, rope->rope_dim / 2, plan,
-                                     static_cast<float *>(d_workspace), as_stream(stream)));
+                                     static_cast<float *>(d_workspace), planes, as_stream(stream)));
+}
+
+int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32_t n_tok,
+                  const uint16_t *d_wq, const uint16_t *d_wk, const uint16_t *d_wv, int32_t n_head,
+                  const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
+                  uint64_t workspace_bytes, void *stream) {
+    return qkv_append_planes(kv, layer, d_x, dim, n_tok, d_wq, d_wk, d_wv, n_head, rope, d_q, d_k, d_v,
+                             d_workspace, workspace_bytes, stream, 1);
+}
+
+int ts_qkv_append_x2(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32_t n_tok,
+                     const uint16_t *d_wq, const uint16_t *d_wk, const uint16_t *d_wv, int32_t n_head,
+                     const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
+                     uint64_t workspace_bytes, void *stream) {
+    return qkv_append_planes(kv, layer, d_x, dim, n_tok, d_wq, d_wk, d_wv, n_head, rope, d_q, d_k, d_v,
+                             d_workspace, workspace_bytes, stream, 2);
 }
 
 int ts_attn_out_proj_workspace(int32_t n_tok, int32_t attn_dim, int32_t dim, uint64_t *bytes) {
     if (!bytes || n_tok < 0 || attn_dim <= 0 || attn_dim % 64 != 0 || dim <= 0) return TS_ERR_INVALID;
-    *bytes = n_tok == 0 ? 0 : ts::proj_plan(n_tok, attn_dim, dim).part_bytes;
+    *bytes = 0;  // enough for f16 rows and for two-plane rows (ts_attn_out_proj_x2)
+    for (int planes = 1; n_tok > 0 && planes <= 2; planes++)
+        *bytes = std::max(*bytes, ts::proj_plan(n_tok, planes * attn_dim, dim).part_bytes);
     return TS_OK;
+}
+
+static int out_proj_planes(const float *d_attn, int32_t n_tok, int32_t attn_dim, const uint16_t *d_wo,
+                           int32_t dim, float *d_act, float *d_stash, void *d_workspace,
+                           uint64_t workspace_bytes, void *stream, int planes) {
+    if (!d_attn || !d_wo || !d_act || n_tok < 0 || attn_dim <= 0 || attn_dim % 64 != 0 || dim <= 0 ||
+        !aligned16(d_attn) || !aligned16(d_wo) || !aligned16(d_act) || !aligned16(d_stash))
+        return TS_ERR_INVALID;
+    if (n_tok == 0) return TS_OK;
+    const ts::ProjPlan plan = ts::proj_plan(n_tok, planes * attn_dim, dim);
+    if (plan.part_bytes > 0 && (!d_workspace || workspace_bytes < plan.part_bytes || !aligned16(d_workspace)))
+        return TS_ERR_WORKSPACE;
+    return hip_status(ts::launch_proj(d_attn, n_tok, attn_dim, d_wo, dim, d_act, d_stash, plan,
+                                      static_cast<float *>(d_workspace), planes, as_stream(stream)));
 }
 
 int ts_attn_out_proj(const float *d_attn, int32_t n_tok, int32_t attn_dim, const uint16_t *d_wo,
                      int32_t dim, float *d_act, float *d_stash, void *d_workspace,
                      uint64_t workspace_bytes, void *stream) {
-    if (!d_attn || !d_wo || !d_act || n_tok < 0 || attn_dim <= 0 || attn_dim % 64 != 0 || dim <= 0 ||
-        !aligned16(d_attn) || !aligned16(d_wo) || !aligned16(d_act) || !aligned16(d_stash))
-        return TS_ERR_INVALID;
-    if (n_tok == 0) return TS_OK;
-    const ts::ProjPlan plan = ts::proj_plan(n_tok, attn_dim, dim);
-    if (plan.part_bytes > 0 && (!d_workspace || workspace_bytes < plan.part_bytes || !aligned16(d_workspace)))
-        return TS_ERR_WORKSPACE;
-    return hip_status(ts::launch_proj(d_attn, n_tok, attn_dim, d_wo, dim, d_act, d_stash, plan,
-                                      static_cast<float *>(d_workspace), as_stream(stream)));
+    return out_proj_planes(d_attn, n_tok, attn_dim, d_wo, dim, d_act, d_stash, d_workspace, workspace_bytes,
+                           stream, 1);
+}
+
+int ts_attn_out_proj_x2(const float *d_attn, int32_t n_tok, int32_t attn_dim, const uint16_t *d_wo,
+                        int32_t dim, float *d_act, float *d_stash, void *d_workspace,
+                        uint64_t workspace_bytes, void *stream) {
+    return out_proj_planes(d_attn, n_tok, attn_dim, d_wo, dim, d_act, d_stash, d_workspace, workspace_bytes,
+                           stream, 2);
 }
 
 }  // extern "C"

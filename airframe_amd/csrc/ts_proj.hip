@@ -29,6 +29,7 @@ struct ProjArgs {
     float *stash;        // [M][N] raw dot, or null
     float *part;         // [n_split][RT][CT][32][256] partials, or null
     int M, N, K;
+    int KW;              // weight row length: K (f16 rows) or 2 K (hi then lo planes)
     int RT, CT, kps, n_split, n_wg;
 };
 
@@ -57,10 +58,10 @@ __global__ __launch_bounds__(256) void proj_tile_kernel(ProjArgs p) {
     const int row0 = 64 * rt, col0 = kPT * ct + 64 * wave;
     const int si = tid >> 2, sc = tid & 3;
     const float *xs = row0 + si < p.M ? p.a + (size_t)(row0 + si) * p.K + 16 * sc : nullptr;
-    const _Float16 *const wp[2] = {p.w + (size_t)min(col0 + j, p.N - 1) * p.K + 32 * hf,
-                                   p.w + (size_t)min(col0 + 32 + j, p.N - 1) * p.K + 32 * hf};
+    const _Float16 *const wp[2] = {p.w + (size_t)min(col0 + j, p.N - 1) * p.KW + 32 * hf,
+                                   p.w + (size_t)min(col0 + 32 + j, p.N - 1) * p.KW + 32 * hf};
     floatx16 acc[2][2];
-    gemm_tile_core<1>(sm, xs, wp, p.K / kKC, tid, acc);
+    gemm_tile_core<1>(sm, xs, wp, p.KW / kKC, p.K / kKC, tid, acc);
 #pragma unroll
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
@@ -79,13 +80,13 @@ __global__ __launch_bounds__(256) void proj_split_kernel(ProjArgs p) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int row0 = 32 * rt, col0 = kPT * ct + 64 * wave;
     const int kb = sp * p.kps;
-    const int nbat = (min(kb + p.kps, p.K) - kb) / (4 * kKC);
+    const int nbat = (min(kb + p.kps, p.KW) - kb) / (4 * kKC);
     const int si = tid >> 3, sc = tid & 7;
-    const float *xs = row0 + si < p.M ? p.a + (size_t)(row0 + si) * p.K + kb + 8 * sc : nullptr;
-    const _Float16 *const wp[2] = {p.w + (size_t)min(col0 + j, p.N - 1) * p.K + kb + 32 * hf,
-                                   p.w + (size_t)min(col0 + 32 + j, p.N - 1) * p.K + kb + 32 * hf};
+    const float *xs = row0 + si < p.M ? p.a + (size_t)(row0 + si) * p.K + 8 * sc : nullptr;
+    const _Float16 *const wp[2] = {p.w + (size_t)min(col0 + j, p.N - 1) * p.KW + kb + 32 * hf,
+                                   p.w + (size_t)min(col0 + 32 + j, p.N - 1) * p.KW + kb + 32 * hf};
     floatx16 acc[2];
-    gemm_split_core(sm, xs, wp, nbat, tid, acc);
+    gemm_split_core(sm, xs, kb / kKC, p.K / kKC, wp, nbat, tid, acc);
     float *dst = p.part + (((size_t)sp * p.RT + rt) * p.CT + ct) * (32 * kPT);
 #pragma unroll
     for (int cb = 0; cb < 2; cb++)
@@ -152,8 +153,8 @@ ProjPlan proj_plan(int M, int K, int N) {
 }
 
 hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, float *act, float *stash,
-                       const ProjPlan &plan, float *part, hipStream_t st) {
-    if (K % kKC != 0 || M <= 0 || N <= 0) return hipErrorInvalidValue;
+                       const ProjPlan &plan, float *part, int planes, hipStream_t st) {
+    if (K % kKC != 0 || M <= 0 || N <= 0 || (planes != 1 && planes != 2)) return hipErrorInvalidValue;
     ProjArgs p;
     p.a = a;
     p.w = reinterpret_cast<const _Float16 *>(w);
@@ -163,6 +164,7 @@ hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, f
     p.M = M;
     p.N = N;
     p.K = K;
+    p.KW = planes * K;
     p.RT = plan.RT;
     p.CT = plan.CT;
     p.kps = plan.kps;

@@ -54,6 +54,7 @@ struct QkvArgs {
     int rope_pairs;
     float *part;           // split partials [n_split][RT][CT][32][256], or null
     int dim, n_tok, n_head;
+    int wld;               // weight row length: dim (f16 rows) or 2 dim (hi then lo planes)
     int hd, hpt;           // head dim; kv heads per column tile (128 / hd)
     int n_qt;              // q column tiles (ceil(n_head * hd / 256))
     int RT, CT;            // row and column tiles
@@ -101,11 +102,11 @@ __device__ inline int x_row(const QkvArgs &a, const RowTile &t, int i) {
 __device__ inline const _Float16 *w_row(const QkvArgs &a, int ct, int n) {
     if (ct < a.n_qt) {
         const int r = min(ct * kNT + n, a.n_head * a.hd - 1);
-        return a.wq + (size_t)r * a.dim;
+        return a.wq + (size_t)r * a.wld;
     }
     const int j = n / (2 * a.hd), c = n % (2 * a.hd);
     const int h = min((ct - a.n_qt) * a.hpt + j, a.L.H - 1);
-    return c < a.hd ? a.wk + ((size_t)h * a.hd + c) * a.dim : a.wv + ((size_t)h * a.hd + c - a.hd) * a.dim;
+    return c < a.hd ? a.wk + ((size_t)h * a.hd + c) * a.wld : a.wv + ((size_t)h * a.hd + c - a.hd) * a.wld;
 }
 
 // Workgroup id -> (row tile, column tile, split), ordered so that each XCD (workgroups are
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(256 * WR) void qkv_tile_kernel(QkvArgs a) {
     const float *xs = xr >= 0 ? a.x + (size_t)xr * a.dim + 16 * sc : nullptr;
     const _Float16 *const wp[2] = {w_row(a, ct, 64 * wc + j) + 32 * hf, w_row(a, ct, 64 * wc + 32 + j) + 32 * hf};
     floatx16 acc[2][2];
-    gemm_tile_core<WR>(sm.x, xs, wp, a.dim / kKC, tid, acc);
+    gemm_tile_core<WR>(sm.x, xs, wp, a.wld / kKC, a.dim / kKC, tid, acc);
 
     // Epilogue, one 32-row block at a time: the waves holding it (wr = b / 2, row block b % 2)
     // write it to the LDS tile, then the first 4 waves run the block's epilogue.  The block
@@ -354,12 +355,12 @@ __global__ __launch_bounds__(256) void qkv_split_kernel(QkvArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int xr = x_row(a, t, tid >> 3);
     const int kb = sp * a.kps;
-    const int nbat = (min(kb + a.kps, a.dim) - kb) / (4 * kKC);
-    const float *xs = xr >= 0 ? a.x + (size_t)xr * a.dim + kb + 8 * (tid & 7) : nullptr;
+    const int nbat = (min(kb + a.kps, a.wld) - kb) / (4 * kKC);
+    const float *xs = xr >= 0 ? a.x + (size_t)xr * a.dim + 8 * (tid & 7) : nullptr;
     const _Float16 *const wp[2] = {w_row(a, ct, 64 * wave + j) + kb + 32 * hf,
                                    w_row(a, ct, 64 * wave + 32 + j) + kb + 32 * hf};
     floatx16 acc[2];
-    gemm_split_core(sm, xs, wp, nbat, tid, acc);
+    gemm_split_core(sm, xs, kb / kKC, a.dim / kKC, wp, nbat, tid, acc);
     // D layout: register 4q + r of column block cb is row 8q + 4hf + r, column 64 wave + 32 cb + j
     float *dst = a.part + (((size_t)sp * a.RT + rt) * a.CT + ct) * (kMT * kNT);
 #pragma unroll
@@ -424,8 +425,8 @@ QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok) {
 hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x, int dim, int n_tok,
                       const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int n_head,
                       float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,
-                      const QkvPlan &plan, float *part, hipStream_t st) {
-    if ((L.hd != 128 && L.hd != 64) || dim % kKC != 0) return hipErrorInvalidValue;
+                      const QkvPlan &plan, float *part, int planes, hipStream_t st) {
+    if ((L.hd != 128 && L.hd != 64) || dim % kKC != 0 || (planes != 1 && planes != 2)) return hipErrorInvalidValue;
     QkvArgs a;
     a.L = L;
     a.len = d_len;
@@ -440,6 +441,7 @@ hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x
     a.rope_pairs = rope ? rope_pairs : 0;
     a.part = plan.n_split > 1 ? part : nullptr;
     a.dim = dim;
+    a.wld = planes * dim;
     a.n_tok = n_tok;
     a.n_head = n_head;
     a.hd = L.hd;

@@ -294,19 +294,25 @@ class KVCache:
 
     def qkv_append(self, layer: int, x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor,
                    wv: torch.Tensor, rope: RopeTable, q_out: torch.Tensor = None,
-                   kv_out: tuple | None = None, workspace: torch.Tensor = None, stream=None):
+                   kv_out: tuple | None = None, workspace: torch.Tensor = None, stream=None,
+                   planes: int = 1):
         """main_qkv + quantize_kv in one pass: q = Wq x (returned), k = Wk x and v = Wv x
         quantized into the cache at len[s] + t.  x: [n_seq, n_tok, dim] f32; wq: [n_head *
         head_dim, dim], wk, wv: [n_head_kv * head_dim, dim] f16.  kv_out: optional (k, v)
-        tensors [n_seq, n_tok, n_head_kv, head_dim] f32 that receive the raw projections."""
+        tensors [n_seq, n_tok, n_head_kv, head_dim] f32 that receive the raw projections.
+        planes=2: weight rows of [hi dim | lo dim] f16 (weights.to_f16x2, the F32 and GGUF block
+        formats at about f32 accuracy) through ts_qkv_append_x2."""
         if x.dim() != 3 or x.shape[0] != self.n_seq:
             raise ValueError("x must be [n_seq, n_tok, dim]")
         n_tok, dim = x.shape[1], x.shape[2]
         n_head = wq.shape[0] // self.head_dim
         kv_rows = self.n_head_kv * self.head_dim
-        if (wq.shape != (n_head * self.head_dim, dim) or wk.shape != (kv_rows, dim)
-                or wv.shape != (kv_rows, dim)):
-            raise ValueError("wq must be [n_head*head_dim, dim], wk/wv [n_head_kv*head_dim, dim]")
+        if planes not in (1, 2):
+            raise ValueError("planes must be 1 or 2")
+        wd = planes * dim
+        if (wq.shape != (n_head * self.head_dim, wd) or wk.shape != (kv_rows, wd)
+                or wv.shape != (kv_rows, wd)):
+            raise ValueError("wq must be [n_head*head_dim, planes*dim], wk/wv [n_head_kv*head_dim, planes*dim]")
         want = (self.n_seq, n_tok, n_head, self.head_dim)
         if q_out is None:
             q_out = torch.empty(want, dtype=torch.float32, device=x.device)
@@ -318,8 +324,9 @@ class KVCache:
             self._check_kv(k_out, v_out, n_tok)
             kp, vp = _ptr(k_out, torch.float32, "k_out"), _ptr(v_out, torch.float32, "v_out")
         ws = workspace if workspace is not None else self.qkv_workspace(dim, n_tok, n_head)
-        check("ts_qkv_append",
-              load().ts_qkv_append(self._h, layer, _ptr(x, torch.float32, "x"), dim, n_tok,
+        fn = "ts_qkv_append" if planes == 1 else "ts_qkv_append_x2"
+        check(fn,
+              getattr(load(), fn)(self._h, layer, _ptr(x, torch.float32, "x"), dim, n_tok,
                                    _ptr(wq, torch.float16, "wq"), _ptr(wk, torch.float16, "wk"),
                                    _ptr(wv, torch.float16, "wv"), n_head, rope.handle,
                                    _ptr(q_out, torch.float32, "q_out"), kp, vp,
@@ -361,15 +368,16 @@ _proj_ws: dict = {}
 
 def attn_out_proj(attn: torch.Tensor, wo: torch.Tensor, act: torch.Tensor,
                   stash: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
-                  stream=None) -> torch.Tensor:
+                  stream=None, planes: int = 1) -> torch.Tensor:
     """main_attn_proj (sh_layer_v1.wgsl:763-821, F16 weights): act += Wo attn per token, the raw
     product into `stash` when given.  attn: [n_tok, attn_dim] f32 (any leading shape flattened
-    to tokens), wo: [dim, attn_dim] f16, act (and stash): [n_tok, dim] f32.  Returns act."""
+    to tokens), wo: [dim, attn_dim] f16, act (and stash): [n_tok, dim] f32.  Returns act.
+    planes=2: wo rows of [hi attn_dim | lo attn_dim] (weights.to_f16x2), ts_attn_out_proj_x2."""
     attn2 = attn.reshape(-1, attn.shape[-1])
     n_tok, attn_dim = attn2.shape
     dim = wo.shape[0]
-    if wo.shape != (dim, attn_dim):
-        raise ValueError("wo must be [dim, attn_dim]")
+    if planes not in (1, 2) or wo.shape != (dim, planes * attn_dim):
+        raise ValueError("wo must be [dim, planes*attn_dim], planes 1 or 2")
     if act.numel() != n_tok * dim or (stash is not None and stash.numel() != n_tok * dim):
         raise ValueError("act/stash must hold [n_tok, dim]")
     ws = workspace
@@ -381,8 +389,9 @@ def attn_out_proj(attn: torch.Tensor, wo: torch.Tensor, act: torch.Tensor,
                   load().ts_attn_out_proj_workspace(n_tok, attn_dim, dim, ctypes.byref(b)))
             _proj_ws[key] = torch.empty(max(b.value, 16), dtype=torch.uint8, device=attn.device)
         ws = _proj_ws[key]
-    check("ts_attn_out_proj",
-          load().ts_attn_out_proj(_ptr(attn2, torch.float32, "attn"), n_tok, attn_dim,
+    fn = "ts_attn_out_proj" if planes == 1 else "ts_attn_out_proj_x2"
+    check(fn,
+          getattr(load(), fn)(_ptr(attn2, torch.float32, "attn"), n_tok, attn_dim,
                                   _ptr(wo, torch.float16, "wo"), dim, _ptr(act, torch.float32, "act"),
                                   _ptr(stash, torch.float32, "stash") if stash is not None else None,
                                   ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))

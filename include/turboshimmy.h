@@ -232,10 +232,44 @@ int ts_attn_decode_append_noalloc(ts_kv *kv, int32_t layer, const float *d_k, co
 int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
                     int32_t n_tok, const ts_rope *rope, float softcap, float *d_out, void *stream);
 
+/* ---- Projection weights in GGUF formats ------------------------------------------------- */
+
+/* GGML type ids (ggml_types.rs) of the weight formats main_qkv and main_attn_proj read
+ * (sh_layer_v1_int4.wgsl:497-520, sh_layer_v1.wgsl:777-790). */
+enum {
+    TS_GGML_F32 = 0,
+    TS_GGML_F16 = 1,
+    TS_GGML_Q4_0 = 2,
+    TS_GGML_Q5_0 = 6,
+    TS_GGML_Q8_0 = 8,
+    TS_GGML_Q4_K = 12,
+    TS_GGML_Q5_K = 13,
+    TS_GGML_Q6_K = 14
+};
+
+/* Bytes of an [n_rows][n_cols] weight matrix of that type (n_cols a multiple of the block:
+ * 32 for Q4_0/Q5_0/Q8_0, 256 for the K formats, 8 for F32/F16).  Host only. */
+int ts_weights_src_bytes(int32_t ggml_type, int64_t n_rows, int64_t n_cols, uint64_t *bytes);
+
+/* Convert a weight matrix of that type on the device into the f16 row-major [n_rows][n_cols]
+ * that ts_qkv_append and ts_attn_out_proj take (d_dst 16-byte aligned), once at load.  Each
+ * element is the reference's CPU dequantized value (src/core/dequant/, the F32 and block
+ * branches of main_qkv) rounded to f16, nearest even: the projections then differ from the
+ * reference's f32-weight dot by that rounding (relative 2^-11 per weight) on top of their own. */
+int ts_weights_to_f16(int32_t ggml_type, const void *d_src, int64_t n_rows, int64_t n_cols,
+                      uint16_t *d_dst, void *stream);
+
+/* The same into two f16 planes per row, d_dst [n_rows][2 n_cols]: the first n_cols the value
+ * rounded to f16 (hi), the next n_cols the rest (value - hi, exact in f32) rounded to f16 (lo).
+ * ts_qkv_append_x2 and ts_attn_out_proj_x2 take such rows and multiply each x by hi + lo, so
+ * the projections keep the f32 weights to about 22 bits. */
+int ts_weights_to_f16x2(int32_t ggml_type, const void *d_src, int64_t n_rows, int64_t n_cols,
+                        uint16_t *d_dst, void *stream);
+
 /* ---- QKV projection with the append as its epilogue ------------------------------------ */
 
-/* Bytes of scratch ts_qkv_append needs for this shape (0 when the projection is not split
- * over dim).  Host only. */
+/* Bytes of scratch ts_qkv_append and ts_qkv_append_x2 need for this shape (0 when the
+ * projection is not split over dim).  Host only. */
 int ts_qkv_workspace(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head, uint64_t *bytes);
 
 /* main_qkv (sh_layer_v1_int4.wgsl:454-575, F16 weights: the formula slot 1 branch at :494-498)
@@ -255,10 +289,18 @@ int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32
                   const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
                   uint64_t workspace_bytes, void *stream);
 
+/* ts_qkv_append with weights of two f16 planes per row ([rows][2 dim], ts_weights_to_f16x2):
+ * the reference's F32 and block-format weights (main_qkv, sh_layer_v1_int4.wgsl:502-520) at
+ * about f32 accuracy.  Twice the weight bytes and matrix work of the f16 form. */
+int ts_qkv_append_x2(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32_t n_tok,
+                     const uint16_t *d_wq, const uint16_t *d_wk, const uint16_t *d_wv, int32_t n_head,
+                     const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
+                     uint64_t workspace_bytes, void *stream);
+
 /* ---- attention output projection ---------------------------------------------------- */
 
-/* Bytes of scratch ts_attn_out_proj needs for this shape (0 when the reduction is not split).
- * Host only. */
+/* Bytes of scratch ts_attn_out_proj and ts_attn_out_proj_x2 need for this shape (0 when the
+ * reduction is not split).  Host only. */
 int ts_attn_out_proj_workspace(int32_t n_tok, int32_t attn_dim, int32_t dim, uint64_t *bytes);
 
 /* main_attn_proj (sh_layer_v1.wgsl:763-821, F16 weights: the formula slot 1 branch at
@@ -271,6 +313,11 @@ int ts_attn_out_proj_workspace(int32_t n_tok, int32_t attn_dim, int32_t dim, uin
 int ts_attn_out_proj(const float *d_attn, int32_t n_tok, int32_t attn_dim, const uint16_t *d_wo,
                      int32_t dim, float *d_act, float *d_stash, void *d_workspace,
                      uint64_t workspace_bytes, void *stream);
+/* ts_attn_out_proj with d_wo of two f16 planes per row ([dim][2 attn_dim], ts_weights_to_f16x2):
+ * main_attn_proj's F32 and block branches (sh_layer_v1.wgsl:782-790). */
+int ts_attn_out_proj_x2(const float *d_attn, int32_t n_tok, int32_t attn_dim, const uint16_t *d_wo,
+                        int32_t dim, float *d_act, float *d_stash, void *d_workspace,
+                        uint64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,10 @@ def lib():
         L.or_rope_table.restype = ctypes.c_int
         L.or_rope_table_yarn.argtypes = [_f32p, ctypes.c_int, ctypes.c_int] + [ctypes.c_float] * 4
         L.or_rope_table_yarn.restype = ctypes.c_int
+        L.or_dequant.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_long, _f32p]
+        L.or_dequant.restype = ctypes.c_int
+        L.or_project_f32.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_int, _f32p]
+        L.or_project_f32.restype = None
         L.or_rope_rotate.argtypes = [_f32p, ctypes.c_int, _f32p]
         L.or_rope_rotate.restype = None
         L.or_quantize_row.argtypes = [_f32p, ctypes.c_int, ctypes.POINTER(ctypes.c_float), _u32p]
@@ -94,6 +98,27 @@ def project(x: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
     assert w_bits.shape[1] == dim
     out = np.zeros((n, n_out), dtype=np.float32)
     lib().or_project(x, n, dim, w_bits, n_out, out)
+    return out
+
+
+def dequant(ggml_type: int, blob: np.ndarray, n: int) -> np.ndarray:
+    """The reference's CPU dequantizers (src/core/dequant/): n f32 element values of a GGUF
+    weight blob of that GGML type (n a whole number of blocks)."""
+    blob = np.ascontiguousarray(blob, dtype=np.uint8)
+    out = np.zeros(n, np.float32)
+    if lib().or_dequant(ggml_type, blob.ctypes.data, n, out) != 0:
+        raise ValueError("unsupported type or partial block")
+    return out
+
+
+def project_f32(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """main_qkv's dot over f32 weights (its F32 and block branches): x [n, dim], w [n_out, dim]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, dim = x.shape
+    assert w.shape[1] == dim
+    out = np.zeros((n, w.shape[0]), dtype=np.float32)
+    lib().or_project_f32(x, n, dim, w, w.shape[0], out)
     return out
 
 

@@ -29,6 +29,9 @@
  *                       sh_dequant_any.wgsl:261-265)
  *   or_project          sh_layer_v1_int4.wgsl:454-575 (main_qkv, F16 branch :494-498): one
  *                       f32 dot per output, `dot += x[col] * w[row][col]` in column order
+ *   or_project_f32      the same dot over f32 weights (F32 and block branches, :502-520)
+ *   or_dequant          src/core/dequant/{q4_0,q5_0,q8_0,q4_k,q5_k,q6_k}.rs (GGUF weight
+ *                       blocks to f32 element values)
  *   or_attn_proj        sh_layer_v1.wgsl:763-821 (main_attn_proj, F16 branch :777-781): the same
  *                       dot over attn_dim, stashed, then act = act + dot
  *   or_attend_head      src/ops/reference/attention.rs:236-313 (per-head QK^T, scale,
@@ -176,6 +179,135 @@ float or_f16_to_f32(uint16_t bits) {
 /* out[r][o] = sum over col of x[r][col] * w[o][col] for r < n_rows, o < n_out: one f32
  * accumulator per output, each product rounded to f32 and added in column order (the
  * reference's per-thread loop).  w: [n_out][dim] f16 bits.  OpenMP over outputs. */
+/* main_qkv's F32 and block-format branches (sh_layer_v1_int4.wgsl:502-520): the same dot over
+ * f32 weights (a block format's weights dequantized first, or_dequant). */
+void or_project_f32(const float *x, int n_rows, int dim, const float *wf, int n_out, float *out) {
+#pragma omp parallel for schedule(static)
+    for (long ro = 0; ro < (long)n_rows * n_out; ro++) {
+        const long r = ro / n_out, o = ro % n_out;
+        const float *xr = x + (size_t)r * dim, *wr = wf + (size_t)o * dim;
+        float dot = 0.0f;
+        for (int c = 0; c < dim; c++) {
+            float prod = xr[c] * wr[c];
+            dot = dot + prod;
+        }
+        out[(size_t)r * n_out + o] = dot;
+    }
+}
+
+/* ---- GGUF weight blocks ---------------------------------------------------------------
+ * Element values of the reference's CPU dequantizers (src/core/dequant/), over n elements
+ * (a whole number of blocks) of GGML type `type` (ggml_types.rs: F32 0, F16 1, Q4_0 2, Q5_0 6,
+ * Q8_0 8, Q4_K 12, Q5_K 13, Q6_K 14).  Every product and difference is rounded on its own, as
+ * in the Rust.  Returns 0, or -1 for an unknown type or a partial block. */
+static float or_h(const uint8_t *p) { return or_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* q4_k.rs:134-143 (q5_k.rs:146-155 is the same): 6-bit scale and min of sub-block j. */
+static void or_scale_min_k4(int j, const uint8_t *q, int *sc, int *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0x0F) | (((q[j - 4] >> 6) & 3) << 4);
+        *m = ((q[j + 4] >> 4) & 0x0F) | (((q[j] >> 6) & 3) << 4);
+    }
+}
+
+int or_dequant(int type, const uint8_t *src, long n, float *dst) {
+    int epb, bpb;
+    switch (type) {
+        case 0: epb = 1; bpb = 4; break;
+        case 1: epb = 1; bpb = 2; break;
+        case 2: epb = 32; bpb = 18; break;
+        case 6: epb = 32; bpb = 22; break;
+        case 8: epb = 32; bpb = 34; break;
+        case 12: epb = 256; bpb = 144; break;
+        case 13: epb = 256; bpb = 176; break;
+        case 14: epb = 256; bpb = 210; break;
+        default: return -1;
+    }
+    if (n % epb) return -1;
+    for (long blk = 0; blk < n / epb; blk++) {
+        const uint8_t *b = src + blk * bpb;
+        float *o = dst + blk * epb;
+        if (type == 0) {
+            memcpy(o, b, 4);
+        } else if (type == 1) {
+            o[0] = or_h(b);
+        } else if (type == 2) { /* q4_0.rs:29-54: low nibbles 0..15, high 16..31, minus 8 */
+            float d = or_h(b);
+            for (int i = 0; i < 16; i++) {
+                o[i] = (float)((b[2 + i] & 0x0F) - 8) * d;
+                o[i + 16] = (float)(((b[2 + i] >> 4) & 0x0F) - 8) * d;
+            }
+        } else if (type == 6) { /* q5_0.rs:46-86: fifth bit of element e is bit e of qh */
+            float d = or_h(b);
+            uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+            for (int j = 0; j < 16; j++) {
+                int v0 = (int)((b[6 + j] & 0x0F) | (((qh >> j) & 1) << 4)) - 16;
+                int v1 = (int)(((b[6 + j] >> 4) & 0x0F) | (((qh >> (j + 16)) & 1) << 4)) - 16;
+                o[j] = (float)v0 * d;
+                o[j + 16] = (float)v1 * d;
+            }
+        } else if (type == 8) { /* q8_0.rs:37-53 */
+            float d = or_h(b);
+            for (int i = 0; i < 32; i++) o[i] = (float)(int8_t)b[2 + i] * d;
+        } else if (type == 12) { /* q4_k.rs:75-123 */
+            float d = or_h(b), dmin = or_h(b + 2);
+            const uint8_t *sc = b + 4, *q = b + 16;
+            for (int c = 0; c < 4; c++) {
+                int s0, m0, s1, m1;
+                or_scale_min_k4(2 * c, sc, &s0, &m0);
+                or_scale_min_k4(2 * c + 1, sc, &s1, &m1);
+                float d1 = d * (float)s0, mm1 = dmin * (float)m0;
+                float d2 = d * (float)s1, mm2 = dmin * (float)m1;
+                for (int l = 0; l < 32; l++) {
+                    float a = d1 * (float)(q[32 * c + l] & 0x0F);
+                    o[64 * c + l] = a - mm1;
+                    float e = d2 * (float)(q[32 * c + l] >> 4);
+                    o[64 * c + 32 + l] = e - mm2;
+                }
+            }
+        } else if (type == 13) { /* q5_k.rs:74-143 */
+            float d = or_h(b), dmin = or_h(b + 2);
+            const uint8_t *sc = b + 4, *qh = b + 16, *qs = b + 48;
+            for (int g = 0; g < 4; g++) {
+                int s0, m0, s1, m1;
+                or_scale_min_k4(2 * g, sc, &s0, &m0);
+                or_scale_min_k4(2 * g + 1, sc, &s1, &m1);
+                float d1 = d * (float)s0, mm1 = dmin * (float)m0;
+                float d2 = d * (float)s1, mm2 = dmin * (float)m1;
+                for (int l = 0; l < 32; l++) {
+                    float q0 = (float)(qs[32 * g + l] & 0x0F) + (float)((qh[l] >> (2 * g)) & 1) * 16.0f;
+                    float q1 = (float)(qs[32 * g + l] >> 4) + (float)((qh[l] >> (2 * g + 1)) & 1) * 16.0f;
+                    float a = d1 * q0;
+                    o[64 * g + l] = a - mm1;
+                    float e = d2 * q1;
+                    o[64 * g + 32 + l] = e - mm2;
+                }
+            }
+        } else { /* q6_k.rs:72-131: two halves of 128, four 32-element parts each */
+            const uint8_t *ql = b, *qh = b + 128;
+            const int8_t *scl = (const int8_t *)(b + 192);
+            float d = or_h(b + 208);
+            for (int h = 0; h < 2; h++)
+                for (int l = 0; l < 32; l++) {
+                    int is = l / 16, li = 64 * h + l, hi = 32 * h + l;
+                    int q1 = ((ql[li] & 0x0F) | ((qh[hi] & 3) << 4)) - 32;
+                    int q2 = ((ql[li + 32] & 0x0F) | (((qh[hi] >> 2) & 3) << 4)) - 32;
+                    int q3 = ((ql[li] >> 4) | (((qh[hi] >> 4) & 3) << 4)) - 32;
+                    int q4 = ((ql[li + 32] >> 4) | (((qh[hi] >> 6) & 3) << 4)) - 32;
+                    float f;
+                    f = d * (float)scl[8 * h + is];     o[128 * h + l] = f * (float)q1;
+                    f = d * (float)scl[8 * h + is + 2]; o[128 * h + l + 32] = f * (float)q2;
+                    f = d * (float)scl[8 * h + is + 4]; o[128 * h + l + 64] = f * (float)q3;
+                    f = d * (float)scl[8 * h + is + 6]; o[128 * h + l + 96] = f * (float)q4;
+                }
+        }
+    }
+    return 0;
+}
+
 void or_project(const float *x, int n_rows, int dim, const uint16_t *w, int n_out, float *out) {
     float *wf = (float *)malloc(sizeof(float) * (size_t)n_out * dim);
     if (!wf) return;

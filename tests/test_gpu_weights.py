@@ -1,0 +1,129 @@
+"""GPU conversion of GGUF projection weights (ts_weights_to_f16) against the oracle's
+dequantizers (src/core/dequant/, pinned in test_oracle_weights.py): every element bit-exact
+with the oracle's f32 value rounded to f16 (nearest even).  Then the projections fed with
+converted weights against the reference's f32-weight dot (main_qkv's block branch), within
+|err| <= 2e-3 + 1e-3*|ref| -- the f16 rounding of the weights included."""
+import numpy as np
+import pytest
+import torch
+
+from airframe_amd import weights
+from airframe_amd.kv_cache import attn_out_proj
+from oracle import oracle
+from tests.gpu_util import Pair, assert_close, dev, say
+
+pytestmark = pytest.mark.gpu
+
+EPB = {weights.F32: 1, weights.F16: 1, weights.Q4_0: 32, weights.Q5_0: 32, weights.Q8_0: 32,
+       weights.Q4_K: 256, weights.Q5_K: 256, weights.Q6_K: 256}
+BPB = {weights.F32: 4, weights.F16: 2, weights.Q4_0: 18, weights.Q5_0: 22, weights.Q8_0: 34,
+       weights.Q4_K: 144, weights.Q5_K: 176, weights.Q6_K: 210}
+
+
+def f16_bytes(rng, n, lo, hi):
+    return np.frombuffer(rng.uniform(lo, hi, n).astype(np.float16).tobytes(), np.uint8).reshape(n, 2)
+
+
+def random_blob(rng, fmt, n_rows, n_cols, scale=2e-3):
+    """Random GGUF bytes of an [n_rows][n_cols] matrix with finite scales of about `scale`."""
+    if fmt == weights.F32:
+        return (rng.standard_normal(n_rows * n_cols) * 0.02).astype(np.float32).view(np.uint8)
+    if fmt == weights.F16:
+        return (rng.standard_normal(n_rows * n_cols) * 0.02).astype(np.float16).view(np.uint8)
+    nb = n_rows * n_cols // EPB[fmt]
+    b = rng.integers(0, 256, (nb, BPB[fmt]), dtype=np.uint8)
+    if fmt in (weights.Q4_0, weights.Q5_0, weights.Q8_0):
+        b[:, 0:2] = f16_bytes(rng, nb, scale, 4 * scale)
+    elif fmt in (weights.Q4_K, weights.Q5_K):
+        b[:, 0:2] = f16_bytes(rng, nb, scale / 16, scale / 4)
+        b[:, 2:4] = f16_bytes(rng, nb, scale / 16, scale / 4)
+    else:
+        b[:, 208:210] = f16_bytes(rng, nb, scale / 64, scale / 16)
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("fmt", [weights.F32, weights.F16, weights.Q4_0, weights.Q5_0, weights.Q8_0,
+                                 weights.Q4_K, weights.Q5_K, weights.Q6_K])
+@pytest.mark.parametrize("n_rows,n_cols", [(48, 512), (3, 1280)])
+def test_weights_to_f16_bit_exact(gpu, fmt, n_rows, n_cols):
+    """One plane: the oracle's value rounded to f16.  Two planes: that (hi), then the rest
+    v - hi (exact in f32) rounded to f16 (lo), per row."""
+    say(f"weights_to_f16 fmt={fmt} {n_rows}x{n_cols}")
+    rng = np.random.default_rng(fmt * 100 + n_rows)
+    blob = random_blob(rng, fmt, n_rows, n_cols)
+    assert blob.size == weights.src_bytes(fmt, n_rows, n_cols)
+    v = oracle.dequant(fmt, blob, n_rows * n_cols).reshape(n_rows, n_cols)
+    hi = v.astype(np.float16)
+    lo = (v - hi.astype(np.float32)).astype(np.float16)
+    out = weights.to_f16(fmt, dev(blob), n_rows, n_cols).cpu().numpy()
+    assert np.array_equal(out.view(np.uint16), hi.view(np.uint16))
+    out2 = weights.to_f16(fmt, dev(blob), n_rows, n_cols, planes=2).cpu().numpy()
+    assert np.array_equal(out2[:, :n_cols].view(np.uint16), hi.view(np.uint16))
+    assert np.array_equal(out2[:, n_cols:].view(np.uint16), lo.view(np.uint16))
+
+
+def test_weights_to_f16_errors(gpu):
+    say("weights_to_f16 errors")
+    with pytest.raises(Exception):
+        weights.src_bytes(weights.Q4_K, 4, 300)  # not a whole number of blocks per row
+    with pytest.raises(Exception):
+        weights.src_bytes(3, 4, 256)             # Q4_1: not a format of the path
+    with pytest.raises(ValueError):
+        weights.to_f16(weights.Q8_0, dev(np.zeros(10, np.uint8)), 1, 32)  # too few bytes
+
+
+@pytest.mark.parametrize("fmt,n_seq,n_tok,dim", [
+    (weights.Q4_K, 8, 1, 4096),    # decode rows: the reduction split over workgroups
+    (weights.Q5_K, 3, 70, 1024),   # block rows: one workgroup per tile over all of dim
+    (weights.F32, 2, 33, 512),     # the F32 branch
+    (weights.Q8_0, 40, 1, 320),    # decode rows in 64-row tiles, dim not a multiple of 256
+])
+def test_qkv_append_with_block_weights(gpu, fmt, n_seq, n_tok, dim):
+    """main_qkv with F32 / block weights (sh_layer_v1_int4.wgsl:502-520): two-plane f16 weights
+    through ts_qkv_append_x2 against the dot over the exact dequantized f32 weights, and the
+    appended codes bit-exact with the quantizer applied to those projections."""
+    say(f"qkv_append_x2 fmt={fmt} n_seq={n_seq} n_tok={n_tok} dim={dim}")
+    rng = np.random.default_rng(fmt + dim)
+    n_head, n_kv, hd = 8, 2, 128
+    p = Pair(n_seq, n_kv, hd, 128, 500000.0)
+    rows = (n_head * hd, n_kv * hd, n_kv * hd)
+    blobs = [random_blob(rng, fmt, r, dim) for r in rows]
+    w2 = [weights.to_f16(fmt, dev(b), r, dim, planes=2) for b, r in zip(blobs, rows)]
+    wf = [oracle.dequant(fmt, b, r * dim).reshape(r, dim) for b, r in zip(blobs, rows)]
+    x = rng.standard_normal((n_seq, n_tok, dim)).astype(np.float32)
+    k_out = torch.empty((n_seq, n_tok, n_kv, hd), dtype=torch.float32, device="cuda")
+    v_out = torch.empty_like(k_out)
+    q = p.gpu.qkv_append(0, dev(x), w2[0], w2[1], w2[2], p.rope, kv_out=(k_out, v_out), planes=2)
+    torch.cuda.synchronize()
+    q, k_out, v_out = q.cpu().numpy(), k_out.cpu().numpy(), v_out.cpu().numpy()
+    xf = x.reshape(-1, dim)
+    assert_close(q.reshape(n_seq * n_tok, -1), oracle.project_f32(xf, wf[0]), "q (block weights)")
+    assert_close(k_out.reshape(n_seq * n_tok, -1), oracle.project_f32(xf, wf[1]), "k (block weights)")
+    assert_close(v_out.reshape(n_seq * n_tok, -1), oracle.project_f32(xf, wf[2]), "v (block weights)")
+    p.ora.append(k_out, v_out)
+    p.advance(n_tok)
+    p.check_codes()
+
+
+@pytest.mark.parametrize("fmt,n_tok,attn_dim,dim", [
+    (weights.Q6_K, 5, 2048, 2048),   # decode: the reduction split
+    (weights.Q8_0, 130, 1024, 768),  # prefill: 64-row tiles over all of attn_dim
+    (weights.Q4_0, 3, 320, 200),     # attn_dim not a multiple of 256
+])
+def test_attn_out_proj_with_block_weights(gpu, fmt, n_tok, attn_dim, dim):
+    """main_attn_proj with block-format weights (sh_layer_v1.wgsl:782-790) through
+    ts_attn_out_proj_x2."""
+    say(f"attn_out_proj_x2 fmt={fmt} n_tok={n_tok} attn_dim={attn_dim} dim={dim}")
+    rng = np.random.default_rng(fmt + n_tok)
+    blob = random_blob(rng, fmt, dim, attn_dim)
+    w2 = weights.to_f16(fmt, dev(blob), dim, attn_dim, planes=2)
+    wf = oracle.dequant(fmt, blob, dim * attn_dim).reshape(dim, attn_dim)
+    a = rng.standard_normal((n_tok, attn_dim)).astype(np.float32)
+    act = rng.standard_normal((n_tok, dim)).astype(np.float32) * 4
+    act_d = dev(act)
+    stash = torch.zeros((n_tok, dim), dtype=torch.float32, device="cuda")
+    attn_out_proj(dev(a), w2, act_d, stash=stash, planes=2)
+    torch.cuda.synchronize()
+    dot = oracle.project_f32(a, wf)
+    assert_close(stash.cpu().numpy(), dot, "projection (block weights)")
+    assert_close(act_d.cpu().numpy(), act + dot, "residual + projection (block weights)")
