@@ -408,8 +408,10 @@ def run_qkv(args, cfg):
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
 
+    P = args.planes  # 2: rows of [hi dim | lo dim] (F32 / GGUF block weights, ts_qkv_append_x2)
+
     def w(rows):
-        return (torch.randn((rows, dim), generator=gen, device=dev) * 0.02).half()
+        return (torch.randn((rows, P * dim), generator=gen, device=dev) * 0.02).half()
 
     ws = [(w(n_head * hd), w(n_kv * hd), w(n_kv * hd)) for _ in range(L)]
     x = torch.randn((B, n_tok, dim), generator=gen, device=dev)
@@ -419,21 +421,67 @@ def run_qkv(args, cfg):
         for layer in range(L):
             kv.set_qk_norm(layer, None, torch.randn(hd, generator=gen, device=dev) * 0.2 + 1.0)
     for layer in range(L):
-        kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch)
+        kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch, planes=P)
     kv.increment(n_tok)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
         for layer in range(L):
-            kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch)
+            kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch, planes=P)
         kv.increment(n_tok)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / (reps * L)
     M, N = B * n_tok, (n_head + 2 * n_kv) * hd
-    byts = N * dim * 2 + M * dim * 4 + M * n_head * hd * 4 + M * n_kv * (hd + 8)
+    byts = N * dim * 2 * P + M * dim * 4 + M * n_head * hd * 4 + M * n_kv * (hd + 8)
     return ms, byts, 2.0 * M * N * dim, M
+
+
+CONVERT_TYPES = {"f32": 0, "q4_0": 2, "q5_0": 6, "q8_0": 8, "q4_k": 12, "q5_k": 13, "q6_k": 14}
+
+
+def run_convert(args, cfg):
+    """ts_weights_to_f16x2 on a matrix of the configuration's Wq shape [n_head hd, dim] holding
+    random blocks of the chosen GGUF type (finite f16 scales).  Returns the mean time of one
+    call (us), its algorithmic bytes (the GGUF bytes read, 4 bytes per element written), rows
+    and cols."""
+    import numpy as np
+    import torch
+
+    from airframe_amd import weights
+
+    t = CONVERT_TYPES[args.convert]
+    rows, cols = cfg["n_head"] * cfg["hd"], cfg["dim"]
+    nbytes = weights.src_bytes(t, rows, cols)
+    rng = np.random.default_rng(args.seed)
+    blob = rng.integers(0, 256, nbytes, dtype=np.uint8)
+    if t != 0:  # every f16 field that is a scale gets a finite value: rewrite the blocks' headers
+        epb, bpb = {2: (32, 18), 6: (32, 22), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}[t]
+        blk = blob.reshape(-1, bpb)
+        sc = np.frombuffer(rng.uniform(1e-4, 1e-3, (blk.shape[0], 2)).astype(np.float16).tobytes(), np.uint8)
+        sc = sc.reshape(-1, 4)
+        if t == 14:
+            blk[:, 208:210] = sc[:, 0:2]
+        else:
+            blk[:, 0:2] = sc[:, 0:2]
+            if t in (12, 13):
+                blk[:, 2:4] = sc[:, 2:4]
+    else:
+        blob = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32).view(np.uint8)
+    src = torch.from_numpy(blob).cuda()
+    for _ in range(3):
+        out = weights.to_f16(t, src, rows, cols, planes=2)
+    torch.cuda.synchronize()
+    reps = 20
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        out = weights.to_f16(t, src, rows, cols, planes=2)
+    e1.record()
+    torch.cuda.synchronize()
+    del out
+    return e0.elapsed_time(e1) * 1e3 / reps, nbytes + rows * cols * 4, rows, cols
 
 
 def run_proj(args, cfg):
@@ -450,22 +498,23 @@ def run_proj(args, cfg):
     M, K = B * cfg.get("chunk", 1), n_head * hd
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
-    ws = [(torch.randn((dim, K), generator=gen, device=dev) * 0.02).half() for _ in range(L)]
+    P = args.planes
+    ws = [(torch.randn((dim, P * K), generator=gen, device=dev) * 0.02).half() for _ in range(L)]
     a = torch.randn((M, K), generator=gen, device=dev)
     act = torch.randn((M, dim), generator=gen, device=dev)
     for layer in range(L):
-        attn_out_proj(a, ws[layer], act)
+        attn_out_proj(a, ws[layer], act, planes=P)
     torch.cuda.synchronize()
     reps = 5
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
         for layer in range(L):
-            attn_out_proj(a, ws[layer], act)
+            attn_out_proj(a, ws[layer], act, planes=P)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / (reps * L)
-    return ms, dim * K * 2 + M * K * 4 + M * dim * 8, 2.0 * M * dim * K, M
+    return ms, dim * K * 2 * P + M * K * 4 + M * dim * 8, 2.0 * M * dim * K, M
 
 
 def run_compact(args, cfg):
@@ -611,6 +660,10 @@ def main():
                     help="time the fused QKV projection + append (ts_qkv_append) instead")
     ap.add_argument("--proj", action="store_true",
                     help="time the attention output projection + residual (ts_attn_out_proj) instead")
+    ap.add_argument("--planes", type=int, default=1, choices=(1, 2),
+                    help="with --qkv/--proj: 2 = two-plane weights (F32 / GGUF formats, the _x2 entry points)")
+    ap.add_argument("--convert", default=None, choices=sorted(CONVERT_TYPES),
+                    help="time ts_weights_to_f16x2 on the configuration's Wq of that GGUF type")
     ap.add_argument("--compact", action="store_true",
                     help="measure sliding-window compaction (ts_kv_shift) on the config's cache "
                          "instead of the decode step")
@@ -652,6 +705,18 @@ def main():
                          "counting": "f32 K and V read, packed K/V rows and two scales written"},
             "data": "synthetic"}), flush=True)
         return
+    if args.convert:
+        us, byts, rows, cols = run_convert(args, cfg)
+        gbs = byts / (us * 1e-6) / 1e9
+        print(json.dumps({
+            "metric": f"GGUF {args.convert} weight conversion to two f16 planes GB/s", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "us_per_call": round(us, 2),
+            "config": {"workload": f"{cfg['name']}_wq_{args.convert}", "rows": rows, "cols": cols},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": byts,
+                         "counting": "GGUF bytes read, two f16 planes written"},
+            "data": "synthetic (random blocks, finite scales)"}), flush=True)
+        return
     if args.qkv or args.proj:
         ms, byts, flops, toks = (run_qkv if args.qkv else run_proj)(args, cfg)
         what = "fused QKV projection + INT4 append" if args.qkv else "attention output projection + residual"
@@ -660,8 +725,8 @@ def main():
         tfs = flops / (ms * 1e-3) / 1e12
         roof = ({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                  "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": byts,
-                 "counting": ("f16 weights and f32 x read, f32 q, packed K/V rows and scales written"
-                              if args.qkv else "f16 weights and f32 attention output read, residual read and written")}
+                 "counting": ("f16 weights (both planes with --planes 2) and f32 x read, f32 q, packed K/V rows and scales written"
+                              if args.qkv else "f16 weights (both planes with --planes 2) and f32 attention output read, residual read and written")}
                 if decode else
                 {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                  "unit": "TFLOP/s", "frac": round(tfs / MFMA_F16_PEAK_TFLOPS, 4),
@@ -672,7 +737,8 @@ def main():
             "value": round(gbs if decode else tfs, 2), "unit": "GB/s" if decode else "TFLOP/s",
             "n_gpus": 1, "higher_is_better": True, "us_per_call": round(ms * 1e3, 2),
             "tokens_per_s": round(toks / (ms * 1e-3), 1),
-            "config": {"workload": cfg["name"] + ("_qkv" if args.qkv else "_oproj") + ("_qknorm" if args.qk_norm else ""),
+            "config": {"workload": cfg["name"] + ("_qkv" if args.qkv else "_oproj") + ("_qknorm" if args.qk_norm else "")
+                       + ("_x2" if args.planes == 2 else ""),
                        "tokens_per_call": toks, "dim": cfg["dim"]},
             "roofline": roof, "data": "synthetic (random f16 weights, N(0,1) x)"}), flush=True)
         return
