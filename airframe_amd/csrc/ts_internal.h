@@ -184,5 +184,6 @@ struct ProjPlan {
 ProjPlan proj_plan(int M, int K, int N);
 hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, float *act, float *stash,
                        const ProjPlan &plan, float *part, int planes, hipStream_t st);
+hipError_t launch_fill_zero(float *p, size_t n, hipStream_t st);
 
 }  // namespace ts

@@ -539,18 +539,45 @@ int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_
 }
 
 static bool qkv_shape_ok(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head) {
-    return (kv->d.head_dim == 128 || kv->d.head_dim == 64) && dim > 0 && dim % 64 == 0 && n_tok >= 0 && heads_ok(kv, n_head);
+    return dim > 0 && dim % 64 == 0 && n_tok >= 0 && heads_ok(kv, n_head);
+}
+
+// head_dim 64 and 128 run the fused kernel (ts_qkv.hip, the append as its epilogue); any other
+// head_dim runs the projection kernel three times (q, K, V, each onto zeroed outputs: 0 + dot
+// is the dot) and then the append kernel on the projected K and V.
+static bool qkv_fused(const ts_kv *kv) { return kv->d.head_dim == 128 || kv->d.head_dim == 64; }
+
+struct QkvGeneric {
+    ts::ProjPlan pq, pk;
+    uint64_t part_bytes;  // split partials, shared by the three projections (256-aligned)
+    uint64_t kv_elems;    // floats of one of K / V: n_seq * n_tok * n_head_kv * head_dim
+};
+
+static QkvGeneric qkv_generic_plan(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head, int planes) {
+    QkvGeneric g;
+    const int M = kv->d.n_seq * n_tok, hd = kv->d.head_dim;
+    g.pq = ts::proj_plan(M, planes * dim, n_head * hd);
+    g.pk = ts::proj_plan(M, planes * dim, kv->d.n_head_kv * hd);
+    g.part_bytes = (std::max(g.pq.part_bytes, g.pk.part_bytes) + 255) / 256 * 256;
+    g.kv_elems = (uint64_t)M * kv->d.n_head_kv * hd;
+    return g;
 }
 
 int ts_qkv_workspace(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head, uint64_t *bytes) {
     if (!kv || !bytes) return TS_ERR_INVALID;
-    if (kv->d.head_dim != 128 && kv->d.head_dim != 64) return TS_ERR_UNSUPPORTED;
     if (!qkv_shape_ok(kv, dim, n_tok, n_head)) return TS_ERR_INVALID;
-    // enough for f16 rows and for two-plane rows (ts_qkv_append_x2)
+    // enough for f16 rows and for two-plane rows (ts_qkv_append_x2); on the unfused path also
+    // room for the projected K and V when the caller does not take them
     *bytes = 0;
-    for (int planes = 1; n_tok > 0 && planes <= 2; planes++)
-        *bytes = std::max(*bytes, ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, planes * dim,
-                                               n_tok).part_bytes);
+    for (int planes = 1; n_tok > 0 && planes <= 2; planes++) {
+        if (qkv_fused(kv)) {
+            *bytes = std::max(*bytes, ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim,
+                                                   planes * dim, n_tok).part_bytes);
+        } else {
+            const QkvGeneric g = qkv_generic_plan(kv, dim, n_tok, n_head, planes);
+            *bytes = std::max(*bytes, g.part_bytes + 2 * g.kv_elems * sizeof(float));
+        }
+    }
     return TS_OK;
 }
 
@@ -559,7 +586,6 @@ static int qkv_append_planes(ts_kv *kv, int32_t layer, const float *d_x, int32_t
                              const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,
                              uint64_t workspace_bytes, void *stream, int planes) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers) return TS_ERR_INVALID;
-    if (kv->d.head_dim != 128 && kv->d.head_dim != 64) return TS_ERR_UNSUPPORTED;
     if (!qkv_shape_ok(kv, dim, n_tok, n_head) || !d_x || !d_wq || !d_wk || !d_wv || !d_q ||
         !aligned16(d_x) || !aligned16(d_wq) || !aligned16(d_wk) || !aligned16(d_wv) ||
         !aligned16(d_q) || (!d_k) != (!d_v) || (d_k && (!aligned16(d_k) || !aligned16(d_v))))
@@ -569,6 +595,26 @@ static int qkv_append_planes(ts_kv *kv, int32_t layer, const float *d_x, int32_t
     int rc = check_rope(rope, kv->d.head_dim, rot_end(kv, n_tok));
     if (rc) return rc;
     if (n_tok == 0) return TS_OK;
+    if (!qkv_fused(kv)) {
+        const QkvGeneric g = qkv_generic_plan(kv, dim, n_tok, n_head, planes);
+        const uint64_t need = g.part_bytes + (d_k ? 0 : 2 * g.kv_elems * sizeof(float));
+        if (need > 0 && (!d_workspace || workspace_bytes < need || !aligned16(d_workspace))) return TS_ERR_WORKSPACE;
+        float *part = static_cast<float *>(d_workspace);
+        float *kb = d_k ? d_k : reinterpret_cast<float *>(static_cast<uint8_t *>(d_workspace) + g.part_bytes);
+        float *vb = d_k ? d_v : kb + g.kv_elems;
+        const hipStream_t st = as_stream(stream);
+        const int M = kv->d.n_seq * n_tok, hd = kv->d.head_dim, H = kv->d.n_head_kv;
+        hipError_t e = ts::launch_fill_zero(d_q, (size_t)M * n_head * hd, st);
+        if (e == hipSuccess) e = ts::launch_fill_zero(kb, g.kv_elems, st);
+        if (e == hipSuccess) e = ts::launch_fill_zero(vb, g.kv_elems, st);
+        if (e == hipSuccess) e = ts::launch_proj(d_x, M, dim, d_wq, n_head * hd, d_q, nullptr, g.pq, part, planes, st);
+        if (e == hipSuccess) e = ts::launch_proj(d_x, M, dim, d_wk, H * hd, kb, nullptr, g.pk, part, planes, st);
+        if (e == hipSuccess) e = ts::launch_proj(d_x, M, dim, d_wv, H * hd, vb, nullptr, g.pk, part, planes, st);
+        if (e == hipSuccess)
+            e = ts::launch_quantize_rows(kv->layer(layer), kb, vb, kv->d_len, 0, n_tok, n_tok, rope->d_table,
+                                         rope->rope_dim / 2, n_tok / 32 + 2, st);
+        return hip_status(e);
+    }
     const ts::QkvPlan plan = ts::qkv_plan(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, planes * dim, n_tok);
     if (plan.part_bytes > 0 && (!d_workspace || workspace_bytes < plan.part_bytes || !aligned16(d_workspace)))
         return TS_ERR_WORKSPACE;

@@ -128,7 +128,22 @@ __global__ __launch_bounds__(256) void proj_reduce_kernel(ProjArgs p) {
     }
 }
 
+__global__ __launch_bounds__(256) void fill_zero_kernel(float4 *p, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256)
+        p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 }  // namespace
+
+// Zeroes n floats (n a multiple of 4, p 16-byte aligned) with a kernel, so that a caller may
+// capture it in a graph.
+hipError_t launch_fill_zero(float *p, size_t n, hipStream_t st) {
+    if (n % 4 || ((uintptr_t)p & 15)) return hipErrorInvalidValue;
+    if (n == 0) return hipSuccess;
+    const size_t n4 = n / 4;
+    fill_zero_kernel<<<(int)std::min<size_t>((n4 + 255) / 256, 4096), 256, 0, st>>>(reinterpret_cast<float4 *>(p), n4);
+    return hipGetLastError();
+}
 
 ProjPlan proj_plan(int M, int K, int N) {
     ProjPlan p;

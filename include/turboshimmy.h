@@ -283,7 +283,10 @@ int ts_qkv_workspace(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head
  * position len[s] + t.  d_q: [n_seq][n_tok][n_head][head_dim] raw q (the attention entry
  * points apply the QK norm and rotation).  d_k, d_v: NULL, or [n_seq][n_tok][n_head_kv]
  * [head_dim] to receive the raw projections as well (the reference's f32 staging cache).
- * head_dim 128 or 64 (else TS_ERR_UNSUPPORTED), dim a multiple of 64.  Lengths do not change. */
+ * dim a multiple of 64.  head_dim 128 and 64 run one fused kernel; any other head_dim of the
+ * cache runs the projection kernel for q, K and V, then the append kernel (the same codes as
+ * ts_append_quant of those K and V; K and V staged in the workspace unless d_k, d_v are given).
+ * Lengths do not change. */
 int ts_qkv_append(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32_t n_tok,
                   const uint16_t *d_wq, const uint16_t *d_wk, const uint16_t *d_wv, int32_t n_head,
                   const ts_rope *rope, float *d_q, float *d_k, float *d_v, void *d_workspace,

@@ -153,3 +153,33 @@ def test_qkv_append_hd64(gpu, n_seq, n_tok, dim, n_head, n_kv):
     p.set_lens(lens)
     run_case(p, rng, n_tok, dim, n_head)
     run_case(p, rng, 3, dim, n_head)
+
+
+@pytest.mark.parametrize("hd,n_seq,n_tok,dim,n_head,n_kv", [
+    (96, 4, 1, 1024, 8, 2),     # decode rows, the projections' reduction split
+    (256, 2, 70, 512, 8, 4),    # Gemma-2's head dim, block rows
+    (40, 3, 33, 256, 6, 3),     # a head dim padded to 64 in the cache
+])
+def test_qkv_append_other_head_dims(gpu, hd, n_seq, n_tok, dim, n_head, n_kv):
+    """main_qkv at head dims other than 64 and 128 (the reference takes any multiple of 8,
+    kv_cache.rs:150-156): projection kernel for q, K and V, then the append -- projections
+    within tolerance, codes bit-exact with the oracle's append of the returned K and V, and the
+    same q and cache bits when K and V are staged in the workspace instead."""
+    say(f"qkv other hd={hd} n_seq={n_seq} n_tok={n_tok} dim={dim}")
+    rng = np.random.default_rng(hd + n_tok)
+    max_seq = 128 + n_tok + 16
+    p = Pair(n_seq, n_kv, hd, max_seq, 1e6)
+    lens = rng.integers(0, 100, size=n_seq).astype(np.int32)
+    p.set_lens(lens)
+    x, (wq, wk, wv), q, lens_before = run_case(p, rng, n_tok, dim, n_head)
+    g2 = KVCache.new_int4(1, n_kv, hd, max_seq, n_seq)
+    for s, l in enumerate(lens_before):
+        g2.set_seq_len(int(l), seq=s)
+    q2 = g2.qkv_append(0, dev(x), dev(wq), dev(wk), dev(wv), p.rope).cpu().numpy()
+    assert np.array_equal(q2.view(np.uint32), q.view(np.uint32))
+    torch.cuda.synchronize()
+    for s in range(n_seq):
+        a = [t.cpu() for t in p.gpu.export(0, s, int(lens_before[s]), n_tok)]
+        b = [t.cpu() for t in g2.export(0, s, int(lens_before[s]), n_tok)]
+        for u, w in zip(a, b):
+            assert torch.equal(u.view(torch.uint8), w.view(torch.uint8))
