@@ -688,22 +688,36 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     const float4 *o4 = reinterpret_cast<const float4 *>(a.ws + hidx * a.n_split * HD);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     float lsum = 0.0f;
-    if (ns <= NG) {
-        // One split per row group: every load is issued at once (each thread reads all ns
-        // maxima itself), no reduction round for the maximum.
-        float mv[NG];
+    if (ns <= 4 * NG) {
+        // Up to 4 splits per row group: every load is issued at once (each thread reads all ns
+        // maxima itself besides its own rows), so the merge is one memory round trip, with no
+        // reduction round for the maximum.  (Batch 1 has more than NG splits per head.)
+        constexpr int R = 4;
+        float mv[R * NG];
 #pragma unroll
-        for (int i = 0; i < NG; i++) mv[i] = i < ns ? mm[i] : kMinit;
-        const bool mine = g < ns;
-        const float4 x = mine ? o4[(size_t)g * V4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float lg = mine ? ll[g] : 0.0f;
-        const float mg = mine ? mm[g] : kMinit;
+        for (int i = 0; i < R * NG; i++) mv[i] = i < ns ? mm[i] : kMinit;
+        float4 x[R];
+        float lg[R], mg[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int i = g + r * NG;
+            const bool mine = i < ns;
+            x[r] = mine ? o4[(size_t)i * V4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            lg[r] = mine ? ll[i] : 0.0f;
+            mg[r] = mine ? mm[i] : kMinit;
+        }
         float M = kMinit;
 #pragma unroll
-        for (int i = 0; i < NG; i++) M = fmaxf(M, mv[i]);
-        const float e = mine ? exp2f(mg - M) : 0.0f;
-        acc = make_float4(e * x.x, e * x.y, e * x.z, e * x.w);
-        lsum = e * lg;
+        for (int i = 0; i < R * NG; i++) M = fmaxf(M, mv[i]);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float e = g + r * NG < ns ? exp2f(mg[r] - M) : 0.0f;
+            acc.x += e * x[r].x;
+            acc.y += e * x[r].y;
+            acc.z += e * x[r].z;
+            acc.w += e * x[r].w;
+            lsum += e * lg[r];
+        }
     } else {
         float M = kMinit;
         for (int i = tid; i < ns; i += 256) M = fmaxf(M, mm[i]);
