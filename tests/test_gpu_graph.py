@@ -176,3 +176,53 @@ def test_graph_replays_prefill_chunks(gpu):
     del graph
     p.set_lens(p.ora.lens.copy())
     p.check_codes()
+
+
+def test_graph_replays_qkv_append_other_head_dim(gpu):
+    """ts_qkv_append at head_dim 96 (projection kernels onto zeroed outputs -- a fill kernel,
+    no memset -- then the append, K and V staged in the workspace) and the increment, captured
+    once and replayed for three tokens: q and the appended cache bits of every replay identical
+    to the same call made eagerly on a second cache, q within tolerance of the oracle."""
+    from airframe_amd.kv_cache import KVCache
+    from oracle import oracle
+    say("graph replays qkv_append hd 96")
+    rng = np.random.default_rng(96)
+    B, n_kv, hd, n_head, dim = 3, 2, 96, 8, 512
+    lens = [0, 40, 77]
+    p = Pair(B, n_kv, hd, 200, 1e6)
+    p.set_lens(lens)
+    g2 = KVCache.new_int4(1, n_kv, hd, 200, B)
+    for s, l in enumerate(lens):
+        g2.set_seq_len(l, seq=s)
+    wq = (rng.standard_normal((n_head * hd, dim)) * 0.02).astype(np.float16)
+    wk = (rng.standard_normal((n_kv * hd, dim)) * 0.02).astype(np.float16)
+    wv = (rng.standard_normal((n_kv * hd, dim)) * 0.02).astype(np.float16)
+    wq_d, wk_d, wv_d = dev(wq), dev(wk), dev(wv)
+    x_in = torch.zeros((B, 1, dim), device="cuda")
+    q_out = torch.empty((B, 1, n_head, hd), device="cuda")
+    ws = p.gpu.qkv_workspace(dim, 1, n_head)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=cap):
+        p.gpu.qkv_append(0, x_in, wq_d, wk_d, wv_d, p.rope, q_out=q_out, workspace=ws)
+        p.gpu.increment(1)
+    torch.cuda.synchronize()
+    for r in range(3):
+        x = rng.standard_normal((B, 1, dim)).astype(np.float32)
+        x_in.copy_(dev(x))
+        graph.replay()
+        torch.cuda.synchronize()
+        q2 = g2.qkv_append(0, dev(x), wq_d, wk_d, wv_d, p.rope).cpu()
+        g2.increment(1)
+        torch.cuda.synchronize()
+        assert torch.equal(q_out.cpu().view(torch.int32), q2.view(torch.int32)), f"replay {r}: q"
+        assert_close(q_out.cpu().numpy().reshape(B, -1), oracle.project(x.reshape(B, dim), wq.view(np.uint16)),
+                     f"replay {r}: q against the oracle")
+        for s in range(B):
+            a = [t.cpu() for t in p.gpu.export(0, s, lens[s] + r, 1)]
+            b = [t.cpu() for t in g2.export(0, s, lens[s] + r, 1)]
+            for u, w in zip(a, b):
+                assert torch.equal(u.view(torch.uint8), w.view(torch.uint8)), f"replay {r}: codes of seq {s}"
+    del graph
