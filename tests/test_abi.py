@@ -131,3 +131,26 @@ def test_out_proj_workspace_sizing_and_validation():
     assert L.ts_qkv_workspace(None, 4096, 1, 32, ctypes.byref(b)) == _lib.TS_ERR_INVALID
     assert L.ts_qkv_append(None, 0, None, 4096, 1, None, None, None, 32, None, None, None, None,
                            None, 0, None) == _lib.TS_ERR_INVALID
+
+
+def test_weights_src_bytes():
+    """GGUF block sizes of the projection weight formats (elements, bytes per block:
+    src/core/dequant/ and ggml_types.rs), host only."""
+    L = airframe_amd.load()
+    b = ctypes.c_uint64()
+    shapes = {0: (1, 4), 1: (1, 2), 2: (32, 18), 6: (32, 22), 8: (32, 34), 12: (256, 144), 13: (256, 176),
+              14: (256, 210)}
+    for t, (epb, bpb) in shapes.items():
+        assert L.ts_weights_src_bytes(t, 3, 512, ctypes.byref(b)) == 0
+        assert b.value == 3 * 512 // epb * bpb
+    assert L.ts_weights_src_bytes(12, 3, 300, ctypes.byref(b)) == _lib.TS_ERR_INVALID   # partial block
+    assert L.ts_weights_src_bytes(3, 3, 512, ctypes.byref(b)) == _lib.TS_ERR_UNSUPPORTED  # Q4_1
+    assert L.ts_weights_src_bytes(8, 0, 512, ctypes.byref(b)) == _lib.TS_ERR_INVALID
+
+
+def test_out_proj_workspace_covers_both_weight_layouts():
+    L = airframe_amd.load()
+    b = ctypes.c_uint64()
+    assert L.ts_attn_out_proj_workspace(1, 4096, 4096, ctypes.byref(b)) == 0
+    assert b.value > 0  # one token: the reduction is split
+    assert L.ts_attn_out_proj_workspace(0, 4096, 4096, ctypes.byref(b)) == 0 and b.value == 0
