@@ -283,6 +283,26 @@ class KVCache:
                                   ctypes.c_void_p(vs.data_ptr()), _stream(stream)))
         return kp, vp, ks, vs
 
+    # The reference's per-layer buffer getters (kv_cache.rs:312-345).  The reference hands out
+    # its buffers; this cache keeps its own tiled layout, so these return copies of one
+    # sequence's whole layer (max_seq_len positions) in the reference layout, through export.
+    def get_k_packed_buffer(self, layer: int, seq: int = 0) -> torch.Tensor:
+        return self.export(layer, seq, 0, self.max_seq_len)[0]
+
+    def get_v_packed_buffer(self, layer: int, seq: int = 0) -> torch.Tensor:
+        return self.export(layer, seq, 0, self.max_seq_len)[1]
+
+    def get_k_scale_buffer(self, layer: int, seq: int = 0) -> torch.Tensor:
+        return self.export(layer, seq, 0, self.max_seq_len)[2]
+
+    def get_v_scale_buffer(self, layer: int, seq: int = 0) -> torch.Tensor:
+        return self.export(layer, seq, 0, self.max_seq_len)[3]
+
+    def calculate_offset(self, pos: int, head: int, dim: int) -> int:
+        """Byte offset of (pos, head, dim) in the reference's f32 staging layout
+        [pos][n_head_kv][head_dim] (kv_cache.rs:366-369)."""
+        return ((pos * self.n_head_kv + head) * self.head_dim + dim) * 4
+
     def qkv_workspace(self, dim: int, n_tok: int, n_head: int) -> torch.Tensor:
         key = ("qkv", dim, n_tok, n_head)
         if key not in self._ws:

@@ -125,3 +125,21 @@ def test_output_shapes_are_checked(gpu):
         p.gpu.attn_prefill(0, dev(synth.normal(rng, (2, 3, 8, 64))), p.rope,
                            out=torch.empty((2, 3, 8, 63), device="cuda"))
     assert p.gpu.seq_lens() == [8, 8]
+
+
+def test_reference_buffer_getters(gpu):
+    """get_{k,v}_{packed,scale}_buffer (kv_cache.rs:312-345) as copies of one sequence's whole
+    layer in the reference layout, and calculate_offset (:366-369)."""
+    say("buffer getters")
+    rng = np.random.default_rng(8)
+    p = Pair(2, 2, 64, 96, 10000.0)
+    fill(p, rng, 40)
+    full = [t.cpu() for t in p.gpu.export(0, 1, 0, 96)]
+    got = [p.gpu.get_k_packed_buffer(0, seq=1), p.gpu.get_v_packed_buffer(0, seq=1),
+           p.gpu.get_k_scale_buffer(0, seq=1), p.gpu.get_v_scale_buffer(0, seq=1)]
+    for a, b in zip(full, got):
+        assert tuple(b.shape) == tuple(a.shape) and torch.equal(a.view(torch.uint8), b.cpu().view(torch.uint8))
+    assert tuple(got[0].shape) == (96, 2, 8) and tuple(got[2].shape) == (96, 2)
+    p.check_codes()
+    assert p.gpu.calculate_offset(0, 0, 0) == 0
+    assert p.gpu.calculate_offset(3, 1, 5) == ((3 * 2 + 1) * 64 + 5) * 4
