@@ -1010,22 +1010,33 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     str.sk = make_rsrc(L.ks + row * L.P, wend * 4);
     str.sv = make_rsrc(L.vs + row * L.P, wend * 4);
 
-    // This wave's windows: w = wave, wave + NW, ... below nwin, taken in rotated order starting
-    // at a per-workgroup offset, so that the workgroups streaming at the same time read
-    // different regions of their streams (spread over the HBM channels).  Window indices past
-    // cnt load from past the bound (zeros, no memory traffic).
+    // This wave's windows: claims j = wave, wave + NW, ... below nwin, taken in rotated order
+    // starting at a per-workgroup offset, so that the workgroups streaming at the same time
+    // read different regions of their streams (spread over the HBM channels).  Claim j reads
+    // window (j + R) mod nwin.  The appending wave starts ~3 us late, so it keeps all but its
+    // last kApp claims, which go round robin to the other waves after their own: the
+    // assignment stays fixed (outputs are bit-reproducible) and the waves end together.
+    // (Without the hand-over the appending wave ended ~2 us after the others: config 3
+    // 1.880 vs 1.855 ms per step, measured with claims through an LDS counter.)  Window
+    // indices past the wave's count load from past the bound (zeros, no memory traffic).
     const int nwin = (end - start + 63) >> 6;
-    const int cnt = wave < nwin ? (nwin - wave + NW - 1) / NW : 0;
+    const int own = wave < nwin ? (nwin - wave + NW - 1) / NW : 0;
+    const int lastc = NW - 1 < nwin ? (nwin - (NW - 1) + NW - 1) / NW : 0;  // the last wave's claims
+    const int kApp = fused ? min(3, lastc / 3) : 0;
+    const int keep = lastc - kApp;  // claims the last wave keeps
+    const int extra = wave < NW - 1 ? (kApp - wave + NW - 2) / (NW - 1) : 0;
+    const int cnt = wave < NW - 1 ? own + extra : keep;
     // (s 13 + h 5 + split 7: the workgroups on one XCD -- the same kv head for one split --
     // start at distinct windows; measured against (row 37 + split 11), whose offsets repeat
     // every 4 sequences of a head: config 3 1.798 vs 1.834 ms per step)
-    const int rot = cnt ? (int)((unsigned)(s * 13 + h * 5 + split * 7) % (unsigned)cnt) : 0;
+    const int R = nwin ? (int)((unsigned)(NW * (s * 13 + h * 5 + split * 7)) % (unsigned)nwin) : 0;
     const int oob = start + 64 * nwin;
     auto win_base = [&](int i) {
         if (i >= cnt) return oob;
-        int r = i + rot;
-        r = r >= cnt ? r - cnt : r;
-        return start + 64 * (wave + NW * r);
+        const int j = i < own ? NW * i + wave : NW * (keep + (NW - 1) * (i - own) + wave) + NW - 1;
+        int r = j + R;
+        r = r >= nwin ? r - nwin : r;
+        return start + 64 * r;
     };
     Window8<HD> w[D];
 
