@@ -152,11 +152,15 @@ def test_golden_fixture_through_gpu(gpu):
         assert np.array_equal(vs.cpu().numpy(), g["v_scale"][s])
 
 
-def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, sample, outliers, fused=False):
-    """One layer at the full BASELINE shape: the GPU runs every sequence; the oracle checks a
-    sample of (sequence, head) pairs on identical inputs (copied back from the device).  With
-    `fused`, the new token goes through ts_attn_decode_append (the launch bench.py times), and
-    its appended K/V row is checked bit-exact for every sequence and kv head."""
+ORACLE_THREADS = min(16, os.cpu_count() or 1)  # the GPU box's CPU share
+
+
+def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, outliers, fused=False):
+    """One layer at the full BASELINE shape: the GPU runs every sequence and the oracle checks
+    every (sequence, head) output on identical inputs (generated on the device and copied
+    back), and every packed word and scale of the cache bit-exact.  With `fused`, the new
+    token goes through ts_attn_decode_append (the launch bench.py times), otherwise through
+    ts_append_quant then ts_attn_decode."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     dims = synth.outlier_dims(n_kv, hd, seed) if outliers else None
@@ -164,19 +168,14 @@ def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, sample, outliers, fuse
     sq = torch.as_tensor(synth.channel_scale(n_head, n_kv, hd, dims)).cuda()
     max_len = max(lens)
     p = Pair(n_seq, n_kv, hd, max_len + 1, base)
-    seqs = sorted({s for s, _ in sample})
-    host_k = {s: [] for s in seqs}
-    host_v = {s: [] for s in seqs}
     step = 2048
     for t0 in range(0, max_len, step):
         m = min(step, max_len - t0)
         k = torch.randn((n_seq, m, n_kv, hd), generator=gen, device="cuda") * skv
         v = torch.randn((n_seq, m, n_kv, hd), generator=gen, device="cuda") * skv
         p.gpu.append_quant(0, k, v, p.rope)
-        p.gpu.increment(m)
-        for s in seqs:
-            host_k[s].append(k[s].cpu().numpy())
-            host_v[s].append(v[s].cpu().numpy())
+        p.ora.append(k.cpu().numpy(), v.cpu().numpy())
+        p.advance(m)
     p.set_lens(lens)
     k1 = torch.randn((n_seq, 1, n_kv, hd), generator=gen, device="cuda") * skv
     v1 = torch.randn((n_seq, 1, n_kv, hd), generator=gen, device="cuda") * skv
@@ -186,48 +185,24 @@ def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, sample, outliers, fuse
     else:
         p.gpu.append_quant(0, k1, v1, p.rope)
         out = p.gpu.attn_decode(0, q, p.rope).cpu().numpy()
-    qh, k1h, v1h = q.cpu().numpy(), k1.cpu().numpy(), v1.cpu().numpy()
-    if fused:
-        # the appended row of every sequence: K rotated at its position, V raw
-        for s in range(n_seq):
-            kp, vp, ks, vs = p.gpu.export(0, s, lens[s], 1)
-            kp, vp = kp.cpu().numpy().view(np.uint32)[0], vp.cpu().numpy().view(np.uint32)[0]
-            ks, vs = ks.cpu().numpy()[0], vs.cpu().numpy()[0]
-            for h in range(n_kv):
-                sk, wk = oracle.quantize_row(oracle.rope_rotate(k1h[s, 0, h], p.ora.table[lens[s]]))
-                sv, wv = oracle.quantize_row(v1h[s, 0, h])
-                assert np.array_equal(kp[h], wk), f"seq {s} head {h}: appended K row differs"
-                assert np.array_equal(vp[h], wv), f"seq {s} head {h}: appended V row differs"
-                assert ks[h].view(np.uint32) == sk.view(np.uint32) and vs[h].view(np.uint32) == sv.view(np.uint32), \
-                    f"seq {s} head {h}: appended scales differ"
-    for s in seqs:
-        kk = np.concatenate(host_k[s])[:lens[s]]
-        vv = np.concatenate(host_v[s])[:lens[s]]
-        kk = np.concatenate([kk, k1h[s]])
-        vv = np.concatenate([vv, v1h[s]])
-        ora = oracle.OracleKV(1, lens[s] + 1, n_kv, hd, p.ora.table)
-        ora.append(kk[None], vv[None])
-        ora.lens[:] = lens[s]
-        for s2, h in sample:
-            if s2 != s:
-                continue
-            ref = ora.attend_one(qh[s][None], 0, h)[0]
-            assert_close(out[s, h], ref, f"full-size seq {s} head {h} (len {lens[s]})")
+    p.ora.append(k1.cpu().numpy(), v1.cpu().numpy())
+    ref = p.ora.attend(q.cpu().numpy()[:, None], 1, threads=ORACLE_THREADS)[:, 0]
+    assert_close(out, ref, f"full-size decode, every sequence and head (lens {min(lens)}..{max(lens)})")
+    # the whole cache, the appended row included
+    p.check_codes(upto=[l + 1 for l in lens])
 
 
 def test_full_size_config3_one_layer(gpu):
-    """Config 3 at full size (batch 32, ctx 8192, outliers), one layer; sample of heads."""
+    """Config 3 at full size (batch 32, ctx 8192, outliers), one layer, every head."""
     say("decode full cfg3")
-    sample = [(0, 0), (0, 31), (17, 5), (31, 12), (31, 30)]
-    _full_size(32, 8, 32, 128, [8192] * 32, 1e6, 33, sample, True)
+    _full_size(32, 8, 32, 128, [8192] * 32, 1e6, 33, True)
 
 
 def test_full_size_config3_fused(gpu):
     """Config 3 at full size through the fused append + decode launch that bench.py times:
-    sampled heads against the oracle, the appended row of every sequence bit-exact."""
+    every head against the oracle, the whole cache (appended row included) bit-exact."""
     say("decode full cfg3 fused")
-    sample = [(0, 3), (5, 0), (17, 22), (31, 31)]
-    _full_size(32, 8, 32, 128, [8192] * 32, 1e6, 34, sample, True, fused=True)
+    _full_size(32, 8, 32, 128, [8192] * 32, 1e6, 34, True, fused=True)
 
 
 def test_full_size_config4_ragged_fused(gpu):
@@ -235,8 +210,7 @@ def test_full_size_config4_ragged_fused(gpu):
     say("decode full cfg4 fused")
     rng = np.random.default_rng(45)
     lens = [int(x) for x in rng.integers(16384, 32768, size=8)]
-    sample = [(1, 4), (6, 30)]
-    _full_size(8, 8, 32, 128, lens, 500000.0, 45, sample, False, fused=True)
+    _full_size(8, 8, 32, 128, lens, 500000.0, 45, False, fused=True)
 
 
 def test_full_size_config4_ragged_one_layer(gpu):
@@ -244,8 +218,14 @@ def test_full_size_config4_ragged_one_layer(gpu):
     say("decode full cfg4")
     rng = np.random.default_rng(44)
     lens = [int(x) for x in rng.integers(16384, 32768, size=8)]
-    sample = [(0, 0), (3, 17), (7, 31)]
-    _full_size(8, 8, 32, 128, lens, 500000.0, 44, sample, False)
+    _full_size(8, 8, 32, 128, lens, 500000.0, 44, False)
+
+
+def test_full_size_config2_fused(gpu):
+    """Config 2's decode step at its largest context (batch 1, 24/8 heads, hd 128, 4352 cached
+    + 1 appended) through the fused launch bench.py times for config 2."""
+    say("decode full cfg2 fused")
+    _full_size(1, 8, 24, 128, [4352], 500000.0, 23, False, fused=True)
 
 
 def test_config2_batch1_long_context(gpu):

@@ -1,5 +1,7 @@
 """GPU parity of the chunked-prefill attention over the INT4 cache (causal, queries at
 len..len+n_tok-1) against the CPU oracle, within |err| <= 2e-3 + 1e-3*|ref|."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -19,7 +21,7 @@ def run_chunks(p: Pair, rng, n_head, chunks, scale_kv=None, scale_q=None, check_
         p.append(k, v)
         out = p.gpu.attn_prefill(0, dev(q), p.rope, softcap=softcap).cpu().numpy()
         if check_heads is None:
-            ref = p.ora.attend(q, n, softcap=softcap, threads=8)
+            ref = p.ora.attend(q, n, softcap=softcap, threads=min(16, os.cpu_count() or 1))
             assert_close(out, ref, f"prefill chunk {n} at {p.ora.lens.tolist()}")
         else:
             for s, h in check_heads:
@@ -70,11 +72,11 @@ def test_softcap_prefill(gpu):
 
 def test_full_size_config5(gpu):
     """Config 5 at full size: Qwen3-4B shape, batch 4, 4 chunks of 512 with fused-RoPE append,
-    then causal attention; the oracle checks a sample of (sequence, head) pairs per chunk."""
+    then causal attention; the oracle checks every (sequence, token, head) output per chunk."""
     say("prefill full cfg5")
     rng = np.random.default_rng(55)
     p = Pair(4, 8, 128, 2048, 1e6)
-    run_chunks(p, rng, 32, [512] * 4, check_heads=[(0, 0), (1, 9), (2, 22), (3, 31)])
+    run_chunks(p, rng, 32, [512] * 4)
     p.check_codes()
     torch.cuda.synchronize()
 
