@@ -328,6 +328,21 @@ int ts_kv_shift(ts_kv *kv, int32_t layer, int32_t seq, int32_t keep_sink, int32_
     // rotation of its own position
     if ((kv->h_sink[seq] != 0 || kv->h_rot[seq] != 0) && kv->h_sink[seq] != keep_sink)
         return TS_ERR_INVALID;
+    // Every argument check runs before the sink count is recorded, so a refused call leaves
+    // the cache as it was.  The move runs in place, in rounds of shift_amt slots (each one
+    // launch), when there are few of them; a short shift of a long window goes through the
+    // workspace instead (export the moved slots in the reference layout, import them at their
+    // new place), and only that path needs the workspace.
+    constexpr int64_t kMaxRounds = 8;
+    const int64_t n_move = (int64_t)kv->h_len[seq] - keep_sink - shift_amt;
+    const bool moves = n_move > 0 && shift_amt > 0;  // elements_to_shift == 0: nothing moves
+    const bool in_place = moves && (n_move + shift_amt - 1) / shift_amt <= kMaxRounds;
+    const uint64_t wpp = (uint64_t)kv->d.n_head_kv * (kv->d.head_dim / 8);  // words per position
+    if (moves && !in_place) {
+        const uint64_t need = (uint64_t)n_move * kv->d.n_head_kv * (kv->d.head_dim + 8);
+        if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
+        if (!aligned16(d_workspace)) return TS_ERR_INVALID;
+    }
     hipStream_t st = as_stream(stream);
     // The first call records the sink count, also when nothing moves, so that a caller who
     // advances the window base after every shift (as the reference's caller does) keeps the
@@ -337,19 +352,9 @@ int ts_kv_shift(ts_kv *kv, int32_t layer, int32_t seq, int32_t keep_sink, int32_
         if (e != hipSuccess) return TS_ERR_HIP;
         kv->h_sink[seq] = keep_sink;
     }
-    const int64_t n_move = (int64_t)kv->h_len[seq] - keep_sink - shift_amt;
-    if (n_move <= 0 || shift_amt == 0) return TS_OK;  // elements_to_shift == 0: nothing moves
-    const uint64_t wpp = (uint64_t)kv->d.n_head_kv * (kv->d.head_dim / 8);  // words per position
-    const uint64_t need = (uint64_t)n_move * kv->d.n_head_kv * (kv->d.head_dim + 8);
-    if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
-    if (!aligned16(d_workspace)) return TS_ERR_INVALID;
+    if (!moves) return TS_OK;
     const ts::KvLayerView L = kv->layer(layer);
-    // In place, in rounds of shift_amt slots (each one launch), when there are few of them; a
-    // short shift of a long window goes through the workspace instead (export the moved slots
-    // in the reference layout, import them at their new place).
-    constexpr int64_t kMaxRounds = 8;
-    if ((n_move + shift_amt - 1) / shift_amt <= kMaxRounds)
-        return hip_status(ts::launch_shift_move(L, seq, keep_sink, shift_amt, (int)n_move, st));
+    if (in_place) return hip_status(ts::launch_shift_move(L, seq, keep_sink, shift_amt, (int)n_move, st));
     uint32_t *kp = (uint32_t *)d_workspace, *vp = kp + n_move * wpp;
     float *ks = (float *)(vp + n_move * wpp), *vs = ks + n_move * kv->d.n_head_kv;
     hipError_t e = ts::launch_export(L, seq, keep_sink + shift_amt, (int)n_move, kp, vp, ks, vs, st);

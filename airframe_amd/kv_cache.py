@@ -85,6 +85,8 @@ class KVCache:
         self.n_layers, self.n_seq, self.n_head_kv = n_layers, n_seq, n_head_kv
         self.head_dim, self.max_seq_len = head_dim, max_seq_len
         self._ws = {}
+        # ts_kv_create allocates on the current device; copies out of the cache go there too
+        self.device = torch.device("cuda", torch.cuda.current_device())
 
     @classmethod
     def new_int4(cls, n_layers, n_head_kv, head_dim, max_seq_len, n_seq=1):
@@ -169,7 +171,7 @@ class KVCache:
             if "shift" not in self._ws:
                 b = ctypes.c_uint64()
                 check("ts_kv_shift_workspace", load().ts_kv_shift_workspace(self._h, ctypes.byref(b)))
-                self._ws["shift"] = torch.empty(max(b.value, 16), dtype=torch.uint8, device="cuda")
+                self._ws["shift"] = torch.empty(max(b.value, 16), dtype=torch.uint8, device=self.device)
             workspace = self._ws["shift"]
         check("ts_kv_shift",
               load().ts_kv_shift(self._h, layer, seq, keep_sink, shift_amt,
@@ -218,7 +220,7 @@ class KVCache:
             b = ctypes.c_uint64()
             check("ts_attn_decode_workspace",
                   load().ts_attn_decode_workspace(self._h, n_head, ctypes.byref(b)))
-            self._ws[n_head] = torch.empty(max(b.value, 4), dtype=torch.uint8, device="cuda")
+            self._ws[n_head] = torch.empty(max(b.value, 4), dtype=torch.uint8, device=self.device)
         return self._ws[n_head]
 
     def attn_decode(self, layer: int, q: torch.Tensor, rope: RopeTable, out: torch.Tensor = None,
@@ -271,8 +273,9 @@ class KVCache:
 
     def export(self, layer: int, seq: int, pos0: int, n_pos: int, stream=None):
         """Packed K/V and scales of positions [pos0, pos0+n_pos) in the reference layout
-        ([pos][n_head_kv][head_dim/8] u32 as int32 bits, [pos][n_head_kv] f32)."""
-        dev = torch.device("cuda")
+        ([pos][n_head_kv][head_dim/8] u32 as int32 bits, [pos][n_head_kv] f32), on the
+        cache's device."""
+        dev = self.device
         kp = torch.empty((n_pos, self.n_head_kv, self.head_dim // 8), dtype=torch.int32, device=dev)
         vp = torch.empty_like(kp)
         ks = torch.empty((n_pos, self.n_head_kv), dtype=torch.float32, device=dev)
@@ -286,17 +289,23 @@ class KVCache:
     # The reference's per-layer buffer getters (kv_cache.rs:312-345).  The reference hands out
     # its buffers; this cache keeps its own tiled layout, so these return copies of one
     # sequence's whole layer (max_seq_len positions) in the reference layout, through export.
+    # Each single getter runs one export of all four arrays and keeps one; a caller that wants
+    # several of them takes get_buffers, which moves the bytes once.
+    def get_buffers(self, layer: int, seq: int = 0):
+        """(k_packed, v_packed, k_scale, v_scale) of one sequence's layer, one export."""
+        return self.export(layer, seq, 0, self.max_seq_len)
+
     def get_k_packed_buffer(self, layer: int, seq: int = 0) -> torch.Tensor:
-        return self.export(layer, seq, 0, self.max_seq_len)[0]
+        return self.get_buffers(layer, seq)[0]
 
     def get_v_packed_buffer(self, layer: int, seq: int = 0) -> torch.Tensor:
-        return self.export(layer, seq, 0, self.max_seq_len)[1]
+        return self.get_buffers(layer, seq)[1]
 
     def get_k_scale_buffer(self, layer: int, seq: int = 0) -> torch.Tensor:
-        return self.export(layer, seq, 0, self.max_seq_len)[2]
+        return self.get_buffers(layer, seq)[2]
 
     def get_v_scale_buffer(self, layer: int, seq: int = 0) -> torch.Tensor:
-        return self.export(layer, seq, 0, self.max_seq_len)[3]
+        return self.get_buffers(layer, seq)[3]
 
     def calculate_offset(self, pos: int, head: int, dim: int) -> int:
         """Byte offset of (pos, head, dim) in the reference's f32 staging layout
@@ -309,7 +318,7 @@ class KVCache:
             b = ctypes.c_uint64()
             check("ts_qkv_workspace",
                   load().ts_qkv_workspace(self._h, dim, n_tok, n_head, ctypes.byref(b)))
-            self._ws[key] = torch.empty(max(b.value, 16), dtype=torch.uint8, device="cuda")
+            self._ws[key] = torch.empty(max(b.value, 16), dtype=torch.uint8, device=self.device)
         return self._ws[key]
 
     def qkv_append(self, layer: int, x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor,

@@ -59,6 +59,43 @@ def append_bytes(batch, n_kv, hd):
     return batch * n_kv * (2 * hd * 4 + hd + 8)
 
 
+def cpu_threads() -> int:
+    """Threads for the OpenMP oracle: the host cores this process may run on (its affinity
+    mask), capped by OMP_NUM_THREADS when that is set (the GPU box grants each GPU's jobs a
+    share of the host's cores and sets it to that share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_info() -> dict:
+    """The host's CPU for the baseline's record: model name, logical CPUs of the host, and the
+    CPUs this process may use."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = None
+    fam = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k in ("cpu family", "model", "stepping", "cpu MHz") and k not in fam:
+                    fam[k] = v.strip()
+                if line.strip() == "":
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": cpu_model(), "cpu_family_model": fam, "host_logical_cpus": os.cpu_count(),
+            "affinity_cpus": aff}
+
+
 def cpu_model() -> str:
     """The host CPU's model name (/proc/cpuinfo), for the baseline's record."""
     try:
@@ -79,7 +116,7 @@ def cpu_baseline(kv, cfg, qs, ks, vs, lens, max_seq, table, layers_mt=2, seqs_st
 
     from oracle import oracle
     n_kv, hd, n_head, B = cfg["n_kv"], cfg["hd"], cfg["n_head"], cfg["batch"]
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     t_mt = 0.0
     t_st = 0.0
     for layer in range(layers_mt):
@@ -255,6 +292,37 @@ def run_decode(args, cfg):
     kb = [kern_bytes[i] for i in range(n_kt) for _ in range(L)]
     result["kernel_ms"] = float(np.mean(kt))
     result["kernel_bytes"] = float(np.mean(kb))
+    result["kernel_timing"] = "HIP events around each decode launch, eager pass of 16 steps"
+    if args.graph:
+        # The decode launches alone (no length increment), captured once as a graph of the L
+        # launches of step 0 and replayed: average time per launch in the same graph context
+        # as the timed steps.  Every replay appends the same token at the same position.
+        reset_lens()
+        kg = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(kg, stream=cap):
+            for layer in range(L):
+                if args.separate:
+                    kv.attn_decode(layer, qs[0][layer], rope, out=out, workspace=ws)
+                else:
+                    kv.attn_decode_append(layer, ks[0][layer], vs[0][layer], qs[0][layer], rope,
+                                          out=out, workspace=ws)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            kg.replay()
+        n_rep = 20
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n_rep):
+            kg.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        result["kernel_ms"] = e0.elapsed_time(e1) / (n_rep * L)
+        result["kernel_bytes"] = float(kern_bytes[0])
+        result["kernel_timing"] = (f"HIP events around {n_rep} replays of a graph holding only the {L} decode "
+                                   "launches of step 0 (split and combine kernels; no length increment)")
+        del kg
 
     cpu = None
     reset_lens()
@@ -330,7 +398,7 @@ def cpu_baseline_prefill(cfg, qs, ks, vs):
     rates are flops of the sample / its time (the same causal-exact counting as the GPU)."""
     from oracle import oracle
     n_head, n_kv, hd, C, NC = cfg["n_head"], cfg["n_kv"], cfg["hd"], cfg["chunk"], cfg["n_chunks"]
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     table = oracle.rope_table(C * NC, hd, cfg["theta"])
 
     def run(n_chunks, thr):
@@ -811,7 +879,7 @@ def main():
                          "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
             "cpu_baseline": None if "cpu" not in r else {
                 "value": round(r["cpu"]["tflops_mt"], 6), "unit": "TFLOP/s", "cores": r["cpu"]["cores"],
-                "kind": "port", "cpu_model": cpu_model(),
+                "kind": "port", **cpu_info(),
                 "single_thread_value": round(r["cpu"]["tflops_st"], 6),
                 "sample": "C oracle: sequence 0 of layer 0, 4 chunks x 512 (append + causal "
                           f"attention, OpenMP over heads, {r['cpu']['cores']} threads); its first "
@@ -837,12 +905,12 @@ def main():
                            f"{split_name}<{cfg['hd']}> with fused append (+ decode_combine_kernel when the plan splits; ts_attn_decode_append)"),
                 "bytes_per_launch": int(r["kernel_bytes"]),
                 "avg_launch_us": round(r["kernel_ms"] * 1e3, 2),
-                "timing": "HIP events around each decode launch, eager pass of 16 steps"}
+                "timing": r["kernel_timing"]}
     cpu_line = None
     if cpu:
         cpu_gbs = r["step_bytes"] / cpu["step_s_mt"] / 1e9
         cpu_line = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": cpu["cores"],
-                    "kind": "port", "cpu_model": cpu_model(),
+                    "kind": "port", **cpu_info(),
                     "tokens_per_s": round(B / cpu["step_s_mt"], 4),
                     "single_thread_tokens_per_s": round(B / cpu["step_s_st"], 5),
                     "sample": f"C oracle: append + attention of step 0 for all {B} sequences of "

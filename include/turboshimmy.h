@@ -152,7 +152,11 @@ int ts_kv_set_qk_norm(ts_kv *kv, int32_t layer, const float *d_q_norm, const flo
 int ts_kv_window_base(const ts_kv *kv, int32_t seq, int32_t *base);
 int ts_kv_advance_window_base(ts_kv *kv, int32_t seq, int32_t shift_amt, void *stream);
 
-/* Device bytes of scratch ts_kv_shift needs at most (a snapshot of the moved slots). */
+/* Device bytes of scratch ts_kv_shift needs at most (a snapshot of the moved slots).  A
+ * shift whose moved slots take at most 8 rounds of shift_amt slots (ceil(n_move / shift_amt)
+ * <= 8, n_move = len - keep_sink - shift_amt) runs in place and needs no workspace (d_workspace
+ * may be NULL); a longer one needs n_move * n_head_kv * (head_dim + 8) bytes, 16-byte aligned,
+ * and is otherwise refused with TS_ERR_WORKSPACE before anything changes. */
 int ts_kv_shift_workspace(const ts_kv *kv, uint64_t *bytes);
 
 /* RopeShiftPipeline::execute_int4 (pipeline_shift.rs:360-566, sh_rope_shift_int4.wgsl:44-84)
@@ -217,8 +221,9 @@ int ts_attn_decode_append(ts_kv *kv, int32_t layer, const float *d_k, const floa
  * split partials go to a scratch array the library keeps on every GPU it runs on (8 MiB each,
  * until the process ends).  No counterpart in the reference: for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * Returns TS_ERR_WORKSPACE when this call's partials, n_seq * n_head * splits * (head_dim + 2)
- * floats, would exceed 8 MiB (a call that needs no split needs none).  All calls on one GPU
+ * Returns TS_ERR_WORKSPACE when this call's partials, n_seq * n_head * splits * (hds + 2)
+ * floats, would exceed 8 MiB, where hds is the stored head dim: head_dim rounded up to 64,
+ * 128 or 256 (a call that needs no split needs none).  All calls on one GPU
  * share the array: calls that overlap on one GPU (other streams, other threads) race. */
 int ts_attn_decode_append_noalloc(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
                                   const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
@@ -262,7 +267,11 @@ int ts_weights_to_f16(int32_t ggml_type, const void *d_src, int64_t n_rows, int6
 /* The same into two f16 planes per row, d_dst [n_rows][2 n_cols]: the first n_cols the value
  * rounded to f16 (hi), the next n_cols the rest (value - hi, exact in f32) rounded to f16 (lo).
  * ts_qkv_append_x2 and ts_attn_out_proj_x2 take such rows and multiply each x by hi + lo, so
- * the projections keep the f32 weights to about 22 bits. */
+ * the projections keep the f32 weights to about 22 bits.  Both forms hold values of f16
+ * range only: a dequantized weight of magnitude 65520 or more (or a non-finite one, such as a
+ * block scale that is inf or NaN) converts to an infinite or NaN hi, and the projections then
+ * return non-finite values; the conversion does not check for it.  Dequantized GGUF weights
+ * of real models stay orders of magnitude below that bound. */
 int ts_weights_to_f16x2(int32_t ggml_type, const void *d_src, int64_t n_rows, int64_t n_cols,
                         uint16_t *d_dst, void *stream);
 

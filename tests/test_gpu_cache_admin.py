@@ -2,11 +2,14 @@
 per-sequence reset of a compacted slot, a shift that moves nothing, and the host-side checks of
 caller-supplied outputs.  Codes and scales bit-exact against the oracle; attention outputs
 within |err| <= 2e-3 + 1e-3*|ref|."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
-from airframe_amd import TsError, synth
+from airframe_amd import TsError, _lib, synth
+from airframe_amd.kv_cache import _stream
 from tests.gpu_util import Pair, assert_close, dev, say
 
 pytestmark = pytest.mark.gpu
@@ -106,6 +109,28 @@ def test_shift_that_moves_nothing_records_sinks(gpu):
     p.gpu.shift_int4(0, 4, 5, seq=0)
     p.ora.shift(0, 4, 5)
     p.check_codes(upto=[p.ora.lens[0] - 5, p.ora.lens[1]])
+
+
+def _shift_raw(p: Pair, seq, keep_sink, shift_amt, ws=None, ws_bytes=0):
+    return _lib.load().ts_kv_shift(p.gpu.handle, 0, seq, keep_sink, shift_amt, ws, ws_bytes, _stream())
+
+
+def test_refused_shift_changes_nothing(gpu):
+    """A shift that needs the workspace (more than 8 in-place rounds) and gets none is refused
+    before the sink count is recorded: a later first shift with another sink count is still
+    accepted.  A shift of at most 8 rounds runs in place with no workspace at all."""
+    say("shift refused without workspace")
+    rng = np.random.default_rng(78)
+    p = Pair(2, 2, 128, 300, 10000.0, rope_n_pos=900)
+    fill(p, rng, 200)
+    # seq 0: keep 4, shift 10 -> 186 moved slots in 19 rounds: needs the workspace
+    assert _shift_raw(p, 0, 4, 10) == _lib.TS_ERR_WORKSPACE
+    p.check_codes()  # nothing moved
+    # seq 0 takes another sink count (none was recorded), in place without a workspace:
+    # keep 2, shift 100 -> 98 moved slots in one round
+    assert _shift_raw(p, 0, 2, 100) == _lib.TS_OK
+    p.ora.shift(0, 2, 100)
+    p.check_codes(upto=[p.ora.lens[0] - 100, p.ora.lens[1]])
 
 
 def test_output_shapes_are_checked(gpu):
