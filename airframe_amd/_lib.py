@@ -66,6 +66,12 @@ SIGNATURES = {
     "ts_attn_decode_append_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i32, _vp, _f, _vp, _vp]),
     "ts_attn_prefill": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _vp, _f, _vp, _vp]),
     "ts_qkv_workspace": (ctypes.c_int, [_vp, _i32, _i32, _i32, _u64p]),
+    "ts_qkv_gguf_workspace": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _u64p]),
+    "ts_qkv_append_gguf": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp,
+                                          _vp, _vp, _vp, ctypes.c_uint64, _vp]),
+    "ts_attn_out_proj_gguf_workspace": (ctypes.c_int, [_i32, _i32, _i32, _i32, _u64p]),
+    "ts_attn_out_proj_gguf": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, ctypes.c_uint64,
+                                             _vp]),
     "ts_qkv_append": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp,
                                      _vp, _vp, _vp, ctypes.c_uint64, _vp]),
     "ts_attn_out_proj_workspace": (ctypes.c_int, [_i32, _i32, _i32, _u64p]),

@@ -41,7 +41,7 @@ SOURCES = {
     "ts_proj.hip": EXACT,
     "ts_weights.hip": EXACT,
 }
-HEADERS = ["ts_internal.h", "ts_mfma.h", "ts_quant.h", "ts_store.h", "ts_gemm.h", os.path.join("..", "..", "include", "turboshimmy.h")]
+HEADERS = ["ts_internal.h", "ts_mfma.h", "ts_quant.h", "ts_store.h", "ts_gemm.h", "ts_kquant.h", os.path.join("..", "..", "include", "turboshimmy.h")]
 
 
 def _compile(src: str, extra: list[str], objdir: str) -> str:

@@ -1,0 +1,250 @@
+// ts_kquant.h -- projection weights in the GGUF K-quant block formats (Q4_K, Q5_K) read at
+// their own size inside the matrix-core loop of the split projections (decode shapes).
+//
+// The reference's main_qkv / main_attn_proj read every weight from the GGUF blob inside the dot
+// product (src/backend/bindless/sh_layer_v1_int4.wgsl:502-520, sh_layer_v1.wgsl:777-790) with
+// the values of src/core/dequant/q4_k.rs:75-123 and q5_k.rs:74-143:
+//     w = (d * sc_j) * q - dmin * m_j      (sub-block j of 32 elements, q 4 or 5 bits).
+// Here the sum over one 256-element super-block is taken apart as
+//     sum_k x_k w_k = d * sum_j sc_j sum_{k in j} x_k q_k  -  dmin * sum_j m_j xsum_j
+// and both inner sums run on v_mfma_f32_32x32x16_f16 with x split hi + lo:
+//   * B operand of the first: q * sc_j, an integer below 2048, so exact in f16.  The k-steps
+//     are arranged so that every lane's 8 elements of one instruction lie in one sub-block:
+//     lane half hf of a 64-element chunk g takes bytes 16 hf .. 16 hf + 15 of the chunk's 32
+//     qs bytes (one 16-byte load) -- k-steps 0, 1 their low nibbles (sub-block 2g), 2, 3
+//     their high nibbles (sub-block 2g + 1).  The x operand reads the same elements.
+//   * the second: xsum_j (the sub-block sums of x, f32 split hi + lo) against m_j, one
+//     instruction per super-block with k = the 8 sub-blocks (the upper 8 k are zero).
+// d and dmin are applied to the two f32 accumulators once per super-block (one FMA each per
+// output).  A weight moves 144 / 256 = 0.5625 bytes (Q4_K) or 176 / 256 = 0.6875 (Q5_K)
+// instead of 4 for the two-plane f16 form.
+#pragma once
+#include "ts_gemm.h"
+
+namespace ts {
+namespace {
+
+constexpr int kGgmlQ4K = 12, kGgmlQ5K = 13;
+
+template <int T>
+struct KQ {
+    static constexpr int BYTES = T == kGgmlQ4K ? 144 : 176;  // one 256-element super-block
+    static constexpr int QS = T == kGgmlQ4K ? 16 : 48;       // offset of the 128 qs bytes
+};
+
+// LDS of the K-quant slice loop: x of one super-block (4 chunks of 64) as hi/lo, and the f32
+// sums of its 8 sub-blocks per row.
+struct KqTiles {
+    SplitTiles x;
+    float xsum[32][8];
+};
+
+// One lane's share of one weight row's super-block: the 16-byte header (d, dmin, 12 packed
+// scale bytes), its 16 qs bytes of each 64-element chunk, and for Q5_K its 16 qh bytes (the
+// fifth bits of elements 16 hf .. 16 hf + 15 of every sub-block).
+struct KqRegs {
+    uint4 hdr, qs[4], qh;
+};
+
+template <int T>
+__device__ __forceinline__ void kq_load(KqRegs &r, const uint8_t *blk, int hf) {
+    r.hdr = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+    for (int g = 0; g < 4; g++) r.qs[g] = *reinterpret_cast<const uint4 *>(blk + KQ<T>::QS + 32 * g + 16 * hf);
+    if constexpr (T == kGgmlQ5K)
+        r.qh = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * hf);
+    else
+        r.qh = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The 6-bit scales and mins of the 8 sub-blocks (q4_k.rs:134-143, get_scale_min_k4), four
+// per word, byte j % 4: sc of sub-blocks 0-3 and 4-7, m of 0-3 and 4-7.
+struct KqScales {
+    uint32_t sc03, sc47, m03, m47;
+};
+__device__ inline KqScales kq_scales(const uint4 &hdr) {
+    const uint32_t y = hdr.y, z = hdr.z, w = hdr.w;  // scale bytes 0-3, 4-7, 8-11
+    KqScales s;
+    s.sc03 = y & 0x3F3F3F3Fu;
+    s.m03 = z & 0x3F3F3F3Fu;
+    s.sc47 = (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
+    s.m47 = ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
+    return s;
+}
+__device__ inline int kq_byte(uint32_t w, int b) { return (int)((w >> (8 * b)) & 0xFFu); }
+
+// The B operands of chunk g for one weight row: k-step q in b[q], element i of the half8 the
+// code of byte 8 (q & 1) + i of the lane's 16 (low nibble for q < 2, high for q >= 2), times
+// its sub-block's scale.  Codes enter as f16 1024 + n (0x6400 | n) or, for a Q4_K high nibble
+// left in place, 1024 + 16 n; one packed FMA per two codes gives n * sc exactly (every
+// intermediate is an integer below 2^16 that f16 holds, or that integer over 16).
+template <int T>
+__device__ __forceinline__ void kq_operands(const KqRegs &r, const KqScales &s, int g, half8 (&b)[4],
+                                            const DeqConst &dk) {
+    const int scl = g < 2 ? kq_byte(s.sc03, 2 * g) : kq_byte(s.sc47, 2 * g - 4);
+    const int sch = g < 2 ? kq_byte(s.sc03, 2 * g + 1) : kq_byte(s.sc47, 2 * g - 3);
+    const _Float16 fl = (_Float16)scl, fh = (_Float16)sch;
+    const half2_t ml = {fl, fl}, al = {(_Float16)(-1024.0f) * fl, (_Float16)(-1024.0f) * fl};
+    // Q4_K high nibbles stay at bits 4-7 (1024 + 16 n): multiply by sc / 16, subtract 64 sc;
+    // Q5_K high codes are moved down first (1024 + n): multiply by sc, subtract 1024 sc
+    const _Float16 fhm = T == kGgmlQ4K ? fh * (_Float16)0.0625f : fh;
+    const _Float16 fha = T == kGgmlQ4K ? (_Float16)(-64.0f) * fh : (_Float16)(-1024.0f) * fh;
+    const half2_t mh = {fhm, fhm}, ah = {fha, fha};
+    const uint32_t w[4] = {r.qs[g].x, r.qs[g].y, r.qs[g].z, r.qs[g].w};
+    const uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // byte pairs (0, 1) and (2, 3) of word i into the two 16-bit halves
+        half2_t lo2[2], hi2[2];
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const uint32_t sel = p ? 0x0C030C02u : 0x0C010C00u;
+            if constexpr (T == kGgmlQ4K) {
+                const uint32_t sp = __builtin_amdgcn_perm(w[i], w[i], sel);
+                lo2[p] = __builtin_bit_cast(half2_t, (sp & dk.lo) | dk.magic);  // 1024 + n
+                hi2[p] = __builtin_bit_cast(half2_t, (sp & dk.hi) | dk.magic);  // 1024 + 16 n
+            } else {
+                // five-bit codes: the qh bit of sub-block 2g (low) / 2g + 1 (high) at bit 4
+                const uint32_t cl = (w[i] & 0x0F0F0F0Fu) | (((h[i] >> (2 * g)) & 0x01010101u) << 4);
+                const uint32_t ch = ((w[i] >> 4) & 0x0F0F0F0Fu) | (((h[i] >> (2 * g + 1)) & 0x01010101u) << 4);
+                lo2[p] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(cl, cl, sel) | dk.magic);
+                hi2[p] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(ch, ch, sel) | dk.magic);
+            }
+            // fused (one rounding of an exact integer): the product alone may exceed 2048,
+            // where f16 drops odd integers
+            lo2[p] = __builtin_elementwise_fma(lo2[p], ml, al);
+            hi2[p] = __builtin_elementwise_fma(hi2[p], mh, ah);
+        }
+        // word i holds bytes 4i .. 4i + 3: k-step (i >> 1) (low) or 2 + (i >> 1) (high),
+        // elements 4 (i & 1) .. + 3
+        const int ql = i >> 1, e = 4 * (i & 1);
+        b[ql][e + 0] = lo2[0][0]; b[ql][e + 1] = lo2[0][1];
+        b[ql][e + 2] = lo2[1][0]; b[ql][e + 3] = lo2[1][1];
+        b[2 + ql][e + 0] = hi2[0][0]; b[2 + ql][e + 1] = hi2[0][1];
+        b[2 + ql][e + 2] = hi2[1][0]; b[2 + ql][e + 3] = hi2[1][1];
+    }
+}
+
+// The B operand of the min product: m_0 .. m_7 of the row's super-block in lane half 0, zeros
+// in lane half 1 (the upper 8 k of the instruction).
+__device__ inline half8 kq_min_operand(const KqScales &s, int hf) {
+    half8 m;
+#pragma unroll
+    for (int j = 0; j < 8; j++) m[j] = hf ? (_Float16)0.0f : (_Float16)(j < 4 ? kq_byte(s.m03, j) : kq_byte(s.m47, j - 4));
+    return m;
+}
+
+// One slice of the reduction for a 32 x 256 tile over nbat super-blocks (the K-quant form of
+// gemm_split_core, same thread roles and D layout): x of a super-block into LDS as hi/lo and
+// its sub-block sums, the weight blocks straight into registers, one memory round trip per
+// super-block.  wb[cb]: the lane's weight row of column block cb at the slice's first
+// super-block; xs: the staging thread's 8 floats of its row at the slice's first chunk (null:
+// a zero row).
+template <int T>
+__device__ __forceinline__ void gemm_split_kq(KqTiles (&sm)[2], const float *xs, const uint8_t *const (&wb)[2],
+                                              int nbat, int tid, floatx16 (&acc)[2]) {
+    constexpr int NB = 4;
+    const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int si = tid >> 3, sc = tid & 7;
+    const DeqConstV dk;
+    zero(acc[0]);
+    zero(acc[1]);
+    // Super-block b + 1's x and weight blocks are loaded while b is multiplied; x goes through
+    // LDS (double-buffered, one barrier per super-block), the weights stay in registers.
+    float4 xu[NB], xv[NB];
+    KqRegs r[2][2];  // [buffer][column block]
+    auto load = [&](int b, KqRegs (&rr)[2]) {
+        const bool on = b < nbat;
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            xu[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[c] = xu[c];
+            if (xs && on) {
+                xu[c] = *reinterpret_cast<const float4 *>(xs + (b * NB + c) * kKC);
+                xv[c] = *reinterpret_cast<const float4 *>(xs + (b * NB + c) * kKC + 4);
+            }
+        }
+        if (on) {
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++) kq_load<T>(rr[cb], wb[cb] + (size_t)b * KQ<T>::BYTES, hf);
+        }
+    };
+    auto stage = [&](KqTiles &t) {
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            half8 h, l;
+            split8(xu[c], xv[c], h, l);
+            *reinterpret_cast<half8 *>(&t.x.hi[c][si][8 * sc]) = h;
+            *reinterpret_cast<half8 *>(&t.x.lo[c][si][8 * sc]) = l;
+            // sub-block sums: 4 staging threads (consecutive lanes) per 32 elements
+            float v = ((xu[c].x + xu[c].y) + (xu[c].z + xu[c].w)) + ((xv[c].x + xv[c].y) + (xv[c].z + xv[c].w));
+            v += __shfl_xor(v, 1, 64);
+            v += __shfl_xor(v, 2, 64);
+            if ((sc & 3) == 0) t.xsum[si][2 * c + (sc >> 2)] = v;
+        }
+    };
+    auto compute = [&](const KqTiles &t, const KqRegs (&rr)[2]) {
+        const KqScales s0 = kq_scales(rr[0].hdr), s1 = kq_scales(rr[1].hdr);
+        floatx16 t0, t1;
+        zero(t0);
+        zero(t1);
+#pragma unroll
+        for (int g = 0; g < NB; g++) {
+            half8 b0[4], b1[4];
+            kq_operands<T>(rr[0], s0, g, b0, dk);
+            kq_operands<T>(rr[1], s1, g, b1, dk);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int ko = 32 * (q >> 1) + 16 * hf + 8 * (q & 1);
+                const half8 ah = *reinterpret_cast<const half8 *>(&t.x.hi[g][j][ko]);
+                const half8 al = *reinterpret_cast<const half8 *>(&t.x.lo[g][j][ko]);
+                t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0[q], t0, 0, 0, 0);
+                t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1[q], t1, 0, 0, 0);
+                t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0[q], t0, 0, 0, 0);
+                t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1[q], t1, 0, 0, 0);
+            }
+        }
+        // the min product: x sums of row j (split hi + lo) against m of the column's sub-blocks
+        half8 sh, sl;
+        {
+            const float4 u = *reinterpret_cast<const float4 *>(&t.xsum[j][0]);
+            const float4 v = *reinterpret_cast<const float4 *>(&t.xsum[j][4]);
+            split8(u, v, sh, sl);
+        }
+        const half8 mb0 = kq_min_operand(s0, hf), mb1 = kq_min_operand(s1, hf);
+        floatx16 u0, u1;
+        zero(u0);
+        zero(u1);
+        u0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, mb0, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh, mb1, u1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl, mb0, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl, mb1, u1, 0, 0, 0);
+        // d and dmin of the lane's column (f16 at bytes 0 and 2 of the block)
+        const float d0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rr[0].hdr.x & 0xFFFFu));
+        const float n0 = -(float)__builtin_bit_cast(_Float16, (uint16_t)(rr[0].hdr.x >> 16));
+        const float d1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(rr[1].hdr.x & 0xFFFFu));
+        const float n1 = -(float)__builtin_bit_cast(_Float16, (uint16_t)(rr[1].hdr.x >> 16));
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            acc[0][e] = __builtin_fmaf(n0, u0[e], __builtin_fmaf(d0, t0[e], acc[0][e]));
+            acc[1][e] = __builtin_fmaf(n1, u1[e], __builtin_fmaf(d1, t1[e], acc[1][e]));
+        }
+    };
+    load(0, r[0]);
+    stage(sm[0]);
+    // two super-blocks per trip so that the register buffers are indexed with constants
+    for (int b = 0; b < nbat; b += 2) {
+        load(b + 1, r[1]);
+        __syncthreads();  // sm[0] staged (and sm[1] no longer read)
+        compute(sm[0], r[0]);
+        if (b + 1 >= nbat) break;  // uniform
+        stage(sm[1]);
+        load(b + 2, r[0]);
+        __syncthreads();
+        compute(sm[1], r[1]);
+        if (b + 2 < nbat) stage(sm[0]);
+    }
+}
+
+}  // namespace
+}  // namespace ts

@@ -644,6 +644,102 @@ int ts_qkv_append_x2(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, in
                              d_workspace, workspace_bytes, stream, 2);
 }
 
+// ---- projections with GGUF K-quant weights read in the loop ----------------------------------
+
+static bool kq_type_ok(int32_t t) { return t == TS_GGML_Q4_K || t == TS_GGML_Q5_K; }
+
+struct QkvGenericKq {
+    ts::ProjPlan pq, pk;
+    uint64_t part_bytes, kv_elems;
+};
+static QkvGenericKq qkv_generic_plan_kq(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head) {
+    QkvGenericKq g;
+    const int M = kv->d.n_seq * n_tok, hd = kv->d.head_dim;
+    g.pq = ts::proj_plan_kq(M, dim, n_head * hd);
+    g.pk = ts::proj_plan_kq(M, dim, kv->d.n_head_kv * hd);
+    g.part_bytes = (std::max(g.pq.part_bytes, g.pk.part_bytes) + 255) / 256 * 256;
+    g.kv_elems = (uint64_t)M * kv->d.n_head_kv * hd;
+    return g;
+}
+
+int ts_qkv_gguf_workspace(const ts_kv *kv, int32_t ggml_type, int32_t dim, int32_t n_tok, int32_t n_head,
+                          uint64_t *bytes) {
+    if (!kv || !bytes || !qkv_shape_ok(kv, dim, n_tok, n_head) || dim % 256 != 0) return TS_ERR_INVALID;
+    if (!kq_type_ok(ggml_type)) return TS_ERR_UNSUPPORTED;
+    *bytes = 0;
+    if (n_tok == 0) return TS_OK;
+    if (qkv_fused(kv)) {
+        *bytes = ts::qkv_plan_kq(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, dim, n_tok).part_bytes;
+    } else {
+        const QkvGenericKq g = qkv_generic_plan_kq(kv, dim, n_tok, n_head);
+        *bytes = g.part_bytes + 2 * g.kv_elems * sizeof(float);
+    }
+    return TS_OK;
+}
+
+int ts_qkv_append_gguf(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, int32_t n_tok, int32_t ggml_type,
+                       const void *d_wq, const void *d_wk, const void *d_wv, int32_t n_head, const ts_rope *rope,
+                       float *d_q, float *d_k, float *d_v, void *d_workspace, uint64_t workspace_bytes,
+                       void *stream) {
+    if (!kv || layer < 0 || layer >= kv->d.n_layers) return TS_ERR_INVALID;
+    if (!qkv_shape_ok(kv, dim, n_tok, n_head) || dim % 256 != 0 || !d_x || !d_wq || !d_wk || !d_wv || !d_q ||
+        !aligned16(d_x) || !aligned16(d_wq) || !aligned16(d_wk) || !aligned16(d_wv) || !aligned16(d_q) ||
+        (!d_k) != (!d_v) || (d_k && (!aligned16(d_k) || !aligned16(d_v))))
+        return TS_ERR_INVALID;
+    if (!kq_type_ok(ggml_type)) return TS_ERR_UNSUPPORTED;
+    int32_t max_len = *std::max_element(kv->h_len.begin(), kv->h_len.end());
+    if ((int64_t)max_len + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;
+    int rc = check_rope(rope, kv->d.head_dim, rot_end(kv, n_tok));
+    if (rc) return rc;
+    if (n_tok == 0) return TS_OK;
+    const hipStream_t st = as_stream(stream);
+    if (!qkv_fused(kv)) {
+        const QkvGenericKq g = qkv_generic_plan_kq(kv, dim, n_tok, n_head);
+        const uint64_t need = g.part_bytes + (d_k ? 0 : 2 * g.kv_elems * sizeof(float));
+        if (!d_workspace || workspace_bytes < need || !aligned16(d_workspace)) return TS_ERR_WORKSPACE;
+        float *part = static_cast<float *>(d_workspace);
+        float *kb = d_k ? d_k : reinterpret_cast<float *>(static_cast<uint8_t *>(d_workspace) + g.part_bytes);
+        float *vb = d_k ? d_v : kb + g.kv_elems;
+        const int M = kv->d.n_seq * n_tok, hd = kv->d.head_dim, H = kv->d.n_head_kv;
+        hipError_t e = ts::launch_fill_zero(d_q, (size_t)M * n_head * hd, st);
+        if (e == hipSuccess) e = ts::launch_fill_zero(kb, g.kv_elems, st);
+        if (e == hipSuccess) e = ts::launch_fill_zero(vb, g.kv_elems, st);
+        if (e == hipSuccess) e = ts::launch_proj_kq(d_x, M, dim, ggml_type, d_wq, n_head * hd, d_q, nullptr, g.pq, part, st);
+        if (e == hipSuccess) e = ts::launch_proj_kq(d_x, M, dim, ggml_type, d_wk, H * hd, kb, nullptr, g.pk, part, st);
+        if (e == hipSuccess) e = ts::launch_proj_kq(d_x, M, dim, ggml_type, d_wv, H * hd, vb, nullptr, g.pk, part, st);
+        if (e == hipSuccess)
+            e = ts::launch_quantize_rows(kv->layer(layer), kb, vb, kv->d_len, 0, n_tok, n_tok, rope->d_table,
+                                         rope->rope_dim / 2, n_tok / 32 + 2, st);
+        return hip_status(e);
+    }
+    const ts::QkvPlan plan = ts::qkv_plan_kq(kv->d.n_seq, kv->d.n_head_kv, n_head, kv->d.head_dim, dim, n_tok);
+    if (!d_workspace || workspace_bytes < plan.part_bytes || !aligned16(d_workspace)) return TS_ERR_WORKSPACE;
+    return hip_status(ts::launch_qkv_kq(kv->layer(layer), kv->d_len, d_x, dim, n_tok, ggml_type, d_wq, d_wk, d_wv,
+                                        n_head, d_q, d_k, d_v, rope->d_table, rope->rope_dim / 2, plan,
+                                        static_cast<float *>(d_workspace), st));
+}
+
+int ts_attn_out_proj_gguf_workspace(int32_t ggml_type, int32_t n_tok, int32_t attn_dim, int32_t dim, uint64_t *bytes) {
+    if (!bytes || n_tok < 0 || attn_dim <= 0 || attn_dim % 256 != 0 || dim <= 0) return TS_ERR_INVALID;
+    if (!kq_type_ok(ggml_type)) return TS_ERR_UNSUPPORTED;
+    *bytes = n_tok > 0 ? ts::proj_plan_kq(n_tok, attn_dim, dim).part_bytes : 0;
+    return TS_OK;
+}
+
+int ts_attn_out_proj_gguf(const float *d_attn, int32_t n_tok, int32_t attn_dim, int32_t ggml_type, const void *d_wo,
+                          int32_t dim, float *d_act, float *d_stash, void *d_workspace, uint64_t workspace_bytes,
+                          void *stream) {
+    if (!d_attn || !d_wo || !d_act || n_tok < 0 || attn_dim <= 0 || attn_dim % 256 != 0 || dim <= 0 ||
+        !aligned16(d_attn) || !aligned16(d_wo) || !aligned16(d_act) || !aligned16(d_stash))
+        return TS_ERR_INVALID;
+    if (!kq_type_ok(ggml_type)) return TS_ERR_UNSUPPORTED;
+    if (n_tok == 0) return TS_OK;
+    const ts::ProjPlan plan = ts::proj_plan_kq(n_tok, attn_dim, dim);
+    if (!d_workspace || workspace_bytes < plan.part_bytes || !aligned16(d_workspace)) return TS_ERR_WORKSPACE;
+    return hip_status(ts::launch_proj_kq(d_attn, n_tok, attn_dim, ggml_type, d_wo, dim, d_act, d_stash, plan,
+                                         static_cast<float *>(d_workspace), as_stream(stream)));
+}
+
 int ts_attn_out_proj_workspace(int32_t n_tok, int32_t attn_dim, int32_t dim, uint64_t *bytes) {
     if (!bytes || n_tok < 0 || attn_dim <= 0 || attn_dim % 64 != 0 || dim <= 0) return TS_ERR_INVALID;
     *bytes = 0;  // enough for f16 rows and for two-plane rows (ts_attn_out_proj_x2)

@@ -15,6 +15,7 @@
 // redo it (n_split-fold reads of the partials) once per column tile.
 #include "ts_gemm.h"
 #include "ts_internal.h"
+#include "ts_kquant.h"
 
 namespace ts {
 namespace {
@@ -25,6 +26,8 @@ constexpr int kMaxPSplit = 16;  // most splits of the reduction
 struct ProjArgs {
     const float *a;      // [M][K] attention output
     const _Float16 *w;   // [N][K]
+    const uint8_t *bw;   // the same rows as GGUF K-quant blocks (the K-quant kernel)
+    size_t brow;         // bytes of one block row
     float *act;          // [M][N], += dot
     float *stash;        // [M][N] raw dot, or null
     float *part;         // [n_split][RT][CT][32][256] partials, or null
@@ -87,6 +90,33 @@ __global__ __launch_bounds__(256) void proj_split_kernel(ProjArgs p) {
                                    p.w + (size_t)min(col0 + 32 + j, p.N - 1) * p.KW + kb + 32 * hf};
     floatx16 acc[2];
     gemm_split_core(sm, xs, kb / kKC, p.K / kKC, wp, nbat, tid, acc);
+    float *dst = p.part + (((size_t)sp * p.RT + rt) * p.CT + ct) * (32 * kPT);
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            dst[(8 * (e >> 2) + 4 * hf + (e & 3)) * kPT + 64 * wave + 32 * cb + j] = acc[cb][e];
+}
+
+// The same with the weights as GGUF K-quant blocks read in the loop (gemm_split_kq); slices of
+// whole super-blocks, one slice when the tiles alone fill the chip.
+template <int T>
+__global__ __launch_bounds__(256) void proj_split_kq_kernel(ProjArgs p) {
+    __shared__ __align__(16) KqTiles sm[2];
+    int rt, ct, sp;
+    proj_tile_of(p, blockIdx.x, rt, ct, sp);
+    if (sp >= p.n_split) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int row0 = 32 * rt, col0 = kPT * ct + 64 * wave;
+    const int kb = sp * p.kps;
+    const int nbat = (min(kb + p.kps, p.K) - kb) / 256;
+    const int si = tid >> 3, sc = tid & 7;
+    const float *xs = row0 + si < p.M ? p.a + (size_t)(row0 + si) * p.K + kb + 8 * sc : nullptr;
+    const size_t boff = (size_t)(kb / 256) * KQ<T>::BYTES;
+    const uint8_t *const wb[2] = {p.bw + (size_t)min(col0 + j, p.N - 1) * p.brow + boff,
+                                  p.bw + (size_t)min(col0 + 32 + j, p.N - 1) * p.brow + boff};
+    floatx16 acc[2];
+    gemm_split_kq<T>(sm, xs, wb, nbat, tid, acc);
     float *dst = p.part + (((size_t)sp * p.RT + rt) * p.CT + ct) * (32 * kPT);
 #pragma unroll
     for (int cb = 0; cb < 2; cb++)
@@ -167,12 +197,60 @@ ProjPlan proj_plan(int M, int K, int N) {
     return p;
 }
 
+ProjPlan proj_plan_kq(int M, int K, int N) {
+    ProjPlan p;
+    p.CT = (N + kPT - 1) / kPT;
+    p.RT = (M + 31) / 32;
+    const int tiles = p.RT * p.CT;
+    // splits for about one workgroup per CU (256): measured on config 3's decode shapes, 512
+    // and 1024 were no faster (the split count is capped at kMaxPSplit anyway)
+    const int want = tiles < 256 ? std::min(kMaxPSplit, std::max(1, (256 + tiles - 1) / tiles)) : 1;
+    const int nbat = K / 256;
+    const int per = (nbat + want - 1) / want;
+    p.kps = per * 256;
+    p.n_split = (nbat + per - 1) / per;
+    p.part_bytes = (uint64_t)p.n_split * tiles * 32 * kPT * sizeof(float);
+    return p;
+}
+
+hipError_t launch_proj_kq(const float *a, int M, int K, int ggml_type, const void *w, int N, float *act,
+                          float *stash, const ProjPlan &plan, float *part, hipStream_t st) {
+    if (K % 256 != 0 || M <= 0 || N <= 0 || !part || (ggml_type != kGgmlQ4K && ggml_type != kGgmlQ5K))
+        return hipErrorInvalidValue;
+    ProjArgs p;
+    p.a = a;
+    p.w = nullptr;
+    p.bw = static_cast<const uint8_t *>(w);
+    p.brow = (size_t)(K / 256) * (ggml_type == kGgmlQ4K ? KQ<kGgmlQ4K>::BYTES : KQ<kGgmlQ5K>::BYTES);
+    p.act = act;
+    p.stash = stash;
+    p.part = part;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.KW = K;
+    p.RT = plan.RT;
+    p.CT = plan.CT;
+    p.kps = plan.kps;
+    p.n_split = plan.n_split;
+    p.n_wg = plan.RT * plan.CT * plan.n_split;
+    const int grid = (p.n_wg + 7) / 8 * 8;
+    if (ggml_type == kGgmlQ4K)
+        proj_split_kq_kernel<kGgmlQ4K><<<grid, 256, 0, st>>>(p);
+    else
+        proj_split_kq_kernel<kGgmlQ5K><<<grid, 256, 0, st>>>(p);
+    proj_reduce_kernel<<<plan.RT * plan.CT * 4, 256, 0, st>>>(p);
+    return hipGetLastError();
+}
+
 hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, float *act, float *stash,
                        const ProjPlan &plan, float *part, int planes, hipStream_t st) {
     if (K % kKC != 0 || M <= 0 || N <= 0 || (planes != 1 && planes != 2)) return hipErrorInvalidValue;
     ProjArgs p;
     p.a = a;
     p.w = reinterpret_cast<const _Float16 *>(w);
+    p.bw = nullptr;
+    p.brow = 0;
     p.act = act;
     p.stash = stash;
     p.part = part;

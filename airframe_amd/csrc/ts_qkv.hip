@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "ts_gemm.h"
+#include "ts_kquant.h"
 #include "ts_store.h"
 
 namespace ts {
@@ -48,6 +49,8 @@ struct QkvArgs {
     const int32_t *len;    // start position of every sequence
     const float *x;        // [S][n_tok][dim]
     const _Float16 *wq, *wk, *wv;  // [n_head*hd][dim], [H*hd][dim], [H*hd][dim]
+    const uint8_t *bq, *bk, *bv;   // the same rows as GGUF K-quant blocks (the K-quant kernels)
+    size_t brow;                   // bytes of one block row: dim / 256 super-blocks
     float *q_out;          // [S][n_tok][n_head][hd]
     float *k_out, *v_out;  // optional raw projections [S][n_tok][H][hd]
     const float *rope;
@@ -107,6 +110,17 @@ __device__ inline const _Float16 *w_row(const QkvArgs &a, int ct, int n) {
     const int j = n / (2 * a.hd), c = n % (2 * a.hd);
     const int h = min((ct - a.n_qt) * a.hpt + j, a.L.H - 1);
     return c < a.hd ? a.wk + ((size_t)h * a.hd + c) * a.wld : a.wv + ((size_t)h * a.hd + c - a.hd) * a.wld;
+}
+
+// Block row of column n of column tile ct (K-quant weights; the same rows as w_row).
+__device__ inline const uint8_t *kq_row(const QkvArgs &a, int ct, int n) {
+    if (ct < a.n_qt) {
+        const int r = min(ct * kNT + n, a.n_head * a.hd - 1);
+        return a.bq + (size_t)r * a.brow;
+    }
+    const int j = n / (2 * a.hd), c = n % (2 * a.hd);
+    const int h = min((ct - a.n_qt) * a.hpt + j, a.L.H - 1);
+    return c < a.hd ? a.bk + ((size_t)h * a.hd + c) * a.brow : a.bv + ((size_t)h * a.hd + c - a.hd) * a.brow;
 }
 
 // Workgroup id -> (row tile, column tile, split), ordered so that each XCD (workgroups are
@@ -370,6 +384,35 @@ __global__ __launch_bounds__(256) void qkv_split_kernel(QkvArgs a) {
             dst[(8 * (e >> 2) + 4 * hf + (e & 3)) * kNT + 64 * wave + 32 * cb + j] = acc[cb][e];
 }
 
+// The same with the weights as GGUF K-quant blocks read in the loop (gemm_split_kq); a slice
+// is a whole number of 256-element super-blocks.  Also used with one slice (no split) for
+// shapes with many tiles, the reduce kernel then only running the epilogue.
+template <int T>
+__global__ __launch_bounds__(256) void qkv_split_kq_kernel(QkvArgs a) {
+    __shared__ __align__(16) KqTiles sm[2];
+
+    int rt, ct, sp;
+    tile_of(a, blockIdx.x, rt, ct, sp);
+    if (sp >= a.n_split) return;
+    const RowTile t = row_tile(a, rt);
+    if (!t.live) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int xr = x_row(a, t, tid >> 3);
+    const int kb = sp * a.kps;
+    const int nbat = (min(kb + a.kps, a.dim) - kb) / 256;
+    const float *xs = xr >= 0 ? a.x + (size_t)xr * a.dim + kb + 8 * (tid & 7) : nullptr;
+    const size_t boff = (size_t)(kb / 256) * KQ<T>::BYTES;
+    const uint8_t *const wb[2] = {kq_row(a, ct, 64 * wave + j) + boff, kq_row(a, ct, 64 * wave + 32 + j) + boff};
+    floatx16 acc[2];
+    gemm_split_kq<T>(sm, xs, wb, nbat, tid, acc);
+    float *dst = a.part + (((size_t)sp * a.RT + rt) * a.CT + ct) * (kMT * kNT);
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            dst[(8 * (e >> 2) + 4 * hf + (e & 3)) * kNT + 64 * wave + 32 * cb + j] = acc[cb][e];
+}
+
 // Sum of the split partials of rows r0 .. r0 + NR - 1 of one tile, in split order, then their
 // epilogue.  Decode rows are independent, so a tile is spread over 32 / NR workgroups (NR = 8);
 // block rows share V words and take the whole tile (NR = 32).  Each thread issues the loads
@@ -422,6 +465,70 @@ QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok) {
     return p;
 }
 
+QkvPlan qkv_plan_kq(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok) {
+    QkvPlan p;
+    const int hpt = 128 / hd;
+    p.CT = (n_head * hd + kNT - 1) / kNT + (n_kv + hpt - 1) / hpt;
+    p.big = false;
+    p.RT = n_tok == 1 ? (n_seq + kMT - 1) / kMT : n_seq * (n_tok / kBlk + 2);
+    const int tiles = p.RT * p.CT;
+    // few tiles: dim split over workgroups; many tiles: one slice over all of dim
+    // splits for about one workgroup per CU (256): measured on config 3's decode shapes, 512
+    // and 1024 were no faster (the split count is capped at kMaxSplit anyway)
+    const int want = tiles < 256 ? std::min(kMaxSplit, std::max(1, (256 + tiles - 1) / tiles)) : 1;
+    const int nbat = dim / 256;
+    const int per = (nbat + want - 1) / want;
+    p.kps = per * 256;
+    p.n_split = (nbat + per - 1) / per;
+    p.part_bytes = (uint64_t)p.n_split * tiles * kMT * kNT * sizeof(float);
+    return p;
+}
+
+hipError_t launch_qkv_kq(const KvLayerView &L, const int32_t *d_len, const float *x, int dim, int n_tok,
+                         int ggml_type, const void *wq, const void *wk, const void *wv, int n_head,
+                         float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,
+                         const QkvPlan &plan, float *part, hipStream_t st) {
+    if ((L.hd != 128 && L.hd != 64) || dim % 256 != 0 || !part || (ggml_type != kGgmlQ4K && ggml_type != kGgmlQ5K))
+        return hipErrorInvalidValue;
+    QkvArgs a;
+    a.L = L;
+    a.len = d_len;
+    a.x = x;
+    a.wq = a.wk = a.wv = nullptr;
+    a.bq = static_cast<const uint8_t *>(wq);
+    a.bk = static_cast<const uint8_t *>(wk);
+    a.bv = static_cast<const uint8_t *>(wv);
+    a.brow = (size_t)(dim / 256) * (ggml_type == kGgmlQ4K ? KQ<kGgmlQ4K>::BYTES : KQ<kGgmlQ5K>::BYTES);
+    a.q_out = q_out;
+    a.k_out = k_out;
+    a.v_out = v_out;
+    a.rope = rope;
+    a.rope_pairs = rope ? rope_pairs : 0;
+    a.part = part;
+    a.dim = dim;
+    a.wld = dim;
+    a.n_tok = n_tok;
+    a.n_head = n_head;
+    a.hd = L.hd;
+    a.hpt = 128 / L.hd;
+    a.n_qt = (n_head * L.hd + kNT - 1) / kNT;
+    a.RT = plan.RT;
+    a.CT = plan.CT;
+    a.kps = plan.kps;
+    a.n_split = plan.n_split;
+    a.n_wg = plan.RT * plan.CT * plan.n_split;
+    const int grid = (a.n_wg + 7) / 8 * 8;
+    if (ggml_type == kGgmlQ4K)
+        qkv_split_kq_kernel<kGgmlQ4K><<<grid, 256, 0, st>>>(a);
+    else
+        qkv_split_kq_kernel<kGgmlQ5K><<<grid, 256, 0, st>>>(a);
+    if (n_tok == 1)
+        qkv_reduce_kernel<8><<<plan.RT * plan.CT * (kMT / 8), 256, 0, st>>>(a);
+    else
+        qkv_reduce_kernel<kMT><<<plan.RT * plan.CT, 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+
 hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x, int dim, int n_tok,
                       const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, int n_head,
                       float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,
@@ -439,6 +546,8 @@ hipError_t launch_qkv(const KvLayerView &L, const int32_t *d_len, const float *x
     a.v_out = v_out;
     a.rope = rope;
     a.rope_pairs = rope ? rope_pairs : 0;
+    a.bq = a.bk = a.bv = nullptr;
+    a.brow = 0;
     a.part = plan.n_split > 1 ? part : nullptr;
     a.dim = dim;
     a.wld = planes * dim;

@@ -362,6 +362,52 @@ class KVCache:
                                    ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
         return q_out
 
+    def qkv_append_gguf(self, layer: int, x: torch.Tensor, ggml_type: int, wq: torch.Tensor,
+                        wk: torch.Tensor, wv: torch.Tensor, rope: RopeTable,
+                        q_out: torch.Tensor = None, kv_out: tuple | None = None,
+                        workspace: torch.Tensor = None, stream=None):
+        """qkv_append with the weights as the GGUF blob's Q4_K / Q5_K blocks (uint8 CUDA
+        tensors of [rows, dim / 256 * block bytes] or flat), read inside the projection loop
+        (ts_qkv_append_gguf).  dim a multiple of 256."""
+        if x.dim() != 3 or x.shape[0] != self.n_seq:
+            raise ValueError("x must be [n_seq, n_tok, dim]")
+        n_tok, dim = x.shape[1], x.shape[2]
+        n_head = q_out.shape[2] if q_out is not None else None
+        from .weights import src_bytes
+        row_bytes = src_bytes(ggml_type, 1, dim)
+        if n_head is None:
+            n_head = wq.numel() // (row_bytes * self.head_dim)
+        kv_rows = self.n_head_kv * self.head_dim
+        for name, wt, rows in (("wq", wq, n_head * self.head_dim), ("wk", wk, kv_rows), ("wv", wv, kv_rows)):
+            if wt.dtype != torch.uint8 or wt.numel() != rows * row_bytes:
+                raise ValueError(f"{name} must hold {rows} rows of {row_bytes} GGUF bytes (uint8)")
+        want = (self.n_seq, n_tok, n_head, self.head_dim)
+        if q_out is None:
+            q_out = torch.empty(want, dtype=torch.float32, device=x.device)
+        elif tuple(q_out.shape) != want:
+            raise ValueError(f"q_out must be {want}")
+        kp = vp = None
+        if kv_out is not None:
+            k_out, v_out = kv_out
+            self._check_kv(k_out, v_out, n_tok)
+            kp, vp = _ptr(k_out, torch.float32, "k_out"), _ptr(v_out, torch.float32, "v_out")
+        ws = workspace
+        if ws is None:
+            key = ("qkv_gguf", ggml_type, dim, n_tok, n_head)
+            if key not in self._ws:
+                b = ctypes.c_uint64()
+                check("ts_qkv_gguf_workspace",
+                      load().ts_qkv_gguf_workspace(self._h, ggml_type, dim, n_tok, n_head, ctypes.byref(b)))
+                self._ws[key] = torch.empty(max(b.value, 16), dtype=torch.uint8, device=self.device)
+            ws = self._ws[key]
+        check("ts_qkv_append_gguf",
+              load().ts_qkv_append_gguf(self._h, layer, _ptr(x, torch.float32, "x"), dim, n_tok, ggml_type,
+                                        _ptr(wq, torch.uint8, "wq"), _ptr(wk, torch.uint8, "wk"),
+                                        _ptr(wv, torch.uint8, "wv"), n_head, rope.handle,
+                                        _ptr(q_out, torch.float32, "q_out"), kp, vp,
+                                        ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
+        return q_out
+
     @staticmethod
     def _out_like(q, out):
         """A caller's output tensor must have q's shape (the kernels write that many floats)."""
@@ -424,4 +470,33 @@ def attn_out_proj(attn: torch.Tensor, wo: torch.Tensor, act: torch.Tensor,
                                   _ptr(wo, torch.float16, "wo"), dim, _ptr(act, torch.float32, "act"),
                                   _ptr(stash, torch.float32, "stash") if stash is not None else None,
                                   ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
+    return act
+
+
+def attn_out_proj_gguf(attn: torch.Tensor, ggml_type: int, wo: torch.Tensor, dim: int, act: torch.Tensor,
+                       stash: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                       stream=None) -> torch.Tensor:
+    """attn_out_proj with wo as the GGUF blob's Q4_K / Q5_K blocks ([dim] rows of attn_dim / 256
+    blocks, uint8), read inside the projection loop (ts_attn_out_proj_gguf).  Returns act."""
+    from .weights import src_bytes
+    attn2 = attn.reshape(-1, attn.shape[-1])
+    n_tok, attn_dim = attn2.shape
+    if wo.dtype != torch.uint8 or wo.numel() != src_bytes(ggml_type, dim, attn_dim):
+        raise ValueError("wo must hold dim rows of attn_dim / 256 GGUF blocks (uint8)")
+    if act.numel() != n_tok * dim or (stash is not None and stash.numel() != n_tok * dim):
+        raise ValueError("act/stash must hold [n_tok, dim]")
+    ws = workspace
+    if ws is None:
+        key = ("gguf", ggml_type, attn.device.index, n_tok, attn_dim, dim)
+        if key not in _proj_ws:
+            b = ctypes.c_uint64()
+            check("ts_attn_out_proj_gguf_workspace",
+                  load().ts_attn_out_proj_gguf_workspace(ggml_type, n_tok, attn_dim, dim, ctypes.byref(b)))
+            _proj_ws[key] = torch.empty(max(b.value, 16), dtype=torch.uint8, device=attn.device)
+        ws = _proj_ws[key]
+    check("ts_attn_out_proj_gguf",
+          load().ts_attn_out_proj_gguf(_ptr(attn2, torch.float32, "attn"), n_tok, attn_dim, ggml_type,
+                                       _ptr(wo, torch.uint8, "wo"), dim, _ptr(act, torch.float32, "act"),
+                                       _ptr(stash, torch.float32, "stash") if stash is not None else None,
+                                       ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)))
     return act

@@ -455,6 +455,21 @@ def run_append(args, cfg):
     return ms, B * n_tok * n_kv * (2 * hd * 4 + hd + 8), B * n_tok
 
 
+KQ_BLOCK = {12: 144, 13: 176}  # bytes of one 256-element Q4_K / Q5_K super-block
+
+
+def kq_blob(gen, rows, cols, ggml_type, dev):
+    """Random Q4_K / Q5_K blocks of an [rows][cols] matrix on the device: random bytes with
+    finite f16 d and dmin of about 1e-4 (weights of about 1e-2)."""
+    import torch
+    nb = rows * cols // 256
+    bb = KQ_BLOCK[ggml_type]
+    b = torch.randint(0, 256, (nb, bb), generator=gen, device=dev, dtype=torch.uint8)
+    dd = (torch.rand((nb, 2), generator=gen, device=dev) * 3e-4 + 1e-4).half()
+    b[:, 0:4] = dd.view(torch.uint8).reshape(nb, 4)
+    return b.reshape(-1)
+
+
 def run_qkv(args, cfg):
     """The fused QKV projection + append (ts_qkv_append) of one step of the configuration:
     one token per sequence for the decode configurations, one 512-token chunk per sequence
@@ -470,7 +485,7 @@ def run_qkv(args, cfg):
                                    cfg["batch"], cfg["dim"])
     n_tok = cfg.get("chunk", 1)
     reps = 5 if n_tok == 1 else 2
-    max_seq = n_tok * (reps + 1) + 8
+    max_seq = n_tok * (reps + 3) + 8  # warmup, one untimed replay, reps replays
     rope = RopeTable(max_seq, hd, cfg["theta"])
     kv = KVCache.new_int4(L, n_kv, hd, max_seq, B)
     gen = torch.Generator(device=dev)
@@ -481,28 +496,50 @@ def run_qkv(args, cfg):
     def w(rows):
         return (torch.randn((rows, P * dim), generator=gen, device=dev) * 0.02).half()
 
-    ws = [(w(n_head * hd), w(n_kv * hd), w(n_kv * hd)) for _ in range(L)]
+    T = CONVERT_TYPES[args.gguf] if args.gguf else None
+    if T is not None:  # GGUF K-quant blocks read in the loop (ts_qkv_append_gguf)
+        ws = [tuple(kq_blob(gen, r, dim, T, dev) for r in (n_head * hd, n_kv * hd, n_kv * hd)) for _ in range(L)]
+        w_bytes_per = KQ_BLOCK[T] / 256
+    else:
+        ws = [(w(n_head * hd), w(n_kv * hd), w(n_kv * hd)) for _ in range(L)]
+        w_bytes_per = 2 * P
     x = torch.randn((B, n_tok, dim), generator=gen, device=dev)
     q = torch.empty((B, n_tok, n_head, hd), device=dev)
-    scratch = kv.qkv_workspace(dim, n_tok, n_head)
+    scratch = kv.qkv_workspace(dim, n_tok, n_head) if T is None else None
     if args.qk_norm:
         for layer in range(L):
             kv.set_qk_norm(layer, None, torch.randn(hd, generator=gen, device=dev) * 0.2 + 1.0)
+
+    def call(layer):
+        if T is not None:
+            kv.qkv_append_gguf(layer, x, T, *ws[layer], rope, q_out=q)
+        else:
+            kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch, planes=P)
+
     for layer in range(L):
-        kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch, planes=P)
+        call(layer)
     kv.increment(n_tok)
+    torch.cuda.synchronize()
+    # one step (every layer's call, then the length increment) captured as a graph and
+    # replayed, so the time is the kernels' and not the host's launch loop
+    gr = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(gr, stream=cap):
+        for layer in range(L):
+            call(layer)
+        kv.increment(n_tok)
+    gr.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
-        for layer in range(L):
-            kv.qkv_append(layer, x, *ws[layer], rope, q_out=q, workspace=scratch, planes=P)
-        kv.increment(n_tok)
+        gr.replay()
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / (reps * L)
     M, N = B * n_tok, (n_head + 2 * n_kv) * hd
-    byts = N * dim * 2 * P + M * dim * 4 + M * n_head * hd * 4 + M * n_kv * (hd + 8)
+    byts = int(N * dim * w_bytes_per) + M * dim * 4 + M * n_head * hd * 4 + M * n_kv * (hd + 8)
     return ms, byts, 2.0 * M * N * dim, M
 
 
@@ -566,23 +603,44 @@ def run_proj(args, cfg):
     M, K = B * cfg.get("chunk", 1), n_head * hd
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
+    from airframe_amd.kv_cache import attn_out_proj_gguf
     P = args.planes
-    ws = [(torch.randn((dim, P * K), generator=gen, device=dev) * 0.02).half() for _ in range(L)]
+    T = CONVERT_TYPES[args.gguf] if args.gguf else None
+    if T is not None:
+        ws = [kq_blob(gen, dim, K, T, dev) for _ in range(L)]
+        w_bytes = dim * K * KQ_BLOCK[T] // 256
+    else:
+        ws = [(torch.randn((dim, P * K), generator=gen, device=dev) * 0.02).half() for _ in range(L)]
+        w_bytes = dim * K * 2 * P
     a = torch.randn((M, K), generator=gen, device=dev)
     act = torch.randn((M, dim), generator=gen, device=dev)
+
+    def call(layer):
+        if T is not None:
+            attn_out_proj_gguf(a, T, ws[layer], dim, act)
+        else:
+            attn_out_proj(a, ws[layer], act, planes=P)
+
     for layer in range(L):
-        attn_out_proj(a, ws[layer], act, planes=P)
+        call(layer)
     torch.cuda.synchronize()
     reps = 5
+    gr = torch.cuda.CUDAGraph()  # every layer's call as one graph, replayed
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(gr, stream=cap):
+        for layer in range(L):
+            call(layer)
+    gr.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
-        for layer in range(L):
-            attn_out_proj(a, ws[layer], act, planes=P)
+        gr.replay()
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / (reps * L)
-    return ms, dim * K * 2 * P + M * K * 4 + M * dim * 8, 2.0 * M * dim * K, M
+    return ms, w_bytes + M * K * 4 + M * dim * 8, 2.0 * M * dim * K, M
 
 
 def run_compact(args, cfg):
@@ -730,6 +788,8 @@ def main():
                     help="time the attention output projection + residual (ts_attn_out_proj) instead")
     ap.add_argument("--planes", type=int, default=1, choices=(1, 2),
                     help="with --qkv/--proj: 2 = two-plane weights (F32 / GGUF formats, the _x2 entry points)")
+    ap.add_argument("--gguf", default=None, choices=("q4_k", "q5_k"),
+                    help="with --qkv/--proj: weights as GGUF K-quant blocks read in the loop (the _gguf entry points)")
     ap.add_argument("--convert", default=None, choices=sorted(CONVERT_TYPES),
                     help="time ts_weights_to_f16x2 on the configuration's Wq of that GGUF type")
     ap.add_argument("--compact", action="store_true",
@@ -793,8 +853,9 @@ def main():
         tfs = flops / (ms * 1e-3) / 1e12
         roof = ({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                  "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": byts,
-                 "counting": ("f16 weights (both planes with --planes 2) and f32 x read, f32 q, packed K/V rows and scales written"
-                              if args.qkv else "f16 weights (both planes with --planes 2) and f32 attention output read, residual read and written")}
+                 "counting": (("GGUF K-quant block bytes" if args.gguf else "f16 weights (both planes with --planes 2)")
+                              + (" and f32 x read, f32 q, packed K/V rows and scales written" if args.qkv
+                                 else " and f32 attention output read, residual read and written"))}
                 if decode else
                 {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                  "unit": "TFLOP/s", "frac": round(tfs / MFMA_F16_PEAK_TFLOPS, 4),
@@ -806,9 +867,12 @@ def main():
             "n_gpus": 1, "higher_is_better": True, "us_per_call": round(ms * 1e3, 2),
             "tokens_per_s": round(toks / (ms * 1e-3), 1),
             "config": {"workload": cfg["name"] + ("_qkv" if args.qkv else "_oproj") + ("_qknorm" if args.qk_norm else "")
-                       + ("_x2" if args.planes == 2 else ""),
+                       + ("_x2" if args.planes == 2 and not args.gguf else "")
+                       + (f"_{args.gguf}_in_loop" if args.gguf else ""),
                        "tokens_per_call": toks, "dim": cfg["dim"]},
-            "roofline": roof, "data": "synthetic (random f16 weights, N(0,1) x)"}), flush=True)
+            "roofline": roof,
+            "data": ("synthetic (random GGUF blocks, f16 d/dmin ~1e-4, N(0,1) x)" if args.gguf
+                     else "synthetic (random f16 weights, N(0,1) x)")}), flush=True)
         return
     if args.stream_ceiling:
         if "ctx" not in cfg or "ragged" in cfg:

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from airframe_amd import weights
-from airframe_amd.kv_cache import attn_out_proj
+from airframe_amd.kv_cache import attn_out_proj, attn_out_proj_gguf
 from oracle import oracle
 from tests.gpu_util import Pair, assert_close, dev, say
 
@@ -127,3 +127,75 @@ def test_attn_out_proj_with_block_weights(gpu, fmt, n_tok, attn_dim, dim):
     dot = oracle.project_f32(a, wf)
     assert_close(stash.cpu().numpy(), dot, "projection (block weights)")
     assert_close(act_d.cpu().numpy(), act + dot, "residual + projection (block weights)")
+
+
+@pytest.mark.parametrize("fmt,n_seq,n_tok,dim,hd", [
+    (weights.Q4_K, 8, 1, 4096, 128),   # decode rows: the reduction split over workgroups
+    (weights.Q5_K, 32, 1, 2048, 128),  # a full 32-row decode tile
+    (weights.Q4_K, 3, 70, 1024, 128),  # block rows (prefill chunk)
+    (weights.Q5_K, 2, 1, 512, 64),     # head dim 64
+    (weights.Q4_K, 4, 1, 768, 96),     # head dim 96: three projections, then the append
+])
+def test_qkv_append_gguf_blocks_in_loop(gpu, fmt, n_seq, n_tok, dim, hd):
+    """ts_qkv_append_gguf: Q4_K / Q5_K blocks read inside the projection loop, against the dot
+    over the oracle's exact dequantized f32 weights (q4_k.rs / q5_k.rs, pinned in
+    test_oracle_weights.py), and the appended codes bit-exact with the quantizer applied to
+    those projections."""
+    say(f"qkv_append_gguf fmt={fmt} n_seq={n_seq} n_tok={n_tok} dim={dim} hd={hd}")
+    rng = np.random.default_rng(7 * fmt + dim + hd)
+    n_head, n_kv = 8, 2
+    p = Pair(n_seq, n_kv, hd, 128, 500000.0)
+    rows = (n_head * hd, n_kv * hd, n_kv * hd)
+    blobs = [random_blob(rng, fmt, r, dim) for r in rows]
+    wf = [oracle.dequant(fmt, b, r * dim).reshape(r, dim) for b, r in zip(blobs, rows)]
+    x = rng.standard_normal((n_seq, n_tok, dim)).astype(np.float32)
+    k_out = torch.empty((n_seq, n_tok, n_kv, hd), dtype=torch.float32, device="cuda")
+    v_out = torch.empty_like(k_out)
+    q = p.gpu.qkv_append_gguf(0, dev(x), fmt, dev(blobs[0]), dev(blobs[1]), dev(blobs[2]), p.rope,
+                              kv_out=(k_out, v_out))
+    torch.cuda.synchronize()
+    q, k_out, v_out = q.cpu().numpy(), k_out.cpu().numpy(), v_out.cpu().numpy()
+    xf = x.reshape(-1, dim)
+    assert_close(q.reshape(n_seq * n_tok, -1), oracle.project_f32(xf, wf[0]), "q (blocks in loop)")
+    assert_close(k_out.reshape(n_seq * n_tok, -1), oracle.project_f32(xf, wf[1]), "k (blocks in loop)")
+    assert_close(v_out.reshape(n_seq * n_tok, -1), oracle.project_f32(xf, wf[2]), "v (blocks in loop)")
+    p.ora.append(k_out, v_out)
+    p.advance(n_tok)
+    p.check_codes()
+
+
+@pytest.mark.parametrize("fmt,n_tok,attn_dim,dim", [
+    (weights.Q4_K, 5, 2048, 2048),    # decode: the reduction split
+    (weights.Q5_K, 130, 1024, 768),   # prefill rows, still split
+    (weights.Q4_K, 1100, 512, 2304),  # many tiles: one slice over all of attn_dim
+])
+def test_attn_out_proj_gguf_blocks_in_loop(gpu, fmt, n_tok, attn_dim, dim):
+    """ts_attn_out_proj_gguf against the oracle's f32-weight dot and the residual add."""
+    say(f"attn_out_proj_gguf fmt={fmt} n_tok={n_tok} attn_dim={attn_dim} dim={dim}")
+    rng = np.random.default_rng(fmt + n_tok + 1)
+    blob = random_blob(rng, fmt, dim, attn_dim)
+    wf = oracle.dequant(fmt, blob, dim * attn_dim).reshape(dim, attn_dim)
+    a = rng.standard_normal((n_tok, attn_dim)).astype(np.float32)
+    act = rng.standard_normal((n_tok, dim)).astype(np.float32) * 4
+    act_d = dev(act)
+    stash = torch.zeros((n_tok, dim), dtype=torch.float32, device="cuda")
+    attn_out_proj_gguf(dev(a), fmt, dev(blob), dim, act_d, stash=stash)
+    torch.cuda.synchronize()
+    dot = oracle.project_f32(a, wf)
+    assert_close(stash.cpu().numpy(), dot, "projection (blocks in loop)")
+    assert_close(act_d.cpu().numpy(), act + dot, "residual + projection (blocks in loop)")
+
+
+def test_gguf_in_loop_refusals(gpu):
+    """Types other than Q4_K / Q5_K and dims that are not whole super-blocks are refused."""
+    say("gguf in-loop refusals")
+    from airframe_amd import TsError
+    p = Pair(1, 2, 128, 16, 500000.0)
+    x = torch.zeros((1, 1, 512), device="cuda")
+    blob6 = dev(np.zeros(weights.src_bytes(weights.Q6_K, 8 * 128, 512), np.uint8))
+    kvb = dev(np.zeros(weights.src_bytes(weights.Q6_K, 2 * 128, 512), np.uint8))
+    with pytest.raises(TsError):
+        p.gpu.qkv_append_gguf(0, x, weights.Q6_K, blob6, kvb, kvb, p.rope)
+    with pytest.raises(TsError):  # 320 inputs: not a whole number of 256-element blocks
+        attn_out_proj_gguf(torch.zeros((1, 320), device="cuda"), weights.Q4_K,
+                           dev(np.zeros(16, np.uint8)), 256, torch.zeros((1, 256), device="cuda"))
