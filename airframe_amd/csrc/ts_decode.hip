@@ -958,15 +958,17 @@ __device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8
 }
 
 // NW waves per workgroup, D windows in registers per wave (D - 1 in flight while one is
-// computed).  The plan places one workgroup of 4 waves per CU (one wave
-// per SIMD).
-template <int HD, bool SOFTCAP, bool NORM, int NW, int D>
+// computed).  The plan places one workgroup of 4 waves per CU (one wave per SIMD).
+// PAD: the caller's head dim hdr is below the stored HD (rows of q, new K/V and the output are
+// hdr floats; the stored dims past them hold code 8 = 0, so the integer QK^T and PV run
+// unchanged over the whole stored row).
+template <int HD, bool SOFTCAP, bool NORM, bool PAD, int NW, int D>
 __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeArgs a) {
     constexpr int NTD = HD / 16;
     constexpr int NM = HD / 64;  // i8 instructions per 16-position tile
     constexpr int OST = HD + 1;
     const KvLayerView &L = a.L;
-    constexpr int hdr = HD;  // (padded head dims take the 16x16 kernel)
+    const int hdr = PAD ? L.hdr : HD;
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
     // grid (kv head, sequence, split): every sequence's split 0 is dispatched before any
     // split 1, so the splits that wait for a free CU are the last ones of the longest
@@ -1265,12 +1267,12 @@ int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
 }
 }  // namespace
 
-DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, bool padded) {
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu) {
     DecodePlan p;
     int max_ctx = 1;
     for (int s = 0; s < n_seq; s++) max_ctx = std::max(max_ctx, (int)n_ctx[s]);
     p.g4 = false;
-    if (G <= 4 && !padded) {
+    if (G <= 4) {
         // Target 7/8 of the CUs, not all of them: a plan that fills every CU of a ragged
         // batch had ~24 busy workgroups wait 9-20 us for a CU (behind busy ones) while idle
         // splits freed others -- the dispatcher does not place a workgroup on just any free
@@ -1324,24 +1326,16 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     constexpr size_t kOnePerCuLds = 64 * 1024;
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
     const bool pad = L.hdr != L.hd;
-    if (pad && plan.g4) return hipErrorInvalidValue;  // decode_plan keeps padded heads off it
 #define TS_SPLIT(HDV, SC, NM)                                                                  \
-    (plan.g4 ? (decode_split4_kernel<HDV, SC, NM, 4, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0) \
+    (plan.g4 ? (pad ? (decode_split4_kernel<HDV, SC, NM, true, 4, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0) \
+                    : (decode_split4_kernel<HDV, SC, NM, false, 4, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0)) \
              : pad ? (decode_split_kernel<HDV, SC, NM, true><<<grid, 64 * kNW16, 0, st>>>(a), 0)         \
                    : (decode_split_kernel<HDV, SC, NM, false><<<grid, 64 * kNW16, 0, st>>>(a), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \
     (cap ? (norm ? TS_SPLIT(HDV, true, true) : TS_SPLIT(HDV, true, false))                    \
          : (norm ? TS_SPLIT(HDV, false, true) : TS_SPLIT(HDV, false, false)))
     if (L.hd == 256) {
-        // (the G <= 4 kernel is not built for 256-dim rows: decode_plan keeps them off it)
-        if (plan.g4) return hipErrorInvalidValue;
-        if (cap) {
-            if (norm) { if (pad) decode_split_kernel<256, true, true, true><<<grid, 64 * kNW16, 0, st>>>(a); else decode_split_kernel<256, true, true, false><<<grid, 64 * kNW16, 0, st>>>(a); }
-            else { if (pad) decode_split_kernel<256, true, false, true><<<grid, 64 * kNW16, 0, st>>>(a); else decode_split_kernel<256, true, false, false><<<grid, 64 * kNW16, 0, st>>>(a); }
-        } else {
-            if (norm) { if (pad) decode_split_kernel<256, false, true, true><<<grid, 64 * kNW16, 0, st>>>(a); else decode_split_kernel<256, false, true, false><<<grid, 64 * kNW16, 0, st>>>(a); }
-            else { if (pad) decode_split_kernel<256, false, false, true><<<grid, 64 * kNW16, 0, st>>>(a); else decode_split_kernel<256, false, false, false><<<grid, 64 * kNW16, 0, st>>>(a); }
-        }
+        TS_SPLIT_HD(256);
         if (plan.n_split > 1) decode_combine_kernel<256><<<dim3(n_head, L.S), 256, 0, st>>>(a);
     } else if (L.hd == 128) {
         TS_SPLIT_HD(128);

@@ -147,12 +147,10 @@ hipError_t launch_shift_move(const KvLayerView &L, int seq, int keep, int shift,
 struct DecodePlan {
     int chunk;    // positions per split (multiple of 64)
     int n_split;  // splits of the longest sequence (grid.x)
-    bool g4;      // the G <= 4 (4x4x4 QK) kernel
+    bool g4;      // the G <= 4 kernel (integer QK^T on v_mfma_i32_16x16x64_i8)
 };
 // n_ctx: keys per sequence (len + 1), on the host; n_cu: compute units of the device.
-// padded: the head dim is stored padded, or is 256 (the G <= 4 kernel takes only unpadded
-// rows of 64 or 128 dims).
-DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, bool padded = false);
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu);
 // Upper bound of plan.n_split for any lengths up to max_seq (sizes the workspace).
 int decode_cap(int n_kv, int max_seq, int n_cu);
 hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,

@@ -769,6 +769,9 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--head-dim", type=int, default=None,
+                    help="decode configurations: another head dim (e.g. 256, Gemma-2's), the workload renamed")
+    ap.add_argument("--n-head", type=int, default=None, help="decode configurations: another query head count")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--separate", action="store_true",
@@ -806,7 +809,13 @@ def main():
                           "by sequence or kv head with no exchange, but "
                           "multi-GPU runs are not part of it", "n_gpus": args.gpus}))
         sys.exit(2)
-    cfg = CONFIGS[args.config]
+    cfg = dict(CONFIGS[args.config])
+    if args.head_dim or args.n_head:
+        if "ctx" not in cfg:
+            sys.exit("--head-dim / --n-head need a decode configuration (1-4)")
+        cfg["hd"] = args.head_dim or cfg["hd"]
+        cfg["n_head"] = args.n_head or cfg["n_head"]
+        cfg["name"] += f"_hd{cfg['hd']}_h{cfg['n_head']}"
     if args.steps is None:
         args.steps = cfg.get("steps", 3) if args.config != 5 else 3
 

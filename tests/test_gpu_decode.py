@@ -246,6 +246,22 @@ def test_config2_batch1_long_context(gpu):
         p.advance(1)
 
 
+@pytest.mark.parametrize("hd,n_kv,n_head,n_seq,ctx,fused", [
+    (256, 8, 16, 4, 8192, True),    # Gemma-2-9B's attention shape: 256-dim rows, 2 q heads per kv head
+    (256, 4, 16, 4, 16000, False),  # 4 q heads per kv head, no append
+    (96, 8, 32, 4, 8000, True),     # padded: stored as 128 dims
+    (200, 4, 16, 8, 8192, True),    # padded: stored as 256 dims
+])
+def test_integer_kernel_wide_and_padded_rows(gpu, hd, n_kv, n_head, n_seq, ctx, fused):
+    """The G <= 4 integer-QK kernel on 256-dim and padded rows, at contexts whose plan gives
+    every wave >= 4 windows (so this kernel runs): every head against the oracle, the whole
+    cache bit-exact."""
+    say(f"decode integer kernel hd={hd} G={n_head // n_kv} ctx={ctx} fused={fused}")
+    rng = np.random.default_rng(hd + ctx)
+    lens = [int(x) for x in rng.integers(ctx - 300, ctx, size=n_seq)]
+    _full_size(n_seq, n_kv, n_head, hd, lens, 10000.0, hd + n_head, False, fused=fused)
+
+
 def test_misaligned_buffers_rejected(gpu):
     """Device arrays must be 16-byte aligned: a misaligned workspace, q or out is refused
     before anything is launched."""
