@@ -78,6 +78,68 @@ __global__ __launch_bounds__(256, 1) void probe_decode_loads_kernel(ProbeArgs a)
     if (acc == 0x9E3779B9u) a.sink[0] = acc;  // keeps the loads; practically never taken
 }
 
+// The same reads handed out dynamically: units of UW windows of one stream (unit u: chunk u /
+// rows of stream u % rows) claimed one at a time from a device counter by a persistent grid,
+// the next claim issued while the current unit streams.  Measures what a launch-wide work
+// queue costs against the static placement above (no per-workgroup start offset is possible:
+// all workgroups start at unit 0, 1, 2, ...).
+template <int HD>
+__global__ __launch_bounds__(256, 1) void probe_claim_loads_kernel(ProbeArgs a, int rows, int uw, int *ctr) {
+    constexpr int NW = 4, ROWB = HD / 2, NKW = HD / 8, NTD = HD / 16, NL = NKW / 4 + NTD / 2 + 2;
+    __shared__ int cl[2];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwin = a.n_ctx / 64, nunits = (nwin / uw) * rows;
+    if (threadIdx.x == 0) cl[0] = atomicAdd(ctr, 1);
+    __syncthreads();
+    int u = cl[0], par = 1;
+    uint32_t acc = 0;
+    while (u < nunits) {  // every workgroup leaves once a claim passes the last unit
+        if (threadIdx.x == 0) cl[par] = atomicAdd(ctr, 1);
+        const int c = u / rows, row = u % rows;
+        const uint32_t wend = (uint32_t)a.n_ctx;
+        const auto rk = rsrc(a.kp + (size_t)row * a.P * ROWB, wend * ROWB);
+        const auto rv = rsrc(a.vp + (size_t)row * (a.P / 32) * (HD * 16), wend / 32 * (HD * 16));
+        const auto rs = rsrc(a.ks + (size_t)row * a.P, wend * 4);
+        const auto rt = rsrc(a.vs + (size_t)row * a.P, wend * 4);
+        const int cnt = uw / NW;
+        u32x4 buf[2][NL];
+        auto load = [&](u32x4 *w, int base) {
+#pragma unroll
+            for (int j = 0; j < NKW / 4; j++) w[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16 + j * 1024, base * ROWB, kNT);
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+#pragma unroll
+                for (int q = 0; q < NTD / 4; q++)
+                    w[NKW / 4 + b * (NTD / 4) + q] =
+                        __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16 + q * 1024 + b * (HD * 16), (base / 32) * (HD * 16), kNT);
+            w[NKW / 4 + NTD / 2] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane & 15) * 16, base * 4, kNT);
+            w[NKW / 4 + NTD / 2 + 1] = __builtin_amdgcn_raw_buffer_load_b128(rt, (lane & 15) * 16, base * 4, kNT);
+        };
+        load(buf[0], 64 * (c * uw + wave));
+        for (int it = 0; it < cnt; it += 2) {
+#pragma unroll
+            for (int d = 0; d < 2; d++) {
+                load(buf[d ^ 1], it + d + 1 < cnt ? 64 * (c * uw + wave + NW * (it + d + 1)) : a.n_ctx);
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+                if (it + d < cnt) {
+#pragma unroll
+                    for (int j = 0; j < NL; j++) acc ^= buf[d][j].x ^ buf[d][j].y ^ buf[d][j].z ^ buf[d][j].w;
+                }
+            }
+        }
+        __syncthreads();
+        u = cl[par];
+        par ^= 1;
+        __syncthreads();
+    }
+    if (acc == 0x9E3779B9u) a.sink[0] = acc;
+}
+
+__global__ __launch_bounds__(256) void probe_empty_kernel(uint32_t *sink) {
+    if (threadIdx.x == 1000) sink[0] = 1;  // never: the launch itself is what is timed
+}
+
 template <int UN>
 __global__ __launch_bounds__(256) void probe_flat_read_kernel(const u32x4 *__restrict__ p, size_t n, uint32_t *sink) {
     uint32_t acc = 0;
@@ -121,5 +183,26 @@ extern "C" int ts_probe_decode_loads(const void *kp, const void *vp, const void 
 // One grid-strided read of n16 16-byte elements.
 extern "C" int ts_probe_flat_read(const void *p, size_t n16, int grid, void *sink, void *stream) {
     probe_flat_read_kernel<4><<<grid, 256, 0, (hipStream_t)stream>>>((const u32x4 *)p, n16, (uint32_t *)sink);
+    return (int)hipGetLastError();
+}
+
+// The decode reads as units of uw windows (uw a multiple of 8 dividing n_ctx / 64) claimed from
+// *counter (zeroed by the caller before each launch) by n_wg persistent workgroups.
+extern "C" int ts_probe_claim_loads(const void *kp, const void *vp, const void *ks, const void *vs,
+                                    int n_seq, int n_kv, int hd, int P, int n_ctx, int uw, int n_wg,
+                                    int *counter, void *sink, void *stream) {
+    if (hd != 128 || P % 64 || n_ctx > P || n_ctx % 64 || uw <= 0 || uw % 8 || (n_ctx / 64) % uw || n_wg <= 0 || !counter)
+        return (int)hipErrorInvalidValue;
+    ProbeArgs a{(const uint8_t *)kp, (const uint8_t *)vp, (const float *)ks, (const float *)vs, P, n_ctx,
+                (uint32_t *)sink};
+    const size_t lds = 96 * 1024;
+    hipFuncSetAttribute((const void *)probe_claim_loads_kernel<128>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    probe_claim_loads_kernel<128><<<n_wg, 256, lds, (hipStream_t)stream>>>(a, n_seq * n_kv, uw, counter);
+    return (int)hipGetLastError();
+}
+
+// An empty launch of `grid` workgroups (the per-launch cost of a kernel in a graph).
+extern "C" int ts_probe_empty(int grid, void *sink, void *stream) {
+    probe_empty_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((uint32_t *)sink);
     return (int)hipGetLastError();
 }

@@ -737,7 +737,38 @@ def run_stream_ceiling(args, cfg):
     n = max(args.steps, 20)
     us_dec = timed(dec, n)
     us_flat = timed(flat_read, n)
-    return dict(bytes=nbytes, us_decode_pattern=us_dec, us_flat=us_flat, launches=n)
+    res = dict(bytes=nbytes, us_decode_pattern=us_dec, us_flat=us_flat, launches=n)
+
+    # the same reads as 16-window units claimed from a launch-wide counter (a work queue)
+    nw = ctx // 64 // 16 * 16
+    if nw >= 16:
+        ctr = torch.zeros(n + 8, dtype=torch.int32, device="cuda")  # one zeroed counter per launch
+        used = [0]
+
+        def claimed(i):
+            kp, vp, ks, vs = sets[i % n_sets]
+            slot = used[0]
+            used[0] += 1
+            rc = lib.ts_probe_claim_loads(ctypes.c_void_p(kp.data_ptr()), ctypes.c_void_p(vp.data_ptr()),
+                                          ctypes.c_void_p(ks.data_ptr()), ctypes.c_void_p(vs.data_ptr()),
+                                          B, H, hd, P, 64 * nw, 16, 256,
+                                          ctypes.c_void_p(ctr.data_ptr() + 4 * slot),
+                                          ctypes.c_void_p(sink.data_ptr()), st)
+            assert rc == 0, rc
+
+        ctr.zero_()
+        res["us_claimed_units"] = timed(claimed, n) * ctx / (64 * nw)  # scaled to the same bytes
+    # the per-launch cost of a kernel in a graph: 36 empty 256-workgroup launches, replayed
+    gr = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(gr, stream=cap):
+        for _ in range(36):
+            lib.ts_probe_empty(256, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(cap.cuda_stream))
+    gr.replay()
+    torch.cuda.synchronize()
+    res["us_empty_launch_in_graph"] = timed(lambda i: gr.replay(), 20) / 36
+    return res
 
 
 def _split_kernel_name(cfg, n_cu=256):
@@ -895,6 +926,8 @@ def main():
             "us_per_launch": round(r["us_decode_pattern"], 2), "frac": round(g_dec / HBM_PEAK_GBS, 4),
             "flat_read": {"GBps": round(g_flat, 1), "us_per_launch": round(r["us_flat"], 2),
                           "frac": round(g_flat / HBM_PEAK_GBS, 4)},
+            "claimed_units_us_per_launch": round(r["us_claimed_units"], 2) if "us_claimed_units" in r else None,
+            "empty_launch_in_graph_us": round(r["us_empty_launch_in_graph"], 2),
             "bytes_per_launch": r["bytes"], "launches": r["launches"],
             "config": {"workload": cfg["name"] + "_loads_only"}, "data": "uninitialised device buffers"}),
             flush=True)
