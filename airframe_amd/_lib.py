@@ -63,6 +63,8 @@ SIGNATURES = {
     "ts_attn_decode": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _f, _vp, _vp, ctypes.c_uint64, _vp]),
     "ts_attn_decode_append": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i32, _vp, _f, _vp, _vp,
                                              ctypes.c_uint64, _vp]),
+    "ts_attn_decode_append_advance": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i32, _vp, _f, _vp, _vp,
+                                             ctypes.c_uint64, _vp]),
     "ts_attn_decode_append_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i32, _vp, _f, _vp, _vp]),
     "ts_attn_prefill": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _vp, _f, _vp, _vp]),
     "ts_qkv_workspace": (ctypes.c_int, [_vp, _i32, _i32, _i32, _u64p]),

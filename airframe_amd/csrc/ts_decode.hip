@@ -59,7 +59,28 @@ struct DecodeArgs {
 
     // Fused append (ts_attn_decode_append): the new token's raw K and V, [S][H][hd], or null.
     const float *k_new, *v_new;
+
+    // ts_attn_decode_append_advance: the lengths to advance by one (the array len points to)
+    // and the arrival counter of the kernel that does it, or null.
+    int32_t *adv_len;
+    int32_t *adv_ctr;
 };
+
+// Every workgroup of the launch's last kernel calls this once, after its last read of the
+// lengths: the workgroup that arrives last (all others have read them by then) advances every
+// length by one and clears the counter for the next launch.  Call from all threads of the
+// workgroup (the barrier orders this workgroup's length reads before its arrival).
+__device__ inline void arrive_and_advance(const DecodeArgs &a) {
+    if (!a.adv_ctr) return;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int n_wg = gridDim.x * gridDim.y * gridDim.z;
+        if (atomicAdd(a.adv_ctr, 1) == n_wg - 1) {
+            for (int s = 0; s < a.L.S; s++) a.adv_len[s] += 1;
+            *a.adv_ctr = 0;
+        }
+    }
+}
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -666,19 +687,13 @@ __global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_ker
     }
 }
 
-// Log-sum-exp merge of the splits of one (sequence, head).  256 threads: HD/4 threads (one
-// float4 of dims each) per split row, 1024/HD row groups striding over the splits, then an
-// LDS reduction over the groups, so the dependent-load chain is ns/groups long, not ns.
+// The merge of one (sequence, head) over its ns > 1 splits (body of decode_combine_kernel).
 template <int HD>
-__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+__device__ __forceinline__ void combine_rows(const DecodeArgs &a, int head, int s, int ns, int tid) {
     constexpr int V4 = HD / 4, NG = 256 / V4;
     __shared__ float4 part[NG][V4];
     __shared__ float lpart[NG];
     __shared__ float wmax[4];
-    const int head = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
-    const int n_ctx = a.len[s] + 1;
-    const int ns = min((n_ctx + a.chunk - 1) / a.chunk, a.n_split);
-    if (ns <= 1) return;
     const size_t hidx = (size_t)s * a.n_head + head;
     const float *ml = a.ws + (size_t)a.L.S * a.n_head * a.n_split * HD;
     const float *mm = ml + hidx * a.n_split;
@@ -760,6 +775,19 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
         o[3] = r.w * inv;
     }
 }
+
+// Log-sum-exp merge of the splits of one (sequence, head).  256 threads: HD/4 threads (one
+// float4 of dims each) per split row, 1024/HD row groups striding over the splits, then an
+// LDS reduction over the groups, so the dependent-load chain is ns/groups long, not ns.
+template <int HD>
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+    const int head = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+    const int n_ctx = a.len[s] + 1;
+    const int ns = min((n_ctx + a.chunk - 1) / a.chunk, a.n_split);
+    if (ns > 1) combine_rows<HD>(a, head, s, ns, tid);
+    arrive_and_advance(a);
+}
+
 
 
 // ---- G <= 4: QK^T on v_mfma_i32_16x16x64_i8 ---------------------------------------------------
@@ -1294,10 +1322,10 @@ int decode_cap(int n_kv, int max_seq, int n_cu) {
     return std::min((max_seq + 63) / 64, 2 * n_cu / n_kv + 2);
 }
 
-hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
+hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,
-                         const float *v_new, hipStream_t st) {
+                         const float *v_new, int32_t *adv, hipStream_t st) {
     DecodeArgs a;
     a.L = L;
     a.len = d_len;
@@ -1316,6 +1344,10 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     a.ws = ws;
     a.k_new = k_new;
     a.v_new = v_new;
+    // with a split the combine kernel advances the lengths (the last of its workgroups to
+    // arrive); without one a length update follows the decode launch
+    a.adv_len = adv && plan.n_split > 1 ? d_len : nullptr;
+    a.adv_ctr = adv && plan.n_split > 1 ? adv : nullptr;
     dim3 grid(plan.n_split, L.H * a.NG, L.S);
     // The G <= 4 kernel does less VALU work per window than the 16x16 one but has the longer
     // per-window dependency chain; it runs when every wave streams at least 4 windows of its
@@ -1348,6 +1380,11 @@ hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float
     }
 #undef TS_SPLIT_HD
 #undef TS_SPLIT
+    if (adv && plan.n_split <= 1) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_len_update(d_len, L.S, -1, 1, 0, st);
+    }
     return hipGetLastError();
 }
 

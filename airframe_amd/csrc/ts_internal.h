@@ -87,8 +87,10 @@ struct ts_kv {
     uint64_t layer_bytes;
     uint8_t *base;            // one allocation for all layers
     int32_t *d_len;           // device mirror of lengths [n_seq], then window bases [n_seq]
-                              // and sink counts [n_seq] (d_rot, d_sink)
+                              // and sink counts [n_seq] (d_rot, d_sink), then d_adv
     int32_t *d_rot, *d_sink;
+    int32_t *d_adv;           // arrival counter of a decode launch that advances the lengths
+                              // (zero between launches)
     std::vector<int32_t> h_len, h_rot, h_sink;
     std::vector<const float *> q_norm, k_norm;  // per layer, device pointers or null
     std::vector<float> norm_eps;
@@ -153,10 +155,13 @@ struct DecodePlan {
 DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu);
 // Upper bound of plan.n_split for any lengths up to max_seq (sizes the workspace).
 int decode_cap(int n_kv, int max_seq, int n_cu);
-hipError_t launch_decode(const KvLayerView &L, const int32_t *d_len, const float *q, int n_head,
+// adv: null, or the cache's arrival counter: the launch then also advances every length by
+// one once all of its workgroups have read them (plans with a split: in the combine kernel;
+// without: a length-update launch after the decode).
+hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,
-                         const float *v_new, hipStream_t st);
+                         const float *v_new, int32_t *adv, hipStream_t st);
 hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const float *q,
                           int n_head, int n_tok, const float *rope, int rope_pairs,
                           float softcap, float *out, hipStream_t st);

@@ -195,14 +195,15 @@ int ts_kv_create(const ts_kv_desc *desc, ts_kv **out) {
         delete kv;
         return TS_ERR_NOMEM;
     }
-    if (hipMalloc(&kv->d_len, sizeof(int32_t) * 3 * desc->n_seq) != hipSuccess) {
+    const size_t len_ints = 3 * (size_t)desc->n_seq + 4;  // lengths, bases, sinks, arrival counter
+    if (hipMalloc(&kv->d_len, sizeof(int32_t) * len_ints) != hipSuccess) {
         hipFree(kv->base);
         delete kv;
         return TS_ERR_NOMEM;
     }
     // Zero fill once at creation: unwritten positions then dequantize to finite values.
     if (hipMemset(kv->base, 0, total) != hipSuccess ||
-        hipMemset(kv->d_len, 0, sizeof(int32_t) * 3 * desc->n_seq) != hipSuccess ||
+        hipMemset(kv->d_len, 0, sizeof(int32_t) * len_ints) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         hipFree(kv->base);
         hipFree(kv->d_len);
@@ -211,6 +212,7 @@ int ts_kv_create(const ts_kv_desc *desc, ts_kv **out) {
     }
     kv->d_rot = kv->d_len + desc->n_seq;
     kv->d_sink = kv->d_len + 2 * desc->n_seq;
+    kv->d_adv = kv->d_len + 3 * desc->n_seq;
     *out = kv;
     return TS_OK;
 }
@@ -444,7 +446,7 @@ int ts_attn_decode_workspace(const ts_kv *kv, int32_t n_head, uint64_t *bytes) {
 static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
                        const ts_rope *rope, float softcap, float *d_out, void *d_workspace,
                        uint64_t workspace_bytes, const float *k_new, const float *v_new,
-                       void *stream, bool noalloc = false) {
+                       void *stream, bool noalloc = false, bool advance = false) {
     if (!kv || layer < 0 || layer >= kv->d.n_layers || !d_q || !d_out || !heads_ok(kv, n_head) ||
         !(softcap >= 0.0f) || !aligned16(d_q) || !aligned16(d_out))
         return TS_ERR_INVALID;
@@ -465,9 +467,13 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
         if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
         if (!aligned16(d_workspace)) return TS_ERR_INVALID;
     }
-    return hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
-                                        rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
-                                        plan, k_new, v_new, as_stream(stream)));
+    const int rc2 = hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
+                                                 rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
+                                                 plan, k_new, v_new, advance ? kv->d_adv : nullptr,
+                                                 as_stream(stream)));
+    if (rc2 == TS_OK && advance)
+        for (auto &l : const_cast<ts_kv *>(kv)->h_len) l += 1;
+    return rc2;
 }
 
 int ts_attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_head,
@@ -483,6 +489,14 @@ int ts_attn_decode_append(ts_kv *kv, int32_t layer, const float *d_k, const floa
     if (!d_k || !d_v || !aligned16(d_k) || !aligned16(d_v)) return TS_ERR_INVALID;
     return attn_decode(kv, layer, d_q, n_head, rope, softcap, d_out, d_workspace, workspace_bytes,
                        d_k, d_v, stream);
+}
+
+int ts_attn_decode_append_advance(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
+                                  const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
+                                  float *d_out, void *d_workspace, uint64_t workspace_bytes, void *stream) {
+    if (!d_k || !d_v || !aligned16(d_k) || !aligned16(d_v)) return TS_ERR_INVALID;
+    return attn_decode(kv, layer, d_q, n_head, rope, softcap, d_out, d_workspace, workspace_bytes,
+                       d_k, d_v, stream, false, true);
 }
 
 // ---- allocation-free decode ----------------------------------------------------------------

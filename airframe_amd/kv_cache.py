@@ -239,10 +239,12 @@ class KVCache:
 
     def attn_decode_append(self, layer: int, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
                            rope: RopeTable, out: torch.Tensor = None, softcap: float = 0.0,
-                           workspace: torch.Tensor = None, stream=None):
+                           workspace: torch.Tensor = None, stream=None, advance: bool = False):
         """append_quant(layer, k, v) + attn_decode(layer, q) in one launch (the quantize_kv +
         main_attn_out_int4 pair of run_layer_with_cache_int4).  k, v: [n_seq, 1, n_head_kv,
-        head_dim] or [n_seq, n_head_kv, head_dim]; q: [n_seq, n_head, head_dim]."""
+        head_dim] or [n_seq, n_head_kv, head_dim]; q: [n_seq, n_head, head_dim].
+        advance=True (the step's last layer): every length then advances by one, as
+        increment(1) would, inside the same launch (ts_attn_decode_append_advance)."""
         n_head = q.shape[1]
         if q.dim() != 3 or q.shape[0] != self.n_seq or q.shape[2] != self.head_dim:
             raise ValueError("q must be [n_seq, n_head, head_dim]")
@@ -250,8 +252,9 @@ class KVCache:
                        v.reshape(self.n_seq, 1, self.n_head_kv, self.head_dim), 1)
         out = self._out_like(q, out)
         ws = workspace if workspace is not None else self.workspace(n_head)
-        check("ts_attn_decode_append",
-              load().ts_attn_decode_append(self._h, layer, _ptr(k, torch.float32, "k"),
+        fn = "ts_attn_decode_append_advance" if advance else "ts_attn_decode_append"
+        check(fn,
+              getattr(load(), fn)(self._h, layer, _ptr(k, torch.float32, "k"),
                                            _ptr(v, torch.float32, "v"), _ptr(q, torch.float32, "q"),
                                            n_head, rope.handle, softcap,
                                            _ptr(out, torch.float32, "out"),

@@ -209,6 +209,8 @@ def run_decode(args, cfg):
     ws = kv.workspace(n_head)
     torch.cuda.synchronize()
 
+    fold = args.fold and not args.separate
+
     def step(i, events=None):
         for layer in range(L):
             if args.separate:
@@ -217,12 +219,14 @@ def run_decode(args, cfg):
                 events[layer][0].record()
             if args.separate:
                 kv.attn_decode(layer, qs[i][layer], rope, out=out, workspace=ws)
-            else:  # quantize_kv + main_attn_out_int4 in one launch
+            else:  # quantize_kv + main_attn_out_int4 in one launch; the last layer's launch
+                # also advances the lengths (cache.increment()) unless --no-fold
                 kv.attn_decode_append(layer, ks[i][layer], vs[i][layer], qs[i][layer], rope,
-                                      out=out, workspace=ws)
+                                      out=out, workspace=ws, advance=fold and layer == L - 1)
             if events is not None:
                 events[layer][1].record()
-        kv.increment(1)
+        if not (fold and not args.separate):
+            kv.increment(1)
 
     def reset_lens():
         for s, l in enumerate(lens0):
@@ -832,6 +836,9 @@ def main():
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="measure the HBM ceiling of the decode's access pattern with no math "
                          "(loads-only probe at the config's shape) and of a flat read of the same size")
+    ap.add_argument("--no-fold", dest="fold", action="store_false",
+                    help="decode: a separate length-update launch per step instead of the last layer's "
+                         "ts_attn_decode_append_advance")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="launch every kernel eagerly instead of replaying captured HIP graphs")
     args = ap.parse_args()

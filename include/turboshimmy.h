@@ -229,6 +229,17 @@ int ts_attn_decode_append_noalloc(ts_kv *kv, int32_t layer, const float *d_k, co
                                   const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
                                   float *d_out, void *stream);
 
+/* ts_attn_decode_append for the last layer of a decode step, followed by ts_kv_increment(kv, 1)
+ * (cache.increment(), server_inference.rs:1355-1358) in the same launch: with a split the
+ * combine kernel advances the lengths once all of its workgroups have read them (an arrival
+ * counter kept in the cache), so the step needs no separate length-update launch; without a
+ * split a length update follows the decode.  Same arguments and errors as
+ * ts_attn_decode_append.  Lengths must not be read or changed by other work on the cache while
+ * the call runs. */
+int ts_attn_decode_append_advance(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
+                                  const float *d_q, int32_t n_head, const ts_rope *rope, float softcap,
+                                  float *d_out, void *d_workspace, uint64_t workspace_bytes, void *stream);
+
 /* Chunked-prefill attention over the INT4 cache.  Stands in for the f32 main_attn_out of
  * batched prefill (sh_layer_v1.wgsl:662-762, inference.rs:1160-1166) with the INT4 cache as
  * its source.  d_q: [n_seq][n_tok][n_head][head_dim] raw f32 for the n_tok tokens just

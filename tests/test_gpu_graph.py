@@ -15,7 +15,7 @@ from tests.test_gpu_decode_append import fill
 pytestmark = pytest.mark.gpu
 
 
-def replay_check(p: Pair, rng, n_head, n_replays):
+def replay_check(p: Pair, rng, n_head, n_replays, advance=False):
     B, n_kv, hd = p.n_seq, p.n_kv, p.hd
     k_in = torch.zeros((B, 1, n_kv, hd), device="cuda")
     v_in = torch.zeros((B, 1, n_kv, hd), device="cuda")
@@ -27,8 +27,11 @@ def replay_check(p: Pair, rng, n_head, n_replays):
     cap = torch.cuda.Stream()
     cap.wait_stream(torch.cuda.current_stream())
     with torch.cuda.graph(graph, stream=cap):
-        p.gpu.attn_decode_append(0, k_in, v_in, q_in, p.rope, out=out, workspace=ws)
-        p.gpu.increment(1)
+        if advance:  # the step's last layer: the lengths advance inside the decode launch
+            p.gpu.attn_decode_append(0, k_in, v_in, q_in, p.rope, out=out, workspace=ws, advance=True)
+        else:
+            p.gpu.attn_decode_append(0, k_in, v_in, q_in, p.rope, out=out, workspace=ws)
+            p.gpu.increment(1)
     torch.cuda.synchronize()
     for r in range(n_replays):
         k = synth.normal(rng, (B, 1, n_kv, hd))
@@ -60,6 +63,58 @@ def test_graph_replays_ragged_split_edges(gpu, n_head):
     fill(p, rng, max(lens))
     p.set_lens(lens)
     replay_check(p, rng, n_head, 5)
+
+
+def test_graph_replays_advance_in_combine(gpu):
+    """ts_attn_decode_append_advance captured once: the combine kernel advances the lengths (the
+    last of its workgroups to arrive), so no length-update launch; five replays across split
+    and window boundaries, each against the oracle at the advanced lengths."""
+    say("graph replays advance in combine")
+    rng = np.random.default_rng(320)
+    lens = [2047, 1023, 4000, 63, 1500, 255]
+    p = Pair(len(lens), 2, 128, 4100, 1e6)
+    fill(p, rng, max(lens))
+    p.set_lens(lens)
+    replay_check(p, rng, 8, 5, advance=True)
+
+
+def test_graph_replays_advance_without_split(gpu):
+    """The same for a plan without a split (256 streams, one workgroup each): the length update
+    follows the decode launch."""
+    say("graph replays advance, no split")
+    rng = np.random.default_rng(321)
+    lens = [int(x) for x in rng.integers(1000, 1100, size=32)]
+    p = Pair(len(lens), 8, 128, 1110, 1e6)
+    fill(p, rng, max(lens), step=1024)
+    p.set_lens(lens)
+    replay_check(p, rng, 32, 3, advance=True)
+
+
+def test_advance_matches_decode_then_increment(gpu):
+    """Eager: decode_append(advance=True) gives bit-identical outputs and cache contents to
+    decode_append followed by increment(1), and the same lengths, for a split plan (batch 1)."""
+    say("advance vs increment")
+    rng = np.random.default_rng(322)
+    a = Pair(1, 8, 128, 700, 500000.0)
+    b = Pair(1, 8, 128, 700, 500000.0)
+    for t0 in range(0, 600, 200):
+        k = synth.normal(rng, (1, 200, 8, 128))
+        v = synth.normal(rng, (1, 200, 8, 128))
+        for c in (a, b):
+            c.append(k, v)
+            c.advance(200)
+    for step in range(3):
+        k = dev(synth.normal(rng, (1, 1, 8, 128)))
+        v = dev(synth.normal(rng, (1, 1, 8, 128)))
+        q = dev(synth.normal(rng, (1, 32, 128)))
+        oa = a.gpu.attn_decode_append(0, k, v, q, a.rope, advance=True)
+        ob = b.gpu.attn_decode_append(0, k, v, q, b.rope)
+        b.gpu.increment(1)
+        torch.cuda.synchronize()
+        assert torch.equal(oa, ob), f"step {step}: outputs differ"
+        assert a.gpu.get_seq_len(0) == b.gpu.get_seq_len(0) == 600 + step + 1
+    for x, y in zip(a.gpu.export(0, 0, 0, 603), b.gpu.export(0, 0, 0, 603)):
+        assert torch.equal(x, y)
 
 
 def test_graph_replays_g4_kernel(gpu):
