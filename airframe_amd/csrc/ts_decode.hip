@@ -495,7 +495,7 @@ __global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_ker
     constexpr int WPG = HD / 32;   // K words per lane group = MFMA k-steps per 16-row tile
     constexpr int NTD = HD / 16;   // 16-dim output tiles
     constexpr int ROWB = HD / 2;   // bytes per K row
-    constexpr int OST = HD + 1;
+    constexpr int OST = HD + 4;  // 16-byte rows of the merge area
     const KvLayerView &L = a.L;
     const int hdr = PAD ? L.hdr : HD;
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
@@ -994,7 +994,7 @@ template <int HD, bool SOFTCAP, bool NORM, bool PAD, int NW, int D>
 __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeArgs a) {
     constexpr int NTD = HD / 16;
     constexpr int NM = HD / 64;  // i8 instructions per 16-position tile
-    constexpr int OST = HD + 1;
+    constexpr int OST = HD + 4;  // 16-byte rows of the merge area
     const KvLayerView &L = a.L;
     const int hdr = PAD ? L.hdr : HD;
     const float *const QN = NORM ? L.qn : nullptr;  // QK norm of q (compiled out when off)
@@ -1017,15 +1017,13 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     const int G = a.G;
     const DeqConst dc;
 
-    union Smem {
-        _Float16 pt[NW][8][64];  // per-wave p*s_v tile, [column][slot]
-        struct {
-            float o[NW][8 * OST];
-            float m[NW][4], l[NW][4];
-        } merge;
-    };
-    __shared__ Smem sm;
-    __shared__ float kd[HD], vd[HD], xnew[8];
+    // per-wave p*s_v tiles, [column][slot]; and the merge area, apart from them so that a wave
+    // writes its share of the merge as soon as its windows are done
+    __shared__ _Float16 pts[NW][8][64];
+    __shared__ __align__(16) float mo[NW][8 * OST];  // O^T columns, OST floats apart
+    __shared__ float mm_[NW][4], ml_[NW][4];
+    __shared__ __align__(16) float kd[HD], vd[HD];
+    __shared__ float xnew[8];
     __shared__ int32_t qsum[NW][16];  // per wave: digit sums of the 16 q rows
     __shared__ float qinv_s[NW][4];   // per wave: 2^-e of each head's q integer scale
 
@@ -1191,7 +1189,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     st.m = kMinit;
     st.l = 0.0f;
     const bool live = (lane >> 4) < G;
-    _Float16 (*pt)[64] = sm.pt[wave];
+    _Float16 (*pt)[64] = pts[wave];
 
     int it = 0;
     if (cnt > 0) {
@@ -1215,44 +1213,55 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
 windows_done:
 
     // ---- merge the waves through LDS ------------------------------------------------------------
+    // Each wave writes its O^T columns (16-byte stores: lane (n, g) holds dims 16 td + 4 g ..
+    // + 3 of column n), its m and l; one barrier; then one float4 of dims per thread.
+    // (Merge area shared with the P tiles, a barrier before the writes, scalar stores and one
+    // dim per thread: ~1.4 us from the last wave's loop end to the output.)
     const float l_run = row_sum16(st.l);
-    __syncthreads();  // all waves are done with their P tiles
     const int n = lane & 15, g = lane >> 4;
     if (n == 0 && g < 4) {
-        sm.merge.m[wave][g] = st.m;
-        sm.merge.l[wave][g] = l_run;
+        mm_[wave][g] = st.m;
+        ml_[wave][g] = l_run;
     }
     if (n < 8) {
 #pragma unroll
-        for (int td = 0; td < NTD; td++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) sm.merge.o[wave][n * OST + 16 * td + 4 * g + r] = st.o[td][r];
+        for (int td = 0; td < NTD; td++) *reinterpret_cast<floatx4 *>(&mo[wave][n * OST + 16 * td + 4 * g]) = st.o[td];
     }
     __syncthreads();
 
-    for (int idx = tid; idx < G * HD; idx += 64 * NW) {
-        const int hh = idx / HD, d = idx % HD;
+    constexpr int V4 = HD / 4;
+    for (int idx = tid; idx < G * V4; idx += 64 * NW) {
+        const int hh = idx / V4, d = 4 * (idx % V4);
         float M = kMinit;
 #pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, sm.merge.m[w][hh]);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, mm_[w][hh]);
         if (fused) M = fmaxf(M, xnew[hh]);
-        float acc = 0.0f, lsum = 0.0f;
+        floatx4 acc = (floatx4)0.0f;
+        float lsum = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const float e = exp2f(sm.merge.m[w][hh] - M);
-            acc += e * (sm.merge.o[w][hh * OST + d] + sm.merge.o[w][(hh + 4) * OST + d]);
-            lsum += e * sm.merge.l[w][hh];
+            const float e = exp2f(mm_[w][hh] - M);
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(&mo[w][hh * OST + d]);
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(&mo[w][(hh + 4) * OST + d]);
+            acc += e * (hi + lo);
+            lsum += e * ml_[w][hh];
         }
         if (fused) {
             const float e = exp2f(xnew[hh] - M);
-            acc += e * vd[d];
+            acc += e * *reinterpret_cast<const floatx4 *>(&vd[d]);
             lsum += e;
         }
         const size_t head = (size_t)s * a.n_head + h * G + hh;
         if (n_split_s == 1) {
-            if (d < hdr) a.out[head * hdr + d] = lsum > 0.0f ? acc / lsum : 0.0f;
+            // hdr is a multiple of 8: a float4 of dims lies wholly inside or outside the row
+            const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+            if (d < hdr) {
+                const floatx4 r = lsum > 0.0f ? acc * inv : (floatx4)0.0f;
+                *reinterpret_cast<float4 *>(a.out + head * hdr + d) = make_float4(r[0], r[1], r[2], r[3]);
+            }
         } else {
-            store_partial(a, head, split, HD, d, acc, M, lsum);
+#pragma unroll
+            for (int k = 0; k < 4; k++) store_partial(a, head, split, HD, d + k, acc[k], M, lsum);
         }
     }
 }
