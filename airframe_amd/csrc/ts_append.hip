@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void quantize_rows64_kernel(KvLayerView L, con
     constexpr int HD = 64;
     const int s = blockIdx.z, h = blockIdx.y;
     const int start = d_start ? d_start[s] : fixed_start;
-    const int end = start + count;
+    const int end = min(start + count, L.P);  // (a graph replayed past capacity writes nothing past it)
     const int blk = start / kBlk + blockIdx.x;
     const int p0 = blk * kBlk;
     if (p0 >= end) return;
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(256) void quantize_rows128_kernel(KvLayerView L, co
     constexpr int HD = 128;
     const int s = blockIdx.z, h = blockIdx.y;
     const int start = d_start ? d_start[s] : fixed_start;
-    const int end = start + count;
+    const int end = min(start + count, L.P);  // (a graph replayed past capacity writes nothing past it)
     const int blk = start / kBlk + blockIdx.x;
     const int p0 = blk * kBlk;
     if (p0 >= end) return;
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(256) void quantize_rows256_kernel(KvLayerView L, co
                                                                 int32_t rope_pairs) {
     const int s = blockIdx.z, h = blockIdx.y;
     const int start = d_start ? d_start[s] : fixed_start;
-    const int end = start + count;
+    const int end = min(start + count, L.P);  // (a graph replayed past capacity writes nothing past it)
     const int blk = start / kBlk + blockIdx.x;
     const int p0 = blk * kBlk;
     if (p0 >= end) return;

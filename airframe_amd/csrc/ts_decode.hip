@@ -539,6 +539,9 @@ __global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_ker
     asm volatile("" ::: "memory");
 
     const int qpos = a.len[s];
+    // a captured launch replayed past the cache's capacity (the host checks lengths only when a
+    // call is made): no work, nothing written
+    if (qpos >= L.P) return;
     const int qrot = rot_of(a.L, s, qpos);  // rotation position of the query
     const int n_ctx = qpos + 1;
     if (start >= n_ctx) return;
@@ -1003,6 +1006,9 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     // sequences (config 4: 1.42 vs 1.45 ms per step against the split-fastest order)
     const int split = blockIdx.z, h = blockIdx.x, s = blockIdx.y;
     const int qpos = a.len[s];
+    // a captured launch replayed past the cache's capacity (the host checks lengths only when a
+    // call is made): no work, nothing written
+    if (qpos >= L.P) return;
     const int qrot = rot_of(a.L, s, qpos);  // rotation position of the query
     const int n_ctx = qpos + 1;
     const int start = split * a.chunk;

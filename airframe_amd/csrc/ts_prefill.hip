@@ -472,7 +472,8 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
     // Query positions this wave covers (inclusive); qmax < 0 for a wave with no columns.
     const int qmin_w = len0 + c_wave / G;
     const int qmax_w = c_wave < n_cols ? len0 + (min(c_wave + kColsPerWave, n_cols) - 1) / G : -1;
-    const int key_end = len0 + (min(c_blk + COLS, n_cols) - 1) / G + 1;
+    // (clamped to the capacity: a graph replayed past it reads nothing past it)
+    const int key_end = min(len0 + (min(c_blk + COLS, n_cols) - 1) / G + 1, L.P);
     const int n_win = (key_end + kWin - 1) / kWin;
 
     floatx16 o[NDB];

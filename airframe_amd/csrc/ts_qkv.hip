@@ -83,7 +83,7 @@ __device__ inline RowTile row_tile(const QkvArgs &a, int rt) {
     const int nb = a.n_tok / kBlk + 2;
     t.s = rt / nb;
     t.start = a.len[t.s];
-    const int end = t.start + a.n_tok;
+    const int end = min(t.start + a.n_tok, a.L.P);
     t.blk = t.start / kBlk + rt % nb;
     const int p0 = t.blk * kBlk;
     t.live = p0 < end;
@@ -151,8 +151,9 @@ __device__ void store_rows_single(const QkvArgs &a, const RowTile &t, const floa
         const bool in_tile = i < r0 + nr;
         const float *trow = tile[min(i, r0 + nr - 1) - r0] + col0;
         const int s = min(t.s + i, L.S - 1);
-        const bool live = in_tile && t.s + i < L.S;
         const int p = a.len[s];
+        // (a graph replayed past the cache's capacity writes nothing past it)
+        const bool live = in_tile && t.s + i < L.S && p < L.P;
         float kx[8], vx[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -304,7 +305,7 @@ __global__ __launch_bounds__(256 * WR) void qkv_tile_kernel(QkvArgs a) {
     const bool single = a.n_tok == 1;  // decode rows: MT sequences, one token each
     const int nb4 = (a.n_tok / kBlk + 2 + NBLK - 1) / NBLK;
     const int s = single ? MT * rt : rt / nb4;
-    const int start = single ? 0 : a.len[s], end = start + a.n_tok;
+    const int start = single ? 0 : a.len[s], end = single ? a.n_tok : min(start + a.n_tok, a.L.P);
     const int blk0 = start / kBlk + NBLK * (rt % nb4);
     if (!single && blk0 * kBlk >= end) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;

@@ -5,14 +5,15 @@ Default workload (the headline): Qwen3-8B attention shape, 36
 seeded f32 N(0,1) Q/K/V with x8 outlier channels on 2% of dims, RoPE theta 1e6.  A step is one
 decode token for all 32 sequences: per layer, RoPE-fused quantize-on-append of the new K/V
 and split-K GQA attention over the INT4 cache in one launch (ts_attn_decode_append; with
---separate, ts_append_quant then ts_attn_decode); then the lengths advance (ts_kv_increment).
+--separate, ts_append_quant then ts_attn_decode); the lengths advance inside the last layer's
+launch (ts_attn_decode_append_advance; --no-fold: a separate ts_kv_increment).
 All inputs are generated on the device before timing.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 
 Prints one JSON line.  `value` = algorithmic HBM bytes of the whole step / step time (GB/s);
 `roofline` = the decode attention kernel (bytes per launch / its average launch time from HIP
-events recorded around every launch in the timed region); `cpu_baseline` = the C oracle on a
+events around replays of a graph holding only the layers' decode launches); `cpu_baseline` = the C oracle on a
 bounded sample of the same workload (same device-generated inputs copied to the host).
 Other configs (--config 1,2,4 decode; 5 chunked prefill) print their own line.
 """
@@ -169,7 +170,11 @@ def run_decode(args, cfg):
         lens0 = [int(x) for x in rng.integers(cfg["ragged"][0], cfg["ragged"][1], size=B)]
     else:
         lens0 = [cfg["ctx"]] * B
-    max_seq = max(lens0) + max(steps, warmup) + 1
+    # positions the run appends: the timed steps, or the warmup replays (whole graphs of
+    # --steps-per-graph steps each), whichever is more; the device lengths are reset between
+    spg = max(1, args.steps_per_graph) if args.graph else 1
+    warm_steps = -(-warmup // spg) * spg
+    max_seq = max(lens0) + max(steps, warm_steps) + 1
     rope = RopeTable(max_seq, hd, cfg["theta"])
     kv = KVCache.new_int4(L, n_kv, hd, max_seq, B)
     dims = synth.outlier_dims(n_kv, hd, args.seed) if cfg["outliers"] else None
@@ -249,17 +254,20 @@ def run_decode(args, cfg):
     # advance inside the graphs exactly as in eager execution.
     graphs = None
     if args.graph:
+        # one graph per step (default), or per group of spg consecutive steps (--steps-per-graph:
+        # the host's launch cost per graph then spreads over spg steps)
         graphs = []
         cap = torch.cuda.Stream()
         cap.wait_stream(torch.cuda.current_stream())
-        for i in range(steps):
+        for i0 in range(0, steps, spg):
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr, stream=cap):
-                step(i)
+                for i in range(i0, min(i0 + spg, steps)):
+                    step(i)
             graphs.append(gr)
         torch.cuda.synchronize()
-        for i in range(warmup):
-            graphs[i % steps].replay()
+        for i in range(-(-warmup // spg)):  # warm_steps steps
+            graphs[i % len(graphs)].replay()
         torch.cuda.synchronize()
         reset_lens()
     else:
@@ -272,10 +280,11 @@ def run_decode(args, cfg):
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record()
-    for i in range(steps):
-        if graphs is not None:
-            graphs[i].replay()
-        else:
+    if graphs is not None:
+        for gr in graphs:
+            gr.replay()
+    else:
+        for i in range(steps):
             step(i)
     t_end.record()
     torch.cuda.synchronize()
@@ -836,6 +845,8 @@ def main():
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="measure the HBM ceiling of the decode's access pattern with no math "
                          "(loads-only probe at the config's shape) and of a flat read of the same size")
+    ap.add_argument("--steps-per-graph", type=int, default=1,
+                    help="decode: capture this many consecutive steps per HIP graph (default 1: one graph per step)")
     ap.add_argument("--no-fold", dest="fold", action="store_false",
                     help="decode: a separate length-update launch per step instead of the last layer's "
                          "ts_attn_decode_append_advance")
@@ -1036,7 +1047,8 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "int4-kv/f32-io (f16 mfma, hi/lo split)",
         "data": "synthetic (seeded N(0,1), x8 outlier channels)" if cfg["outliers"] else "synthetic (seeded N(0,1))",
         "tokens_per_s": round(tok_s, 1), "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
-        "launch": "hip-graph replay per step" if args.graph else "eager",
+        "launch": ("eager" if not args.graph else "hip-graph replay per step" if args.steps_per_graph <= 1
+                   else f"hip-graph replay per {args.steps_per_graph} steps"),
         "config": {"workload": cfg["name"] + ("_qknorm" if args.qk_norm else ""), "global_batch": B,
                    "seq_len": cfg.get("ctx"),
                    "layers": L, "n_head": cfg["n_head"], "n_head_kv": cfg["n_kv"],
