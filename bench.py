@@ -314,13 +314,17 @@ def run_decode(args, cfg):
         kg = torch.cuda.CUDAGraph()
         cap = torch.cuda.Stream()
         cap.wait_stream(torch.cuda.current_stream())
+        # at least 32 launches per graph (the layers repeated), so that a one-layer config's
+        # replays measure the launches and not the host's graph launch
+        n_copies = -(-32 // L)
         with torch.cuda.graph(kg, stream=cap):
-            for layer in range(L):
-                if args.separate:
-                    kv.attn_decode(layer, qs[0][layer], rope, out=out, workspace=ws)
-                else:
-                    kv.attn_decode_append(layer, ks[0][layer], vs[0][layer], qs[0][layer], rope,
-                                          out=out, workspace=ws)
+            for _ in range(n_copies):
+                for layer in range(L):
+                    if args.separate:
+                        kv.attn_decode(layer, qs[0][layer], rope, out=out, workspace=ws)
+                    else:
+                        kv.attn_decode_append(layer, ks[0][layer], vs[0][layer], qs[0][layer], rope,
+                                              out=out, workspace=ws)
         torch.cuda.synchronize()
         for _ in range(3):
             kg.replay()
@@ -331,10 +335,11 @@ def run_decode(args, cfg):
             kg.replay()
         e1.record()
         torch.cuda.synchronize()
-        result["kernel_ms"] = e0.elapsed_time(e1) / (n_rep * L)
+        result["kernel_ms"] = e0.elapsed_time(e1) / (n_rep * L * n_copies)
         result["kernel_bytes"] = float(kern_bytes[0])
-        result["kernel_timing"] = (f"HIP events around {n_rep} replays of a graph holding only the {L} decode "
-                                   "launches of step 0 (split and combine kernels; no length increment)")
+        result["kernel_timing"] = (f"HIP events around {n_rep} replays of a graph holding only the {L * n_copies} "
+                                   "decode launches of step 0" + (f" ({n_copies} copies of the {L} layers)" if n_copies > 1 else "")
+                                   + " (split and combine kernels; no length increment)")
         del kg
 
     cpu = None
