@@ -199,3 +199,34 @@ def test_gguf_in_loop_refusals(gpu):
     with pytest.raises(TsError):  # 320 inputs: not a whole number of 256-element blocks
         attn_out_proj_gguf(torch.zeros((1, 320), device="cuda"), weights.Q4_K,
                            dev(np.zeros(16, np.uint8)), 256, torch.zeros((1, 256), device="cuda"))
+
+
+@pytest.mark.parametrize("n_tok", [1, 40])
+def test_qkv_append_gguf_with_qk_norm(gpu, n_tok):
+    """The K-quant projections with Qwen3's QK norm set: the appended K is normalized before its
+    rotation (the epilogue shared with the f16 path), codes bit-exact against the oracle's
+    append of the kernel's own raw K/V, q returned raw."""
+    say(f"qkv_append_gguf with QK norm n_tok={n_tok}")
+    rng = np.random.default_rng(940 + n_tok)
+    n_seq, n_head, n_kv, hd, dim = 3, 8, 2, 128, 768
+    p = Pair(n_seq, n_kv, hd, 128, 1e6)
+    wq_n = (rng.standard_normal(hd) * 0.4 + 1.0).astype(np.float32)
+    wk_n = (rng.standard_normal(hd) * 0.4 + 1.0).astype(np.float32)
+    p.gpu.set_qk_norm(0, dev(wq_n), dev(wk_n), 1e-6)
+    p.ora.q_norm, p.ora.k_norm, p.ora.norm_eps = wq_n, wk_n, 1e-6
+    rows = (n_head * hd, n_kv * hd, n_kv * hd)
+    blobs = [random_blob(rng, weights.Q4_K, r, dim) for r in rows]
+    wf = [oracle.dequant(weights.Q4_K, b, r * dim).reshape(r, dim) for b, r in zip(blobs, rows)]
+    x = rng.standard_normal((n_seq, n_tok, dim)).astype(np.float32)
+    k_out = torch.empty((n_seq, n_tok, n_kv, hd), dtype=torch.float32, device="cuda")
+    v_out = torch.empty_like(k_out)
+    q = p.gpu.qkv_append_gguf(0, dev(x), weights.Q4_K, dev(blobs[0]), dev(blobs[1]), dev(blobs[2]),
+                              p.rope, kv_out=(k_out, v_out))
+    torch.cuda.synchronize()
+    q, k_out, v_out = q.cpu().numpy(), k_out.cpu().numpy(), v_out.cpu().numpy()
+    xf = x.reshape(-1, dim)
+    assert_close(q.reshape(n_seq * n_tok, -1), oracle.project_f32(xf, wf[0]), "raw q (QK norm set)")
+    assert_close(k_out.reshape(n_seq * n_tok, -1), oracle.project_f32(xf, wf[1]), "raw k (QK norm set)")
+    p.ora.append(k_out, v_out)
+    p.advance(n_tok)
+    p.check_codes()
