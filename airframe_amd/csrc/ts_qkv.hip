@@ -446,13 +446,14 @@ QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok) {
     p.n_split = 1;
     p.part_bytes = 0;
     // Fewer 32-row tiles than CUs (decode, short chunks): dim split into slices of whole 256s
-    // (at most kMaxSplit) so that about 512 workgroups stream the weights.
+    // (at most kMaxSplit), as many as keep all workgroups in one round on the 256 CUs; going just
+    // past 256 leaves a short second round that costs more than the longer slices.
     const int rt32 = n_tok == 1 ? (n_seq + kMT - 1) / kMT : n_seq * (n_tok / kBlk + 2);
     const int tiles = rt32 * p.CT;
     if (tiles < 256 && dim % 256 == 0 && dim >= 512) {
         p.big = false;
         p.RT = rt32;
-        const int want = std::min(kMaxSplit, std::max(2, (512 + tiles - 1) / tiles));
+        const int want = std::min(kMaxSplit, std::max(2, 256 / tiles));
         const int nbat = dim / 256;
         const int per = (nbat + want - 1) / want;  // 256s per split
         p.kps = per * 256;
