@@ -36,6 +36,31 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert exported == set(names)
 
 
+def _param_counts_c():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, args in re.findall(r"\b(ts_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text):
+        args = " ".join(args.split())
+        out[name] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_integration_rust_block_matches_header():
+    """The Rust extern block a maintainer would paste declares every C entry point, with the
+    same number of arguments."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = text[text.index('extern "C" {'):]
+    block = block[:block.index("\n}")]
+    rust = {}
+    for name, args in re.findall(r"pub fn (ts_[a-z0-9_]+)\(([^)]*)\)", block, flags=re.S):
+        args = " ".join(args.split()).rstrip(",")
+        rust[name] = 0 if not args else args.count(",") + 1
+    c = _param_counts_c()
+    assert set(c) == set(declared_functions())
+    assert set(rust) == set(c), sorted(set(rust) ^ set(c))
+    assert rust == c, {k: (rust[k], c[k]) for k in c if rust[k] != c[k]}
+
+
 def test_header_compiles_as_c():
     src = f'#include "{HEADER}"\nint main(void){{ ts_kv_desc d = {{1,1,1,64,1}}; (void)d; return 0; }}\n'
     r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-x", "c", "-", "-fsyntax-only"],
