@@ -819,8 +819,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--head-dim", type=int, default=None,
-                    help="decode configurations: another head dim (e.g. 256, Gemma-2's), the workload renamed")
-    ap.add_argument("--n-head", type=int, default=None, help="decode configurations: another query head count")
+                    help="another head dim (e.g. 256, Gemma-2's), the workload renamed")
+    ap.add_argument("--n-head", type=int, default=None, help="another query head count")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--separate", action="store_true",
@@ -865,8 +865,6 @@ def main():
         sys.exit(2)
     cfg = dict(CONFIGS[args.config])
     if args.head_dim or args.n_head:
-        if "ctx" not in cfg:
-            sys.exit("--head-dim / --n-head need a decode configuration (1-4)")
         cfg["hd"] = args.head_dim or cfg["hd"]
         cfg["n_head"] = args.n_head or cfg["n_head"]
         cfg["name"] += f"_hd{cfg['hd']}_h{cfg['n_head']}"
