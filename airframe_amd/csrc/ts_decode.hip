@@ -886,13 +886,15 @@ __device__ inline float row_sum16(float v) {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-// Running state of one wave: O^T accumulators (column n < 4: head n from the high parts of
-// p*s_v, 4 <= n < 8: head n - 4 from the low parts), and for this lane's head (lane / 16) the
-// exponent reference (uniform over the lane's row) and its share of the softmax sum.
-template <int HD>
+// Running state of one wave.  GH = 1 (G <= 4): O^T column n < 4 is head n from the high parts
+// of p*s_v, 4 <= n < 8 head n - 4 from the low parts; GH = 2 (G <= 8): column n < 8 is head n
+// from the high parts, 8 <= n < 16 head n - 8 from the low parts.  Lane 16 hg + n runs the
+// softmax of heads hg (half 0) and 4 + hg (half 1): the exponent reference of each (uniform over
+// the lane's row) and this lane's share of its softmax sum.
+template <int HD, int GH>
 struct WaveState8 {
     floatx4 o[HD / 16];
-    float m, l;
+    float m[GH], l[GH];
 };
 
 // LDS slot of position `key` (0..63) of a window in the PV operand order: lane (n, g) of the
@@ -901,95 +903,114 @@ __device__ inline int p_slot(int key) {
     return 32 * (key >> 5) + 8 * ((key >> 2) & 3) + 2 * (key & 3) + ((key >> 4) & 1);
 }
 
-template <int HD, bool SOFTCAP>
-__device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8<HD> &st,
-                                                const i32x4 (&qa)[HD / 64], const i32x4 &bias,
-                                                float qinv, _Float16 (*pt)[64], int base, int end,
-                                                int lane, bool live, float softcap, const DeqConst &dc) {
+// One window.  Half hf of the heads (4 hf .. 4 hf + 3) has its own q operand qa[hf] and bias:
+// one i8 instruction per half and k-group, both on the same unpacked K operand.  pt: the wave's
+// P tile, 8 GH columns.
+template <int HD, bool SOFTCAP, int GH>
+__device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8<HD, GH> &st,
+                                                const i32x4 (&qa)[GH][HD / 64], const i32x4 (&bias)[GH],
+                                                const float (&qinv)[GH], _Float16 (*pt)[64], int base, int end,
+                                                int lane, const bool (&live)[GH], float softcap, const DeqConst &dc) {
     constexpr int NTD = HD / 16, NM = HD / 64;
     const int n = lane & 15, hg = lane >> 4;
     // ---- S = Q K^T, exact -----------------------------------------------------------------
-    i32x4 acc[4];
+    i32x4 acc[GH][4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        acc[t] = bias;
+#pragma unroll
+        for (int hf = 0; hf < GH; hf++) acc[hf][t] = bias[hf];
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             const uint32_t w0 = w.kw[2 * (t * NM + m)], w1 = w.kw[2 * (t * NM + m) + 1];
             const i32x4 kb = {(int)(w0 & 0x0F0F0F0Fu), (int)((w0 >> 4) & 0x0F0F0F0Fu),
                               (int)(w1 & 0x0F0F0F0Fu), (int)((w1 >> 4) & 0x0F0F0F0Fu)};
-            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[m], kb, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int hf = 0; hf < GH; hf++)
+                acc[hf][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[hf][m], kb, acc[hf][t], 0, 0, 0);
         }
     }
-    // ---- softmax of head hg at positions base + 4n + t ------------------------------------
-    float x[4], sv[4];
+    // ---- softmax of heads hg (+ 4 hf) at positions base + 4n + t --------------------------
+    float x[GH][4], sv[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        // digits 0..3 carry weights 2^21, 2^14, 2^7, 1; each digit sum is an exact integer
-        // below 2^18, so the first step is exact and the whole score rounds ~once.
-        float v = fmaf(fmaf(fmaf((float)acc[t][0], 128.0f, (float)acc[t][1]), 128.0f, (float)acc[t][2]), 128.0f,
-                       (float)acc[t][3]);
-        v *= qinv * w.sk[t];
-        if constexpr (SOFTCAP) v = tanhf(v * (1.0f / kLog2e) / softcap) * softcap * kLog2e;
-        x[t] = v;
-        sv[t] = w.sv[t];
-    }
+        sv[t] = base + 4 * n + t >= end ? 0.0f : w.sv[t];  // positions past the split's end
 #pragma unroll
-    for (int t = 0; t < 4; t++) {  // positions past the split's end
-        if (base + 4 * n + t >= end) {
-            x[t] = -INFINITY;
-            sv[t] = 0.0f;
+        for (int hf = 0; hf < GH; hf++) {
+            // digits 0..3 carry weights 2^21, 2^14, 2^7, 1; each digit sum is an exact integer
+            // below 2^18, so the first step is exact and the whole score rounds ~once.
+            float v = fmaf(fmaf(fmaf((float)acc[hf][t][0], 128.0f, (float)acc[hf][t][1]), 128.0f,
+                                (float)acc[hf][t][2]),
+                           128.0f, (float)acc[hf][t][3]);
+            v *= qinv[hf] * w.sk[t];
+            if constexpr (SOFTCAP) v = tanhf(v * (1.0f / kLog2e) / softcap) * softcap * kLog2e;
+            x[hf][t] = base + 4 * n + t >= end ? -INFINITY : v;
         }
     }
     // P = 2^(x - m) * s_v must stay <= 2^8 (f16 range for its two parts, with room).  The
     // reference m of a head moves only when some position of the window breaks that: a ballot
     // in the common case, row reductions only then (to m = max(x) + log2(max s_v), P <= 1).
-    float p[4], pv[4];
+    float p[GH][4], pv[GH][4];
     bool need = false;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        p[t] = live ? fast_exp2(x[t] - st.m) : 0.0f;
-        pv[t] = p[t] * sv[t];
-        need |= !(pv[t] <= 256.0f);
-    }
+    for (int hf = 0; hf < GH; hf++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            p[hf][t] = live[hf] ? fast_exp2(x[hf][t] - st.m[hf]) : 0.0f;
+            pv[hf][t] = p[hf][t] * sv[t];
+            need |= !(pv[hf][t] <= 256.0f);
+        }
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
         asm volatile("" ::: "memory");  // keep this a branch: the rescale is the rare case
         const float svl = __builtin_amdgcn_logf(row_max16(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))));
-        const float xm = row_max16(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-        const float mw = fminf(fmaxf(xm + svl, xm - 64.0f), xm + 64.0f);
-        const float m_new = fmaxf(st.m, mw);
-        const float al = fast_exp2(st.m - m_new);
-        st.l *= al;
-        st.m = m_new;
+        float al[GH];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            p[t] = live ? fast_exp2(x[t] - st.m) : 0.0f;
-            pv[t] = p[t] * sv[t];
+        for (int hf = 0; hf < GH; hf++) {
+            const float xm = row_max16(fmaxf(fmaxf(x[hf][0], x[hf][1]), fmaxf(x[hf][2], x[hf][3])));
+            const float mw = fminf(fmaxf(xm + svl, xm - 64.0f), xm + 64.0f);
+            const float m_new = fmaxf(st.m[hf], mw);
+            al[hf] = fast_exp2(st.m[hf] - m_new);
+            st.l[hf] *= al[hf];
+            st.m[hf] = m_new;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                p[hf][t] = live[hf] ? fast_exp2(x[hf][t] - st.m[hf]) : 0.0f;
+                pv[hf][t] = p[hf][t] * sv[t];
+            }
         }
-        // the O^T column of head c (c and c + 4) takes the factor of row c
-        const float f0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 0));
-        const float f1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 16));
-        const float f2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 32));
-        const float f3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al), 48));
-        const int c = lane & 3;
-        const float f = c == 0 ? f0 : c == 1 ? f1 : c == 2 ? f2 : f3;
+        // the O^T columns of head c take the factor of its row: head c of half hf is row c % 4
+        // of al[hf] (lane 16 (c % 4))
+        const int c = GH == 1 ? (lane & 3) : (lane & 7);
+        float f = 1.0f;
+#pragma unroll
+        for (int hf = 0; hf < GH; hf++) {
+            const float f0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al[hf]), 0));
+            const float f1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al[hf]), 16));
+            const float f2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al[hf]), 32));
+            const float f3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(al[hf]), 48));
+            const int cc = c & 3;
+            if ((c >> 2) == hf) f = cc == 0 ? f0 : cc == 1 ? f1 : cc == 2 ? f2 : f3;
+        }
 #pragma unroll
         for (int td = 0; td < NTD; td++) st.o[td] *= f;
     }
-    st.l += (p[0] + p[1]) + (p[2] + p[3]);
+#pragma unroll
+    for (int hf = 0; hf < GH; hf++) st.l[hf] += (p[hf][0] + p[hf][1]) + (p[hf][2] + p[hf][3]);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const int slot = p_slot(4 * n + t);
-        const float hi = split_hi(pv[t]);
-        pt[hg][slot] = (_Float16)hi;
-        pt[4 + hg][slot] = (_Float16)(pv[t] - hi);
+#pragma unroll
+        for (int hf = 0; hf < GH; hf++) {
+            const float hi = split_hi(pv[hf][t]);
+            pt[4 * hf + hg][slot] = (_Float16)hi;
+            pt[4 * GH + 4 * hf + hg][slot] = (_Float16)(pv[hf][t] - hi);
+        }
     }
     // ---- O^T += V^T P^T (the wave's own LDS writes are ordered before its reads) -------------
     const int g = lane >> 4;
 #pragma unroll
     for (int b = 0; b < 2; b++) {
-        // columns 8..15 read real p values: their outputs are never used
-        const half8 pb = *reinterpret_cast<const half8 *>(&pt[n & 7][32 * b + 8 * g]);
+        // GH = 1: columns 8..15 read real p values; their outputs are never used
+        const half8 pb = *reinterpret_cast<const half8 *>(&pt[GH == 1 ? (n & 7) : n][32 * b + 8 * g]);
         // every word of the block dequantized into its own registers first, so the conversions
         // of later words overlap the matrix instructions of earlier ones
         half8 va[NTD];
@@ -1006,7 +1027,8 @@ __device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8
 // PAD: the caller's head dim hdr is below the stored HD (rows of q, new K/V and the output are
 // hdr floats; the stored dims past them hold code 8 = 0, so the integer QK^T and PV run
 // unchanged over the whole stored row).
-template <int HD, bool SOFTCAP, bool NORM, bool PAD, int NW, int D>
+// GH: halves of 4 query heads (1: G <= 4, 2: G <= 8).
+template <int HD, bool SOFTCAP, bool NORM, bool PAD, int NW, int D, int GH>
 __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeArgs a) {
     constexpr int NTD = HD / 16;
     constexpr int NM = HD / 64;  // i8 instructions per 16-position tile
@@ -1038,13 +1060,13 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
 
     // per-wave p*s_v tiles, [column][slot]; and the merge area, apart from them so that a wave
     // writes its share of the merge as soon as its windows are done
-    __shared__ _Float16 pts[NW][8][64];
-    __shared__ __align__(16) float mo[NW][8 * OST];  // O^T columns, OST floats apart
-    __shared__ float mm_[NW][4], ml_[NW][4];
+    __shared__ _Float16 pts[NW][8 * GH][64];
+    __shared__ __align__(16) float mo[NW][8 * GH * OST];  // O^T columns, OST floats apart
+    __shared__ float mm_[NW][4 * GH], ml_[NW][4 * GH];
     __shared__ __align__(16) float kd[HD], vd[HD];
     __shared__ float xnew[8];
-    __shared__ int32_t qsum[NW][16];  // per wave: digit sums of the 16 q rows
-    __shared__ float qinv_s[NW][4];   // per wave: 2^-e of each head's q integer scale
+    __shared__ int32_t qsum[NW][GH][16];  // per wave and half: digit sums of the 16 q rows
+    __shared__ float qinv_s[NW][GH][4];   // per wave and half: 2^-e of each head's q scale
 
     const size_t row = (size_t)s * L.H + h;
     constexpr int ROWB = HD / 2;
@@ -1092,25 +1114,39 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     // dims, even dims of word 8m + 2g + 1, its odd dims] like the K operand.  The raw q loads
     // go out before the windows' prefetch: loads complete in order, so consuming q then does
     // not wait for the windows.
-    i32x4 qa[NM], bias;
-    float qinv;
+    i32x4 qa[GH][NM], bias[GH];
+    float qinv[GH];
     const bool appender = fused && wave == NW - 1;
     AppendIn<HD> ain;
-    float2 qp[4][AppendIn<HD>::PPL];
+    float2 qp[4 * GH][AppendIn<HD>::PPL];
     {
+        // half hf: lane 16 g + n holds digit dg of head hh + 4 hf
         const int n = lane & 15, g = lane >> 4, hh = n >> 2, dg = n & 3;
-        const bool hl = hh < G;
-        const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (hl ? hh : 0)) * hdr;
-        float qx[NM][16], nwv[NM][16];
+        bool hl[GH];
+        float qx[GH][NM][16], nwv[NM][16];
         float2 qcs[NM][8];
+#pragma unroll
+        for (int hf = 0; hf < GH; hf++) {
+            hl[hf] = hh + 4 * hf < G;
+            const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (hl[hf] ? hh + 4 * hf : 0)) * hdr;
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const int d0 = 64 * m + 16 * g;
+#pragma unroll
+                for (int e4 = 0; e4 < 4; e4++) {
+                    const bool in = d0 + 4 * e4 < hdr;  // stored dims past the row are 0
+                    const float4 v4 = keep4(in, *reinterpret_cast<const float4 *>(qrow + (in ? d0 + 4 * e4 : 0)));
+                    qx[hf][m][4 * e4] = v4.x; qx[hf][m][4 * e4 + 1] = v4.y;
+                    qx[hf][m][4 * e4 + 2] = v4.z; qx[hf][m][4 * e4 + 3] = v4.w;
+                }
+            }
+        }
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             const int d0 = 64 * m + 16 * g;
 #pragma unroll
             for (int e4 = 0; e4 < 4; e4++) {
-                const bool in = d0 + 4 * e4 < hdr;  // stored dims past the row are 0
-                const float4 v4 = keep4(in, *reinterpret_cast<const float4 *>(qrow + (in ? d0 + 4 * e4 : 0)));
-                qx[m][4 * e4] = v4.x; qx[m][4 * e4 + 1] = v4.y; qx[m][4 * e4 + 2] = v4.z; qx[m][4 * e4 + 3] = v4.w;
+                const bool in = d0 + 4 * e4 < hdr;
                 if (QN) {
                     const float4 n4 = *reinterpret_cast<const float4 *>(QN + (in ? d0 + 4 * e4 : 0));  // (only
                     // multiplies dims that are zero past the row)
@@ -1125,21 +1161,27 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
                                 : make_float2(1.0f, 0.0f);
             }
         }
-        const float ns = QN ? q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * hdr, G, hl ? hh : 0,
-                                                    L.norm_eps, hdr)
-                            : 1.0f;
+        float ns[GH];
+        ns[GH - 1] = 1.0f;
+        if (QN)
+            ns[0] = q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * hdr, G, hl[0] ? hh : 0, L.norm_eps,
+                                          hdr, GH == 2 && hl[GH - 1] ? hh + 4 : -1, ns[GH - 1]);
+        else
+            ns[0] = 1.0f;
         // The appending wave (the last: it has the fewest windows) quantizes the new token and
         // scores it against every head before its windows; the others start at once.  Its
         // loads go out with q's.  kd, vd and xnew are read after the barrier that opens the
         // merge.
         if (appender) {
             append_load<HD, NORM>(a, s, h, qpos, lane, ain, hdr);
-            load_q_pairs<HD, 4>(a, s, h * G, G, lane, qp, hdr);
+            load_q_pairs<HD, 4 * GH>(a, s, h * G, G, lane, qp, hdr);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int d = 0; d < D - 1; d++) load_window8<HD>(w[d], str, win_base(d), lane);
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hf = 0; hf < GH; hf++) {
         // rotated q times log2(e)/sqrt(hd) (rope.rs:186-196 after the optional QK norm)
         float qm = 0.0f;
 #pragma unroll
@@ -1147,15 +1189,15 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
 #pragma clang fp contract(off)
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                float x0 = qx[m][2 * i], x1 = qx[m][2 * i + 1];
+                float x0 = qx[hf][m][2 * i], x1 = qx[hf][m][2 * i + 1];
                 if (QN) {
-                    x0 = qk_norm_apply(x0, ns, nwv[m][2 * i]);
-                    x1 = qk_norm_apply(x1, ns, nwv[m][2 * i + 1]);
+                    x0 = qk_norm_apply(x0, ns[hf], nwv[m][2 * i]);
+                    x1 = qk_norm_apply(x1, ns[hf], nwv[m][2 * i + 1]);
                 }
                 if ((64 * m + 16 * g) / 2 + i < a.rope_pairs) rope_rotate(x0, x1, qcs[m][i]);
-                qx[m][2 * i] = x0 * (a.inv_sqrt_hd * kLog2e);
-                qx[m][2 * i + 1] = x1 * (a.inv_sqrt_hd * kLog2e);
-                qm = fmaxf(qm, fmaxf(fabsf(qx[m][2 * i]), fabsf(qx[m][2 * i + 1])));
+                qx[hf][m][2 * i] = x0 * (a.inv_sqrt_hd * kLog2e);
+                qx[hf][m][2 * i + 1] = x1 * (a.inv_sqrt_hd * kLog2e);
+                qm = fmaxf(qm, fmaxf(fabsf(qx[hf][m][2 * i]), fabsf(qx[hf][m][2 * i + 1])));
             }
         }
         // head hh's integer scale 2^e: max |q| 2^e in [2^26, 2^27), so every digit fits int8
@@ -1174,7 +1216,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
             uint32_t reg[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int el = 0; el < 16; el++) {
-                const int Q = hl ? (int)rintf(qx[m][el] * sc) : 0;
+                const int Q = hl[hf] ? (int)rintf(qx[hf][m][el] * sc) : 0;
                 const uint32_t dig = ((uint32_t)(Q + 135274560) >> sh) & msk;
                 dsum_raw += dig;
                 // element el = dim 64 m + 16 g + el: word 8m + 2g + el / 8, parity el % 2 selects
@@ -1182,32 +1224,40 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
                 const int rr = 2 * (el >> 3) + (el & 1), by = (el & 7) >> 1;
                 reg[rr] |= ((dig + 192u) & 0xFFu) << (8 * by);  // the byte of D_c - 64
             }
-            qa[m] = (i32x4){(int)reg[0], (int)reg[1], (int)reg[2], (int)reg[3]};
+            qa[hf][m] = (i32x4){(int)reg[0], (int)reg[1], (int)reg[2], (int)reg[3]};
         }
         int dsum = (int)dsum_raw - 64 * 16 * NM;
         // bias of accumulator (head hg, digit r): -8 * (digit sum of row 4 hg + r)
         dsum += __shfl_xor(dsum, 16, 64);
         dsum += __shfl_xor(dsum, 32, 64);
-        if (g == 0) qsum[wave][n] = dsum;
-        if (g == 0 && dg == 0) qinv_s[wave][hh] = ldexpf(1.0f, -e);
+        if (g == 0) qsum[wave][hf][n] = dsum;
+        if (g == 0 && dg == 0) qinv_s[wave][hf][hh] = ldexpf(1.0f, -e);
+        }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
         __builtin_amdgcn_wave_barrier();
         const int hg = lane >> 4;
-        bias = (i32x4){-8 * qsum[wave][4 * hg], -8 * qsum[wave][4 * hg + 1], -8 * qsum[wave][4 * hg + 2],
-                       -8 * qsum[wave][4 * hg + 3]};
-        qinv = qinv_s[wave][hg];
+#pragma unroll
+        for (int hf = 0; hf < GH; hf++) {
+            bias[hf] = (i32x4){-8 * qsum[wave][hf][4 * hg], -8 * qsum[wave][hf][4 * hg + 1],
+                               -8 * qsum[wave][hf][4 * hg + 2], -8 * qsum[wave][hf][4 * hg + 3]};
+            qinv[hf] = qinv_s[wave][hf][hg];
+        }
     }
     if (appender) {
         append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd, hdr);
-        new_token_scores<HD, SOFTCAP, NORM, 4>(a, s, h * G, G, lane, qp, ain.cs, kd, xnew, hdr);
+        new_token_scores<HD, SOFTCAP, NORM, 4 * GH>(a, s, h * G, G, lane, qp, ain.cs, kd, xnew, hdr);
     }
 
-    WaveState8<HD> st;
+    WaveState8<HD, GH> st;
 #pragma unroll
     for (int td = 0; td < NTD; td++) st.o[td] = (floatx4)0.0f;
-    st.m = kMinit;
-    st.l = 0.0f;
-    const bool live = (lane >> 4) < G;
+    bool live[GH];
+#pragma unroll
+    for (int hf = 0; hf < GH; hf++) {
+        st.m[hf] = kMinit;
+        st.l[hf] = 0.0f;
+        live[hf] = (lane >> 4) + 4 * hf < G;
+    }
     _Float16 (*pt)[64] = pts[wave];
 
     int it = 0;
@@ -1224,7 +1274,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
                 // (one form for every window, the tail mask included: a branch between a masked
                 // and an unmasked copy made the compiler shuffle the accumulators at the join,
                 // ~30 moves per window; config 4 1.396 vs 1.408 ms per step)
-                process_window8<HD, SOFTCAP>(w[d], st, qa, bias, qinv, pt, win_base(it), end, lane, live, a.softcap, dc);
+                process_window8<HD, SOFTCAP, GH>(w[d], st, qa, bias, qinv, pt, win_base(it), end, lane, live, a.softcap, dc);
                 if (++it >= cnt) goto windows_done;
             }
         }
@@ -1236,13 +1286,16 @@ windows_done:
     // + 3 of column n), its m and l; one barrier; then one float4 of dims per thread.
     // (Merge area shared with the P tiles, a barrier before the writes, scalar stores and one
     // dim per thread: ~1.4 us from the last wave's loop end to the output.)
-    const float l_run = row_sum16(st.l);
     const int n = lane & 15, g = lane >> 4;
-    if (n == 0 && g < 4) {
-        mm_[wave][g] = st.m;
-        ml_[wave][g] = l_run;
+#pragma unroll
+    for (int hf = 0; hf < GH; hf++) {
+        const float l_run = row_sum16(st.l[hf]);
+        if (n == 0) {
+            mm_[wave][4 * hf + g] = st.m[hf];
+            ml_[wave][4 * hf + g] = l_run;
+        }
     }
-    if (n < 8) {
+    if (n < 8 * GH) {
 #pragma unroll
         for (int td = 0; td < NTD; td++) *reinterpret_cast<floatx4 *>(&mo[wave][n * OST + 16 * td + 4 * g]) = st.o[td];
     }
@@ -1261,7 +1314,7 @@ windows_done:
         for (int w = 0; w < NW; w++) {
             const float e = exp2f(mm_[w][hh] - M);
             const floatx4 hi = *reinterpret_cast<const floatx4 *>(&mo[w][hh * OST + d]);
-            const floatx4 lo = *reinterpret_cast<const floatx4 *>(&mo[w][(hh + 4) * OST + d]);
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(&mo[w][(hh + 4 * GH) * OST + d]);
             acc += e * (hi + lo);
             lsum += e * ml_[w][hh];
         }
@@ -1319,6 +1372,11 @@ int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
         const int mid = (lo + hi) / 2;
         if (busy(64 * mid) <= target) hi = mid; else lo = mid + 1;
     }
+    // More streams than the target (many sequences): no chunk meets it.  The balanced chunk
+    // (the batch's work over the target) still splits the sequences much longer than the rest,
+    // which would otherwise stream alone after the others finished; for a uniform batch it is
+    // the whole sequence anyway.
+    if (busy(64 * lo) > target) return lo_c;
     return 64 * lo;
 }
 }  // namespace
@@ -1328,7 +1386,7 @@ DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_c
     int max_ctx = 1;
     for (int s = 0; s < n_seq; s++) max_ctx = std::max(max_ctx, (int)n_ctx[s]);
     p.g4 = false;
-    if (G <= 4) {
+    if (G <= 8) {  // the integer kernel: one half of 4 query heads (G <= 4) or two
         // Target 7/8 of the CUs, not all of them: a plan that fills every CU of a ragged
         // batch had ~24 busy workgroups wait 9-20 us for a CU (behind busy ones) while idle
         // splits freed others -- the dispatcher does not place a workgroup on just any free
@@ -1386,9 +1444,12 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, i
     constexpr size_t kOnePerCuLds = 64 * 1024;
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
     const bool pad = L.hdr != L.hd;
+    const bool g8 = a.Gt > 4;  // the integer kernel with two halves of 4 query heads
 #define TS_SPLIT(HDV, SC, NM)                                                                  \
-    (plan.g4 ? (pad ? (decode_split4_kernel<HDV, SC, NM, true, 4, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0) \
-                    : (decode_split4_kernel<HDV, SC, NM, false, 4, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0)) \
+    (plan.g4 ? (g8 ? (pad ? (decode_split4_kernel<HDV, SC, NM, true, 4, 2, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0) \
+                          : (decode_split4_kernel<HDV, SC, NM, false, 4, 2, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0)) \
+                    : (pad ? (decode_split4_kernel<HDV, SC, NM, true, 4, 2, 1><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0) \
+                           : (decode_split4_kernel<HDV, SC, NM, false, 4, 2, 1><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0))) \
              : pad ? (decode_split_kernel<HDV, SC, NM, true><<<grid, 64 * kNW16, 0, st>>>(a), 0)         \
                    : (decode_split_kernel<HDV, SC, NM, false><<<grid, 64 * kNW16, 0, st>>>(a), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \

@@ -156,13 +156,14 @@ __device__ inline float wave_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// apply_qk_norm scale of query head `mine` of the G (<= 8) consecutive head rows at q, computed
-// by the whole wave: every row's squares are summed as a tree across the lanes (the query side
+// apply_qk_norm scale of query head `mine` (and in out2 that of head `mine2`, when it is one of
+// them) of the G (<= 8) consecutive head rows at q, computed by the whole wave: every row's squares are summed as a tree across the lanes (the query side
 // only feeds the softmax, compared within tolerance, so the order of the sum is free) and no
 // LDS or barrier is involved.  All lanes must call it.
 // Rows of hdr floats (stride hdr), hdr <= HD.
 template <int HD>
-__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps, int hdr = HD) {
+__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps, int hdr, int mine2,
+                                          float &out2) {
     static_assert(HD % 64 == 0, "whole float lanes per row");
     constexpr int PER = HD / 64;
     const int lane = __lane_id();
@@ -181,9 +182,16 @@ __device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float
             for (int e = 0; e < PER; e++) ss += x[g][e] * x[g][e];
             const float sc = qk_norm_scale_from_sum(wave_sum(ss), hdr, eps);
             out = g == mine ? sc : out;
+            out2 = g == mine2 ? sc : out2;
         }
     }
     return out;
+}
+// The same for one head only.
+template <int HD>
+__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps, int hdr = HD) {
+    float unused = 1.0f;
+    return q_norm_scale_wave<HD>(q, G, mine, eps, hdr, -1, unused);
 }
 
 // encode(x, scale) with the quotient taken as x * rcp(scale) wherever that cannot change the

@@ -155,12 +155,13 @@ def test_golden_fixture_through_gpu(gpu):
 ORACLE_THREADS = min(16, os.cpu_count() or 1)  # the GPU box's CPU share
 
 
-def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, outliers, fused=False):
+def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, outliers, fused=False, softcap=0.0, norm=False):
     """One layer at the full BASELINE shape: the GPU runs every sequence and the oracle checks
     every (sequence, head) output on identical inputs (generated on the device and copied
     back), and every packed word and scale of the cache bit-exact.  With `fused`, the new
     token goes through ts_attn_decode_append (the launch bench.py times), otherwise through
-    ts_append_quant then ts_attn_decode."""
+    ts_append_quant then ts_attn_decode.  `softcap`: Gemma-2's score cap; `norm`: Qwen3's QK
+    norm with random weights."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     dims = synth.outlier_dims(n_kv, hd, seed) if outliers else None
@@ -168,6 +169,12 @@ def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, outliers, fused=False)
     sq = torch.as_tensor(synth.channel_scale(n_head, n_kv, hd, dims)).cuda()
     max_len = max(lens)
     p = Pair(n_seq, n_kv, hd, max_len + 1, base)
+    if norm:
+        wrng = np.random.default_rng(seed)
+        wq = (wrng.standard_normal(hd) * 0.4 + 1.0).astype(np.float32)
+        wk = (wrng.standard_normal(hd) * 0.4 + 1.0).astype(np.float32)
+        p.gpu.set_qk_norm(0, dev(wq), dev(wk), 1e-6)
+        p.ora.q_norm, p.ora.k_norm, p.ora.norm_eps = wq, wk, 1e-6
     step = 2048
     for t0 in range(0, max_len, step):
         m = min(step, max_len - t0)
@@ -181,12 +188,12 @@ def _full_size(n_seq, n_kv, n_head, hd, lens, base, seed, outliers, fused=False)
     v1 = torch.randn((n_seq, 1, n_kv, hd), generator=gen, device="cuda") * skv
     q = torch.randn((n_seq, n_head, hd), generator=gen, device="cuda") * sq
     if fused:
-        out = p.gpu.attn_decode_append(0, k1, v1, q, p.rope).cpu().numpy()
+        out = p.gpu.attn_decode_append(0, k1, v1, q, p.rope, softcap=softcap).cpu().numpy()
     else:
         p.gpu.append_quant(0, k1, v1, p.rope)
-        out = p.gpu.attn_decode(0, q, p.rope).cpu().numpy()
+        out = p.gpu.attn_decode(0, q, p.rope, softcap=softcap).cpu().numpy()
     p.ora.append(k1.cpu().numpy(), v1.cpu().numpy())
-    ref = p.ora.attend(q.cpu().numpy()[:, None], 1, threads=ORACLE_THREADS)[:, 0]
+    ref = p.ora.attend(q.cpu().numpy()[:, None], 1, softcap=softcap, threads=ORACLE_THREADS)[:, 0]
     assert_close(out, ref, f"full-size decode, every sequence and head (lens {min(lens)}..{max(lens)})")
     # the whole cache, the appended row included
     p.check_codes(upto=[l + 1 for l in lens])
@@ -251,15 +258,41 @@ def test_config2_batch1_long_context(gpu):
     (256, 4, 16, 4, 16000, False),  # 4 q heads per kv head, no append
     (96, 8, 32, 4, 8000, True),     # padded: stored as 128 dims
     (200, 4, 16, 8, 8192, True),    # padded: stored as 256 dims
+    # two halves of 4 query heads (G 5..8)
+    (128, 8, 64, 8, 8192, True),    # Llama-3-70B's attention shape: G = 8
+    (128, 4, 28, 8, 8192, False),   # Qwen2.5-7B's: G = 7
+    (64, 8, 40, 8, 8192, True),     # G = 5 on 64-dim rows
+    (256, 4, 24, 8, 8192, True),    # G = 6 on 256-dim rows
+    (96, 8, 48, 8, 8000, True),     # G = 6, padded: stored as 128 dims
 ])
 def test_integer_kernel_wide_and_padded_rows(gpu, hd, n_kv, n_head, n_seq, ctx, fused):
-    """The G <= 4 integer-QK kernel on 256-dim and padded rows, at contexts whose plan gives
-    every wave >= 4 windows (so this kernel runs): every head against the oracle, the whole
-    cache bit-exact."""
+    """The integer-QK kernel on 64-, 128-, 256-dim and padded rows with 2..8 query heads per kv
+    head, at contexts whose plan gives every wave >= 4 windows (so this kernel runs): every
+    head against the oracle, the whole cache bit-exact."""
     say(f"decode integer kernel hd={hd} G={n_head // n_kv} ctx={ctx} fused={fused}")
     rng = np.random.default_rng(hd + ctx)
     lens = [int(x) for x in rng.integers(ctx - 300, ctx, size=n_seq)]
     _full_size(n_seq, n_kv, n_head, hd, lens, 10000.0, hd + n_head, False, fused=fused)
+
+
+@pytest.mark.parametrize("G,softcap,norm", [(8, 30.0, False), (8, 0.0, True), (6, 50.0, True), (3, 30.0, True)])
+def test_integer_kernel_softcap_and_qk_norm(gpu, G, softcap, norm):
+    """The integer-QK kernel with Gemma-2's score cap and Qwen3's QK norm, one or two halves of
+    query heads, fused append: every head against the oracle, the cache bit-exact."""
+    say(f"decode integer kernel G={G} softcap={softcap} norm={norm}")
+    rng = np.random.default_rng(G * 7 + int(softcap))
+    lens = [int(x) for x in rng.integers(7800, 8192, size=8)]
+    _full_size(8, 8, 8 * G, 128, lens, 1e6, 50 + G, True, fused=True, softcap=softcap, norm=norm)
+
+
+def test_one_long_sequence_among_many_short(gpu):
+    """More (sequence, kv head) streams than the plan's workgroup target, one sequence far
+    longer than the rest: the plan still splits that one (its splits merge in the combine);
+    every head against the oracle, the cache bit-exact."""
+    say("decode one long sequence among 31 short")
+    rng = np.random.default_rng(77)
+    lens = [20000] + [int(x) for x in rng.integers(64, 400, size=31)]
+    _full_size(32, 8, 32, 128, lens, 1e6, 78, False, fused=True)
 
 
 def test_misaligned_buffers_rejected(gpu):
