@@ -12,7 +12,7 @@
 //   and scales exactly once for all G = n_head/n_kv query heads that share them.  The chunk
 //   is planned from the total context of the batch, so ragged batches get more splits for
 //   their long sequences and the count of busy workgroups stays at the planned one.
-// * each wave takes 64-position windows round robin; in the G <= 4 kernel every 16-byte load
+// * each wave takes 64-position windows round robin; in the integer kernel every 16-byte load
 //   instruction reads one contiguous kilobyte (the cache's chunk order puts each lane's K row
 //   segment and V words there), non-temporally, and each workgroup starts its windows at its
 //   own offset, so the concurrent streams spread over the HBM channels.
@@ -49,7 +49,7 @@ struct DecodeArgs {
     int n_head;
     int G;   // query heads per workgroup: n_head / n_kv, at most 8 per group (16x16 kernel)
     int Gt;  // query heads per kv head (n_head / n_kv)
-    int NG;  // head groups per kv head: grid.y = n_kv * NG (G4 kernel: 1)
+    int NG;  // head groups per kv head: grid.y = n_kv * NG (integer kernel: 1)
     int chunk;
     int n_split;  // grid.x: the last split of a sequence runs to its end
     float inv_sqrt_hd;
@@ -806,9 +806,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
 
 
 
-// ---- G <= 4: QK^T on v_mfma_i32_16x16x64_i8 ---------------------------------------------------
+// ---- G <= 8: QK^T on v_mfma_i32_16x16x64_i8 ---------------------------------------------------
 //
-// QK^T runs in exact integer arithmetic.  The B operand is K^T: column n of tile t is position
+// QK^T runs in exact integer arithmetic, for up to 8 query heads per kv head in one or two
+// halves of 4 heads (the description below is of one half; a second half has its own q operand
+// and accumulators against the same K operand).  The B operand is K^T: column n of tile t is position
 // 4n + t of the window, and lane 16 g + n supplies 16 dims of it as unsigned bytes -- the
 // nibbles of two K words, even dims from (w & 0x0F0F0F0F), odd dims from (w >> 4) & 0x0F0F0F0F,
 // 3 VALU ops per word.  The A operand holds q: row 4 h + c is base-128 digit c (c = 0 most
@@ -828,7 +830,7 @@ struct Window8 {
     floatx4 sk, sv;       // scales of positions base + 4n .. base + 4n + 3 (n = lane % 16)
 };
 
-// Buffer resources of one split for the G <= 4 kernel: K, V and both scale arrays (loads past
+// Buffer resources of one split for the integer kernel: K, V and both scale arrays (loads past
 // the bound return zeros and touch no memory).
 struct Streams4 {
     __amdgpu_buffer_rsrc_t k, v, sk, sv;
@@ -1340,8 +1342,8 @@ windows_done:
 
 }  // namespace
 
-// Split plan.  The G <= 4 kernel runs one workgroup of 4 waves per CU, the 16x16 kernel two
-// per CU.  The chunk (positions per split, a multiple of 64) is the smallest one for which
+// Split plan.  The integer kernel (G <= 8) runs one workgroup of 4 waves per CU, the 16x16
+// kernel two per CU.  The chunk (positions per split, a multiple of 64) is the smallest one for which
 // the busy workgroups of the whole batch, n_kv * sum_s ceil(n_ctx[s] / chunk), fit in that
 // target: the batch's total context spread evenly, so ragged batches give their long
 // sequences more splits and no CU gets a second workgroup.  (Measured on the config-3 shape
@@ -1349,7 +1351,7 @@ windows_done:
 // two 44.7 us, three 45.6 us.)  Splits shorter than kMinChunk leave waves without a window.
 namespace {
 constexpr int kMinChunk = 256;
-constexpr int kG4MinChunk = 1024;  // the G <= 4 kernel needs >= 4 windows per wave to pay off
+constexpr int kG4MinChunk = 1024;  // the integer kernel needs >= 4 windows per wave to pay off
 
 int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
     int64_t total = 0;
@@ -1435,13 +1437,14 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, i
     a.adv_len = adv && plan.n_split > 1 ? d_len : nullptr;
     a.adv_ctr = adv && plan.n_split > 1 ? adv : nullptr;
     dim3 grid(plan.n_split, L.H * a.NG, L.S);
-    // The G <= 4 kernel does less VALU work per window than the 16x16 one but has the longer
+    // The integer kernel does less VALU work per window than the 16x16 one but has the longer
     // per-window dependency chain; it runs when every wave streams at least 4 windows of its
     // split (plan.g4).  It fits two workgroups per CU by registers, but the plan wants one per
-    // CU: the unused dynamic LDS reservation (with the kernel's own ~17 KB, more than half of
-    // the CU's 160 KB) makes the dispatcher place busy workgroups on distinct CUs, also when
-    // the grid holds idle ones (splits past a short sequence's end) that exit at once.
-    constexpr size_t kOnePerCuLds = 64 * 1024;
+    // CU: the unused dynamic LDS reservation (with the kernel's own 13.8 KB (hd 64, one half)
+    // to 76.7 KB (hd 256, two halves), more than half of the CU's 160 KB and at most all of it)
+    // makes the dispatcher place busy workgroups on distinct CUs, also when the grid holds idle
+    // ones (splits past a short sequence's end) that exit at once.
+    constexpr size_t kOnePerCuLds = 82 * 1024;
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
     const bool pad = L.hdr != L.hd;
     const bool g8 = a.Gt > 4;  // the integer kernel with two halves of 4 query heads

@@ -149,7 +149,7 @@ hipError_t launch_shift_move(const KvLayerView &L, int seq, int keep, int shift,
 struct DecodePlan {
     int chunk;    // positions per split (multiple of 64)
     int n_split;  // splits of the longest sequence (grid.x)
-    bool g4;      // the G <= 4 kernel (integer QK^T on v_mfma_i32_16x16x64_i8)
+    bool g4;      // the integer kernel, G <= 8 (QK^T on v_mfma_i32_16x16x64_i8)
 };
 // n_ctx: keys per sequence (len + 1), on the host; n_cu: compute units of the device.
 DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu);
