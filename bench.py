@@ -802,13 +802,14 @@ def _split_kernel_name(cfg, n_cu=256):
     def chunk_for(target):
         busy = lambda c: sum(-(-x // c) for x in ctx) * cfg["n_kv"]
         hi = max(256, -(-max(ctx) // 64) * 64)
-        c = min(hi, max(256, -(-sum(ctx) * cfg["n_kv"] // target)))
-        c = -(-c // 64) * 64
+        lo = min(hi, max(256, -(-sum(ctx) * cfg["n_kv"] // target)))
+        lo = -(-lo // 64) * 64
+        c = lo
         while c < hi and busy(c) > target:
             c += 64
-        return c
+        return lo if busy(c) > target else c  # no chunk meets the target: the balanced one
 
-    g4 = cfg["n_head"] // cfg["n_kv"] <= 4 and chunk_for(n_cu - n_cu // 8) >= 1024
+    g4 = cfg["n_head"] // cfg["n_kv"] <= 8 and chunk_for(n_cu - n_cu // 8) >= 1024
     return "decode_split4_kernel" if g4 else "decode_split_kernel"
 
 
@@ -974,7 +975,7 @@ def main():
     # this configuration, as recorded in its profile summary; null when none was taken.
     traffic = traffic_commit = None
     tpath = os.path.join(ROOT, "profiles", f"decode_cfg{args.config}.md")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath) and not (args.head_dim or args.n_head):  # that profile's own workload
         with open(tpath) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
