@@ -1025,7 +1025,8 @@ __device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8
 }
 
 // NW waves per workgroup, D windows in registers per wave (D - 1 in flight while one is
-// computed).  The plan places one workgroup of 4 waves per CU (one wave per SIMD).
+// computed).  The plan places one workgroup per CU (NW = 4: one wave per SIMD; NW = 8 for
+// 64-dim rows: two).
 // PAD: the caller's head dim hdr is below the stored HD (rows of q, new K/V and the output are
 // hdr floats; the stored dims past them hold code 8 = 0, so the integer QK^T and PV run
 // unchanged over the whole stored row).
@@ -1342,8 +1343,8 @@ windows_done:
 
 }  // namespace
 
-// Split plan.  The integer kernel (G <= 8) runs one workgroup of 4 waves per CU, the 16x16
-// kernel two per CU.  The chunk (positions per split, a multiple of 64) is the smallest one for which
+// Split plan.  The integer kernel (G <= 8) runs one workgroup per CU (4 waves, 8 for 64-dim
+// rows), the 16x16 kernel two per CU.  The chunk (positions per split, a multiple of 64) is the smallest one for which
 // the busy workgroups of the whole batch, n_kv * sum_s ceil(n_ctx[s] / chunk), fit in that
 // target: the batch's total context spread evenly, so ragged batches give their long
 // sequences more splits and no CU gets a second workgroup.  (Measured on the config-3 shape
@@ -1410,6 +1411,48 @@ int decode_cap(int n_kv, int max_seq, int n_cu) {
     return std::min((max_seq + 63) / 64, 2 * n_cu / n_kv + 2);
 }
 
+namespace {
+// The integer kernel's static LDS (the arrays it declares), for the dynamic reservation below.
+template <int HD, int NW, int GH>
+constexpr size_t split4_static_lds() {
+    return (size_t)NW * 8 * GH * 64 * 2          // pts
+           + (size_t)NW * 8 * GH * (HD + 4) * 4  // mo
+           + (size_t)2 * NW * 4 * GH * 4         // mm_, ml_
+           + (size_t)2 * HD * 4 + 8 * 4           // kd, vd, xnew
+           + (size_t)NW * GH * 16 * 4 + (size_t)NW * GH * 4 * 4;  // qsum, qinv_s
+}
+
+// One integer-kernel launch.  The kernel fits two workgroups per CU by registers, but the plan
+// wants one per CU: an unused dynamic LDS reservation that takes the workgroup to 84 KB (more
+// than half of a CU's 160 KB, and at most all of it) makes the dispatcher place busy workgroups
+// on distinct CUs, also when the grid holds idle ones (splits past a short sequence's end)
+// that exit at once.
+template <int HD, bool SC, bool NM, bool PAD, int NW, int GH>
+void launch_split4(const DecodeArgs &a, int n_split, hipStream_t st) {
+    constexpr size_t kOne = 84 * 1024, own = split4_static_lds<HD, NW, GH>();
+    static_assert(own <= 160 * 1024, "integer kernel LDS");
+    constexpr size_t lds = own >= kOne ? 0 : kOne - own;
+    decode_split4_kernel<HD, SC, NM, PAD, NW, 2, GH><<<dim3(a.L.H, a.L.S, n_split), 64 * NW, lds, st>>>(a);
+}
+
+// 64-dim rows carry half the bytes per position for the same per-position softmax work: they
+// run 8 waves (two per SIMD), so that one wave's softmax overlaps the other's loads.  Config-3
+// shape with 64-dim rows: 1.170 vs 1.378 ms per step at 8 query heads per kv head, 1.017 vs
+// 1.030 at 4; ragged config 4: 0.837 vs 0.886.  (With 128-dim rows and two halves of heads 8
+// waves measured slower: 1.970 vs 1.888.)
+template <int HD, bool SC, bool NM>
+void launch_integer(const DecodeArgs &a, int n_split, bool pad, bool g8, hipStream_t st) {
+    constexpr int NW = HD == 64 ? 8 : 4;
+    if (g8) {
+        if (pad) launch_split4<HD, SC, NM, true, NW, 2>(a, n_split, st);
+        else launch_split4<HD, SC, NM, false, NW, 2>(a, n_split, st);
+    } else {
+        if (pad) launch_split4<HD, SC, NM, true, NW, 1>(a, n_split, st);
+        else launch_split4<HD, SC, NM, false, NW, 1>(a, n_split, st);
+    }
+}
+}  // namespace
+
 hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,
@@ -1439,20 +1482,12 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, i
     dim3 grid(plan.n_split, L.H * a.NG, L.S);
     // The integer kernel does less VALU work per window than the 16x16 one but has the longer
     // per-window dependency chain; it runs when every wave streams at least 4 windows of its
-    // split (plan.g4).  It fits two workgroups per CU by registers, but the plan wants one per
-    // CU: the unused dynamic LDS reservation (with the kernel's own 13.8 KB (hd 64, one half)
-    // to 76.7 KB (hd 256, two halves), more than half of the CU's 160 KB and at most all of it)
-    // makes the dispatcher place busy workgroups on distinct CUs, also when the grid holds idle
-    // ones (splits past a short sequence's end) that exit at once.
-    constexpr size_t kOnePerCuLds = 82 * 1024;
+    // split (plan.g4).
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
     const bool pad = L.hdr != L.hd;
     const bool g8 = a.Gt > 4;  // the integer kernel with two halves of 4 query heads
 #define TS_SPLIT(HDV, SC, NM)                                                                  \
-    (plan.g4 ? (g8 ? (pad ? (decode_split4_kernel<HDV, SC, NM, true, 4, 2, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0) \
-                          : (decode_split4_kernel<HDV, SC, NM, false, 4, 2, 2><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0)) \
-                    : (pad ? (decode_split4_kernel<HDV, SC, NM, true, 4, 2, 1><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0) \
-                           : (decode_split4_kernel<HDV, SC, NM, false, 4, 2, 1><<<dim3(L.H, L.S, plan.n_split), 256, kOnePerCuLds, st>>>(a), 0))) \
+    (plan.g4 ? (launch_integer<HDV, SC, NM>(a, plan.n_split, pad, g8, st), 0) \
              : pad ? (decode_split_kernel<HDV, SC, NM, true><<<grid, 64 * kNW16, 0, st>>>(a), 0)         \
                    : (decode_split_kernel<HDV, SC, NM, false><<<grid, 64 * kNW16, 0, st>>>(a), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \

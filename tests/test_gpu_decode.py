@@ -262,6 +262,7 @@ def test_config2_batch1_long_context(gpu):
     (128, 8, 64, 8, 8192, True),    # Llama-3-70B's attention shape: G = 8
     (128, 4, 28, 8, 8192, False),   # Qwen2.5-7B's: G = 7
     (64, 8, 40, 8, 8192, True),     # G = 5 on 64-dim rows
+    (64, 8, 32, 8, 8192, False),    # Llama-3.2-1B's attention shape at batch 8: G = 4, 64-dim rows
     (256, 4, 24, 8, 8192, True),    # G = 6 on 256-dim rows
     (96, 8, 48, 8, 8000, True),     # G = 6, padded: stored as 128 dims
 ])
