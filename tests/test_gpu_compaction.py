@@ -99,12 +99,12 @@ def test_separate_append_and_decode_after_compaction(gpu):
     p.check_codes()
 
 
-def test_long_split_kernel_after_compaction(gpu):
-    """32 sequences x 8 kv heads at ~4200 slots after compaction: splits of 1088 positions run
-    the 4x4x4 QK decode kernel."""
-    say("compaction long splits")
-    rng = np.random.default_rng(320)
-    n_head = 32
+@pytest.mark.parametrize("n_head", [32, 64])
+def test_long_split_kernel_after_compaction(gpu, n_head):
+    """32 sequences x 8 kv heads at ~4200 slots after compaction: the integer-QK decode kernel
+    (one split per stream) with 4 and with 8 query heads per kv head."""
+    say(f"compaction long splits, {n_head} q heads")
+    rng = np.random.default_rng(320 + n_head)
     p = Pair(32, 8, 128, 5200, 1e6, rope_n_pos=6200)
     fill(p, rng, 5000, step=1024)
     for s in range(32):

@@ -117,16 +117,18 @@ def test_advance_matches_decode_then_increment(gpu):
         assert torch.equal(x, y)
 
 
-def test_graph_replays_g4_kernel(gpu):
-    """Batch 8 of 4K-8K contexts, 32/8 heads (the G <= 4 kernel, splits of 1024 and more), with
-    two sequences one short of a multiple of 1024; four replays."""
-    say("graph replays G<=4 kernel")
+@pytest.mark.parametrize("n_head", [32, 64])
+def test_graph_replays_g4_kernel(gpu, n_head):
+    """Batch 8 of 4K-8K contexts, 8 kv heads with 4 or 8 query heads each (the integer kernel,
+    splits of 1024 and more), with two sequences one short of a multiple of 1024; four
+    replays."""
+    say(f"graph replays integer kernel, {n_head} q heads")
     rng = np.random.default_rng(310)
     lens = [8191, 8000, 6143, 7000, 5000, 8100, 4095, 6500]
     p = Pair(len(lens), 8, 128, 8300, 1e6)
     fill(p, rng, max(lens), step=1024)
     p.set_lens(lens)
-    replay_check(p, rng, 32, 4)
+    replay_check(p, rng, n_head, 4)
 
 
 def test_graph_replays_noalloc_bit_identical(gpu):
