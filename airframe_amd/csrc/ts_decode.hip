@@ -434,10 +434,13 @@ __device__ void new_token_scores(const DecodeArgs &a, int s, int hb, int G, int 
     constexpr int PPL = AppendIn<HD>::PPL;
     const float *const QN = NORM ? a.L.qn : nullptr;
     const float *qg = a.q + ((size_t)s * a.n_head + hb) * hdr;
+    float nhs[GMAX];
+    if (QN) q_norm_scales_wave<HD, GMAX>(qg, G, a.L.norm_eps, hdr, nhs);
+    // (a guard, not a break: the loop unrolls fully, so qp stays in registers)
 #pragma unroll
     for (int hh = 0; hh < GMAX; hh++) {
-        if (hh >= G) break;
-        const float nh = QN ? q_norm_scale_wave<HD>(qg, G, hh, a.L.norm_eps, hdr) : 1.0f;
+        if (hh >= G) continue;
+        const float nh = QN ? nhs[hh] : 1.0f;
         float dot = 0.0f;
 #pragma unroll
         for (int j = 0; j < PPL; j++) {
@@ -890,12 +893,15 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 // Running state of one wave.  GH = 1 (G <= 4): O^T column n < 4 is head n from the high parts
 // of p*s_v, 4 <= n < 8 head n - 4 from the low parts; GH = 2 (G <= 8): column n < 8 is head n
-// from the high parts, 8 <= n < 16 head n - 8 from the low parts.  Lane 16 hg + n runs the
-// softmax of heads hg (half 0) and 4 + hg (half 1): the exponent reference of each (uniform over
-// the lane's row) and this lane's share of its softmax sum.
+// from the high parts, 8 <= n < 16 head n - 8 from the low parts; GH = 4 (G <= 16): two sets
+// of 16 columns, column n of set 0 head n from the high parts, of set 1 from the low parts.
+// Lane 16 hg + n runs the softmax of heads hg + 4 hf (half hf): the exponent reference of each
+// (uniform over the lane's row) and this lane's share of its softmax sum.
+template <int GH>
+constexpr int kPvSets = GH == 4 ? 2 : 1;
 template <int HD, int GH>
 struct WaveState8 {
-    floatx4 o[HD / 16];
+    floatx4 o[kPvSets<GH>][HD / 16];
     float m[GH], l[GH];
 };
 
@@ -981,7 +987,7 @@ __device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8
         }
         // the O^T columns of head c take the factor of its row: head c of half hf is row c % 4
         // of al[hf] (lane 16 (c % 4))
-        const int c = GH == 1 ? (lane & 3) : (lane & 7);
+        const int c = GH == 1 ? (lane & 3) : GH == 2 ? (lane & 7) : (lane & 15);
         float f = 1.0f;
 #pragma unroll
         for (int hf = 0; hf < GH; hf++) {
@@ -993,7 +999,9 @@ __device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8
             if ((c >> 2) == hf) f = cc == 0 ? f0 : cc == 1 ? f1 : cc == 2 ? f2 : f3;
         }
 #pragma unroll
-        for (int td = 0; td < NTD; td++) st.o[td] *= f;
+        for (int ps = 0; ps < kPvSets<GH>; ps++)
+#pragma unroll
+            for (int td = 0; td < NTD; td++) st.o[ps][td] *= f;
     }
 #pragma unroll
     for (int hf = 0; hf < GH; hf++) st.l[hf] += (p[hf][0] + p[hf][1]) + (p[hf][2] + p[hf][3]);
@@ -1012,15 +1020,20 @@ __device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8
 #pragma unroll
     for (int b = 0; b < 2; b++) {
         // GH = 1: columns 8..15 read real p values; their outputs are never used
-        const half8 pb = *reinterpret_cast<const half8 *>(&pt[GH == 1 ? (n & 7) : n][32 * b + 8 * g]);
+        half8 pb[kPvSets<GH>];
+#pragma unroll
+        for (int ps = 0; ps < kPvSets<GH>; ps++)
+            pb[ps] = *reinterpret_cast<const half8 *>(&pt[GH == 1 ? (n & 7) : 16 * ps + n][32 * b + 8 * g]);
         // every word of the block dequantized into its own registers first, so the conversions
         // of later words overlap the matrix instructions of earlier ones
         half8 va[NTD];
 #pragma unroll
         for (int td = 0; td < NTD; td++) va[td] = dequant8(w.vw[b][td], dc);
 #pragma unroll
-        for (int td = 0; td < NTD; td++)
-            st.o[td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[td], pb, st.o[td], 0, 0, 0);
+        for (int ps = 0; ps < kPvSets<GH>; ps++)
+#pragma unroll
+            for (int td = 0; td < NTD; td++)
+                st.o[ps][td] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[td], pb[ps], st.o[ps][td], 0, 0, 0);
     }
 }
 
@@ -1067,7 +1080,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     __shared__ __align__(16) float mo[NW][8 * GH * OST];  // O^T columns, OST floats apart
     __shared__ float mm_[NW][4 * GH], ml_[NW][4 * GH];
     __shared__ __align__(16) float kd[HD], vd[HD];
-    __shared__ float xnew[8];
+    __shared__ float xnew[4 * GH < 8 ? 8 : 4 * GH];
     __shared__ int32_t qsum[NW][GH][16];  // per wave and half: digit sums of the 16 q rows
     __shared__ float qinv_s[NW][GH][4];   // per wave and half: 2^-e of each head's q scale
 
@@ -1164,13 +1177,18 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
                                 : make_float2(1.0f, 0.0f);
             }
         }
+        // QK norm scale of this lane's head in each half (all heads' scales, then a select)
         float ns[GH];
-        ns[GH - 1] = 1.0f;
-        if (QN)
-            ns[0] = q_norm_scale_wave<HD>(a.q + ((size_t)s * a.n_head + h * G) * hdr, G, hl[0] ? hh : 0, L.norm_eps,
-                                          hdr, GH == 2 && hl[GH - 1] ? hh + 4 : -1, ns[GH - 1]);
-        else
-            ns[0] = 1.0f;
+#pragma unroll
+        for (int hf = 0; hf < GH; hf++) ns[hf] = 1.0f;
+        if (QN) {
+            float nall[4 * GH];
+            q_norm_scales_wave<HD, 4 * GH>(a.q + ((size_t)s * a.n_head + h * G) * hdr, G, L.norm_eps, hdr, nall);
+#pragma unroll
+            for (int hf = 0; hf < GH; hf++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) ns[hf] = hh == c ? nall[4 * hf + c] : ns[hf];
+        }
         // The appending wave (the last: it has the fewest windows) quantizes the new token and
         // scores it against every head before its windows; the others start at once.  Its
         // loads go out with q's.  kd, vd and xnew are read after the barrier that opens the
@@ -1253,7 +1271,9 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
 
     WaveState8<HD, GH> st;
 #pragma unroll
-    for (int td = 0; td < NTD; td++) st.o[td] = (floatx4)0.0f;
+    for (int ps = 0; ps < kPvSets<GH>; ps++)
+#pragma unroll
+        for (int td = 0; td < NTD; td++) st.o[ps][td] = (floatx4)0.0f;
     bool live[GH];
 #pragma unroll
     for (int hf = 0; hf < GH; hf++) {
@@ -1298,10 +1318,13 @@ windows_done:
             ml_[wave][4 * hf + g] = l_run;
         }
     }
-    if (n < 8 * GH) {
 #pragma unroll
-        for (int td = 0; td < NTD; td++) *reinterpret_cast<floatx4 *>(&mo[wave][n * OST + 16 * td + 4 * g]) = st.o[td];
-    }
+    for (int ps = 0; ps < kPvSets<GH>; ps++)
+        if (16 * ps + n < 8 * GH) {
+#pragma unroll
+            for (int td = 0; td < NTD; td++)
+                *reinterpret_cast<floatx4 *>(&mo[wave][(16 * ps + n) * OST + 16 * td + 4 * g]) = st.o[ps][td];
+        }
     __syncthreads();
 
     constexpr int V4 = HD / 4;
@@ -1384,12 +1407,12 @@ int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
 }
 }  // namespace
 
-DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu) {
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, int int_gmax) {
     DecodePlan p;
     int max_ctx = 1;
     for (int s = 0; s < n_seq; s++) max_ctx = std::max(max_ctx, (int)n_ctx[s]);
     p.g4 = false;
-    if (G <= 8) {  // the integer kernel: one half of 4 query heads (G <= 4) or two
+    if (G <= int_gmax) {  // the integer kernel: one, two or four halves of 4 query heads
         // Target 7/8 of the CUs, not all of them: a plan that fills every CU of a ragged
         // batch had ~24 busy workgroups wait 9-20 us for a CU (behind busy ones) while idle
         // splits freed others -- the dispatcher does not place a workgroup on just any free
@@ -1418,7 +1441,7 @@ constexpr size_t split4_static_lds() {
     return (size_t)NW * 8 * GH * 64 * 2          // pts
            + (size_t)NW * 8 * GH * (HD + 4) * 4  // mo
            + (size_t)2 * NW * 4 * GH * 4         // mm_, ml_
-           + (size_t)2 * HD * 4 + 8 * 4           // kd, vd, xnew
+           + (size_t)2 * HD * 4 + (4 * GH < 8 ? 8 : 4 * GH) * 4  // kd, vd, xnew
            + (size_t)NW * GH * 16 * 4 + (size_t)NW * GH * 4 * 4;  // qsum, qinv_s
 }
 
@@ -1441,9 +1464,17 @@ void launch_split4(const DecodeArgs &a, int n_split, hipStream_t st) {
 // 1.030 at 4; ragged config 4: 0.837 vs 0.886.  (With 128-dim rows and two halves of heads 8
 // waves measured slower: 1.970 vs 1.888.)
 template <int HD, bool SC, bool NM>
-void launch_integer(const DecodeArgs &a, int n_split, bool pad, bool g8, hipStream_t st) {
+void launch_integer(const DecodeArgs &a, int n_split, bool pad, int Gt, hipStream_t st) {
     constexpr int NW = HD == 64 ? 8 : 4;
-    if (g8) {
+    if constexpr (HD <= 128) {
+        if (Gt > 8) {  // four halves of query heads (the plan allows them up to 128-dim rows),
+                       // 4 waves: their registers need a SIMD each
+            if (pad) launch_split4<HD, SC, NM, true, 4, 4>(a, n_split, st);
+            else launch_split4<HD, SC, NM, false, 4, 4>(a, n_split, st);
+            return;
+        }
+    }
+    if (Gt > 4) {
         if (pad) launch_split4<HD, SC, NM, true, NW, 2>(a, n_split, st);
         else launch_split4<HD, SC, NM, false, NW, 2>(a, n_split, st);
     } else {
@@ -1466,7 +1497,7 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, i
     a.n_head = n_head;
     a.Gt = n_head / L.H;
     a.NG = plan.g4 ? 1 : (a.Gt + 7) / 8;
-    a.G = std::min(a.Gt, 8);
+    a.G = plan.g4 ? a.Gt : std::min(a.Gt, 8);
     a.chunk = plan.chunk;
     a.n_split = plan.n_split;
     a.inv_sqrt_hd = 1.0f / sqrtf((float)L.hdr);
@@ -1485,9 +1516,8 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, i
     // split (plan.g4).
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr || L.kn != nullptr;
     const bool pad = L.hdr != L.hd;
-    const bool g8 = a.Gt > 4;  // the integer kernel with two halves of 4 query heads
 #define TS_SPLIT(HDV, SC, NM)                                                                  \
-    (plan.g4 ? (launch_integer<HDV, SC, NM>(a, plan.n_split, pad, g8, st), 0) \
+    (plan.g4 ? (launch_integer<HDV, SC, NM>(a, plan.n_split, pad, a.Gt, st), 0) \
              : pad ? (decode_split_kernel<HDV, SC, NM, true><<<grid, 64 * kNW16, 0, st>>>(a), 0)         \
                    : (decode_split_kernel<HDV, SC, NM, false><<<grid, 64 * kNW16, 0, st>>>(a), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \

@@ -149,10 +149,14 @@ hipError_t launch_shift_move(const KvLayerView &L, int seq, int keep, int shift,
 struct DecodePlan {
     int chunk;    // positions per split (multiple of 64)
     int n_split;  // splits of the longest sequence (grid.x)
-    bool g4;      // the integer kernel, G <= 8 (QK^T on v_mfma_i32_16x16x64_i8)
+    bool g4;      // the integer kernel, G <= 16 (QK^T on v_mfma_i32_16x16x64_i8)
 };
 // n_ctx: keys per sequence (len + 1), on the host; n_cu: compute units of the device.
-DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu);
+// int_gmax: the most query heads per kv head the integer kernel takes at this stored head dim.
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, int int_gmax);
+// The integer kernel takes up to 16 query heads per kv head on stored rows up to 128 dims, 8 on
+// 256-dim rows.
+inline int decode_int_gmax(int stored_hd) { return stored_hd <= 128 ? 16 : 8; }
 // Upper bound of plan.n_split for any lengths up to max_seq (sizes the workspace).
 int decode_cap(int n_kv, int max_seq, int n_cu);
 // adv: null, or the cache's arrival counter: the launch then also advances every length by

@@ -156,14 +156,13 @@ __device__ inline float wave_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// apply_qk_norm scale of query head `mine` (and in out2 that of head `mine2`, when it is one of
-// them) of the G (<= 8) consecutive head rows at q, computed by the whole wave: every row's squares are summed as a tree across the lanes (the query side
+// apply_qk_norm scale of query head `mine` of the G (<= 8) consecutive head rows at q, computed
+// by the whole wave: every row's squares are summed as a tree across the lanes (the query side
 // only feeds the softmax, compared within tolerance, so the order of the sum is free) and no
 // LDS or barrier is involved.  All lanes must call it.
 // Rows of hdr floats (stride hdr), hdr <= HD.
 template <int HD>
-__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps, int hdr, int mine2,
-                                          float &out2) {
+__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps, int hdr = HD) {
     static_assert(HD % 64 == 0, "whole float lanes per row");
     constexpr int PER = HD / 64;
     const int lane = __lane_id();
@@ -182,16 +181,31 @@ __device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float
             for (int e = 0; e < PER; e++) ss += x[g][e] * x[g][e];
             const float sc = qk_norm_scale_from_sum(wave_sum(ss), hdr, eps);
             out = g == mine ? sc : out;
-            out2 = g == mine2 ? sc : out2;
         }
     }
     return out;
 }
-// The same for one head only.
-template <int HD>
-__device__ inline float q_norm_scale_wave(const float *q, int G, int mine, float eps, int hdr = HD) {
-    float unused = 1.0f;
-    return q_norm_scale_wave<HD>(q, G, mine, eps, hdr, -1, unused);
+
+// The apply_qk_norm scales of all G (<= GMAX) consecutive query head rows at q, the same in
+// every lane (1 past G); computed by the whole wave like q_norm_scale_wave.
+template <int HD, int GMAX>
+__device__ inline void q_norm_scales_wave(const float *q, int G, float eps, int hdr, float (&out)[GMAX]) {
+    static_assert(HD % 64 == 0, "whole float lanes per row");
+    constexpr int PER = HD / 64;
+    const int lane = __lane_id();
+#pragma unroll
+    for (int g = 0; g < GMAX; g++) {
+        out[g] = 1.0f;
+        if (g < G) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < PER; e++) {
+                const float x = PER * lane + e < hdr ? q[(size_t)g * hdr + PER * lane + e] : 0.0f;
+                ss += x * x;
+            }
+            out[g] = qk_norm_scale_from_sum(wave_sum(ss), hdr, eps);
+        }
+    }
 }
 
 // encode(x, scale) with the quotient taken as x * rcp(scale) wherever that cannot change the

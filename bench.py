@@ -809,7 +809,9 @@ def _split_kernel_name(cfg, n_cu=256):
             c += 64
         return lo if busy(c) > target else c  # no chunk meets the target: the balanced one
 
-    g4 = cfg["n_head"] // cfg["n_kv"] <= 8 and chunk_for(n_cu - n_cu // 8) >= 1024
+    stored = 64 if cfg["hd"] <= 64 else 128 if cfg["hd"] <= 128 else 256
+    gmax = 16 if stored <= 128 else 8  # decode_int_gmax (ts_internal.h)
+    g4 = cfg["n_head"] // cfg["n_kv"] <= gmax and chunk_for(n_cu - n_cu // 8) >= 1024
     return "decode_split4_kernel" if g4 else "decode_split_kernel"
 
 

@@ -99,10 +99,10 @@ def test_separate_append_and_decode_after_compaction(gpu):
     p.check_codes()
 
 
-@pytest.mark.parametrize("n_head", [32, 64])
+@pytest.mark.parametrize("n_head", [32, 64, 128])
 def test_long_split_kernel_after_compaction(gpu, n_head):
     """32 sequences x 8 kv heads at ~4200 slots after compaction: the integer-QK decode kernel
-    (one split per stream) with 4 and with 8 query heads per kv head."""
+    (one split per stream) with 4, 8 and 16 query heads per kv head."""
     say(f"compaction long splits, {n_head} q heads")
     rng = np.random.default_rng(320 + n_head)
     p = Pair(32, 8, 128, 5200, 1e6, rope_n_pos=6200)

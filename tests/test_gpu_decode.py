@@ -265,9 +265,13 @@ def test_config2_batch1_long_context(gpu):
     (64, 8, 32, 8, 8192, False),    # Llama-3.2-1B's attention shape at batch 8: G = 4, 64-dim rows
     (256, 4, 24, 8, 8192, True),    # G = 6 on 256-dim rows
     (96, 8, 48, 8, 8000, True),     # G = 6, padded: stored as 128 dims
+    # four halves (G 9..16)
+    (128, 8, 128, 8, 8192, True),   # Llama-3.1-405B's attention shape: G = 16
+    (64, 4, 48, 8, 8192, False),    # G = 12 on 64-dim rows
+    (96, 8, 80, 8, 8000, True),     # G = 10, padded: stored as 128 dims
 ])
 def test_integer_kernel_wide_and_padded_rows(gpu, hd, n_kv, n_head, n_seq, ctx, fused):
-    """The integer-QK kernel on 64-, 128-, 256-dim and padded rows with 2..8 query heads per kv
+    """The integer-QK kernel on 64-, 128-, 256-dim and padded rows with 2..16 query heads per kv
     head, at contexts whose plan gives every wave >= 4 windows (so this kernel runs): every
     head against the oracle, the whole cache bit-exact."""
     say(f"decode integer kernel hd={hd} G={n_head // n_kv} ctx={ctx} fused={fused}")
@@ -276,7 +280,8 @@ def test_integer_kernel_wide_and_padded_rows(gpu, hd, n_kv, n_head, n_seq, ctx, 
     _full_size(n_seq, n_kv, n_head, hd, lens, 10000.0, hd + n_head, False, fused=fused)
 
 
-@pytest.mark.parametrize("G,softcap,norm", [(8, 30.0, False), (8, 0.0, True), (6, 50.0, True), (3, 30.0, True)])
+@pytest.mark.parametrize("G,softcap,norm", [(8, 30.0, False), (8, 0.0, True), (6, 50.0, True), (3, 30.0, True),
+                                             (16, 30.0, True), (13, 0.0, True)])
 def test_integer_kernel_softcap_and_qk_norm(gpu, G, softcap, norm):
     """The integer-QK kernel with Gemma-2's score cap and Qwen3's QK norm, one or two halves of
     query heads, fused append: every head against the oracle, the cache bit-exact."""
