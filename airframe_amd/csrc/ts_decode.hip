@@ -847,26 +847,26 @@ constexpr int kNT = 2;
 // contiguous kilobyte (the cache's chunk order puts exactly this lane's operand words there);
 // the scale instructions read the window's 256 bytes, every 16 bytes by the 4 lanes of a
 // column.
-template <int HD>
+template <int HD, int POL = kNT>
 __device__ __forceinline__ void load_window8(Window8<HD> &w, const Streams4 &st, int base, int lane) {
     constexpr int NKW = HD / 8, NTD = HD / 16, ROWB = HD / 2;
 #pragma unroll
     for (int j = 0; j < NKW / 4; j++) {
-        const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, lane * 16 + j * 1024, base * ROWB, kNT);
+        const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.k, lane * 16 + j * 1024, base * ROWB, POL);
         w.kw[4 * j + 0] = t4[0]; w.kw[4 * j + 1] = t4[1]; w.kw[4 * j + 2] = t4[2]; w.kw[4 * j + 3] = t4[3];
     }
 #pragma unroll
     for (int b = 0; b < 2; b++) {
 #pragma unroll
         for (int q4 = 0; q4 < NTD / 4; q4++) {
-            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.v, lane * 16 + q4 * 1024 + b * (HD * 16), (base / 32) * (HD * 16), kNT);
+            const u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(st.v, lane * 16 + q4 * 1024 + b * (HD * 16), (base / 32) * (HD * 16), POL);
             w.vw[b][4 * q4 + 0] = t4[0]; w.vw[b][4 * q4 + 1] = t4[1];
             w.vw[b][4 * q4 + 2] = t4[2]; w.vw[b][4 * q4 + 3] = t4[3];
         }
     }
     const int so = (lane & 15) * 16;
-    w.sk = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(st.sk, so, base * 4, kNT));
-    w.sv = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(st.sv, so, base * 4, kNT));
+    w.sk = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(st.sk, so, base * 4, POL));
+    w.sv = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(st.sv, so, base * 4, POL));
 }
 
 template <int CTRL>
@@ -1043,8 +1043,11 @@ __device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8
 // PAD: the caller's head dim hdr is below the stored HD (rows of q, new K/V and the output are
 // hdr floats; the stored dims past them hold code 8 = 0, so the integer QK^T and PV run
 // unchanged over the whole stored row).
-// GH: halves of 4 query heads (1: G <= 4, 2: G <= 8).
-template <int HD, bool SOFTCAP, bool NORM, bool PAD, int NW, int D, int GH>
+// GH: halves of 4 query heads per wave (1: G <= 4, 2: G <= 8, 4: G <= 16).  HG: head groups of
+// the workgroup: with HG = 2, waves 0 .. NW/2 - 1 take query heads 0..7 and the others heads
+// 8..15, both groups over the same windows in the same order (the second read of a window
+// comes from L2, so cached loads), each with NW/2 waves.
+template <int HD, bool SOFTCAP, bool NORM, bool PAD, int NW, int D, int GH, int HG = 1>
 __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeArgs a) {
     constexpr int NTD = HD / 16;
     constexpr int NM = HD / 64;  // i8 instructions per 16-position tile
@@ -1080,7 +1083,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     __shared__ __align__(16) float mo[NW][8 * GH * OST];  // O^T columns, OST floats apart
     __shared__ float mm_[NW][4 * GH], ml_[NW][4 * GH];
     __shared__ __align__(16) float kd[HD], vd[HD];
-    __shared__ float xnew[4 * GH < 8 ? 8 : 4 * GH];
+    __shared__ float xnew[4 * GH * HG < 8 ? 8 : 4 * GH * HG];
     __shared__ int32_t qsum[NW][GH][16];  // per wave and half: digit sums of the 16 q rows
     __shared__ float qinv_s[NW][GH][4];   // per wave and half: 2^-e of each head's q scale
 
@@ -1104,26 +1107,33 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     // (Without the hand-over the appending wave ended ~2 us after the others: config 3
     // 1.880 vs 1.855 ms per step, measured with claims through an LDS counter.)  Window
     // indices past the wave's count load from past the bound (zeros, no memory traffic).
+    // (per head group: NWG waves, wave wl of group hgp; only the appending wave's group hands
+    // windows over)
+    constexpr int NWG = NW / HG;
+    const int hgp = __builtin_amdgcn_readfirstlane(wave / NWG), wl = wave - NWG * hgp;
     const int nwin = (end - start + 63) >> 6;
-    const int own = wave < nwin ? (nwin - wave + NW - 1) / NW : 0;
-    const int lastc = NW - 1 < nwin ? (nwin - (NW - 1) + NW - 1) / NW : 0;  // the last wave's claims
-    const int kApp = fused ? min(3, lastc / 3) : 0;
+    const int own = wl < nwin ? (nwin - wl + NWG - 1) / NWG : 0;
+    const int lastc = NWG - 1 < nwin ? (nwin - (NWG - 1) + NWG - 1) / NWG : 0;  // the last wave's claims
+    const int kApp = fused && hgp == HG - 1 ? min(3, lastc / 3) : 0;
     const int keep = lastc - kApp;  // claims the last wave keeps
-    const int extra = wave < NW - 1 ? (kApp - wave + NW - 2) / (NW - 1) : 0;
-    const int cnt = wave < NW - 1 ? own + extra : keep;
+    const int extra = wl < NWG - 1 ? (kApp - wl + NWG - 2) / (NWG - 1) : 0;
+    const int cnt = wl < NWG - 1 ? own + extra : keep;
     // (s 13 + h 5 + split 7: the workgroups on one XCD -- the same kv head for one split --
     // start at distinct windows; measured against (row 37 + split 11), whose offsets repeat
     // every 4 sequences of a head: config 3 1.798 vs 1.834 ms per step)
-    const int R = nwin ? (int)((unsigned)(NW * (s * 13 + h * 5 + split * 7)) % (unsigned)nwin) : 0;
+    const int R = nwin ? (int)((unsigned)(NWG * (s * 13 + h * 5 + split * 7)) % (unsigned)nwin) : 0;
     const int oob = start + 64 * nwin;
     auto win_base = [&](int i) {
         if (i >= cnt) return oob;
-        const int j = i < own ? NW * i + wave : NW * (keep + (NW - 1) * (i - own) + wave) + NW - 1;
+        const int j = i < own ? NWG * i + wl : NWG * (keep + (NWG - 1) * (i - own) + wl) + NWG - 1;
         int r = j + R;
         r = r >= nwin ? r - nwin : r;
         return start + 64 * r;
     };
     Window8<HD> w[D];
+    // this wave's query heads: Gg of them from head hgb of the sequence (HG = 2: up to 8 a group)
+    const int Gg = HG == 1 ? G : max(0, min(8, G - 8 * hgp));
+    const int hgb = h * G + (HG == 1 ? 0 : 8 * hgp);
 
     // q operand: lane 16 g + n holds row n = 4 hh + c (digit c of head hh) for k-group g, i.e.
     // dims 64 m + 16 g .. + 15 of instruction m, bytes [even dims of word 8m + 2g, its odd
@@ -1134,7 +1144,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     float qinv[GH];
     const bool appender = fused && wave == NW - 1;
     AppendIn<HD> ain;
-    float2 qp[4 * GH][AppendIn<HD>::PPL];
+    float2 qp[4 * GH * HG][AppendIn<HD>::PPL];
     {
         // half hf: lane 16 g + n holds digit dg of head hh + 4 hf
         const int n = lane & 15, g = lane >> 4, hh = n >> 2, dg = n & 3;
@@ -1143,8 +1153,8 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         float2 qcs[NM][8];
 #pragma unroll
         for (int hf = 0; hf < GH; hf++) {
-            hl[hf] = hh + 4 * hf < G;
-            const float *qrow = a.q + ((size_t)s * a.n_head + h * G + (hl[hf] ? hh + 4 * hf : 0)) * hdr;
+            hl[hf] = hh + 4 * hf < Gg;
+            const float *qrow = a.q + ((size_t)s * a.n_head + hgb + (hl[hf] ? hh + 4 * hf : 0)) * hdr;
 #pragma unroll
             for (int m = 0; m < NM; m++) {
                 const int d0 = 64 * m + 16 * g;
@@ -1183,7 +1193,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         for (int hf = 0; hf < GH; hf++) ns[hf] = 1.0f;
         if (QN) {
             float nall[4 * GH];
-            q_norm_scales_wave<HD, 4 * GH>(a.q + ((size_t)s * a.n_head + h * G) * hdr, G, L.norm_eps, hdr, nall);
+            q_norm_scales_wave<HD, 4 * GH>(a.q + ((size_t)s * a.n_head + hgb) * hdr, Gg, L.norm_eps, hdr, nall);
 #pragma unroll
             for (int hf = 0; hf < GH; hf++)
 #pragma unroll
@@ -1195,11 +1205,11 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         // merge.
         if (appender) {
             append_load<HD, NORM>(a, s, h, qpos, lane, ain, hdr);
-            load_q_pairs<HD, 4 * GH>(a, s, h * G, G, lane, qp, hdr);
+            load_q_pairs<HD, 4 * GH * HG>(a, s, h * G, G, lane, qp, hdr);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int d = 0; d < D - 1; d++) load_window8<HD>(w[d], str, win_base(d), lane);
+        for (int d = 0; d < D - 1; d++) load_window8<HD, HG == 1 ? kNT : 0>(w[d], str, win_base(d), lane);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int hf = 0; hf < GH; hf++) {
@@ -1266,7 +1276,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     }
     if (appender) {
         append_store<HD, NORM>(a, s, h, qpos, lane, ain, kd, vd, hdr);
-        new_token_scores<HD, SOFTCAP, NORM, 4 * GH>(a, s, h * G, G, lane, qp, ain.cs, kd, xnew, hdr);
+        new_token_scores<HD, SOFTCAP, NORM, 4 * GH * HG>(a, s, h * G, G, lane, qp, ain.cs, kd, xnew, hdr);
     }
 
     WaveState8<HD, GH> st;
@@ -1279,7 +1289,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     for (int hf = 0; hf < GH; hf++) {
         st.m[hf] = kMinit;
         st.l[hf] = 0.0f;
-        live[hf] = (lane >> 4) + 4 * hf < G;
+        live[hf] = (lane >> 4) + 4 * hf < Gg;
     }
     _Float16 (*pt)[64] = pts[wave];
 
@@ -1288,7 +1298,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
         while (true) {
 #pragma unroll
             for (int d = 0; d < D; d++) {
-                load_window8<HD>(w[(d + D - 1) % D], str, win_base(it + D - 1), lane);
+                load_window8<HD, HG == 1 ? kNT : 0>(w[(d + D - 1) % D], str, win_base(it + D - 1), lane);
                 // keep the prefetch here: the scheduler would otherwise sink it below the use.
                 // (Refilling a slot right after its window is processed instead measured
                 // slower: config 3 1.871 vs 1.848 ms per step, config 4 1.63 vs 1.46.)
@@ -1330,19 +1340,21 @@ windows_done:
     constexpr int V4 = HD / 4;
     for (int idx = tid; idx < G * V4; idx += 64 * NW) {
         const int hh = idx / V4, d = 4 * (idx % V4);
+        // head hh is head lh of group grp, held by that group's NWG waves from wave wb
+        const int grp = HG == 1 ? 0 : hh >> 3, lh = hh - 8 * grp, wb = NWG * grp;
         float M = kMinit;
 #pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, mm_[w][hh]);
+        for (int w = 0; w < NWG; w++) M = fmaxf(M, mm_[wb + w][lh]);
         if (fused) M = fmaxf(M, xnew[hh]);
         floatx4 acc = (floatx4)0.0f;
         float lsum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float e = exp2f(mm_[w][hh] - M);
-            const floatx4 hi = *reinterpret_cast<const floatx4 *>(&mo[w][hh * OST + d]);
-            const floatx4 lo = *reinterpret_cast<const floatx4 *>(&mo[w][(hh + 4 * GH) * OST + d]);
+        for (int w = 0; w < NWG; w++) {
+            const float e = exp2f(mm_[wb + w][lh] - M);
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(&mo[wb + w][lh * OST + d]);
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(&mo[wb + w][(lh + 4 * GH) * OST + d]);
             acc += e * (hi + lo);
-            lsum += e * ml_[w][hh];
+            lsum += e * ml_[wb + w][lh];
         }
         if (fused) {
             const float e = exp2f(xnew[hh] - M);
@@ -1436,12 +1448,12 @@ int decode_cap(int n_kv, int max_seq, int n_cu) {
 
 namespace {
 // The integer kernel's static LDS (the arrays it declares), for the dynamic reservation below.
-template <int HD, int NW, int GH>
+template <int HD, int NW, int GH, int HG>
 constexpr size_t split4_static_lds() {
     return (size_t)NW * 8 * GH * 64 * 2          // pts
            + (size_t)NW * 8 * GH * (HD + 4) * 4  // mo
            + (size_t)2 * NW * 4 * GH * 4         // mm_, ml_
-           + (size_t)2 * HD * 4 + (4 * GH < 8 ? 8 : 4 * GH) * 4  // kd, vd, xnew
+           + (size_t)2 * HD * 4 + (4 * GH * HG < 8 ? 8 : 4 * GH * HG) * 4  // kd, vd, xnew
            + (size_t)NW * GH * 16 * 4 + (size_t)NW * GH * 4 * 4;  // qsum, qinv_s
 }
 
@@ -1450,12 +1462,12 @@ constexpr size_t split4_static_lds() {
 // than half of a CU's 160 KB, and at most all of it) makes the dispatcher place busy workgroups
 // on distinct CUs, also when the grid holds idle ones (splits past a short sequence's end)
 // that exit at once.
-template <int HD, bool SC, bool NM, bool PAD, int NW, int GH>
+template <int HD, bool SC, bool NM, bool PAD, int NW, int GH, int HG = 1>
 void launch_split4(const DecodeArgs &a, int n_split, hipStream_t st) {
-    constexpr size_t kOne = 84 * 1024, own = split4_static_lds<HD, NW, GH>();
+    constexpr size_t kOne = 84 * 1024, own = split4_static_lds<HD, NW, GH, HG>();
     static_assert(own <= 160 * 1024, "integer kernel LDS");
     constexpr size_t lds = own >= kOne ? 0 : kOne - own;
-    decode_split4_kernel<HD, SC, NM, PAD, NW, 2, GH><<<dim3(a.L.H, a.L.S, n_split), 64 * NW, lds, st>>>(a);
+    decode_split4_kernel<HD, SC, NM, PAD, NW, 2, GH, HG><<<dim3(a.L.H, a.L.S, n_split), 64 * NW, lds, st>>>(a);
 }
 
 // 64-dim rows carry half the bytes per position for the same per-position softmax work: they
@@ -1467,10 +1479,19 @@ template <int HD, bool SC, bool NM>
 void launch_integer(const DecodeArgs &a, int n_split, bool pad, int Gt, hipStream_t st) {
     constexpr int NW = HD == 64 ? 8 : 4;
     if constexpr (HD <= 128) {
-        if (Gt > 8) {  // four halves of query heads (the plan allows them up to 128-dim rows),
-                       // 4 waves: their registers need a SIMD each
-            if (pad) launch_split4<HD, SC, NM, true, 4, 4>(a, n_split, st);
-            else launch_split4<HD, SC, NM, false, 4, 4>(a, n_split, st);
+        // More than 8 query heads per kv head (the plan allows them up to 128-dim rows).  On
+        // 64-dim rows: two head groups of 4 waves, two halves each (config-3 shape with 128 q
+        // heads 1.955 vs 2.199 ms per step); on 128-dim rows: four halves in one wave per SIMD
+        // (2.86 vs 3.39 ms with head groups, whose second read of each window does not all come
+        // from L2).
+        if (Gt > 8) {
+            if constexpr (HD == 64) {
+                if (pad) launch_split4<HD, SC, NM, true, 8, 2, 2>(a, n_split, st);
+                else launch_split4<HD, SC, NM, false, 8, 2, 2>(a, n_split, st);
+            } else {
+                if (pad) launch_split4<HD, SC, NM, true, 4, 4>(a, n_split, st);
+                else launch_split4<HD, SC, NM, false, 4, 4>(a, n_split, st);
+            }
             return;
         }
     }

@@ -267,7 +267,8 @@ def test_config2_batch1_long_context(gpu):
     (96, 8, 48, 8, 8000, True),     # G = 6, padded: stored as 128 dims
     # four halves (G 9..16)
     (128, 8, 128, 8, 8192, True),   # Llama-3.1-405B's attention shape: G = 16
-    (64, 4, 48, 8, 8192, False),    # G = 12 on 64-dim rows
+    (64, 4, 48, 8, 8192, False),    # G = 12 on 64-dim rows (two head groups of waves)
+    (64, 8, 128, 8, 8192, True),    # G = 16 on 64-dim rows
     (96, 8, 80, 8, 8000, True),     # G = 10, padded: stored as 128 dims
 ])
 def test_integer_kernel_wide_and_padded_rows(gpu, hd, n_kv, n_head, n_seq, ctx, fused):
@@ -280,15 +281,17 @@ def test_integer_kernel_wide_and_padded_rows(gpu, hd, n_kv, n_head, n_seq, ctx, 
     _full_size(n_seq, n_kv, n_head, hd, lens, 10000.0, hd + n_head, False, fused=fused)
 
 
-@pytest.mark.parametrize("G,softcap,norm", [(8, 30.0, False), (8, 0.0, True), (6, 50.0, True), (3, 30.0, True),
-                                             (16, 30.0, True), (13, 0.0, True)])
-def test_integer_kernel_softcap_and_qk_norm(gpu, G, softcap, norm):
-    """The integer-QK kernel with Gemma-2's score cap and Qwen3's QK norm, one or two halves of
-    query heads, fused append: every head against the oracle, the cache bit-exact."""
-    say(f"decode integer kernel G={G} softcap={softcap} norm={norm}")
-    rng = np.random.default_rng(G * 7 + int(softcap))
+@pytest.mark.parametrize("G,softcap,norm,hd", [(8, 30.0, False, 128), (8, 0.0, True, 128), (6, 50.0, True, 128),
+                                                (3, 30.0, True, 128), (16, 30.0, True, 128), (13, 0.0, True, 128),
+                                                (16, 30.0, True, 64), (7, 0.0, True, 64)])
+def test_integer_kernel_softcap_and_qk_norm(gpu, G, softcap, norm, hd):
+    """The integer-QK kernel with Gemma-2's score cap and Qwen3's QK norm, one, two or four
+    halves of query heads (on 64-dim rows also two head groups of waves), fused append: every
+    head against the oracle, the cache bit-exact."""
+    say(f"decode integer kernel G={G} hd={hd} softcap={softcap} norm={norm}")
+    rng = np.random.default_rng(G * 7 + int(softcap) + hd)
     lens = [int(x) for x in rng.integers(7800, 8192, size=8)]
-    _full_size(8, 8, 8 * G, 128, lens, 1e6, 50 + G, True, fused=True, softcap=softcap, norm=norm)
+    _full_size(8, 8, 8 * G, hd, lens, 1e6, 50 + G, True, fused=True, softcap=softcap, norm=norm)
 
 
 def test_one_long_sequence_among_many_short(gpu):
