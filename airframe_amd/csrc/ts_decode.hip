@@ -47,7 +47,8 @@ struct DecodeArgs {
     const float *rope;
     int rope_pairs;
     int n_head;
-    int G;   // query heads per workgroup: n_head / n_kv, at most 8 per group (16x16 kernel)
+    int G;   // query heads per workgroup: n_head / n_kv (integer kernel, up to 16), at most 8 per
+             // group (16x16 kernel)
     int Gt;  // query heads per kv head (n_head / n_kv)
     int NG;  // head groups per kv head: grid.y = n_kv * NG (integer kernel: 1)
     int chunk;
