@@ -810,11 +810,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
 
 
 
-// ---- G <= 8: QK^T on v_mfma_i32_16x16x64_i8 ---------------------------------------------------
+// ---- G <= 16: QK^T on v_mfma_i32_16x16x64_i8 --------------------------------------------------
 //
-// QK^T runs in exact integer arithmetic, for up to 8 query heads per kv head in one or two
-// halves of 4 heads (the description below is of one half; a second half has its own q operand
-// and accumulators against the same K operand).  The B operand is K^T: column n of tile t is position
+// QK^T runs in exact integer arithmetic, for up to 16 query heads per kv head in one, two or
+// four halves of 4 heads (the description below is of one half; every other half has its own q
+// operand and accumulators against the same K operand).  The B operand is K^T: column n of tile t is position
 // 4n + t of the window, and lane 16 g + n supplies 16 dims of it as unsigned bytes -- the
 // nibbles of two K words, even dims from (w & 0x0F0F0F0F), odd dims from (w >> 4) & 0x0F0F0F0F,
 // 3 VALU ops per word.  The A operand holds q: row 4 h + c is base-128 digit c (c = 0 most
