@@ -270,6 +270,9 @@ def test_config2_batch1_long_context(gpu):
     (64, 4, 48, 8, 8192, False),    # G = 12 on 64-dim rows (two head groups of waves)
     (64, 8, 128, 8, 8192, True),    # G = 16 on 64-dim rows
     (96, 8, 80, 8, 8000, True),     # G = 10, padded: stored as 128 dims
+    # one kv head (Gemma-2B's 8 q / 1 kv): few streams, ~7 splits per sequence and the combine
+    (128, 1, 8, 32, 8192, True),
+    (128, 1, 16, 32, 8192, False),
 ])
 def test_integer_kernel_wide_and_padded_rows(gpu, hd, n_kv, n_head, n_seq, ctx, fused):
     """The integer-QK kernel on 64-, 128-, 256-dim and padded rows with 2..16 query heads per kv
