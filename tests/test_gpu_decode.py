@@ -76,6 +76,26 @@ def test_gqa3_hd128_llama32_3b_shape(gpu):
     p.check_codes()
 
 
+def test_tinyllama_shape_batch1(gpu):
+    """TinyLlama-1.1B's attention (32 q / 4 kv heads, group 8, hd 64, theta 1e4), the model of the
+    reference's own INT4 soak test, at batch 1 and ctx 2048: fused append + decode over several
+    steps against the oracle, the cache bit-exact."""
+    say("decode tinyllama shape")
+    rng = np.random.default_rng(11)
+    p = Pair(1, 4, 64, 2100, 10000.0)
+    prefill_cache(p, rng, 2040)
+    for _ in range(3):
+        k = synth.normal(rng, (1, 1, 4, 64))
+        v = synth.normal(rng, (1, 1, 4, 64))
+        q = synth.normal(rng, (1, 32, 64))
+        out = p.gpu.attn_decode_append(0, dev(k), dev(v), dev(q), p.rope).cpu().numpy()
+        p.ora.append(k, v)
+        ref = p.ora.attend(q[:, None], 1, threads=8)[:, 0]
+        p.advance(1)
+        assert_close(out, ref, "tinyllama out")
+    p.check_codes()
+
+
 def test_batch_outliers_qwen3_shape(gpu):
     """Config 3's shape (32/8, hd 128, theta 1e6, x8 outlier channels on 2% of dims) at
     batch 4 and context 3000."""
