@@ -946,10 +946,10 @@ __device__ __forceinline__ void process_window8(const Window8<HD> &w, WaveState8
 #pragma unroll
         for (int hf = 0; hf < GH; hf++) {
             // digits 0..3 carry weights 2^21, 2^14, 2^7, 1; each digit sum is an exact integer
-            // below 2^18, so the first step is exact and the whole score rounds ~once.
-            float v = fmaf(fmaf(fmaf((float)acc[hf][t][0], 128.0f, (float)acc[hf][t][1]), 128.0f,
-                                (float)acc[hf][t][2]),
-                           128.0f, (float)acc[hf][t][3]);
+            // below 2^18, so the two pairs combine exactly in i32 (below 2^26) and the score
+            // takes two conversions and one FMA.
+            const int dhi = acc[hf][t][0] * 128 + acc[hf][t][1], dlo = acc[hf][t][2] * 128 + acc[hf][t][3];
+            float v = fmaf((float)dhi, 16384.0f, (float)dlo);
             v *= qinv[hf] * w.sk[t];
             if constexpr (SOFTCAP) v = tanhf(v * (1.0f / kLog2e) / softcap) * softcap * kLog2e;
             x[hf][t] = base + 4 * n + t >= end ? -INFINITY : v;
