@@ -1022,20 +1022,18 @@ def main():
     B, L = cfg["batch"], cfg["layers"]
     gbs = r["step_bytes"] / (r["ms_step"] * 1e-3) / 1e9
     tok_s = B / (r["ms_step"] * 1e-3)
-    roof = None
-    if True:
-        ach = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
-        split_name = _split_kernel_name(cfg)
-        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "traffic_source": (f"profiles/decode_cfg{args.config}.md (rocprofv3 --pmc FETCH_SIZE / "
-                                   f"WRITE_SIZE at commit {traffic_commit})") if traffic else None,
-                "kernel": (f"{split_name}<{cfg['hd']}> (+ decode_combine_kernel when the plan splits; ts_attn_decode)"
-                           if args.separate else
-                           f"{split_name}<{cfg['hd']}> with fused append (+ decode_combine_kernel when the plan splits; ts_attn_decode_append)"),
-                "bytes_per_launch": int(r["kernel_bytes"]),
-                "avg_launch_us": round(r["kernel_ms"] * 1e3, 2),
-                "timing": r["kernel_timing"]}
+    ach = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+    split_name = _split_kernel_name(cfg)
+    roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "traffic_source": (f"profiles/decode_cfg{args.config}.md (rocprofv3 --pmc FETCH_SIZE / "
+                               f"WRITE_SIZE at commit {traffic_commit})") if traffic else None,
+            "kernel": (f"{split_name}<{cfg['hd']}> (+ decode_combine_kernel when the plan splits; ts_attn_decode)"
+                       if args.separate else
+                       f"{split_name}<{cfg['hd']}> with fused append (+ decode_combine_kernel when the plan splits; ts_attn_decode_append)"),
+            "bytes_per_launch": int(r["kernel_bytes"]),
+            "avg_launch_us": round(r["kernel_ms"] * 1e3, 2),
+            "timing": r["kernel_timing"]}
     cpu_line = None
     if cpu:
         cpu_gbs = r["step_bytes"] / cpu["step_s_mt"] / 1e9
@@ -1050,7 +1048,9 @@ def main():
         "metric": "INT4-KV decode-attn HBM GB/s (% of peak) + tokens/s, 8B shape ctx 8K b32",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(r["ms_step"], 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "int4-kv/f32-io (f16 mfma, hi/lo split)",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": ("int4-kv/f32-io (i8 mfma QK^T exact, f16 hi/lo PV)" if split_name == "decode_split4_kernel"
+                  else "int4-kv/f32-io (f16 mfma, hi/lo split)"),
         "data": "synthetic (seeded N(0,1), x8 outlier channels)" if cfg["outliers"] else "synthetic (seeded N(0,1))",
         "tokens_per_s": round(tok_s, 1), "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "launch": ("eager" if not args.graph else "hip-graph replay per step" if args.steps_per_graph <= 1
