@@ -15,8 +15,10 @@
 //   while the current window is computed, then converts it to exact f16 integer codes in a
 //   double-buffered LDS tile, so each code is converted once per workgroup and read by all
 //   4 waves.
-// * S^T = K Q^T with q split hi + lo (two f16 MFMAs into one f32 accumulator) and
-//   1/sqrt(hd)*log2(e) and a power-of-two range scale folded into q.  K rows enter the MFMA in
+// * S^T = K Q^T with q split into an f16 high half (f16 MFMAs) and a low half as two fp6 terms
+//   (one scaled fp6 MFMA per term and 64 dims, the K codes converted to fp6 from the same f16
+//   operand registers), all into one f32 accumulator, with 1/sqrt(hd)*log2(e) and a
+//   power-of-two range scale folded into q.  K rows enter the MFMA in
 //   the order that leaves every lane holding, per 16-key step, exactly the 8 keys it supplies
 //   to the PV operand, so P never moves between lanes.  The score is scaled by s_k in f32,
 //   masked only in windows that cross the causal diagonal, and enters an online softmax in
@@ -254,14 +256,80 @@ __device__ inline void stage_scales(SM &sm, int buf, const Pending<HD, NW> &pd, 
         sm.sk[buf][tid] = pd.scale * inv_s;  // undo the q operand scale (a power of two: exact)
     } else if (tid < 2 * kWin) {
         sm.sv[buf][tid - kWin] = pd.scale;
-        float m = pd.scale;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        // (one whole wave: threads kWin .. 2 kWin - 1; the scales are >= 0)
+        const float m = wave_max_nonneg(pd.scale);
         if (tid == kWin) sm.svlog[buf] = __log2f(m);
     }
 }
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef int int6v __attribute__((ext_vector_type(6)));
+typedef int int8v __attribute__((ext_vector_type(8)));
+typedef _Float16 half32 __attribute__((ext_vector_type(32)));
+typedef float float32v __attribute__((ext_vector_type(32)));
+
+// q's low half on the fp6 matrix-core path.  The low half q - f16(q) needs only a few bits of
+// its own: it enters v_mfma_scale_f32_32x32x64_f8f6f4 as fp6 e2m3 (3 mantissa bits, largest
+// 7.5) with a power-of-two scale, while the K codes on the other side (integers -7..7) are
+// exact in e2m3.  That MFMA does 64 k-steps of 32x32 in about the time of one 32x32x16 f16
+// MFMA (a quarter of the four f16 MFMAs it replaces); two terms (the second one the rounding
+// rest of the first) keep q to about f16 hi + lo accuracy.
+__device__ inline float exp2i(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
+
+// 4 k-steps of an f16 operand (32 values per lane, in operand order) as fp6 divided by s.
+__device__ inline int6v fp6_of(const half8 (&x)[4], float s) {
+    half32 v;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[8 * u + j] = x[u][j];
+    return __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(v, s);
+}
+
+// o += a b^T over 64 k-steps, a: fp6 codes (scale 1), b: fp6 with scale 2^(e8 - 127).
+__device__ inline floatx16 mfma_lo6(int6v a, int6v b, floatx16 c, int e8) {
+    const int8v a8 = {a[0], a[1], a[2], a[3], a[4], a[5], 0, 0};
+    const int8v b8 = {b[0], b[1], b[2], b[3], b[4], b[5], 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 2, 2, 0, 127, 0, e8);
+}
+
+// q's low half over one group of 4 k-steps (32 values lo[], f32) as two fp6 terms with fixed
+// scales: q is scaled so that |q| < 2^14 (q_scale), so its f16 high half leaves |lo| <= 4
+// (half an f16 ulp at 2^13); t1 = fp6(lo) rounds that to within 0.125, and t2 = fp6((lo - t1)
+// / 2^-5) keeps the rest to 2^-8: q to ~2^-22 of its bound, as a second f16 half would.
+constexpr int kQlo1E8 = 127, kQlo2E8 = 127 - 5;
+__device__ inline void q_lo_terms(const float (&lo)[32], int6v &t1, int6v &t2) {
+    floatx16 a, b;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {  // the conversion interleaves its two sources
+        a[i] = lo[2 * i];
+        b[i] = lo[2 * i + 1];
+    }
+    t1 = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(a, b, 1.0f);
+    const float32v back = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(t1, 1.0f);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        a[i] = lo[2 * i] - back[2 * i];
+        b[i] = lo[2 * i + 1] - back[2 * i + 1];
+    }
+    t2 = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(a, b, exp2i(-5));
+}
+
+// split_q8 with the low half kept in f32 (the fp6 terms are taken from it).
+__device__ inline void split_q8_f32(float (&x)[8], const float2 (&cs)[4], int u, int rope_pairs, float mul,
+                                    half8 &hi, float *lo) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (4 * u + i < rope_pairs) rope_rotate(x[2 * i], x[2 * i + 1], cs[i]);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float v = opaque(x[kPerm[j]] * mul);
+        const _Float16 h = (_Float16)v;
+        hi[j] = h;
+        lo[j] = v - (float)h;
+    }
+}
 
 // Max / sum over the two lane halves (lanes l and l^32) that hold one column.
 __device__ inline float half_max(float v) {
@@ -366,6 +434,7 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
     constexpr int NW = kPrefillNW;
     constexpr int NKS = HD / 16;   // MFMA k-steps over the head dim
     constexpr int NDB = HD / 32;   // 32-dim output tiles
+    constexpr int NG = NKS / 4;    // groups of 4 k-steps (one fp6 MFMA each)
     constexpr int ROWB = HD / 2;
     constexpr int COLS = NW * kColsPerWave;  // columns per block
     const KvLayerView &L = a.L;
@@ -457,17 +526,24 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
         for (int w = 0; w < NW; w++) qb = fmaxf(qb, sm_qb[w]);
         q_scale(qb * qmul, q_s, inv_s);
     }
-    // q operands of this lane's column: k-step t holds dims 8(2t + hf) .. +7.
-    half8 qh[NKS], ql[NKS];
-    {
+    // q operands of this lane's column: k-step t holds dims 8(2t + hf) .. +7 in f16 (hi); the
+    // rest as two fp6 terms per group of 4 k-steps.
+    half8 qh[NKS];
+    int6v ql1[NG], ql2[NG];
 #pragma unroll
-        for (int t = 0; t < NKS; t++) {
-            split_q8(xq[t], cs[t], 2 * t + hf, a.rope_pairs, qmul * q_s, qh[t], ql[t]);
+    for (int g = 0; g < NG; g++) {
+        float lo[32];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = 4 * g + u;
+            split_q8_f32(xq[t], cs[t], 2 * t + hf, a.rope_pairs, qmul * q_s, qh[t], lo + 8 * u);
             if (!live) {
                 qh[t] = (half8)(_Float16)0.0f;
-                ql[t] = (half8)(_Float16)0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) lo[8 * u + j] = 0.0f;
             }
         }
+        q_lo_terms(lo, ql1[g], ql2[g]);
     }
     // Query positions this wave covers (inclusive); qmax < 0 for a wave with no columns.
     const int qmin_w = len0 + c_wave / G;
@@ -501,19 +577,34 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
         using PD = Pending<HD, NW>;
         constexpr int NPART = PD::SPLIT ? 0 : 8 * PD::NK;  // staging parts, spread over k-steps
 #pragma unroll
-        for (int t = 0; t < NKS; t++) {
-            const half8 ka0 = sm.k[buf][krow][k_slot<HD>(krow, 2 * t + hf)];
-            const half8 ka1 = sm.k[buf][32 + krow][k_slot<HD>(32 + krow, 2 * t + hf)];
-            sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0, qh[t], sc[0], 0, 0, 0);
-            sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1, qh[t], sc[1], 0, 0, 0);
-            sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0, ql[t], sc[0], 0, 0, 0);
-            sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1, ql[t], sc[1], 0, 0, 0);
-            // (after the last window this writes the unused buffer)
-            if constexpr (NPART > 0) {
+        for (int g = 0; g < NG; g++) {
+            half8 ka0[4], ka1[4];
+            ka0[0] = sm.k[buf][krow][k_slot<HD>(krow, 2 * (4 * g) + hf)];
+            ka1[0] = sm.k[buf][32 + krow][k_slot<HD>(32 + krow, 2 * (4 * g) + hf)];
 #pragma unroll
-                for (int part = t * NPART / NKS; part < (t + 1) * NPART / NKS; part++)
-                    stage_part<HD, NW>(sm, buf ^ 1, pd, tid, part, dk);
+            for (int u = 0; u < 4; u++) {
+                const int t = 4 * g + u;
+                if (u + 1 < 4) {
+                    ka0[u + 1] = sm.k[buf][krow][k_slot<HD>(krow, 2 * (t + 1) + hf)];
+                    ka1[u + 1] = sm.k[buf][32 + krow][k_slot<HD>(32 + krow, 2 * (t + 1) + hf)];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka0[u], qh[t], sc[0], 0, 0, 0);
+                sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka1[u], qh[t], sc[1], 0, 0, 0);
+                // (after the last window this writes the unused buffer)
+                if constexpr (NPART > 0) {
+#pragma unroll
+                    for (int part = t * NPART / NKS; part < (t + 1) * NPART / NKS; part++)
+                        stage_part<HD, NW>(sm, buf ^ 1, pd, tid, part, dk);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
+            // the low half of q over these 64 dims: the same codes as fp6
+            const int6v k0 = fp6_of(ka0, 1.0f), k1 = fp6_of(ka1, 1.0f);
+            sc[0] = mfma_lo6(k0, ql1[g], sc[0], kQlo1E8);
+            sc[1] = mfma_lo6(k1, ql1[g], sc[1], kQlo1E8);
+            sc[0] = mfma_lo6(k0, ql2[g], sc[0], kQlo2E8);
+            sc[1] = mfma_lo6(k1, ql2[g], sc[1], kQlo2E8);
         }
         if constexpr (NPART == 0) stage_codes<HD, NW>(sm, buf ^ 1, pd, tid, wave, dk);
         __builtin_amdgcn_s_setprio(0);

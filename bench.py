@@ -1001,7 +1001,7 @@ def main():
             "value": round(r["flops_layer"] * cfg["layers"] / (r["total_ms"] * 1e-3) / 1e12, 3),
             "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(r["total_ms"], 4), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "f16-mfma(hi/lo split)+int4", "data": "synthetic",
+            "vs_baseline": None, "dtype": "int4-kv; f16 mfma (q and p*s_v high halves, p*s_v low half) + fp6 mfma (q low half, two terms)", "data": "synthetic",
             "config": {"workload": cfg["name"], "global_batch": cfg["batch"],
                        "seq_len": cfg["chunk"] * cfg["n_chunks"], "parallelism": "none"},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
