@@ -166,9 +166,10 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, i
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,
                          const float *v_new, int32_t *adv, hipStream_t st);
+// n_cu: compute units of the device (the launch staggers its q reads when the grid fits them).
 hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const float *q,
                           int n_head, int n_tok, const float *rope, int rope_pairs,
-                          float softcap, float *out, hipStream_t st);
+                          float softcap, float *out, int n_cu, hipStream_t st);
 
 // Fused QKV projection + append (ts_qkv.hip): tiles and split of the reduction over dim.
 struct QkvPlan {

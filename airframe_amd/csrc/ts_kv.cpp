@@ -554,7 +554,7 @@ int ts_attn_prefill(const ts_kv *kv, int32_t layer, const float *d_q, int32_t n_
     if (n_tok == 0) return TS_OK;
     return hip_status(ts::launch_prefill(kv->layer(layer), kv->d_len, d_q, n_head, n_tok,
                                          rope->d_table, rope->rope_dim / 2, softcap, d_out,
-                                         as_stream(stream)));
+                                         kv->n_cu, as_stream(stream)));
 }
 
 static bool qkv_shape_ok(const ts_kv *kv, int32_t dim, int32_t n_tok, int32_t n_head) {

@@ -42,6 +42,7 @@ struct PrefillArgs {
     float inv_sqrt_hd;
     float softcap;
     float *out;
+    int q_delay;  // sleeps of ~1 us before the q read of the lightest column block (0: none)
 };
 
 constexpr int kPrefillNW = 4;  // waves per workgroup
@@ -500,6 +501,15 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
     Pending<HD, NW> pd;
     const DeqConstV dk;
     fetch_window<HD, NW>(pd, kbase, vbase, ksb, vsb, 0, tid, wave);
+    // Every workgroup reads its q rows at the start, all at once (33.5 MB for a 4 x 512-token
+    // chunk of 32 heads), so the read is HBM-bound for several us.  When the whole grid runs in
+    // one round, the blocks of the lighter half hold their reads back, the lightest longest
+    // (a lighter block attends to fewer keys, so it still ends before the heavy ones), and the
+    // heavy blocks, which set the launch's length, get their q sooner.
+    if (a.q_delay > 0 && n_blk >= 2 && 2 * cblk < n_blk) {
+        const int steps = (n_blk / 2 - cblk) * a.q_delay / (n_blk / 2);
+        for (int i = 0; i < steps; i++) __builtin_amdgcn_s_sleep(32);  // 2048 clocks each
+    }
 
     // q of this lane's column, read once: the QK norm scale (its q row walked in order), then
     // one power-of-two q scale per workgroup from a bound over all its columns, then the
@@ -657,7 +667,7 @@ __global__ __launch_bounds__(64 * kPrefillNW, HD > 128 ? 1 : 2) void prefill_ker
 
 hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const float *q,
                           int n_head, int n_tok, const float *rope, int rope_pairs,
-                          float softcap, float *out, hipStream_t st) {
+                          float softcap, float *out, int n_cu, hipStream_t st) {
     PrefillArgs a;
     a.L = L;
     a.len = d_len;
@@ -674,6 +684,10 @@ hipError_t launch_prefill(const KvLayerView &L, const int32_t *d_len, const floa
     const int cols = kPrefillNW * kColsPerWave;
     const int n_blk = (n_cols + cols - 1) / cols;
     dim3 grid(n_blk, L.H, L.S);
+    // (the kernel fits two workgroups per CU below 256 dims, one at 256; measured on config
+    // 5's shape: 8 sleep steps for the lightest block, +3.5%)
+    const int64_t n_wg = (int64_t)n_blk * L.H * L.S;
+    a.q_delay = n_wg <= (int64_t)n_cu * (L.hd > 128 ? 1 : 2) ? 8 : 0;
     const bool cap = softcap > 0.0f, norm = L.qn != nullptr;
 #define TS_PF3(HDV, SC, NM, PD)                                                                          \
     {                                                                                                     \
