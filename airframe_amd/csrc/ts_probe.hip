@@ -8,6 +8,8 @@
 // while the previous one is consumed.  Consuming is an XOR into a register, so the launch time
 // is the memory system's time for this pattern.  probe_flat_read_kernel reads one flat buffer
 // grid-strided (every workgroup a different 4 KB piece at a time), the pattern HBM likes best.
+// probe_mfma_rate_kernel issues independent matrix-core instructions back to back, 4 chains
+// per wave, so the launch time is the matrix cores' issue rate for that instruction.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -154,7 +156,59 @@ __global__ __launch_bounds__(256) void probe_flat_read_kernel(const u32x4 *__res
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+typedef _Float16 half8p __attribute__((ext_vector_type(8)));
+typedef int int8p __attribute__((ext_vector_type(8)));
+typedef float float16p __attribute__((ext_vector_type(16)));
+
+// KIND 0: v_mfma_f32_32x32x16_f16; 1: v_mfma_scale_f32_32x32x64_f8f6f4 with fp6 e2m3 operands;
+// 2: the same with fp8 e4m3 operands; 3: fp6 A, fp8 B.
+template <int KIND>
+__global__ __launch_bounds__(256) void probe_mfma_rate_kernel(int iters, float *sink) {
+    float16p c0 = (float16p)0.0f, c1 = (float16p)0.0f, c2 = (float16p)0.0f, c3 = (float16p)0.0f;
+    const int l = threadIdx.x;
+    const int8p a = {l, l + 1, l + 2, l + 3, l + 4, l + 5, 0, 0};
+    const int8p b = {l, l + 1, l + 2, l + 3, l + 4, l + 5, l + 6, l + 7};
+    const half8p h = (half8p)(_Float16)(l * 0.001f);
+    for (int i = 0; i < iters; i++) {
+        if constexpr (KIND == 0) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, h, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, h, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, h, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, h, c3, 0, 0, 0);
+        } else {
+            constexpr int FA = KIND == 2 ? 0 : 2, FB = KIND == 1 ? 2 : 0;
+            const int8p aa = KIND == 2 ? b : a, bb = KIND == 1 ? a : b;
+            c0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aa, bb, c0, FA, FB, 0, 127, 0, 127);
+            c1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aa, bb, c1, FA, FB, 0, 127, 0, 127);
+            c2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aa, bb, c2, FA, FB, 0, 127, 0, 127);
+            c3 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(aa, bb, c3, FA, FB, 0, 127, 0, 127);
+        }
+    }
+    const float16p c = c0 + c1 + c2 + c3;
+    float t = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 16; v++) t += c[v];
+    if (t == 1234.5f) sink[0] = t;  // keeps the chains live
+}
+
 }  // namespace
+
+// One launch of `grid` 256-thread workgroups, each wave issuing 4 * iters matrix-core
+// instructions of kind `kind` (see probe_mfma_rate_kernel); returns a hipError_t.  Flops per
+// instruction: 32768 for kind 0, 131072 for the others.
+extern "C" int ts_probe_mfma_rate(int kind, int grid, int iters, void *sink, void *stream) {
+    if (grid <= 0 || iters <= 0) return (int)hipErrorInvalidValue;
+    const hipStream_t st = (hipStream_t)stream;
+    float *sk = (float *)sink;
+    switch (kind) {
+        case 0: probe_mfma_rate_kernel<0><<<grid, 256, 0, st>>>(iters, sk); break;
+        case 1: probe_mfma_rate_kernel<1><<<grid, 256, 0, st>>>(iters, sk); break;
+        case 2: probe_mfma_rate_kernel<2><<<grid, 256, 0, st>>>(iters, sk); break;
+        case 3: probe_mfma_rate_kernel<3><<<grid, 256, 0, st>>>(iters, sk); break;
+        default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
 
 // One loads-only pass of the decode pattern over rows = n_seq * n_kv streams of n_ctx
 // positions (P = padded positions per stream, a multiple of 64).  Returns a hipError_t.

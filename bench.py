@@ -702,6 +702,40 @@ def run_compact(args, cfg):
     return ms, 2 * per * B * L, B * L
 
 
+def run_mfma_rates(args):
+    """Issue rates of the matrix-core instructions the attention kernels use
+    (airframe_amd/csrc/ts_probe.hip): independent chains back to back on every SIMD, no
+    memory traffic.  The prefill kernel runs q's low half as scaled fp6 MFMAs because of the
+    ratio between the first two lines."""
+    import ctypes
+    import torch
+    from airframe_amd.build import PROBE_PATH
+    if not os.path.exists(PROBE_PATH):
+        sys.exit(f"{PROBE_PATH} is missing: run python -m airframe_amd.build")
+    lib = ctypes.CDLL(PROBE_PATH)
+    sink = torch.zeros(4, dtype=torch.float32, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    grid, iters = 2048, 2000
+    names = {0: "f16 v_mfma_f32_32x32x16_f16", 1: "fp6 e2m3 v_mfma_scale_f32_32x32x64_f8f6f4",
+             2: "fp8 e4m3 v_mfma_scale_f32_32x32x64_f8f6f4", 3: "fp6 x fp8 v_mfma_scale_f32_32x32x64_f8f6f4"}
+    out = {}
+    for kind, name in names.items():
+        flops = (32768 if kind == 0 else 131072) * 4 * iters * grid * 4  # 4 waves, 4 chains
+        for _ in range(2):
+            assert lib.ts_probe_mfma_rate(kind, grid, iters, ctypes.c_void_p(sink.data_ptr()), st) == 0
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        assert lib.ts_probe_mfma_rate(kind, grid, iters, ctypes.c_void_p(sink.data_ptr()), st) == 0
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        out[name] = round(flops / (ms * 1e-3) / 1e12, 1)
+    return {"metric": "matrix-core issue rate, TFLOP/s (dense, independent chains)", "rates": out,
+            "n_gpus": 1, "grid": grid, "iters": iters, "config": {"workload": "mfma_rate_probe"},
+            "data": "register operands, no memory traffic"}
+
+
 def run_stream_ceiling(args, cfg):
     """HBM ceilings for the decode step's reads (airframe_amd/csrc/ts_probe.hip): the decode
     kernel's exact access pattern with no math (one launch reads what one layer's decode
@@ -850,6 +884,8 @@ def main():
     ap.add_argument("--compact", action="store_true",
                     help="measure sliding-window compaction (ts_kv_shift) on the config's cache "
                          "instead of the decode step")
+    ap.add_argument("--mfma-rates", action="store_true",
+                    help="matrix-core issue rates of f16 and scaled fp6/fp8 MFMAs (ts_probe.hip)")
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="measure the HBM ceiling of the decode's access pattern with no math "
                          "(loads-only probe at the config's shape) and of a flat read of the same size")
@@ -937,6 +973,9 @@ def main():
             "roofline": roof,
             "data": ("synthetic (random GGUF blocks, f16 d/dmin ~1e-4, N(0,1) x)" if args.gguf
                      else "synthetic (random f16 weights, N(0,1) x)")}), flush=True)
+        return
+    if args.mfma_rates:
+        print(json.dumps(run_mfma_rates(args)), flush=True)
         return
     if args.stream_ceiling:
         if "ctx" not in cfg or "ragged" in cfg:
