@@ -390,6 +390,7 @@ def run_prefill(args, cfg):
         run()
     torch.cuda.synchronize()
     reps = max(args.steps, 1)
+    # Per-launch prefill time: events around each eager prefill launch.
     evs = [[[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)] for _ in range(NC)] for _ in range(reps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
@@ -400,11 +401,31 @@ def run_prefill(args, cfg):
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1) / reps
     kt = [evs[r][c][l][0].elapsed_time(evs[r][c][l][1]) for r in range(reps) for c in range(NC) for l in range(L)]
+    launch = "eager"
+    if args.graph:
+        # The step (reset, then every chunk's appends, prefills and length increment) captured
+        # once as a HIP graph and replayed: device lengths restart at 0 in every replay.
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=cap):
+            run()
+        torch.cuda.synchronize()
+        for _ in range(2):
+            gr.replay()
+        torch.cuda.synchronize()
+        t0.record()
+        for r in range(reps):
+            gr.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        total_ms = t0.elapsed_time(t1) / reps
+        launch = "hip-graph replay per step"
     # causal-exact flops per layer: QK^T and PV, 2 flops per MAC, over all chunks
     n_tot = C * NC
     flops_layer = 4 * hd * n_head * B * (n_tot * (n_tot + 1) // 2)
     kernel_ms_layer = float(np.sum(kt)) / reps / L
-    res = dict(total_ms=total_ms, kernel_ms_layer=kernel_ms_layer, flops_layer=flops_layer)
+    res = dict(total_ms=total_ms, kernel_ms_layer=kernel_ms_layer, flops_layer=flops_layer, launch=launch)
     if not args.no_cpu:
         res["cpu"] = cpu_baseline_prefill(cfg, qs, ks, vs)
     return res
@@ -1041,11 +1062,15 @@ def main():
             "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(r["total_ms"], 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "int4-kv; f16 mfma (q and p*s_v high halves, p*s_v low half) + fp6 mfma (q low half, two terms)", "data": "synthetic",
+            "launch": r["launch"],
             "config": {"workload": cfg["name"], "global_batch": cfg["batch"],
                        "seq_len": cfg["chunk"] * cfg["n_chunks"], "parallelism": "none"},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+                         "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                         "avg_launch_us": round(r["kernel_ms_layer"] * 1e3 / cfg["n_chunks"], 2),
+                         "timing": (f"HIP events around each eager prefill launch ({cfg['n_chunks']} chunks x "
+                                    f"{cfg['layers']} layers per step); avg_launch_us over all chunks")},
             "cpu_baseline": None if "cpu" not in r else {
                 "value": round(r["cpu"]["tflops_mt"], 6), "unit": "TFLOP/s", "cores": r["cpu"]["cores"],
                 "kind": "port", **cpu_info(),
