@@ -179,7 +179,7 @@ struct QkvPlan {
     uint64_t part_bytes;  // scratch for the split partials (0 without a split)
 };
 QkvPlan qkv_plan(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok);
-// GGUF K-quant weights (Q4_K, Q5_K) read in the loop: always the split form (dim a multiple of
+// GGUF block weights (Q4_K, Q5_K, Q8_0, Q4_0) read in the loop: always the split form (dim a multiple of
 // 256), partials always in `part` (part_bytes > 0).
 QkvPlan qkv_plan_kq(int n_seq, int n_kv, int n_head, int hd, int dim, int n_tok);
 hipError_t launch_qkv_kq(const KvLayerView &L, const int32_t *d_len, const float *x, int dim, int n_tok,
@@ -197,7 +197,7 @@ struct ProjPlan {
     uint64_t part_bytes;
 };
 ProjPlan proj_plan(int M, int K, int N);
-ProjPlan proj_plan_kq(int M, int K, int N);  // K-quant weights: split form, K a multiple of 256
+ProjPlan proj_plan_kq(int M, int K, int N);  // block weights: split form, K a multiple of 256
 hipError_t launch_proj_kq(const float *a, int M, int K, int ggml_type, const void *w, int N, float *act,
                           float *stash, const ProjPlan &plan, float *part, hipStream_t st);
 hipError_t launch_proj(const float *a, int M, int K, const uint16_t *w, int N, float *act, float *stash,

@@ -1,5 +1,6 @@
-// ts_kquant.h -- projection weights in the GGUF K-quant block formats (Q4_K, Q5_K) read at
-// their own size inside the matrix-core loop of the split projections (decode shapes).
+// ts_kquant.h -- projection weights in the GGUF block formats Q4_K, Q5_K (below) and Q8_0,
+// Q4_0 (further down) read at their own size inside the matrix-core loop of the split
+// projections (decode shapes).
 //
 // The reference's main_qkv / main_attn_proj read every weight from the GGUF blob inside the dot
 // product (src/backend/bindless/sh_layer_v1_int4.wgsl:502-520, sh_layer_v1.wgsl:777-790) with
@@ -24,13 +25,21 @@
 namespace ts {
 namespace {
 
-constexpr int kGgmlQ4K = 12, kGgmlQ5K = 13;
+constexpr int kGgmlQ4_0 = 2, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGgmlQ5K = 13;
 
+// Bytes of 256 elements of a row: one K-quant super-block, or 8 blocks of 32 (Q4_0: 18 bytes,
+// Q8_0: 34 bytes each).
 template <int T>
 struct KQ {
-    static constexpr int BYTES = T == kGgmlQ4K ? 144 : 176;  // one 256-element super-block
-    static constexpr int QS = T == kGgmlQ4K ? 16 : 48;       // offset of the 128 qs bytes
+    static constexpr int BYTES = T == kGgmlQ4K ? 144 : T == kGgmlQ5K ? 176 : T == kGgmlQ4_0 ? 144 : 272;
+    static constexpr int QS = T == kGgmlQ4K ? 16 : 48;       // offset of the 128 qs bytes (K formats)
 };
+__host__ __device__ constexpr bool kq_type(int t) {
+    return t == kGgmlQ4_0 || t == kGgmlQ8_0 || t == kGgmlQ4K || t == kGgmlQ5K;
+}
+__host__ __device__ constexpr int kq_bytes(int t) {
+    return t == kGgmlQ4K ? 144 : t == kGgmlQ5K ? 176 : t == kGgmlQ4_0 ? 144 : 272;
+}
 
 // LDS of the K-quant slice loop: x of one super-block (4 chunks of 64) as hi/lo, and the f32
 // sums of its 8 sub-blocks per row.
@@ -244,6 +253,198 @@ __device__ __forceinline__ void gemm_split_kq(KqTiles (&sm)[2], const float *xs,
         compute(sm[1], r[1]);
         if (b + 2 < nbat) stage(sm[0]);
     }
+}
+
+
+// ---- Q4_0 / Q8_0: 32-element blocks with one f16 scale each --------------------------------
+//
+// The reference's values (src/core/dequant/q4_0.rs, q8_0.rs): w = d * (n - 8) for the nibbles
+// of Q4_0 (element e of a block: low nibble of byte e, element 16 + e: its high nibble) and
+// w = d * q for the int8 codes of Q8_0.  The codes are exact in f16, the scale d is not
+// foldable into them exactly, so each block's 32 elements run on the matrix cores into an
+// accumulator of their own (two k-steps of v_mfma_f32_32x32x16_f16, x split hi + lo), which is
+// then added to the row's sum times d (16 FMAs per lane).  With the k-step order of the
+// K-quant loop, lane half hf takes elements 16 hf .. 16 hf + 15 of every block: Q8_0 bytes
+// 16 hf .. 16 hf + 15 of its codes, Q4_0 nibble half hf of all 16 bytes.
+//
+// The blocks (18 / 34 bytes) are not 4-byte aligned in every position, but 256 elements are
+// 144 / 272 bytes, a multiple of 16, so the alignment of block i within its 256 is fixed:
+// codes start 2 mod 4 in the even blocks (read from the dword that holds d, 5 dwords, one
+// byte-align per code word) and 0 mod 4 in the odd ones.  The scale of an odd block sits in
+// the top half of the dword before its codes: for Q4_0 the last dword of the even block's
+// read; for Q8_0 the last dword that lane half 1 reads of the even block (lane half 0 holds
+// the even block's d), and one lane-half swap per block pair gives every lane both.
+struct QbRegs {
+    uint4 c[8];     // block i: the 4 dwords from the lane's first read position
+    uint32_t t[4];  // even block 2k: its fifth dword
+};
+
+template <int T>
+__device__ __forceinline__ void qb_load(QbRegs &r, const uint8_t *sb, int hf) {
+    typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+    constexpr int BB = T == kGgmlQ8_0 ? 34 : 18;
+    const int off = T == kGgmlQ8_0 ? 16 * hf : 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int at = BB * i + off + ((i & 1) ? 2 : 0);  // a multiple of 4
+        const u32x4a v = *reinterpret_cast<const u32x4a *>(sb + at);
+        r.c[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        if (!(i & 1)) r.t[i >> 1] = *reinterpret_cast<const uint32_t *>(sb + at + 16);
+    }
+}
+
+// The lane's 16 code bytes of block i (4 words, byte 4w + b: code byte 4w + b of its share).
+template <int T>
+__device__ __forceinline__ void qb_words(const QbRegs &r, int i, uint32_t (&w)[4]) {
+    const uint4 c = r.c[i];
+    if (i & 1) {
+        w[0] = c.x; w[1] = c.y; w[2] = c.z; w[3] = c.w;
+    } else {
+        const uint32_t t = r.t[i >> 1];
+        w[0] = __builtin_amdgcn_alignbyte(c.y, c.x, 2);
+        w[1] = __builtin_amdgcn_alignbyte(c.z, c.y, 2);
+        w[2] = __builtin_amdgcn_alignbyte(c.w, c.z, 2);
+        w[3] = __builtin_amdgcn_alignbyte(t, c.w, 2);
+    }
+}
+
+// The scales of blocks 2k and 2k + 1.
+template <int T>
+__device__ __forceinline__ void qb_scales(const QbRegs &r, int k, int hf, float &d0, float &d1) {
+    const uint32_t lo = r.c[2 * k].x & 0xFFFFu;  // d of the even block (Q8_0: lane half 0's read)
+    const uint32_t hi = r.t[k] >> 16;             // d of the odd block (Q8_0: lane half 1's read)
+    uint32_t e = lo, o = hi;
+    if constexpr (T == kGgmlQ8_0) {
+        const uint32_t mine = hf ? hi : lo;
+        // element 0: lane half 0's value, element 1: lane half 1's, in every lane
+        const auto sw = __builtin_amdgcn_permlane32_swap(mine, mine, false, false);
+        e = sw[0];
+        o = sw[1];
+    }
+    d0 = (float)__builtin_bit_cast(_Float16, (uint16_t)e);
+    d1 = (float)__builtin_bit_cast(_Float16, (uint16_t)o);
+}
+
+// The B operands of block i's two k-steps: b[u] element e = code of byte 8u + e of the share
+// (Q4_0: its nibble half hf), exact integers in f16.
+template <int T>
+__device__ __forceinline__ void qb_operands(const QbRegs &r, int i, int hf, half8 (&b)[2], const DeqConst &dk) {
+    uint32_t w[4];
+    qb_words<T>(r, i, w);
+    const half2_t off = T == kGgmlQ8_0 ? half2_t{(_Float16)1152.0f, (_Float16)1152.0f}
+                                       : half2_t{(_Float16)1032.0f, (_Float16)1032.0f};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const uint32_t sel = p ? 0x0C030C02u : 0x0C010C00u;
+            const uint32_t sp = __builtin_amdgcn_perm(w[q], w[q], sel);  // bytes 2p, 2p+1 -> halves
+            uint32_t u;
+            if constexpr (T == kGgmlQ8_0)
+                u = (sp ^ 0x00800080u) | dk.magic;  // 1024 + (q + 128)
+            else
+                u = ((hf ? (sp >> 4) : sp) & dk.lo) | dk.magic;  // 1024 + n
+            const half2_t v = __builtin_bit_cast(half2_t, u) - off;
+            b[q >> 1][4 * (q & 1) + 2 * p] = v[0];
+            b[q >> 1][4 * (q & 1) + 2 * p + 1] = v[1];
+        }
+    }
+}
+
+// gemm_split_kq for Q4_0 / Q8_0 rows (same thread roles, LDS x tiles and D layout).
+template <int T>
+__device__ __forceinline__ void gemm_split_qb(KqTiles (&sm)[2], const float *xs, const uint8_t *const (&wb)[2],
+                                              int nbat, int tid, floatx16 (&acc)[2]) {
+    constexpr int NB = 4;
+    const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int si = tid >> 3, sc = tid & 7;
+    const DeqConstV dk;
+    zero(acc[0]);
+    zero(acc[1]);
+    float4 xu[NB], xv[NB];
+    QbRegs r[2][2];  // [buffer][column block]
+    auto load = [&](int b, QbRegs (&rr)[2]) {
+        const bool on = b < nbat;
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            xu[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[c] = xu[c];
+            if (xs && on) {
+                xu[c] = *reinterpret_cast<const float4 *>(xs + (b * NB + c) * kKC);
+                xv[c] = *reinterpret_cast<const float4 *>(xs + (b * NB + c) * kKC + 4);
+            }
+        }
+        if (on) {
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++) qb_load<T>(rr[cb], wb[cb] + (size_t)b * KQ<T>::BYTES, hf);
+        }
+    };
+    auto stage = [&](KqTiles &t) {
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            half8 h, l;
+            split8(xu[c], xv[c], h, l);
+            *reinterpret_cast<half8 *>(&t.x.hi[c][si][8 * sc]) = h;
+            *reinterpret_cast<half8 *>(&t.x.lo[c][si][8 * sc]) = l;
+        }
+    };
+    auto compute = [&](const KqTiles &t, const QbRegs (&rr)[2]) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float d[2][2];
+            qb_scales<T>(rr[0], k, hf, d[0][0], d[0][1]);
+            qb_scales<T>(rr[1], k, hf, d[1][0], d[1][1]);
+#pragma unroll
+            for (int ii = 0; ii < 2; ii++) {
+                const int i = 2 * k + ii, g = i >> 1;  // block i: chunk g, k-steps 2 (i & 1) + u
+                half8 b0[2], b1[2];
+                qb_operands<T>(rr[0], i, hf, b0, dk);
+                qb_operands<T>(rr[1], i, hf, b1, dk);
+                floatx16 t0, t1;
+                zero(t0);
+                zero(t1);
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int q = 2 * (i & 1) + u;
+                    const int ko = 32 * (q >> 1) + 16 * hf + 8 * (q & 1);
+                    const half8 ah = *reinterpret_cast<const half8 *>(&t.x.hi[g][j][ko]);
+                    const half8 al = *reinterpret_cast<const half8 *>(&t.x.lo[g][j][ko]);
+                    t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0[u], t0, 0, 0, 0);
+                    t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1[u], t1, 0, 0, 0);
+                    t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0[u], t0, 0, 0, 0);
+                    t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1[u], t1, 0, 0, 0);
+                }
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    acc[0][e] = __builtin_fmaf(d[0][ii], t0[e], acc[0][e]);
+                    acc[1][e] = __builtin_fmaf(d[1][ii], t1[e], acc[1][e]);
+                }
+            }
+        }
+    };
+    load(0, r[0]);
+    stage(sm[0]);
+    for (int b = 0; b < nbat; b += 2) {
+        load(b + 1, r[1]);
+        __syncthreads();
+        compute(sm[0], r[0]);
+        if (b + 1 >= nbat) break;  // uniform
+        stage(sm[1]);
+        load(b + 2, r[0]);
+        __syncthreads();
+        compute(sm[1], r[1]);
+        if (b + 2 < nbat) stage(sm[0]);
+    }
+}
+
+// The slice loop of any block type read in the loop.
+template <int T>
+__device__ __forceinline__ void gemm_split_blocks(KqTiles (&sm)[2], const float *xs, const uint8_t *const (&wb)[2],
+                                                  int nbat, int tid, floatx16 (&acc)[2]) {
+    if constexpr (T == kGgmlQ4K || T == kGgmlQ5K)
+        gemm_split_kq<T>(sm, xs, wb, nbat, tid, acc);
+    else
+        gemm_split_qb<T>(sm, xs, wb, nbat, tid, acc);
 }
 
 }  // namespace

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void proj_split_kq_kernel(ProjArgs p) {
     const uint8_t *const wb[2] = {p.bw + (size_t)min(col0 + j, p.N - 1) * p.brow + boff,
                                   p.bw + (size_t)min(col0 + 32 + j, p.N - 1) * p.brow + boff};
     floatx16 acc[2];
-    gemm_split_kq<T>(sm, xs, wb, nbat, tid, acc);
+    gemm_split_blocks<T>(sm, xs, wb, nbat, tid, acc);
     float *dst = p.part + (((size_t)sp * p.RT + rt) * p.CT + ct) * (32 * kPT);
 #pragma unroll
     for (int cb = 0; cb < 2; cb++)
@@ -216,13 +216,12 @@ ProjPlan proj_plan_kq(int M, int K, int N) {
 
 hipError_t launch_proj_kq(const float *a, int M, int K, int ggml_type, const void *w, int N, float *act,
                           float *stash, const ProjPlan &plan, float *part, hipStream_t st) {
-    if (K % 256 != 0 || M <= 0 || N <= 0 || !part || (ggml_type != kGgmlQ4K && ggml_type != kGgmlQ5K))
-        return hipErrorInvalidValue;
+    if (K % 256 != 0 || M <= 0 || N <= 0 || !part || !kq_type(ggml_type)) return hipErrorInvalidValue;
     ProjArgs p;
     p.a = a;
     p.w = nullptr;
     p.bw = static_cast<const uint8_t *>(w);
-    p.brow = (size_t)(K / 256) * (ggml_type == kGgmlQ4K ? KQ<kGgmlQ4K>::BYTES : KQ<kGgmlQ5K>::BYTES);
+    p.brow = (size_t)(K / 256) * kq_bytes(ggml_type);
     p.act = act;
     p.stash = stash;
     p.part = part;
@@ -238,8 +237,12 @@ hipError_t launch_proj_kq(const float *a, int M, int K, int ggml_type, const voi
     const int grid = (p.n_wg + 7) / 8 * 8;
     if (ggml_type == kGgmlQ4K)
         proj_split_kq_kernel<kGgmlQ4K><<<grid, 256, 0, st>>>(p);
-    else
+    else if (ggml_type == kGgmlQ5K)
         proj_split_kq_kernel<kGgmlQ5K><<<grid, 256, 0, st>>>(p);
+    else if (ggml_type == kGgmlQ8_0)
+        proj_split_kq_kernel<kGgmlQ8_0><<<grid, 256, 0, st>>>(p);
+    else
+        proj_split_kq_kernel<kGgmlQ4_0><<<grid, 256, 0, st>>>(p);
     proj_reduce_kernel<<<plan.RT * plan.CT * (32 / kPRows), 256, 0, st>>>(p);
     return hipGetLastError();
 }

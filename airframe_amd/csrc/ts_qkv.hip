@@ -405,7 +405,7 @@ __global__ __launch_bounds__(256) void qkv_split_kq_kernel(QkvArgs a) {
     const size_t boff = (size_t)(kb / 256) * KQ<T>::BYTES;
     const uint8_t *const wb[2] = {kq_row(a, ct, 64 * wave + j) + boff, kq_row(a, ct, 64 * wave + 32 + j) + boff};
     floatx16 acc[2];
-    gemm_split_kq<T>(sm, xs, wb, nbat, tid, acc);
+    gemm_split_blocks<T>(sm, xs, wb, nbat, tid, acc);
     float *dst = a.part + (((size_t)sp * a.RT + rt) * a.CT + ct) * (kMT * kNT);
 #pragma unroll
     for (int cb = 0; cb < 2; cb++)
@@ -491,8 +491,7 @@ hipError_t launch_qkv_kq(const KvLayerView &L, const int32_t *d_len, const float
                          int ggml_type, const void *wq, const void *wk, const void *wv, int n_head,
                          float *q_out, float *k_out, float *v_out, const float *rope, int rope_pairs,
                          const QkvPlan &plan, float *part, hipStream_t st) {
-    if ((L.hd != 128 && L.hd != 64) || dim % 256 != 0 || !part || (ggml_type != kGgmlQ4K && ggml_type != kGgmlQ5K))
-        return hipErrorInvalidValue;
+    if ((L.hd != 128 && L.hd != 64) || dim % 256 != 0 || !part || !kq_type(ggml_type)) return hipErrorInvalidValue;
     QkvArgs a;
     a.L = L;
     a.len = d_len;
@@ -501,7 +500,7 @@ hipError_t launch_qkv_kq(const KvLayerView &L, const int32_t *d_len, const float
     a.bq = static_cast<const uint8_t *>(wq);
     a.bk = static_cast<const uint8_t *>(wk);
     a.bv = static_cast<const uint8_t *>(wv);
-    a.brow = (size_t)(dim / 256) * (ggml_type == kGgmlQ4K ? KQ<kGgmlQ4K>::BYTES : KQ<kGgmlQ5K>::BYTES);
+    a.brow = (size_t)(dim / 256) * kq_bytes(ggml_type);
     a.q_out = q_out;
     a.k_out = k_out;
     a.v_out = v_out;
@@ -523,8 +522,12 @@ hipError_t launch_qkv_kq(const KvLayerView &L, const int32_t *d_len, const float
     const int grid = (a.n_wg + 7) / 8 * 8;
     if (ggml_type == kGgmlQ4K)
         qkv_split_kq_kernel<kGgmlQ4K><<<grid, 256, 0, st>>>(a);
-    else
+    else if (ggml_type == kGgmlQ5K)
         qkv_split_kq_kernel<kGgmlQ5K><<<grid, 256, 0, st>>>(a);
+    else if (ggml_type == kGgmlQ8_0)
+        qkv_split_kq_kernel<kGgmlQ8_0><<<grid, 256, 0, st>>>(a);
+    else
+        qkv_split_kq_kernel<kGgmlQ4_0><<<grid, 256, 0, st>>>(a);
     if (n_tok == 1)
         qkv_reduce_kernel<4><<<plan.RT * plan.CT * (kMT / 4), 256, 0, st>>>(a);
     else

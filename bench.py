@@ -494,18 +494,26 @@ def run_append(args, cfg):
     return ms, B * n_tok * n_kv * (2 * hd * 4 + hd + 8), B * n_tok
 
 
-KQ_BLOCK = {12: 144, 13: 176}  # bytes of one 256-element Q4_K / Q5_K super-block
+KQ_BLOCK = {12: 144, 13: 176, 8: 272, 2: 144}  # bytes of 256 elements of a Q4_K / Q5_K / Q8_0 / Q4_0 row
 
 
 def kq_blob(gen, rows, cols, ggml_type, dev):
-    """Random Q4_K / Q5_K blocks of an [rows][cols] matrix on the device: random bytes with
-    finite f16 d and dmin of about 1e-4 (weights of about 1e-2)."""
+    """Random GGUF blocks of an [rows][cols] matrix on the device: random bytes with finite f16
+    scales (d and dmin of the K formats; d of every 32-element Q8_0 / Q4_0 block) of about 1e-4
+    (weights of about 1e-2)."""
     import torch
-    nb = rows * cols // 256
-    bb = KQ_BLOCK[ggml_type]
+    if ggml_type in (12, 13):
+        nb = rows * cols // 256
+        bb = KQ_BLOCK[ggml_type]
+        b = torch.randint(0, 256, (nb, bb), generator=gen, device=dev, dtype=torch.uint8)
+        dd = (torch.rand((nb, 2), generator=gen, device=dev) * 3e-4 + 1e-4).half()
+        b[:, 0:4] = dd.view(torch.uint8).reshape(nb, 4)
+        return b.reshape(-1)
+    nb = rows * cols // 32
+    bb = KQ_BLOCK[ggml_type] // 8
     b = torch.randint(0, 256, (nb, bb), generator=gen, device=dev, dtype=torch.uint8)
-    dd = (torch.rand((nb, 2), generator=gen, device=dev) * 3e-4 + 1e-4).half()
-    b[:, 0:4] = dd.view(torch.uint8).reshape(nb, 4)
+    dd = (torch.rand((nb, 1), generator=gen, device=dev) * 3e-4 + 1e-4).half()
+    b[:, 0:2] = dd.view(torch.uint8).reshape(nb, 2)
     return b.reshape(-1)
 
 
@@ -898,8 +906,8 @@ def main():
                     help="time the attention output projection + residual (ts_attn_out_proj) instead")
     ap.add_argument("--planes", type=int, default=1, choices=(1, 2),
                     help="with --qkv/--proj: 2 = two-plane weights (F32 / GGUF formats, the _x2 entry points)")
-    ap.add_argument("--gguf", default=None, choices=("q4_k", "q5_k"),
-                    help="with --qkv/--proj: weights as GGUF K-quant blocks read in the loop (the _gguf entry points)")
+    ap.add_argument("--gguf", default=None, choices=("q4_k", "q5_k", "q8_0", "q4_0"),
+                    help="with --qkv/--proj: weights as GGUF blocks read in the loop (the _gguf entry points)")
     ap.add_argument("--convert", default=None, choices=sorted(CONVERT_TYPES),
                     help="time ts_weights_to_f16x2 on the configuration's Wq of that GGUF type")
     ap.add_argument("--compact", action="store_true",
@@ -974,7 +982,7 @@ def main():
         tfs = flops / (ms * 1e-3) / 1e12
         roof = ({"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                  "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": byts,
-                 "counting": (("GGUF K-quant block bytes" if args.gguf else "f16 weights (both planes with --planes 2)")
+                 "counting": (("GGUF block bytes" if args.gguf else "f16 weights (both planes with --planes 2)")
                               + (" and f32 x read, f32 q, packed K/V rows and scales written" if args.qkv
                                  else " and f32 attention output read, residual read and written"))}
                 if decode else
@@ -992,7 +1000,7 @@ def main():
                        + (f"_{args.gguf}_in_loop" if args.gguf else ""),
                        "tokens_per_call": toks, "dim": cfg["dim"]},
             "roofline": roof,
-            "data": ("synthetic (random GGUF blocks, f16 d/dmin ~1e-4, N(0,1) x)" if args.gguf
+            "data": ("synthetic (random GGUF blocks, f16 scales ~1e-4, N(0,1) x)" if args.gguf
                      else "synthetic (random f16 weights, N(0,1) x)")}), flush=True)
         return
     if args.mfma_rates:

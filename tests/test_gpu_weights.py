@@ -135,9 +135,14 @@ def test_attn_out_proj_with_block_weights(gpu, fmt, n_tok, attn_dim, dim):
     (weights.Q4_K, 3, 70, 1024, 128),  # block rows (prefill chunk)
     (weights.Q5_K, 2, 1, 512, 64),     # head dim 64
     (weights.Q4_K, 4, 1, 768, 96),     # head dim 96: three projections, then the append
+    (weights.Q8_0, 8, 1, 4096, 128),   # 32-element blocks: decode rows, split reduction
+    (weights.Q4_0, 32, 1, 2048, 128),  # a full 32-row decode tile
+    (weights.Q8_0, 3, 70, 1024, 128),  # block rows
+    (weights.Q4_0, 2, 1, 512, 64),     # head dim 64
+    (weights.Q8_0, 4, 1, 768, 96),     # head dim 96
 ])
 def test_qkv_append_gguf_blocks_in_loop(gpu, fmt, n_seq, n_tok, dim, hd):
-    """ts_qkv_append_gguf: Q4_K / Q5_K blocks read inside the projection loop, against the dot
+    """ts_qkv_append_gguf: Q4_K / Q5_K / Q8_0 / Q4_0 blocks read inside the projection loop, against the dot
     over the oracle's exact dequantized f32 weights (q4_k.rs / q5_k.rs, pinned in
     test_oracle_weights.py), and the appended codes bit-exact with the quantizer applied to
     those projections."""
@@ -168,6 +173,10 @@ def test_qkv_append_gguf_blocks_in_loop(gpu, fmt, n_seq, n_tok, dim, hd):
     (weights.Q4_K, 5, 2048, 2048),    # decode: the reduction split
     (weights.Q5_K, 130, 1024, 768),   # prefill rows, still split
     (weights.Q4_K, 1100, 512, 2304),  # many tiles: one slice over all of attn_dim
+    (weights.Q8_0, 5, 2048, 2048),
+    (weights.Q4_0, 130, 1024, 768),
+    (weights.Q8_0, 1100, 512, 2304),
+    (weights.Q4_0, 1, 3072, 3072),    # batch 1 (config 2's attention width)
 ])
 def test_attn_out_proj_gguf_blocks_in_loop(gpu, fmt, n_tok, attn_dim, dim):
     """ts_attn_out_proj_gguf against the oracle's f32-weight dot and the residual add."""
@@ -187,7 +196,7 @@ def test_attn_out_proj_gguf_blocks_in_loop(gpu, fmt, n_tok, attn_dim, dim):
 
 
 def test_gguf_in_loop_refusals(gpu):
-    """Types other than Q4_K / Q5_K and dims that are not whole super-blocks are refused."""
+    """Types without an in-loop form (Q6_K) and dims that are not whole 256s are refused."""
     say("gguf in-loop refusals")
     from airframe_amd import TsError
     p = Pair(1, 2, 128, 16, 500000.0)
