@@ -1043,7 +1043,7 @@ def main():
         return
     # HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated) for
     # this configuration, as recorded in its profile summary; null when none was taken.
-    traffic = traffic_commit = None
+    traffic = traffic_commit = rocprof_us = None
     tpath = os.path.join(ROOT, "profiles", f"decode_cfg{args.config}.md")
     if os.path.exists(tpath) and not (args.head_dim or args.n_head):  # that profile's own workload
         with open(tpath) as f:
@@ -1052,6 +1052,8 @@ def main():
                     traffic = int(float(line.split(":")[1]))
                 elif line.startswith("traffic_measured_at_commit:"):
                     traffic_commit = line.split(":", 1)[1].strip()
+                elif line.startswith("rocprof_avg_us_per_launch:"):
+                    rocprof_us = float(line.split(":")[1])
 
     if args.copy_calib:
         x = torch.empty(2**28, dtype=torch.float32, device="cuda")
@@ -1106,6 +1108,11 @@ def main():
             "bytes_per_launch": int(r["kernel_bytes"]),
             "avg_launch_us": round(r["kernel_ms"] * 1e3, 2),
             "timing": r["kernel_timing"]}
+    if rocprof_us and not args.separate:
+        # the same launch as rocprofv3 --kernel-trace times it (every dispatch on its own), from
+        # the profile that also gives the traffic
+        roof["rocprof_avg_launch_us"] = rocprof_us
+        roof["rocprof_frac"] = round(r["kernel_bytes"] / (rocprof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     cpu_line = None
     if cpu:
         cpu_gbs = r["step_bytes"] / cpu["step_s_mt"] / 1e9
