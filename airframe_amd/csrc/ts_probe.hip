@@ -260,3 +260,41 @@ extern "C" int ts_probe_empty(int grid, void *sink, void *stream) {
     probe_empty_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((uint32_t *)sink);
     return (int)hipGetLastError();
 }
+
+// Launch n instantiated graphs in order on one stream from a compiled loop: the timed steps of
+// bench.py --host-loop c, so that the host's cost per step is that of hipGraphLaunch alone (as
+// for a compiled host such as the reference's Rust one) and not the Python interpreter's.
+extern "C" int ts_probe_graph_launch(void *const *execs, int n, void *stream) {
+    if (n < 0 || (n > 0 && !execs)) return (int)hipErrorInvalidValue;
+    for (int i = 0; i < n; i++) {
+        const hipError_t e = hipGraphLaunch((hipGraphExec_t)execs[i], (hipStream_t)stream);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+}
+
+// n_steps decode steps of n_layers layers from a compiled loop, each layer one call of the
+// library's ts_attn_decode_append (fn_mid) or, for the step's last layer,
+// ts_attn_decode_append_advance (fn_last), with the function pointers the caller looked up in
+// libturboshimmy.so: what a compiled host (the reference's Rust one) would issue per step.
+// k, v, q: n_sets x n_layers device pointers, step i taking set i % n_sets.
+typedef int (*ts_probe_decode_fn)(void *kv, int32_t layer, const float *k, const float *v, const float *q,
+                                  int32_t n_head, const void *rope, float softcap, float *out, void *ws,
+                                  uint64_t ws_bytes, void *stream);
+extern "C" int ts_probe_decode_steps(void *fn_mid, void *fn_last, void *kv, int n_layers, int n_steps, int n_sets,
+                                     const float *const *k, const float *const *v, const float *const *q,
+                                     int n_head, const void *rope, float *out, void *ws, uint64_t ws_bytes,
+                                     void *stream) {
+    if (!fn_mid || !fn_last || n_layers <= 0 || n_steps < 0 || n_sets <= 0) return (int)hipErrorInvalidValue;
+    const ts_probe_decode_fn mid = (ts_probe_decode_fn)fn_mid, last = (ts_probe_decode_fn)fn_last;
+    for (int i = 0; i < n_steps; i++) {
+        const int set = i % n_sets;
+        for (int l = 0; l < n_layers; l++) {
+            const size_t at = (size_t)set * n_layers + l;
+            const int rc = (l == n_layers - 1 ? last : mid)(kv, l, k[at], v[at], q[at], n_head, rope, 0.0f, out,
+                                                             ws, ws_bytes, stream);
+            if (rc != 0) return rc;
+        }
+    }
+    return 0;
+}

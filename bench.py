@@ -20,6 +20,7 @@ Other configs (--config 1,2,4 decode; 5 chunked prefill) print their own line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -279,8 +280,45 @@ def run_decode(args, cfg):
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    launcher = None
+    if graphs is None and args.host_loop == "c":
+        # the timed steps as calls of the library's decode entry points from a compiled loop
+        # (ts_probe_decode_steps), eager launches as a compiled host would issue them
+        if args.separate or not fold:
+            sys.exit("--host-loop c without graphs runs the fused, folded step only")
+        from airframe_amd._lib import load as load_ts
+        from airframe_amd.build import PROBE_PATH
+        tl = load_ts()
+        plib = ctypes.CDLL(PROBE_PATH)
+        vp = ctypes.c_void_p
+        plib.ts_probe_decode_steps.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               vp, vp, vp, ctypes.c_int, vp, vp, vp, ctypes.c_uint64, vp]
+        arr = lambda ts_: (vp * (n_sets * L))(*[t.data_ptr() for row in ts_ for t in row])  # noqa: E731
+        k_a, v_a, q_a = arr(ks), arr(vs), arr(qs)
+        fmid = ctypes.cast(tl.ts_attn_decode_append, vp)
+        flast = ctypes.cast(tl.ts_attn_decode_append_advance, vp)
+        cur = vp(torch.cuda.current_stream().cuda_stream)
+        launcher = lambda: plib.ts_probe_decode_steps(  # noqa: E731
+            fmid, flast, kv.handle, L, steps, n_sets, k_a, v_a, q_a, n_head, rope.handle,
+            vp(out.data_ptr()), vp(ws.data_ptr()), ws.numel(), cur)
+    if graphs is not None and args.host_loop == "c":
+        # every step's graph launched from a compiled loop (ts_probe_graph_launch)
+        from airframe_amd.build import PROBE_PATH
+        plib = ctypes.CDLL(PROBE_PATH)
+        plib.ts_probe_graph_launch.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_void_p]
+        execs = (ctypes.c_void_p * len(graphs))(*[gr.raw_cuda_graph_exec() for gr in graphs])
+        cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        launcher = lambda: plib.ts_probe_graph_launch(execs, len(graphs), cur)  # noqa: E731
+        assert launcher() == 0  # one untimed pass (the lengths are reset below)
+        torch.cuda.synchronize()
+        reset_lens()
+        torch.cuda.synchronize()
     t_start.record()
-    if graphs is not None:
+    if launcher is not None:
+        rc = launcher()
+        if rc != 0:
+            sys.exit(f"hipGraphLaunch failed: {rc}")
+    elif graphs is not None:
         for gr in graphs:
             gr.replay()
     else:
@@ -306,41 +344,41 @@ def run_decode(args, cfg):
     result["kernel_ms"] = float(np.mean(kt))
     result["kernel_bytes"] = float(np.mean(kb))
     result["kernel_timing"] = "HIP events around each decode launch, eager pass of 16 steps"
-    if args.graph:
-        # The decode launches alone (no length increment), captured once as a graph of the L
-        # launches of step 0 and replayed: average time per launch in the same graph context
-        # as the timed steps.  Every replay appends the same token at the same position.
-        reset_lens()
-        kg = torch.cuda.CUDAGraph()
-        cap = torch.cuda.Stream()
-        cap.wait_stream(torch.cuda.current_stream())
-        # at least 32 launches per graph (the layers repeated), so that a one-layer config's
-        # replays measure the launches and not the host's graph launch
-        n_copies = -(-32 // L)
-        with torch.cuda.graph(kg, stream=cap):
-            for _ in range(n_copies):
-                for layer in range(L):
-                    if args.separate:
-                        kv.attn_decode(layer, qs[0][layer], rope, out=out, workspace=ws)
-                    else:
-                        kv.attn_decode_append(layer, ks[0][layer], vs[0][layer], qs[0][layer], rope,
-                                              out=out, workspace=ws)
-        torch.cuda.synchronize()
-        for _ in range(3):
-            kg.replay()
-        n_rep = 20
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(n_rep):
-            kg.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        result["kernel_ms"] = e0.elapsed_time(e1) / (n_rep * L * n_copies)
-        result["kernel_bytes"] = float(kern_bytes[0])
-        result["kernel_timing"] = (f"HIP events around {n_rep} replays of a graph holding only the {L * n_copies} "
-                                   "decode launches of step 0" + (f" ({n_copies} copies of the {L} layers)" if n_copies > 1 else "")
-                                   + " (split and combine kernels; no length increment)")
-        del kg
+    # The decode launches alone (no length increment), captured once as a graph of the L
+    # launches of step 0 and replayed: the average time per launch without the host's
+    # issue gaps between launches (also when the timed steps run eagerly).  Every replay
+    # appends the same token at the same position.
+    reset_lens()
+    kg = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    # at least 32 launches per graph (the layers repeated), so that a one-layer config's
+    # replays measure the launches and not the host's graph launch
+    n_copies = -(-32 // L)
+    with torch.cuda.graph(kg, stream=cap):
+        for _ in range(n_copies):
+            for layer in range(L):
+                if args.separate:
+                    kv.attn_decode(layer, qs[0][layer], rope, out=out, workspace=ws)
+                else:
+                    kv.attn_decode_append(layer, ks[0][layer], vs[0][layer], qs[0][layer], rope,
+                                          out=out, workspace=ws)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        kg.replay()
+    n_rep = 20
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n_rep):
+        kg.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    result["kernel_ms"] = e0.elapsed_time(e1) / (n_rep * L * n_copies)
+    result["kernel_bytes"] = float(kern_bytes[0])
+    result["kernel_timing"] = (f"HIP events around {n_rep} replays of a graph holding only the {L * n_copies} "
+                               "decode launches of step 0" + (f" ({n_copies} copies of the {L} layers)" if n_copies > 1 else "")
+                               + " (split and combine kernels; no length increment)")
+    del kg
 
     cpu = None
     reset_lens()
@@ -918,6 +956,14 @@ def main():
     ap.add_argument("--stream-ceiling", action="store_true",
                     help="measure the HBM ceiling of the decode's access pattern with no math "
                          "(loads-only probe at the config's shape) and of a flat read of the same size")
+    ap.add_argument("--host-loop", default="auto", choices=("auto", "python", "c"),
+                    help="who issues the timed decode steps: Python (graph replays, or the KVCache "
+                         "methods with --no-graph) or a compiled loop (hipGraphLaunch of the step "
+                         "graphs, or with --no-graph the library's C entry points, as a compiled "
+                         "host calls them: ts_probe_graph_launch / ts_probe_decode_steps); auto: "
+                         "the compiled loop of library calls for the batch-1 configurations 1 and 2, "
+                         "whose steps are short enough for the host's issue cost to show, else "
+                         "Python graph replays")
     ap.add_argument("--steps-per-graph", type=int, default=1,
                     help="decode: capture this many consecutive steps per HIP graph (default 1: one graph per step)")
     ap.add_argument("--no-fold", dest="fold", action="store_false",
@@ -938,6 +984,11 @@ def main():
         cfg["name"] += f"_hd{cfg['hd']}_h{cfg['n_head']}"
     if args.steps is None:
         args.steps = cfg.get("steps", 3) if args.config != 5 else 3
+    if args.host_loop == "auto":
+        if args.config in (1, 2) and args.fold and not args.separate and args.steps_per_graph <= 1:
+            args.host_loop, args.graph = "c", False
+        else:
+            args.host_loop = "python"
 
     import torch
     import airframe_amd
@@ -1132,8 +1183,10 @@ def main():
                   else "int4-kv/f32-io (f16 mfma, hi/lo split)"),
         "data": "synthetic (seeded N(0,1), x8 outlier channels)" if cfg["outliers"] else "synthetic (seeded N(0,1))",
         "tokens_per_s": round(tok_s, 1), "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
-        "launch": ("eager" if not args.graph else "hip-graph replay per step" if args.steps_per_graph <= 1
-                   else f"hip-graph replay per {args.steps_per_graph} steps"),
+        "launch": (("eager" if not args.graph else "hip-graph replay per step" if args.steps_per_graph <= 1
+                    else f"hip-graph replay per {args.steps_per_graph} steps")
+                   + ((", graphs launched from a compiled loop" if args.graph else
+                       ", library calls from a compiled loop") if args.host_loop == "c" else "")),
         "config": {"workload": cfg["name"] + ("_qknorm" if args.qk_norm else ""), "global_batch": B,
                    "seq_len": cfg.get("ctx"),
                    "layers": L, "n_head": cfg["n_head"], "n_head_kv": cfg["n_kv"],
