@@ -25,20 +25,20 @@
 namespace ts {
 namespace {
 
-constexpr int kGgmlQ4_0 = 2, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGgmlQ5K = 13;
+constexpr int kGgmlQ4_0 = 2, kGgmlQ5_0 = 6, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGgmlQ5K = 13;
 
 // Bytes of 256 elements of a row: one K-quant super-block, or 8 blocks of 32 (Q4_0: 18 bytes,
-// Q8_0: 34 bytes each).
+// Q5_0: 22, Q8_0: 34 each).
+__host__ __device__ constexpr int kq_bytes(int t) {
+    return t == kGgmlQ4K ? 144 : t == kGgmlQ5K ? 176 : t == kGgmlQ4_0 ? 144 : t == kGgmlQ5_0 ? 176 : 272;
+}
 template <int T>
 struct KQ {
-    static constexpr int BYTES = T == kGgmlQ4K ? 144 : T == kGgmlQ5K ? 176 : T == kGgmlQ4_0 ? 144 : 272;
+    static constexpr int BYTES = kq_bytes(T);
     static constexpr int QS = T == kGgmlQ4K ? 16 : 48;       // offset of the 128 qs bytes (K formats)
 };
 __host__ __device__ constexpr bool kq_type(int t) {
-    return t == kGgmlQ4_0 || t == kGgmlQ8_0 || t == kGgmlQ4K || t == kGgmlQ5K;
-}
-__host__ __device__ constexpr int kq_bytes(int t) {
-    return t == kGgmlQ4K ? 144 : t == kGgmlQ5K ? 176 : t == kGgmlQ4_0 ? 144 : 272;
+    return t == kGgmlQ4_0 || t == kGgmlQ5_0 || t == kGgmlQ8_0 || t == kGgmlQ4K || t == kGgmlQ5K;
 }
 
 // LDS of the K-quant slice loop: x of one super-block (4 chunks of 64) as hi/lo, and the f32
@@ -256,11 +256,12 @@ __device__ __forceinline__ void gemm_split_kq(KqTiles (&sm)[2], const float *xs,
 }
 
 
-// ---- Q4_0 / Q8_0: 32-element blocks with one f16 scale each --------------------------------
+// ---- Q4_0 / Q5_0 / Q8_0: 32-element blocks with one f16 scale each ------------------------
 //
-// The reference's values (src/core/dequant/q4_0.rs, q8_0.rs): w = d * (n - 8) for the nibbles
-// of Q4_0 (element e of a block: low nibble of byte e, element 16 + e: its high nibble) and
-// w = d * q for the int8 codes of Q8_0.  The codes are exact in f16, the scale d is not
+// The reference's values (src/core/dequant/q4_0.rs, q5_0.rs, q8_0.rs): w = d * (n - 8) for the
+// nibbles of Q4_0 (element e of a block: low nibble of byte e, element 16 + e: its high
+// nibble), w = d * (n + 16 h - 16) for Q5_0 (the same nibbles, h = bit e of its 32-bit word of
+// fifth bits) and w = d * q for the int8 codes of Q8_0.  The codes are exact in f16, the scale d is not
 // foldable into them exactly, so each block's 32 elements run on the matrix cores into an
 // accumulator of their own (two k-steps of v_mfma_f32_32x32x16_f16, x split hi + lo), which is
 // then added to the row's sum times d (16 FMAs per lane).  With the k-step order of the
@@ -277,12 +278,14 @@ __device__ __forceinline__ void gemm_split_kq(KqTiles (&sm)[2], const float *xs,
 struct QbRegs {
     uint4 c[8];     // block i: the 4 dwords from the lane's first read position
     uint32_t t[4];  // even block 2k: its fifth dword
+    uint32_t x[4];  // Q5_0: odd block 2k + 1: its fifth dword
+    uint32_t y[4];  // Q5_0: even block 2k: its sixth dword
 };
 
 template <int T>
 __device__ __forceinline__ void qb_load(QbRegs &r, const uint8_t *sb, int hf) {
     typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
-    constexpr int BB = T == kGgmlQ8_0 ? 34 : 18;
+    constexpr int BB = T == kGgmlQ8_0 ? 34 : T == kGgmlQ5_0 ? 22 : 18;
     const int off = T == kGgmlQ8_0 ? 16 * hf : 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -290,13 +293,36 @@ __device__ __forceinline__ void qb_load(QbRegs &r, const uint8_t *sb, int hf) {
         const u32x4a v = *reinterpret_cast<const u32x4a *>(sb + at);
         r.c[i] = make_uint4(v[0], v[1], v[2], v[3]);
         if (!(i & 1)) r.t[i >> 1] = *reinterpret_cast<const uint32_t *>(sb + at + 16);
+        if constexpr (T == kGgmlQ5_0) {
+            if (i & 1)
+                r.x[i >> 1] = *reinterpret_cast<const uint32_t *>(sb + at + 16);
+            else
+                r.y[i >> 1] = *reinterpret_cast<const uint32_t *>(sb + at + 20);
+        }
     }
 }
 
-// The lane's 16 code bytes of block i (4 words, byte 4w + b: code byte 4w + b of its share).
+// The lane's 16 code bytes of block i (4 words, byte 4w + b: code byte 4w + b of its share);
+// Q5_0: the 16 qs bytes, and its qh word in *qh.
 template <int T>
-__device__ __forceinline__ void qb_words(const QbRegs &r, int i, uint32_t (&w)[4]) {
+__device__ __forceinline__ void qb_words(const QbRegs &r, int i, uint32_t (&w)[4], uint32_t *qh = nullptr) {
     const uint4 c = r.c[i];
+    if constexpr (T == kGgmlQ5_0) {
+        // even block: dwords c.x .. c.w, t, x from the block's start (d, qh, qs, next d);
+        // odd block: qh, then the 16 qs bytes in c.y .. c.w and x
+        if (i & 1) {
+            *qh = c.x;
+            w[0] = c.y; w[1] = c.z; w[2] = c.w; w[3] = r.x[i >> 1];
+        } else {
+            const uint32_t t = r.t[i >> 1], u = r.y[i >> 1];
+            *qh = __builtin_amdgcn_alignbyte(c.y, c.x, 2);
+            w[0] = __builtin_amdgcn_alignbyte(c.z, c.y, 2);
+            w[1] = __builtin_amdgcn_alignbyte(c.w, c.z, 2);
+            w[2] = __builtin_amdgcn_alignbyte(t, c.w, 2);
+            w[3] = __builtin_amdgcn_alignbyte(u, t, 2);
+        }
+        return;
+    }
     if (i & 1) {
         w[0] = c.x; w[1] = c.y; w[2] = c.z; w[3] = c.w;
     } else {
@@ -312,7 +338,8 @@ __device__ __forceinline__ void qb_words(const QbRegs &r, int i, uint32_t (&w)[4
 template <int T>
 __device__ __forceinline__ void qb_scales(const QbRegs &r, int k, int hf, float &d0, float &d1) {
     const uint32_t lo = r.c[2 * k].x & 0xFFFFu;  // d of the even block (Q8_0: lane half 0's read)
-    const uint32_t hi = r.t[k] >> 16;             // d of the odd block (Q8_0: lane half 1's read)
+    // d of the odd block (Q8_0: lane half 1's read; Q5_0: the even block's sixth dword)
+    const uint32_t hi = (T == kGgmlQ5_0 ? r.y[k] : r.t[k]) >> 16;
     uint32_t e = lo, o = hi;
     if constexpr (T == kGgmlQ8_0) {
         const uint32_t mine = hf ? hi : lo;
@@ -329,9 +356,11 @@ __device__ __forceinline__ void qb_scales(const QbRegs &r, int k, int hf, float 
 // (Q4_0: its nibble half hf), exact integers in f16.
 template <int T>
 __device__ __forceinline__ void qb_operands(const QbRegs &r, int i, int hf, half8 (&b)[2], const DeqConst &dk) {
-    uint32_t w[4];
-    qb_words<T>(r, i, w);
+    uint32_t w[4], qh = 0;
+    qb_words<T>(r, i, w, &qh);
+    const uint32_t hq = qh >> (16 * hf);  // Q5_0: the fifth bits of the lane's 16 elements
     const half2_t off = T == kGgmlQ8_0 ? half2_t{(_Float16)1152.0f, (_Float16)1152.0f}
+                      : T == kGgmlQ5_0 ? half2_t{(_Float16)1040.0f, (_Float16)1040.0f}
                                        : half2_t{(_Float16)1032.0f, (_Float16)1032.0f};
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -340,10 +369,16 @@ __device__ __forceinline__ void qb_operands(const QbRegs &r, int i, int hf, half
             const uint32_t sel = p ? 0x0C030C02u : 0x0C010C00u;
             const uint32_t sp = __builtin_amdgcn_perm(w[q], w[q], sel);  // bytes 2p, 2p+1 -> halves
             uint32_t u;
-            if constexpr (T == kGgmlQ8_0)
+            if constexpr (T == kGgmlQ8_0) {
                 u = (sp ^ 0x00800080u) | dk.magic;  // 1024 + (q + 128)
-            else
+            } else {
                 u = ((hf ? (sp >> 4) : sp) & dk.lo) | dk.magic;  // 1024 + n
+                if constexpr (T == kGgmlQ5_0) {
+                    // bits 4q + 2p and 4q + 2p + 1 of hq to bit 4 of either half
+                    const uint32_t b2 = hq >> (4 * q + 2 * p);
+                    u |= ((b2 & 1u) << 4) | ((b2 & 2u) << 19);  // 1024 + n + 16 h
+                }
+            }
             const half2_t v = __builtin_bit_cast(half2_t, u) - off;
             b[q >> 1][4 * (q & 1) + 2 * p] = v[0];
             b[q >> 1][4 * (q & 1) + 2 * p + 1] = v[1];
@@ -351,7 +386,7 @@ __device__ __forceinline__ void qb_operands(const QbRegs &r, int i, int hf, half
     }
 }
 
-// gemm_split_kq for Q4_0 / Q8_0 rows (same thread roles, LDS x tiles and D layout).
+// gemm_split_kq for Q4_0 / Q5_0 / Q8_0 rows (same thread roles, LDS x tiles and D layout).
 template <int T>
 __device__ __forceinline__ void gemm_split_qb(KqTiles (&sm)[2], const float *xs, const uint8_t *const (&wb)[2],
                                               int nbat, int tid, floatx16 (&acc)[2]) {

@@ -661,7 +661,7 @@ int ts_qkv_append_x2(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, in
 // ---- projections with GGUF K-quant weights read in the loop ----------------------------------
 
 static bool kq_type_ok(int32_t t) {
-    return t == TS_GGML_Q4_K || t == TS_GGML_Q5_K || t == TS_GGML_Q4_0 || t == TS_GGML_Q8_0;
+    return t == TS_GGML_Q4_K || t == TS_GGML_Q5_K || t == TS_GGML_Q4_0 || t == TS_GGML_Q5_0 || t == TS_GGML_Q8_0;
 }
 
 struct QkvGenericKq {

@@ -241,6 +241,8 @@ hipError_t launch_proj_kq(const float *a, int M, int K, int ggml_type, const voi
         proj_split_kq_kernel<kGgmlQ5K><<<grid, 256, 0, st>>>(p);
     else if (ggml_type == kGgmlQ8_0)
         proj_split_kq_kernel<kGgmlQ8_0><<<grid, 256, 0, st>>>(p);
+    else if (ggml_type == kGgmlQ5_0)
+        proj_split_kq_kernel<kGgmlQ5_0><<<grid, 256, 0, st>>>(p);
     else
         proj_split_kq_kernel<kGgmlQ4_0><<<grid, 256, 0, st>>>(p);
     proj_reduce_kernel<<<plan.RT * plan.CT * (32 / kPRows), 256, 0, st>>>(p);

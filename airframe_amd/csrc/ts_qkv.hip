@@ -526,6 +526,8 @@ hipError_t launch_qkv_kq(const KvLayerView &L, const int32_t *d_len, const float
         qkv_split_kq_kernel<kGgmlQ5K><<<grid, 256, 0, st>>>(a);
     else if (ggml_type == kGgmlQ8_0)
         qkv_split_kq_kernel<kGgmlQ8_0><<<grid, 256, 0, st>>>(a);
+    else if (ggml_type == kGgmlQ5_0)
+        qkv_split_kq_kernel<kGgmlQ5_0><<<grid, 256, 0, st>>>(a);
     else
         qkv_split_kq_kernel<kGgmlQ4_0><<<grid, 256, 0, st>>>(a);
     if (n_tok == 1)

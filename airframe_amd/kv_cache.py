@@ -369,8 +369,8 @@ class KVCache:
                         wk: torch.Tensor, wv: torch.Tensor, rope: RopeTable,
                         q_out: torch.Tensor = None, kv_out: tuple | None = None,
                         workspace: torch.Tensor = None, stream=None):
-        """qkv_append with the weights as the GGUF blob's Q4_K / Q5_K / Q8_0 / Q4_0 blocks (uint8
-        CUDA tensors of [rows, the row's block bytes] or flat), read inside the projection loop
+        """qkv_append with the weights as the GGUF blob's Q4_K / Q5_K / Q8_0 / Q4_0 / Q5_0 blocks
+        (uint8 CUDA tensors of [rows, the row's block bytes] or flat), read inside the projection loop
         (ts_qkv_append_gguf).  dim a multiple of 256."""
         if x.dim() != 3 or x.shape[0] != self.n_seq:
             raise ValueError("x must be [n_seq, n_tok, dim]")
@@ -479,7 +479,7 @@ def attn_out_proj(attn: torch.Tensor, wo: torch.Tensor, act: torch.Tensor,
 def attn_out_proj_gguf(attn: torch.Tensor, ggml_type: int, wo: torch.Tensor, dim: int, act: torch.Tensor,
                        stash: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
                        stream=None) -> torch.Tensor:
-    """attn_out_proj with wo as the GGUF blob's Q4_K / Q5_K / Q8_0 / Q4_0 blocks ([dim] rows of
+    """attn_out_proj with wo as the GGUF blob's Q4_K / Q5_K / Q8_0 / Q4_0 / Q5_0 blocks ([dim] rows of
     attn_dim elements, uint8), read inside the projection loop (ts_attn_out_proj_gguf).  Returns
     act."""
     from .weights import src_bytes

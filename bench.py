@@ -532,7 +532,7 @@ def run_append(args, cfg):
     return ms, B * n_tok * n_kv * (2 * hd * 4 + hd + 8), B * n_tok
 
 
-KQ_BLOCK = {12: 144, 13: 176, 8: 272, 2: 144}  # bytes of 256 elements of a Q4_K / Q5_K / Q8_0 / Q4_0 row
+KQ_BLOCK = {12: 144, 13: 176, 8: 272, 2: 144, 6: 176}  # bytes of 256 elements of a Q4_K / Q5_K / Q8_0 / Q4_0 / Q5_0 row
 
 
 def kq_blob(gen, rows, cols, ggml_type, dev):
@@ -944,7 +944,7 @@ def main():
                     help="time the attention output projection + residual (ts_attn_out_proj) instead")
     ap.add_argument("--planes", type=int, default=1, choices=(1, 2),
                     help="with --qkv/--proj: 2 = two-plane weights (F32 / GGUF formats, the _x2 entry points)")
-    ap.add_argument("--gguf", default=None, choices=("q4_k", "q5_k", "q8_0", "q4_0"),
+    ap.add_argument("--gguf", default=None, choices=("q4_k", "q5_k", "q8_0", "q4_0", "q5_0"),
                     help="with --qkv/--proj: weights as GGUF blocks read in the loop (the _gguf entry points)")
     ap.add_argument("--convert", default=None, choices=sorted(CONVERT_TYPES),
                     help="time ts_weights_to_f16x2 on the configuration's Wq of that GGUF type")

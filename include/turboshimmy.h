@@ -345,14 +345,16 @@ int ts_attn_out_proj_x2(const float *d_attn, int32_t n_tok, int32_t attn_dim, co
 /* ---- projections with GGUF block weights read at their own size --------------------------- */
 
 /* Bytes of scratch ts_qkv_append_gguf needs for this shape (ggml_type TS_GGML_Q4_K,
- * TS_GGML_Q5_K, TS_GGML_Q8_0 or TS_GGML_Q4_0; dim a multiple of 256).  Host only. */
+ * TS_GGML_Q5_K, TS_GGML_Q8_0, TS_GGML_Q4_0 or TS_GGML_Q5_0; dim a multiple of 256).  Host
+ * only. */
 int ts_qkv_gguf_workspace(const ts_kv *kv, int32_t ggml_type, int32_t dim, int32_t n_tok, int32_t n_head,
                           uint64_t *bytes);
 
-/* ts_qkv_append with the weights as the GGUF blob's own Q4_K, Q5_K, Q8_0 or Q4_0 blocks, read
- * inside the projection loop as main_qkv reads them (sh_layer_v1_int4.wgsl:502-520; the values
- * of q4_k.rs:75-123, q5_k.rs:74-143, q8_0.rs, q4_0.rs), so a weight moves 0.5625 (Q4_K, Q4_0),
- * 0.6875 (Q5_K) or 1.0625 (Q8_0) bytes instead of the 4 of ts_qkv_append_x2's planes.  d_wq:
+/* ts_qkv_append with the weights as the GGUF blob's own Q4_K, Q5_K, Q8_0, Q4_0 or Q5_0 blocks,
+ * read inside the projection loop as main_qkv reads them (sh_layer_v1_int4.wgsl:502-520; the
+ * values of q4_k.rs:75-123, q5_k.rs:74-143, q8_0.rs, q4_0.rs, q5_0.rs), so a weight moves
+ * 0.5625 (Q4_K, Q4_0), 0.6875 (Q5_K, Q5_0) or 1.0625 (Q8_0) bytes instead of the 4 of
+ * ts_qkv_append_x2's planes.  d_wq:
  * [n_head*head_dim] rows of dim elements, d_wk, d_wv: [n_head_kv*head_dim] rows, all 16-byte
  * aligned (the blocks of one type for all three); dim a multiple of 256.  Results agree with the
  * f32-weight dot to f32 rounding (x is split hi + lo in f16, |x| < 65504, as in ts_qkv_append).
@@ -367,7 +369,7 @@ int ts_qkv_append_gguf(ts_kv *kv, int32_t layer, const float *d_x, int32_t dim, 
 int ts_attn_out_proj_gguf_workspace(int32_t ggml_type, int32_t n_tok, int32_t attn_dim, int32_t dim,
                                     uint64_t *bytes);
 
-/* ts_attn_out_proj with d_wo as the GGUF blob's Q4_K, Q5_K, Q8_0 or Q4_0 blocks ([dim] rows of
+/* ts_attn_out_proj with d_wo as the GGUF blob's Q4_K, Q5_K, Q8_0, Q4_0 or Q5_0 blocks ([dim] rows of
  * attn_dim elements, 16-byte aligned; attn_dim a multiple of 256), read in the loop as
  * main_attn_proj reads them (sh_layer_v1.wgsl:782-790). */
 int ts_attn_out_proj_gguf(const float *d_attn, int32_t n_tok, int32_t attn_dim, int32_t ggml_type, const void *d_wo,

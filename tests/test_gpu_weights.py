@@ -140,9 +140,12 @@ def test_attn_out_proj_with_block_weights(gpu, fmt, n_tok, attn_dim, dim):
     (weights.Q8_0, 3, 70, 1024, 128),  # block rows
     (weights.Q4_0, 2, 1, 512, 64),     # head dim 64
     (weights.Q8_0, 4, 1, 768, 96),     # head dim 96
+    (weights.Q5_0, 8, 1, 2048, 128),
+    (weights.Q5_0, 3, 70, 1024, 128),
+    (weights.Q5_0, 4, 1, 768, 96),
 ])
 def test_qkv_append_gguf_blocks_in_loop(gpu, fmt, n_seq, n_tok, dim, hd):
-    """ts_qkv_append_gguf: Q4_K / Q5_K / Q8_0 / Q4_0 blocks read inside the projection loop, against the dot
+    """ts_qkv_append_gguf: Q4_K / Q5_K / Q8_0 / Q4_0 / Q5_0 blocks read inside the projection loop, against the dot
     over the oracle's exact dequantized f32 weights (q4_k.rs / q5_k.rs, pinned in
     test_oracle_weights.py), and the appended codes bit-exact with the quantizer applied to
     those projections."""
@@ -177,6 +180,8 @@ def test_qkv_append_gguf_blocks_in_loop(gpu, fmt, n_seq, n_tok, dim, hd):
     (weights.Q4_0, 130, 1024, 768),
     (weights.Q8_0, 1100, 512, 2304),
     (weights.Q4_0, 1, 3072, 3072),    # batch 1 (config 2's attention width)
+    (weights.Q5_0, 5, 2048, 2048),
+    (weights.Q5_0, 1100, 512, 2304),
 ])
 def test_attn_out_proj_gguf_blocks_in_loop(gpu, fmt, n_tok, attn_dim, dim):
     """ts_attn_out_proj_gguf against the oracle's f32-weight dot and the residual add."""
