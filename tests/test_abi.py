@@ -68,6 +68,64 @@ def test_header_compiles_as_c():
     assert r.returncode == 0, r.stderr
 
 
+HEADER_HPP = os.path.join(os.path.dirname(HEADER), "turboshimmy.hpp")
+
+
+def test_cpp_host_side_header_compiles():
+    """include/turboshimmy.hpp (the C++ mirror of kv_cache.rs's KVCache) compiles as C++17
+    with every member used."""
+    src = f"""#include "{HEADER_HPP}"
+namespace t = turboshimmy;
+int use(t::KVCache &kv, t::RopeTable &r, float *p, unsigned *u, void *ws) {{
+    kv.append_quant(0, p, p, 1, r); kv.requant_all(0, p, p, 1, 1, &r);
+    kv.attn_decode(0, p, 8, r, p, ws, 0); kv.attn_decode_append(0, p, p, p, 8, r, p, ws, 0, true);
+    kv.attn_prefill(0, p, 8, 1, r, p); kv.shift_int4(0, 4, 8, 0, ws, 0); kv.set_qk_norm(0, p, p);
+    kv.export_layer(0, 0, 0, 1, u, u, p, p); kv.reset(); kv.reset(0, nullptr); kv.set_seq_len(1);
+    kv.advance_window_base(1); t::Status s = kv.increment();
+    return (int)kv.get_seq_len() + (int)kv.max_len() + (int)kv.get_window_base() + (int)kv.is_int4() +
+           (int)kv.calculate_offset(0, 0, 0) + (int)kv.decode_workspace_bytes(8) + (int)kv.shift_workspace_bytes() +
+           s.code + r.n_pos() + r.rope_dim() + (r.device_table() != nullptr);
+}}
+"""
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-x", "c++", "-", "-fsyntax-only"],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_cpp_host_side_host_only_calls(tmp_path):
+    """The C++ mirror's host-only members against the library on the CPU: the RoPE host
+    table equals the oracle's bit for bit, bytes_for equals ts_kv_bytes, and a head_dim that
+    is not a multiple of 8 is refused with an Error carrying TS_ERR_INVALID."""
+    from oracle import oracle
+    src = f"""#include "{HEADER_HPP}"
+#include <cstdio>
+int main() {{
+    const auto t = turboshimmy::RopeTable::host_table(40, 64, 500000.0f);
+    std::fwrite(t.data(), sizeof(float), t.size(), stdout);
+    std::fprintf(stderr, "%llu\\n", (unsigned long long)turboshimmy::KVCache::bytes_for(2, 8, 128, 100, 3));
+    try {{ (void)turboshimmy::KVCache::bytes_for(1, 8, 60, 16); }}
+    catch (const turboshimmy::Error &e) {{ std::fprintf(stderr, "%d\\n", e.code()); }}
+    return 0;
+}}
+"""
+    exe = tmp_path / "host_only"
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-x", "c++", "-", "-o", str(exe),
+                        f"-L{libdir}", "-lturboshimmy", f"-Wl,-rpath,{libdir}"],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True)
+    assert r.returncode == 0, r.stderr
+    got = np.frombuffer(r.stdout, dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), oracle.rope_table(40, 64, 500000.0).reshape(-1).view(np.uint32))
+    lines = r.stderr.decode().split()
+    want = ctypes.c_uint64()
+    d = _lib.KvDesc(2, 3, 8, 128, 100)
+    assert airframe_amd.load().ts_kv_bytes(ctypes.byref(d), ctypes.byref(want)) == 0
+    assert int(lines[0]) == want.value
+    assert int(lines[1]) == _lib.TS_ERR_INVALID
+
+
 def test_status_strings():
     L = airframe_amd.load()
     assert L.ts_status_string(0) == b"ok"
