@@ -43,6 +43,10 @@ namespace {
 struct DecodeArgs {
     KvLayerView L;
     const int32_t *len;
+    // hlen >= 0 (one sequence): its length, given by the host with the launch (as the
+    // reference passes its uniforms) instead of read from len[] first: an eager call whose
+    // host length is known to match the device's.  -1: read len[].
+    int hlen;
     const float *q;
     const float *rope;
     int rope_pairs;
@@ -542,7 +546,7 @@ __global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_ker
     for (int t = 0; t < WPG; t++) q_read8(qrow, k16_word<HD>(g, t), nullptr, 1.0f, qraw[t], hdr);
     asm volatile("" ::: "memory");
 
-    const int qpos = a.len[s];
+    const int qpos = a.hlen >= 0 ? a.hlen : a.len[s];
     // a captured launch replayed past the cache's capacity (the host checks lengths only when a
     // call is made): no work, nothing written
     if (qpos >= L.P) return;
@@ -802,7 +806,7 @@ __device__ __forceinline__ void combine_rows(const DecodeArgs &a, int head, int 
 template <int HD>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     const int head = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
-    const int n_ctx = a.len[s] + 1;
+    const int n_ctx = (a.hlen >= 0 ? a.hlen : a.len[s]) + 1;
     const int ns = min((n_ctx + a.chunk - 1) / a.chunk, a.n_split);
     if (ns > 1) combine_rows<HD>(a, head, s, ns, tid);
     arrive_and_advance(a);
@@ -1060,7 +1064,7 @@ __global__ __launch_bounds__(64 * NW, NW / 4) void decode_split4_kernel(DecodeAr
     // split 1, so the splits that wait for a free CU are the last ones of the longest
     // sequences (config 4: 1.42 vs 1.45 ms per step against the split-fastest order)
     const int split = blockIdx.z, h = blockIdx.x, s = blockIdx.y;
-    const int qpos = a.len[s];
+    const int qpos = a.hlen >= 0 ? a.hlen : a.len[s];
     // a captured launch replayed past the cache's capacity (the host checks lengths only when a
     // call is made): no work, nothing written
     if (qpos >= L.P) return;
@@ -1506,13 +1510,14 @@ void launch_integer(const DecodeArgs &a, int n_split, bool pad, int Gt, hipStrea
 }
 }  // namespace
 
-hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, int n_head,
+hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const int32_t *h_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,
                          const float *v_new, int32_t *adv, hipStream_t st) {
     DecodeArgs a;
     a.L = L;
     a.len = d_len;
+    a.hlen = h_len && L.S == 1 ? h_len[0] : -1;
     a.q = q;
     a.rope = rope;
     a.rope_pairs = rope_pairs;

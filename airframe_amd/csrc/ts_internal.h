@@ -95,6 +95,10 @@ struct ts_kv {
     std::vector<const float *> q_norm, k_norm;  // per layer, device pointers or null
     std::vector<float> norm_eps;
     std::vector<int32_t> h_ctx;  // scratch for the decode plan: len + 1 per sequence
+    // Set once a call that changes the device lengths was captured into a graph: replays of it
+    // advance the device lengths without the host knowing, so decode launches read the device
+    // lengths from then on instead of taking the host's as arguments.
+    bool len_captured = false;
     int device;
     int n_cu;                    // compute units of the device (the decode plan's target)
     int hdp;                     // stored head dim (KvLayerView::hd)
@@ -161,8 +165,11 @@ inline int decode_int_gmax(int stored_hd) { return stored_hd <= 128 ? 16 : 8; }
 int decode_cap(int n_kv, int max_seq, int n_cu);
 // adv: null, or the cache's arrival counter: the launch then also advances every length by
 // one once all of its workgroups have read them (plans with a split: in the combine kernel;
-// without: a length-update launch after the decode).
-hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const float *q, int n_head,
+// without: a length-update launch after the decode).  h_len: null, or the lengths of the n_seq
+// sequences as the host knows them when they are known to match the device's (an eager
+// call): with one sequence the kernels then take its length as an argument instead of reading
+// d_len first.
+hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const int32_t *h_len, const float *q, int n_head,
                          const float *rope, int rope_pairs, float softcap, float *out,
                          float *ws, const DecodePlan &plan, const float *k_new,
                          const float *v_new, int32_t *adv, hipStream_t st);

@@ -16,6 +16,16 @@ namespace {
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// True when work enqueued on the stream now goes into a graph being captured.
+static bool capturing(void *stream) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(as_stream(stream), &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+// A call that changes the device lengths: note when it is being captured.
+static void note_len_change(ts_kv *kv, void *stream) {
+    if (capturing(stream)) kv->len_captured = true;
+}
+
 int hip_status(hipError_t e) { return e == hipSuccess ? TS_OK : TS_ERR_HIP; }
 
 bool desc_valid(const ts_kv_desc *d) {
@@ -248,6 +258,7 @@ int ts_kv_increment(ts_kv *kv, int32_t n_tok, void *stream) {
     for (int32_t l : kv->h_len)
         if ((int64_t)l + n_tok > kv->d.max_seq) return TS_ERR_OVERFLOW;
     if (n_tok == 0) return TS_OK;
+    note_len_change(kv, stream);
     hipError_t e = ts::launch_len_update(kv->d_len, kv->d.n_seq, -1, n_tok, 0, as_stream(stream));
     if (e != hipSuccess) return TS_ERR_HIP;
     for (auto &l : kv->h_len) l += n_tok;
@@ -257,6 +268,7 @@ int ts_kv_increment(ts_kv *kv, int32_t n_tok, void *stream) {
 int ts_kv_set_seq_len(ts_kv *kv, int32_t seq, int32_t len, void *stream) {
     if (!kv || seq < 0 || seq >= kv->d.n_seq || len < 0) return TS_ERR_INVALID;
     if (len > kv->d.max_seq) return TS_ERR_OVERFLOW;
+    note_len_change(kv, stream);
     hipError_t e = ts::launch_len_update(kv->d_len, kv->d.n_seq, seq, len, 1, as_stream(stream));
     if (e != hipSuccess) return TS_ERR_HIP;
     kv->h_len[seq] = len;
@@ -266,6 +278,7 @@ int ts_kv_set_seq_len(ts_kv *kv, int32_t seq, int32_t len, void *stream) {
 int ts_kv_reset(ts_kv *kv, void *stream) {
     if (!kv) return TS_ERR_INVALID;
     // lengths, window bases and sink counts: 3 n_seq consecutive ints
+    note_len_change(kv, stream);
     hipError_t e = ts::launch_len_update(kv->d_len, 3 * kv->d.n_seq, -1, 0, 1, as_stream(stream));
     if (e != hipSuccess) return TS_ERR_HIP;
     std::fill(kv->h_len.begin(), kv->h_len.end(), 0);
@@ -277,6 +290,7 @@ int ts_kv_reset(ts_kv *kv, void *stream) {
 int ts_kv_reset_seq(ts_kv *kv, int32_t seq, void *stream) {
     if (!kv || seq < 0 || seq >= kv->d.n_seq) return TS_ERR_INVALID;
     hipStream_t st = as_stream(stream);
+    note_len_change(kv, stream);
     hipError_t e = ts::launch_len_update(kv->d_len, kv->d.n_seq, seq, 0, 1, st);
     if (e == hipSuccess) e = ts::launch_len_update(kv->d_rot, kv->d.n_seq, seq, 0, 1, st);
     if (e == hipSuccess) e = ts::launch_len_update(kv->d_sink, kv->d.n_seq, seq, 0, 1, st);
@@ -308,6 +322,7 @@ int ts_kv_advance_window_base(ts_kv *kv, int32_t seq, int32_t shift_amt, void *s
     if (!kv || seq < 0 || seq >= kv->d.n_seq || shift_amt < 0) return TS_ERR_INVALID;
     if ((int64_t)kv->h_rot[seq] + shift_amt > INT32_MAX / 2) return TS_ERR_OVERFLOW;
     if (shift_amt == 0) return TS_OK;
+    note_len_change(kv, stream);
     hipError_t e = ts::launch_len_update(kv->d_rot, kv->d.n_seq, seq, shift_amt, 0, as_stream(stream));
     if (e != hipSuccess) return TS_ERR_HIP;
     kv->h_rot[seq] += shift_amt;
@@ -467,7 +482,14 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
         if (!d_workspace || workspace_bytes < need) return TS_ERR_WORKSPACE;
         if (!aligned16(d_workspace)) return TS_ERR_INVALID;
     }
-    const int rc2 = hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, d_q, n_head, rope->d_table,
+    // An eager call takes the host's lengths as launch arguments (the device's agree with them
+    // unless a captured call changed them); one being captured reads the device lengths, so
+    // that replays see the lengths of their time.
+    ts_kv *mkv = const_cast<ts_kv *>(kv);
+    const bool cap = capturing(stream);
+    if (cap && advance) mkv->len_captured = true;
+    const int32_t *h_len = cap || kv->len_captured ? nullptr : kv->h_len.data();
+    const int rc2 = hip_status(ts::launch_decode(kv->layer(layer), kv->d_len, h_len, d_q, n_head, rope->d_table,
                                                  rope->rope_dim / 2, softcap, d_out, (float *)d_workspace,
                                                  plan, k_new, v_new, advance ? kv->d_adv : nullptr,
                                                  as_stream(stream)));

@@ -283,3 +283,62 @@ def test_graph_replays_qkv_append_other_head_dim(gpu):
             for u, w in zip(a, b):
                 assert torch.equal(u.view(torch.uint8), w.view(torch.uint8)), f"replay {r}: codes of seq {s}"
     del graph
+
+
+def test_eager_after_replays_reads_device_lengths(gpu):
+    """Batch 1: eager decode calls take the host's length as a launch argument (as the
+    reference passes its uniforms).  Once a call that advances the lengths has been captured,
+    replays move the device length past the host's; the eager calls after them must read the
+    device length (no host resynchronisation in between) and still match the oracle."""
+    say("eager decode after replays that advanced the device length")
+    rng = np.random.default_rng(330)
+    n_head = 8
+    p = Pair(1, 2, 128, 3000, 1e6)
+    fill(p, rng, 1500)
+
+    def eager_step(advance):
+        k = synth.normal(rng, (1, 1, 2, 128))
+        v = synth.normal(rng, (1, 1, 2, 128))
+        q = synth.normal(rng, (1, n_head, 128))
+        out = p.gpu.attn_decode_append(0, dev(k), dev(v), dev(q), p.rope, advance=advance).cpu().numpy()
+        p.ora.append(k, v)
+        ref = p.ora.attend(q[:, None], 1, threads=8)[:, 0]
+        p.ora.advance(1)
+        if not advance:
+            p.gpu.increment(1)
+        return out, ref
+
+    for t in range(2):  # eager: the host length as the launch argument
+        out, ref = eager_step(advance=t == 1)
+        assert_close(out, ref, f"eager step {t}")
+    k_in = torch.zeros((1, 1, 2, 128), device="cuda")
+    v_in = torch.zeros_like(k_in)
+    q_in = torch.zeros((1, n_head, 128), device="cuda")
+    out = torch.empty((1, n_head, 128), device="cuda")
+    ws = p.gpu.workspace(n_head)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=cap):
+        p.gpu.attn_decode_append(0, k_in, v_in, q_in, p.rope, out=out, workspace=ws, advance=True)
+    torch.cuda.synchronize()
+    for r in range(3):
+        k = synth.normal(rng, (1, 1, 2, 128))
+        v = synth.normal(rng, (1, 1, 2, 128))
+        q = synth.normal(rng, (1, n_head, 128))
+        k_in.copy_(dev(k))
+        v_in.copy_(dev(v))
+        q_in.copy_(dev(q))
+        graph.replay()
+        torch.cuda.synchronize()
+        p.ora.append(k, v)
+        ref = p.ora.attend(q[:, None], 1, threads=8)[:, 0]
+        p.ora.advance(1)
+        assert_close(out.cpu().numpy(), ref, f"replay {r}")
+    del graph
+    # the host length advanced once (at capture), the device's three times: 2 ahead
+    assert p.gpu.get_seq_len(0) == int(p.ora.lens[0]) - 2
+    out, ref = eager_step(advance=False)
+    assert_close(out, ref, "eager step after the replays, at the device length")
+    p.check_codes()
