@@ -28,7 +28,13 @@ struct ProbeArgs {
     const float *ks, *vs;    // [rows][P]
     int P, n_ctx;
     uint32_t *sink;
+    // null, or per workgroup (row): start and end of its loads on the 100 MHz constant clock
+    // (s_memrealtime) and the XCD it ran on (hardware register XCC_ID)
+    uint64_t *stamps;
 };
+
+// XCC_ID (hardware register 20 on gfx94x/gfx950), bits 0..3: the XCD of this wave.
+__device__ inline uint32_t xcd_id() { return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 0xFu; }
 
 template <int HD>
 __global__ __launch_bounds__(256, 1) void probe_decode_loads_kernel(ProbeArgs a) {
@@ -64,6 +70,8 @@ __global__ __launch_bounds__(256, 1) void probe_decode_loads_kernel(ProbeArgs a)
         w[NKW / 4 + NTD / 2 + 1] = __builtin_amdgcn_raw_buffer_load_b128(rt, (lane & 15) * 16, base * 4, kNT);
     };
     uint32_t acc = 0;
+    uint64_t t0 = 0;
+    if (a.stamps) t0 = __builtin_amdgcn_s_memrealtime();
     load(buf[0], win_base(0));
     for (int it = 0; it < cnt; it += 2) {
 #pragma unroll
@@ -78,6 +86,14 @@ __global__ __launch_bounds__(256, 1) void probe_decode_loads_kernel(ProbeArgs a)
         }
     }
     if (acc == 0x9E3779B9u) a.sink[0] = acc;  // keeps the loads; practically never taken
+    if (a.stamps) {
+        __syncthreads();  // every wave's last window consumed
+        if (threadIdx.x == 0) {
+            a.stamps[3 * row] = t0;
+            a.stamps[3 * row + 1] = __builtin_amdgcn_s_memrealtime();
+            a.stamps[3 * row + 2] = xcd_id();
+        }
+    }
 }
 
 // The same reads handed out dynamically: units of UW windows of one stream (unit u: chunk u /
@@ -212,12 +228,13 @@ extern "C" int ts_probe_mfma_rate(int kind, int grid, int iters, void *sink, voi
 
 // One loads-only pass of the decode pattern over rows = n_seq * n_kv streams of n_ctx
 // positions (P = padded positions per stream, a multiple of 64).  Returns a hipError_t.
+// stamps: null, or 3 x n_seq x n_kv u64 (per workgroup: start, end, XCD).
 extern "C" int ts_probe_decode_loads(const void *kp, const void *vp, const void *ks, const void *vs,
                                      int n_seq, int n_kv, int hd, int P, int n_ctx, void *sink,
-                                     void *stream) {
+                                     void *stamps, void *stream) {
     if (P % 64 || n_ctx > P || n_ctx <= 0 || n_seq <= 0 || n_kv <= 0) return (int)hipErrorInvalidValue;
     ProbeArgs a{(const uint8_t *)kp, (const uint8_t *)vp, (const float *)ks, (const float *)vs, P, n_ctx,
-                (uint32_t *)sink};
+                (uint32_t *)sink, (uint64_t *)stamps};
     const dim3 grid(n_kv, n_seq);
     // one workgroup per CU, as the decode's plan places them: an unused LDS reservation of
     // more than half the CU's 160 KB keeps a second one off

@@ -841,11 +841,12 @@ def run_stream_ceiling(args, cfg):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n * 1e3
 
-    def dec(i):
+    def dec(i, stamps=None):
         kp, vp, ks, vs = sets[i % n_sets]
         rc = lib.ts_probe_decode_loads(ctypes.c_void_p(kp.data_ptr()), ctypes.c_void_p(vp.data_ptr()),
                                        ctypes.c_void_p(ks.data_ptr()), ctypes.c_void_p(vs.data_ptr()),
-                                       B, H, hd, P, ctx, ctypes.c_void_p(sink.data_ptr()), st)
+                                       B, H, hd, P, ctx, ctypes.c_void_p(sink.data_ptr()),
+                                       ctypes.c_void_p(stamps.data_ptr() if stamps is not None else 0), st)
         assert rc == 0, rc
 
     def flat_read(i):
@@ -857,6 +858,23 @@ def run_stream_ceiling(args, cfg):
     us_dec = timed(dec, n)
     us_flat = timed(flat_read, n)
     res = dict(bytes=nbytes, us_decode_pattern=us_dec, us_flat=us_flat, launches=n)
+
+    # per-workgroup stamps of 8 launches (start and end of its loads, 100 MHz clock, and its
+    # XCD): the per-XCD medians of the workgroups' streaming time and of their end times
+    stamps = torch.zeros(3 * B * H, dtype=torch.int64, device="cuda")
+    per_xcd, ends = {}, {}
+    for i in range(8):
+        dec(i, stamps)
+        torch.cuda.synchronize()
+        t = stamps.view(-1, 3).cpu().numpy()
+        t0 = t[:, 0].min()
+        for start, end, x in t:
+            per_xcd.setdefault(int(x), []).append((end - start) * 0.01)  # us
+            ends.setdefault(int(x), []).append((end - t0) * 0.01)
+    med = {x: float(np.median(v)) for x, v in sorted(per_xcd.items())}
+    res["per_xcd_median_stream_us"] = {str(x): round(v, 2) for x, v in med.items()}
+    res["per_xcd_median_end_us"] = {str(x): round(float(np.median(v)), 2) for x, v in sorted(ends.items())}
+    res["xcd_spread"] = round(max(med.values()) / min(med.values()), 4) if med else None
 
     # the same reads as 16-window units claimed from a launch-wide counter (a work queue)
     nw = ctx // 64 // 16 * 16
@@ -1071,6 +1089,9 @@ def main():
                           "frac": round(g_flat / HBM_PEAK_GBS, 4)},
             "claimed_units_us_per_launch": round(r["us_claimed_units"], 2) if "us_claimed_units" in r else None,
             "empty_launch_in_graph_us": round(r["us_empty_launch_in_graph"], 2),
+            "per_xcd_median_stream_us": r["per_xcd_median_stream_us"],
+            "per_xcd_median_end_us": r["per_xcd_median_end_us"],
+            "xcd_spread": r["xcd_spread"],
             "bytes_per_launch": r["bytes"], "launches": r["launches"],
             "config": {"workload": cfg["name"] + "_loads_only"}, "data": "uninitialised device buffers"}),
             flush=True)
