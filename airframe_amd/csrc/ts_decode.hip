@@ -27,15 +27,12 @@
 //   and scores carry f32-level accuracy; the probabilities enter PV split the same way.
 // * online softmax in the exp2 domain with one cross-lane max per 64 positions and lazy
 //   rescaling; s_v is folded into the probabilities under a per-window exponent bound so they
-//   never leave f16 range.  The 4 waves merge through LDS; splits merge in a second kernel
-//   (log-sum-exp combine) unless a sequence fits one split.
+//   never leave f16 range.  A workgroup's waves merge through LDS; splits merge in a second
+//   kernel (log-sum-exp combine) unless a sequence fits one split.
 #include <stdlib.h>
 
 #include "ts_mfma.h"
 #include "ts_quant.h"
-
-// Waves per workgroup of the 16x16 kernel.
-constexpr int kNW16 = 4;
 
 namespace ts {
 namespace {
@@ -496,9 +493,11 @@ __device__ inline void store_partial(const DecodeArgs &a, size_t head, int split
 
 // PAD: the caller's head dim hdr is below the stored HD (rows of q, new K/V and the output are
 // hdr floats; the stored dims past them hold zeros).
-template <int HD, bool SOFTCAP, bool NORM, bool PAD>
-__global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_kernel(DecodeArgs a) {
-    constexpr int NW = kNW16;  // waves per workgroup
+// NW waves per workgroup: 4 (two workgroups per CU up to 128 dims), or 8 / 16 for a plan that
+// gives every (sequence, kv head) stream one workgroup (a CU) of its own and no split: the
+// small-batch case, where the combine launch would be most of the step.
+template <int HD, bool SOFTCAP, bool NORM, bool PAD, int NW>
+__global__ __launch_bounds__(64 * NW, NW > 4 ? 1 : (HD > 128 ? 1 : 2)) void decode_split_kernel(DecodeArgs a) {
     constexpr int SPAN = 64 * NW;     // positions one round of windows covers
     constexpr int WPG = HD / 32;   // K words per lane group = MFMA k-steps per 16-row tile
     constexpr int NTD = HD / 16;   // 16-dim output tiles
@@ -548,11 +547,15 @@ __global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_ker
 
     const int qpos = a.hlen >= 0 ? a.hlen : a.len[s];
     // a captured launch replayed past the cache's capacity (the host checks lengths only when a
-    // call is made): no work, nothing written
-    if (qpos >= L.P) return;
+    // call is made): no work, nothing written (the lengths still advance, as the combine
+    // kernel's do)
+    if (qpos >= L.P) {
+        if (a.n_split == 1) arrive_and_advance(a);
+        return;
+    }
     const int qrot = rot_of(a.L, s, qpos);  // rotation position of the query
     const int n_ctx = qpos + 1;
-    if (start >= n_ctx) return;
+    if (start >= n_ctx) return;  // (only with a split: its combine kernel advances the lengths)
     const int n_split_s = min((n_ctx + a.chunk - 1) / a.chunk, a.n_split);
     // With the fused append, this split's workgroup writes position qpos itself and adds its
     // score from registers; the window loop then stops short of it.
@@ -657,7 +660,7 @@ __global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_ker
     }
 #undef TS_STEP
 
-    // ---- merge the 4 waves through LDS ---------------------------------------------------------
+    // ---- merge the waves through LDS -----------------------------------------------------------
     // Each wave writes its O^T columns (16-byte stores), m and l; one barrier; then one float4
     // of dims per thread.  (Merge area shared with the q operands, a barrier before the writes,
     // scalar stores and one dim per thread: 0.1-0.3 us more per layer on configs 1 and 2.)
@@ -709,6 +712,8 @@ __global__ __launch_bounds__(64 * kNW16, HD > 128 ? 1 : 2) void decode_split_ker
             for (int k = 0; k < 4; k++) store_partial(a, head, split, HD, d + k, acc[k], M, lsum);
         }
     }
+    // without a split this is the launch's last kernel: it advances the lengths itself
+    if (a.n_split == 1) arrive_and_advance(a);
 }
 
 // The merge of one (sequence, head) over its ns > 1 splits (body of decode_combine_kernel).
@@ -1424,8 +1429,10 @@ int plan_chunk(const int32_t *n_ctx, int n_seq, int n_kv, int target) {
 }
 }  // namespace
 
-DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, int int_gmax) {
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, int stored_hd, bool fused) {
+    const int int_gmax = decode_int_gmax(stored_hd);
     DecodePlan p;
+    p.nw = 4;
     int max_ctx = 1;
     for (int s = 0; s < n_seq; s++) max_ctx = std::max(max_ctx, (int)n_ctx[s]);
     p.g4 = false;
@@ -1442,6 +1449,25 @@ DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_c
     // the 16x16 kernel takes up to 8 query heads per workgroup: more as several head groups
     if (!p.g4) p.chunk = plan_chunk(n_ctx, n_seq, n_kv * ((G + 7) / 8), 2 * n_cu);
     p.n_split = (max_ctx + p.chunk - 1) / p.chunk;
+    // Few streams, short context: one wide workgroup per stream instead of a split, when its
+    // waves cover the longest sequence's windows (the positions before the new token with the
+    // fused append, which scores that one from registers) in one round.  No combine launch
+    // (the split kernel then also advances the lengths), the merge stays in LDS.  The fewest
+    // waves that cover it: 8 waves measured 9.1 us per step on config 1's shape (512 positions
+    // + the new token), 16 waves 10.1, four-wave splits and a combine 10.5.  More than one
+    // window per wave does not pay: 8.5 windows per wave took 26.6 us per layer on config 2's
+    // shape against 10.0 with splits and a combine.
+    const int n_win = (max_ctx - (fused ? 1 : 0) + 63) / 64;
+    if (!p.g4 && n_win > 4 && (int64_t)n_seq * n_kv * ((G + 7) / 8) <= n_cu) {
+        const int wmax = stored_hd <= 64 ? 16 : stored_hd <= 128 ? 8 : 4;
+        for (int nw = 8; nw <= wmax; nw *= 2)
+            if (n_win <= nw) {
+                p.nw = nw;
+                p.chunk = (max_ctx + 63) / 64 * 64;
+                p.n_split = 1;
+                break;
+            }
+    }
     return p;
 }
 
@@ -1480,6 +1506,22 @@ void launch_split4(const DecodeArgs &a, int n_split, hipStream_t st) {
 // shape with 64-dim rows: 1.170 vs 1.378 ms per step at 8 query heads per kv head, 1.017 vs
 // 1.030 at 4; ragged config 4: 0.837 vs 0.886.  (With 128-dim rows and two halves of heads 8
 // waves measured slower: 1.970 vs 1.888.)
+template <int HD, bool SC, bool NM, bool PAD>
+void launch_16x16_pad(const DecodeArgs &a, dim3 grid, int nw, hipStream_t st) {
+    if (HD <= 128 && nw == 8)
+        decode_split_kernel<HD, SC, NM, PAD, HD <= 128 ? 8 : 4><<<grid, 64 * 8, 0, st>>>(a);
+    else if (HD <= 64 && nw == 16)
+        decode_split_kernel<HD, SC, NM, PAD, HD <= 64 ? 16 : 4><<<grid, 64 * 16, 0, st>>>(a);
+    else
+        decode_split_kernel<HD, SC, NM, PAD, 4><<<grid, 64 * 4, 0, st>>>(a);
+}
+
+template <int HD, bool SC, bool NM>
+void launch_16x16(const DecodeArgs &a, dim3 grid, int nw, bool pad, hipStream_t st) {
+    if (pad) launch_16x16_pad<HD, SC, NM, true>(a, grid, nw, st);
+    else launch_16x16_pad<HD, SC, NM, false>(a, grid, nw, st);
+}
+
 template <int HD, bool SC, bool NM>
 void launch_integer(const DecodeArgs &a, int n_split, bool pad, int Gt, hipStream_t st) {
     constexpr int NW = HD == 64 ? 8 : 4;
@@ -1535,8 +1577,10 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const int32_t *h_
     a.v_new = v_new;
     // with a split the combine kernel advances the lengths (the last of its workgroups to
     // arrive); without one a length update follows the decode launch
-    a.adv_len = adv && plan.n_split > 1 ? d_len : nullptr;
-    a.adv_ctr = adv && plan.n_split > 1 ? adv : nullptr;
+    // (the 16x16 kernel does it itself when there is no split)
+    const bool adv_in_kernel = plan.n_split > 1 || !plan.g4;
+    a.adv_len = adv && adv_in_kernel ? d_len : nullptr;
+    a.adv_ctr = adv && adv_in_kernel ? adv : nullptr;
     dim3 grid(plan.n_split, L.H * a.NG, L.S);
     // The integer kernel does less VALU work per window than the 16x16 one but has the longer
     // per-window dependency chain; it runs when every wave streams at least 4 windows of its
@@ -1545,8 +1589,7 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const int32_t *h_
     const bool pad = L.hdr != L.hd;
 #define TS_SPLIT(HDV, SC, NM)                                                                  \
     (plan.g4 ? (launch_integer<HDV, SC, NM>(a, plan.n_split, pad, a.Gt, st), 0) \
-             : pad ? (decode_split_kernel<HDV, SC, NM, true><<<grid, 64 * kNW16, 0, st>>>(a), 0)         \
-                   : (decode_split_kernel<HDV, SC, NM, false><<<grid, 64 * kNW16, 0, st>>>(a), 0))
+             : (launch_16x16<HDV, SC, NM>(a, grid, plan.nw, pad, st), 0))
 #define TS_SPLIT_HD(HDV)                                                                      \
     (cap ? (norm ? TS_SPLIT(HDV, true, true) : TS_SPLIT(HDV, true, false))                    \
          : (norm ? TS_SPLIT(HDV, false, true) : TS_SPLIT(HDV, false, false)))
@@ -1564,7 +1607,7 @@ hipError_t launch_decode(const KvLayerView &L, int32_t *d_len, const int32_t *h_
     }
 #undef TS_SPLIT_HD
 #undef TS_SPLIT
-    if (adv && plan.n_split <= 1) {
+    if (adv && !adv_in_kernel) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         return launch_len_update(d_len, L.S, -1, 1, 0, st);

@@ -154,10 +154,12 @@ struct DecodePlan {
     int chunk;    // positions per split (multiple of 64)
     int n_split;  // splits of the longest sequence (grid.x)
     bool g4;      // the integer kernel, G <= 16 (QK^T on v_mfma_i32_16x16x64_i8)
+    int nw;       // waves per workgroup of the 16x16 kernel (4, or 8 / 16 without a split)
 };
-// n_ctx: keys per sequence (len + 1), on the host; n_cu: compute units of the device.
-// int_gmax: the most query heads per kv head the integer kernel takes at this stored head dim.
-DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, int int_gmax);
+// n_ctx: keys per sequence (len + 1), on the host; n_cu: compute units of the device;
+// stored_hd: the stored head dim (64, 128 or 256); fused: the launch appends the new token
+// (its position is scored from registers, not streamed).
+DecodePlan decode_plan(const int32_t *n_ctx, int n_seq, int n_kv, int G, int n_cu, int stored_hd, bool fused);
 // The integer kernel takes up to 16 query heads per kv head on stored rows up to 128 dims, 8 on
 // 256-dim rows.
 inline int decode_int_gmax(int stored_hd) { return stored_hd <= 128 ? 16 : 8; }

@@ -472,7 +472,7 @@ static int attn_decode(const ts_kv *kv, int32_t layer, const float *d_q, int32_t
     std::vector<int32_t> &ctx = const_cast<ts_kv *>(kv)->h_ctx;
     for (int s = 0; s < kv->d.n_seq; s++) ctx[s] = kv->h_len[s] + 1;
     ts::DecodePlan plan = ts::decode_plan(ctx.data(), kv->d.n_seq, kv->d.n_head_kv, n_head / kv->d.n_head_kv,
-                                          kv->n_cu, ts::decode_int_gmax(kv->hdp));
+                                          kv->n_cu, kv->hdp, k_new != nullptr);
     if (plan.n_split > 1) {
         uint64_t need = 0;
         if (noalloc)  // partials [S][n_head][n_split][hd], then m and l [S][n_head][n_split]

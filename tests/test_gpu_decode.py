@@ -50,6 +50,42 @@ def test_config1_llama32_1b_single_layer(gpu):
     p.check_codes()
 
 
+@pytest.mark.parametrize("hd,n_kv,G,ctx,softcap", [
+    (64, 8, 4, 300, 0.0),     # 5 windows: one 8-wave workgroup per stream
+    (64, 8, 4, 1000, 30.0),   # 16 windows: 16 waves
+    (40, 2, 6, 700, 0.0),     # 40-dim rows stored as 64: 16 waves
+    (128, 8, 3, 511, 0.0),    # 8 windows of 128-dim rows: 8 waves
+    (96, 4, 8, 450, 30.0),    # 96-dim rows stored as 128
+    (64, 8, 12, 600, 0.0),    # two head groups of the 16x16 kernel per kv head
+])
+def test_wide_no_split_plans(gpu, hd, n_kv, G, ctx, softcap):
+    """Batch 1, 5-16 windows of context: one 8- or 16-wave workgroup per stream, no split and
+    no combine launch.  The separate append + attention, the fused one, and the fused one that
+    advances the lengths inside the kernel, each within tolerance; codes bit-exact."""
+    say(f"decode wide hd={hd} n_kv={n_kv} G={G} ctx={ctx} softcap={softcap}")
+    rng = np.random.default_rng(40 + ctx)
+    n_head = n_kv * G
+    p = Pair(1, n_kv, hd, ctx + 4, 500000.0)
+    prefill_cache(p, rng, ctx)
+    out, ref = decode_step(p, rng, n_head, softcap=softcap)
+    assert_close(out, ref, "separate")
+    for adv in (False, True):
+        k = synth.normal(rng, (1, 1, n_kv, hd))
+        v = synth.normal(rng, (1, 1, n_kv, hd))
+        q = synth.normal(rng, (1, n_head, hd))
+        out = p.gpu.attn_decode_append(0, dev(k), dev(v), dev(q), p.rope, softcap=softcap,
+                                       advance=adv).cpu().numpy()
+        p.ora.append(k, v)
+        ref = p.ora.attend(q[:, None], 1, softcap=softcap, threads=8)[:, 0]
+        if adv:
+            p.ora.advance(1)
+        else:
+            p.advance(1)
+        assert_close(out, ref, f"fused, advance={adv}")
+    assert p.gpu.seq_lens() == [ctx + 3]
+    p.check_codes()
+
+
 @pytest.mark.parametrize("scale,yarn", [(0.25, (1.0, 32.0)), (0.5, (0.0, 0.0))])
 def test_scaled_rope_tables(gpu, scale, yarn):
     """A YaRN (preflight.rs:77-97) and a linear (scale < 1, :88-90) table: the appended codes

@@ -90,6 +90,20 @@ def test_graph_replays_advance_without_split(gpu):
     replay_check(p, rng, 32, 3, advance=True)
 
 
+@pytest.mark.parametrize("hd,n_kv,n_head,len0", [(64, 8, 32, 508), (128, 4, 12, 509)])
+def test_graph_replays_wide_plan(gpu, hd, n_kv, n_head, len0):
+    """Batch 1 with 8 windows before the new token: the captured plan is one 8-wave workgroup
+    per stream, no split, the lengths advanced inside the decode kernel.  Replays run the
+    length past 512, where one wave streams a second window the captured plan did not count
+    on."""
+    say(f"graph replays wide plan hd={hd} len0={len0}")
+    rng = np.random.default_rng(330 + hd)
+    p = Pair(1, n_kv, hd, 530, 1e6)
+    fill(p, rng, len0)
+    p.set_lens([len0])
+    replay_check(p, rng, n_head, 7, advance=True)
+
+
 def test_advance_matches_decode_then_increment(gpu):
     """Eager: decode_append(advance=True) gives bit-identical outputs and cache contents to
     decode_append followed by increment(1), and the same lengths, for a split plan (batch 1)."""
