@@ -74,6 +74,12 @@ struct DecodeArgs {
 // workgroup (the barrier orders this workgroup's length reads before its arrival).
 __device__ inline void arrive_and_advance(const DecodeArgs &a) {
     if (!a.adv_ctr) return;
+    if (a.hlen >= 0) {
+        // the length came with the launch and no workgroup reads len[]: one plain store of the
+        // advanced value, no arrival count (a returning atomic's round trip saved)
+        if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) a.adv_len[0] = a.hlen + 1;
+        return;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
         const int n_wg = gridDim.x * gridDim.y * gridDim.z;
