@@ -231,9 +231,11 @@ int ts_attn_decode_append_noalloc(ts_kv *kv, int32_t layer, const float *d_k, co
 
 /* ts_attn_decode_append for the last layer of a decode step, followed by ts_kv_increment(kv, 1)
  * (cache.increment(), server_inference.rs:1355-1358) in the same launch: with a split the
- * combine kernel advances the lengths once all of its workgroups have read them (an arrival
- * counter kept in the cache), so the step needs no separate length-update launch; without a
- * split a length update follows the decode.  Same arguments and errors as
+ * launch's last kernel (the combine kernel with a split, the 16x16 decode kernel without one)
+ * advances the lengths once all of its workgroups have read them (an arrival counter kept in
+ * the cache; with one sequence in an eager call, whose length is a launch argument, a plain
+ * store), so the step needs no separate length-update launch; the integer decode kernel's
+ * plans without a split are followed by a length update.  Same arguments and errors as
  * ts_attn_decode_append.  Lengths must not be read or changed by other work on the cache while
  * the call runs. */
 int ts_attn_decode_append_advance(ts_kv *kv, int32_t layer, const float *d_k, const float *d_v,
